@@ -1,0 +1,127 @@
+/*
+ * kvq.h - C ABI of libkvq.so, the MI355X (gfx950) quantized-KV attention library.
+ *
+ * The library implements the hot path of the reference's memory-bounded attention over an
+ * MLX-layout affine-quantized KV cache:
+ *   - quantize-and-append of new K/V rows into the cache   (reference: mlx-lm
+ *     QuantizedKVCache.update_and_fetch, reached from m5engine/attention.py:106-112 and the
+ *     per-layer attention call; the quantizer is mx.quantize, restated in oracle/quantize.py)
+ *   - attention of queries against the quantized cache      (reference:
+ *     m5engine/attention.py:29-103 blocked_quantized_sdpa, and the L == 1 fallback at :42-45)
+ *
+ * Layout (MLX conventions, all little-endian):
+ *   queries / outputs   T[B][Hq][L][D], last dimension contiguous, other strides free.
+ *   K or V cache        codes  uint32[B][H][S_cap][D*bits/32]  (code k of a word at bits
+ *                                                               [k*bits, (k+1)*bits), LSB first)
+ *                       scales T[B][H][S_cap][D/group]
+ *                       biases T[B][H][S_cap][D/group]
+ *                       dequantized value = scale * code + bias
+ *   T is float16 or bfloat16; scales and biases have the same dtype as the K/V rows.
+ *
+ * Conventions:
+ *   - Every entry point returns KVQ_OK (0) or a negative status; it never throws and never
+ *     aborts. kvq_last_error() returns a message for the calling thread's last failure.
+ *   - All pointers are device pointers, except the kvq_rows / kvq_qtensor descriptors
+ *     themselves, which are read on the host during the call.
+ *   - Launches are asynchronous on `stream` (a hipStream_t; NULL = the default stream).
+ *   - The library allocates no device memory: scratch space (the attention workspace) is
+ *     owned by the caller; its size comes from the *_workspace_size functions.
+ *   - Strides are in elements of the pointed-to type.
+ */
+#ifndef KVQ_H
+#define KVQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KVQ_ABI_VERSION 1
+
+/* Element types of queries, K/V rows, outputs, scales and biases. */
+#define KVQ_DTYPE_F16 0
+#define KVQ_DTYPE_BF16 1
+
+/* Status codes. */
+#define KVQ_OK 0
+#define KVQ_ERR_INVALID (-1)     /* bad argument: null pointer, shape, stride, dtype, bits    */
+#define KVQ_ERR_UNSUPPORTED (-2) /* well-formed but not built: head_dim, group size, head ratio */
+#define KVQ_ERR_WORKSPACE (-3)   /* workspace missing or smaller than *_workspace_size()       */
+#define KVQ_ERR_HIP (-4)         /* the HIP runtime reported an error at launch                */
+
+/* A strided T[B][H][L][D] array (D contiguous). */
+typedef struct kvq_rows {
+  void* data;
+  int64_t stride_b, stride_h, stride_l;
+} kvq_rows;
+
+/* A quantized K or V cache view: the (codes, scales, biases) triple of the reference. */
+typedef struct kvq_qtensor {
+  uint32_t* codes;
+  void* scales;
+  void* biases;
+  int64_t codes_stride_b, codes_stride_h, codes_stride_s; /* in uint32 words; the row itself is contiguous */
+  int64_t sb_stride_b, sb_stride_h, sb_stride_s;          /* in T elements; shared by scales and biases    */
+} kvq_qtensor;
+
+/* ABI version the library was built with (KVQ_ABI_VERSION). */
+int kvq_abi_version(void);
+
+/* Message describing the calling thread's most recent failure ("" if none). */
+const char* kvq_last_error(void);
+
+/*
+ * Quantize rows [0, L) of k_src (and v_src, when not NULL) with MLX's affine quantizer and
+ * write them to rows [row_offset, row_offset + L) of k_dst (and v_dst), in one launch.
+ * Replaces: mx.quantize inside mlx-lm QuantizedKVCache.update_and_fetch (third-party, called
+ * per layer by the model's attention) and KVCache.to_quantized, used by
+ * m5engine/attention.py:106-112 (safe_maybe_quantize_kv_cache). Codes, scales and biases are
+ * bit-identical to the CPU restatement in oracle/quantize.py.
+ * Supported: bits in {2, 4, 8}; group_size in {32, 64, 128}; D a multiple of group_size and of 8.
+ */
+int kvq_quantize_append(const kvq_rows* k_src, const kvq_qtensor* k_dst,
+                        const kvq_rows* v_src, const kvq_qtensor* v_dst,
+                        int64_t row_offset, int B, int H, int L, int D,
+                        int bits, int group_size, int dtype, void* stream);
+
+/*
+ * Attention of L query rows per sequence against a quantized cache, for small L (decode):
+ * out = softmax(scale * q K^T + mask) V over the dequantized K/V.
+ * Replaces: m5engine/attention.py:42-45 (the L == 1 hand-off to mlx-lm's
+ * quantized_scaled_dot_product_attention) and, for L > 1, the blocked loop at :64-103.
+ * Requirements: (Hq / Hkv) * L <= 16 * 64 / D; D in {64, 128}; group_size 64; bits in {4, 8}.
+ *   seq_lens: NULL (every sequence has S keys) or device int32[B] with 1 <= seq_lens[b] <= S.
+ *   causal:   query l of sequence b sits at position seq_len_b - L + l and sees keys <= it.
+ *   window:   0 = none; otherwise keys k > position - window only (sliding window).
+ *   workspace: device buffer of at least kvq_decode_workspace_size(...) bytes.
+ */
+int kvq_decode_attn(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v,
+                    const int32_t* seq_lens, const kvq_rows* out,
+                    int B, int Hq, int Hkv, int L, int D, int S,
+                    int bits, int group_size, int dtype,
+                    float scale, int causal, int window,
+                    void* workspace, size_t workspace_bytes, void* stream);
+
+size_t kvq_decode_workspace_size(int B, int Hq, int Hkv, int L, int D, int S, int window);
+
+/*
+ * Attention for prefill chunks (any L): same contract as kvq_decode_attn, MFMA tiles with
+ * K/V tiles dequantized into LDS. Replaces m5engine/attention.py:29-103 for L > 1.
+ * Requirements: D == 128; group_size 64; bits in {4, 8}; Hq a multiple of Hkv.
+ */
+int kvq_prefill_attn(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v,
+                     const int32_t* seq_lens, const kvq_rows* out,
+                     int B, int Hq, int Hkv, int L, int D, int S,
+                     int bits, int group_size, int dtype,
+                     float scale, int causal, int window,
+                     void* workspace, size_t workspace_bytes, void* stream);
+
+size_t kvq_prefill_workspace_size(int B, int Hq, int Hkv, int L, int D, int S, int window);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KVQ_H */

@@ -1,0 +1,161 @@
+"""ctypes binding of libkvq.so (declared in include/kvq.h).
+
+The library is loaded once, after torch, so that it binds to the HIP runtime torch already
+loaded (it is linked against torch/lib/libamdhip64.so). A missing or stale library raises at
+load time; there is no fallback path.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from ctypes import POINTER, c_char_p, c_float, c_int, c_int64, c_size_t, c_void_p
+from pathlib import Path
+
+import torch  # noqa: F401  (binds the HIP runtime before libkvq.so is loaded)
+
+LIB_PATH = Path(__file__).resolve().parent / "libkvq.so"
+ABI_VERSION = 1
+
+DTYPE_F16 = 0
+DTYPE_BF16 = 1
+
+OK = 0
+ERR_INVALID = -1
+ERR_UNSUPPORTED = -2
+ERR_WORKSPACE = -3
+ERR_HIP = -4
+
+# Function name -> (restype, argtypes); the complete export list of include/kvq.h.
+
+
+class Rows(ctypes.Structure):
+    """kvq_rows: a strided T[B][H][L][D] array (D contiguous)."""
+
+    _fields_ = [("data", c_void_p), ("stride_b", c_int64), ("stride_h", c_int64), ("stride_l", c_int64)]
+
+
+class QTensor(ctypes.Structure):
+    """kvq_qtensor: the (codes, scales, biases) triple of one quantized K or V cache view."""
+
+    _fields_ = [
+        ("codes", c_void_p),
+        ("scales", c_void_p),
+        ("biases", c_void_p),
+        ("codes_stride_b", c_int64),
+        ("codes_stride_h", c_int64),
+        ("codes_stride_s", c_int64),
+        ("sb_stride_b", c_int64),
+        ("sb_stride_h", c_int64),
+        ("sb_stride_s", c_int64),
+    ]
+
+
+_ATTN_ARGS = [
+    POINTER(Rows), POINTER(QTensor), POINTER(QTensor), c_void_p, POINTER(Rows),
+    c_int, c_int, c_int, c_int, c_int, c_int,  # B Hq Hkv L D S
+    c_int, c_int, c_int,  # bits group dtype
+    c_float, c_int, c_int,  # scale causal window
+    c_void_p, c_size_t, c_void_p,  # workspace bytes stream
+]
+_WS_ARGS = [c_int, c_int, c_int, c_int, c_int, c_int, c_int]
+
+SIGNATURES = {
+    "kvq_abi_version": (c_int, []),
+    "kvq_last_error": (c_char_p, []),
+    "kvq_quantize_append": (
+        c_int,
+        [POINTER(Rows), POINTER(QTensor), POINTER(Rows), POINTER(QTensor), c_int64,
+         c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_void_p],
+    ),
+    "kvq_decode_attn": (c_int, _ATTN_ARGS),
+    "kvq_decode_workspace_size": (c_size_t, _WS_ARGS),
+    "kvq_prefill_attn": (c_int, _ATTN_ARGS),
+    "kvq_prefill_workspace_size": (c_size_t, _WS_ARGS),
+}
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+
+def lib() -> ctypes.CDLL:
+    """Load libkvq.so (once) and declare its signatures. Raises if it is missing or stale."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not LIB_PATH.exists():
+            raise ImportError(
+                f"{LIB_PATH} is missing: build it with `python -m myinfer_amd._build` "
+                "(the HIP kernels have no fallback)"
+            )
+        handle = ctypes.CDLL(str(LIB_PATH))
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        ver = handle.kvq_abi_version()
+        if ver != ABI_VERSION:
+            raise ImportError(f"{LIB_PATH} has ABI version {ver}, expected {ABI_VERSION}; rebuild it")
+        _lib = handle
+        return handle
+
+
+def last_error() -> str:
+    msg = lib().kvq_last_error()
+    return msg.decode() if msg else ""
+
+
+def check(rc: int, what: str) -> None:
+    """Map a kvq status code to a Python exception."""
+    if rc == OK:
+        return
+    msg = f"{what}: {last_error()}"
+    if rc == ERR_INVALID:
+        raise ValueError(msg)
+    if rc == ERR_UNSUPPORTED:
+        raise NotImplementedError(msg)
+    raise RuntimeError(f"{msg} (status {rc})")
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    if dtype == torch.float16:
+        return DTYPE_F16
+    if dtype == torch.bfloat16:
+        return DTYPE_BF16
+    raise ValueError(f"unsupported dtype {dtype}: expected float16 or bfloat16")
+
+
+def rows(t: torch.Tensor) -> Rows:
+    """Descriptor of a [B, H, L, D] tensor whose last dimension is contiguous."""
+    if t.dim() != 4:
+        raise ValueError(f"expected a 4-D [B, H, L, D] tensor, got shape {tuple(t.shape)}")
+    if t.stride(-1) != 1:
+        raise ValueError("the last dimension must be contiguous")
+    return Rows(t.data_ptr(), t.stride(0), t.stride(1), t.stride(2))
+
+
+def qtensor(codes: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor) -> QTensor:
+    """Descriptor of a quantized [B, H, S, *] triple (codes uint32, scales/biases in T)."""
+    for name, t in (("codes", codes), ("scales", scales), ("biases", biases)):
+        if t.dim() != 4:
+            raise ValueError(f"{name} must be 4-D [B, H, S, *], got shape {tuple(t.shape)}")
+        if t.stride(-1) != 1:
+            raise ValueError(f"{name}: the last dimension must be contiguous")
+    if codes.dtype not in (torch.uint32, torch.int32):
+        raise ValueError(f"codes must be uint32, got {codes.dtype}")
+    if scales.dtype != biases.dtype:
+        raise ValueError("scales and biases must share a dtype")
+    if scales.stride() != biases.stride() or scales.shape != biases.shape:
+        raise ValueError("scales and biases must have identical shapes and strides")
+    return QTensor(
+        codes.data_ptr(), scales.data_ptr(), biases.data_ptr(),
+        codes.stride(0), codes.stride(1), codes.stride(2),
+        scales.stride(0), scales.stride(1), scales.stride(2),
+    )
+
+
+def stream_ptr(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream

@@ -1,0 +1,163 @@
+"""Memory-bounded attention over a quantized KV cache, on MI355X.
+
+Drop-in counterpart of m5engine/attention.py: the same public names and argument meaning,
+over torch tensors in MLX layout on the GPU, executed by libkvq.so's HIP kernels.
+
+  blocked_quantized_sdpa(queries, q_keys, q_values, scale, mask, group_size=64, bits=8)
+      reference: m5engine/attention.py:29-103. The GPU kernels stream the cache in 32-key
+      tiles with an online softmax (split-K decode for small L, MFMA tiles for prefill), so no
+      score matrix is ever materialised; the only transient memory is the split workspace.
+  quantized_scaled_dot_product_attention(...)
+      the L == 1 entry mlx-lm calls (captured at m5engine/attention.py:19, used at :42-45);
+      here it is the same kernels.
+  safe_maybe_quantize_kv_cache(prompt_cache, quantized_kv_start, kv_group_size, kv_bits)
+      reference: m5engine/attention.py:106-112.
+  install(base_module=None, generate_module=None)
+      reference: m5engine/attention.py:115-126 (idempotent patch of the host framework's
+      quantized-SDPA and cache-quantization hooks).
+
+``score_budget_bytes`` and ``MIN_BLOCK`` keep the reference's values (:21-22) and its block rule
+(:40-41, ``block_size``) for callers and tests that read them; the GPU path does not need them.
+
+Masks (the reference accepts None, a string, or an array):
+  None                  every cached key is visible
+  any str               causal, queries at positions S - L .. S - 1 (reference :55-58)
+  bool tensor           recognised when it is a causal mask, a causal sliding window, or either
+                        with right padding per batch row (keys >= S_b masked); anything else
+                        raises NotImplementedError
+  additive float        all-zero only; anything else raises NotImplementedError
+Keyword extensions: ``window=`` (sliding window) and ``seq_lens=`` (int32 [B] valid key counts)
+give the same structure without building a mask.
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from . import kernels
+from .cache import KVCache
+
+score_budget_bytes = 512 * 1024**2
+MIN_BLOCK = 256
+
+
+def block_size(B: int, n_q_heads: int, L: int) -> int:
+    """The reference's key-block length (m5engine/attention.py:40-41), read at call time."""
+    per_key = B * n_q_heads * L * 4 * 3
+    return max(MIN_BLOCK, score_budget_bytes // max(per_key, 1))
+
+
+def _slice_keys(q, start, end):
+    """Slice every member of a (codes, scales, biases) triple along the key axis (:25-26)."""
+    return tuple(x[..., start:end, :] for x in q)
+
+
+def _expected_mask(L: int, S: int, S_b: torch.Tensor, causal: bool, window: int, device) -> torch.Tensor:
+    k = torch.arange(S, device=device)[None, None, :]
+    pos = (S_b[:, None] - L + torch.arange(L, device=device)[None, :])[:, :, None]
+    m = k < S_b[:, None, None]
+    if causal:
+        m = m & (k <= pos)
+    if window > 0:
+        m = m & (k > pos - window)
+    return m  # [B, L, S]
+
+
+def mask_structure(mask, B: int, n_q_heads: int, L: int, S: int):
+    """Translate a reference-style mask into (causal, window, seq_lens) for the kernels."""
+    if mask is None:
+        return False, 0, None
+    if isinstance(mask, str):
+        return True, 0, None
+    if not torch.is_tensor(mask):
+        raise NotImplementedError(f"unsupported mask type {type(mask)}")
+    if mask.dtype != torch.bool:
+        if bool((mask == 0).all()):
+            return False, 0, None
+        raise NotImplementedError("additive masks other than all-zero are not supported by the GPU kernels")
+    m = mask
+    while m.dim() < 4:
+        m = m.unsqueeze(0)
+    if m.shape[-2:] != (L, S):
+        raise ValueError(f"mask's last two dims {tuple(m.shape[-2:])} do not match (L, S) = {(L, S)}")
+    m = m.expand(B, m.shape[1], L, S)
+    if m.shape[1] > 1 and not bool((m == m[:, :1]).all()):
+        raise NotImplementedError("per-head masks are not supported by the GPU kernels")
+    m = m[:, 0]  # [B, L, S]
+    # valid key count of each sequence = one past the last visible key of its last query row
+    last = m[:, L - 1]
+    idx = torch.arange(1, S + 1, device=m.device)
+    S_b = torch.where(last, idx, torch.zeros_like(idx)).amax(dim=1)
+    first_row_count = m[:, L - 1].sum(dim=1)
+    full = bool((S_b == S).all())
+    for causal in (True, False):
+        # window = number of visible keys of the last row when it is smaller than S_b
+        win_t = torch.where(first_row_count < S_b, first_row_count, torch.zeros_like(first_row_count))
+        windows = set(win_t.tolist())
+        if len(windows) != 1:
+            continue
+        window = int(windows.pop())
+        if window and not causal:
+            continue
+        if bool(torch.equal(m, _expected_mask(L, S, S_b, causal, window, m.device))):
+            seq = None if full else S_b.to(torch.int32)
+            return causal, window, seq
+    raise NotImplementedError("this boolean mask is not a causal / sliding-window / right-padding mask")
+
+
+def blocked_quantized_sdpa(queries: torch.Tensor, q_keys, q_values, scale: float, mask, group_size: int = 64,
+                           bits: int = 8, *, window: int = 0, seq_lens: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """softmax(scale * Q K^T + mask) V over an affine-quantized cache (m5engine/attention.py:29-103).
+
+    queries [B, Hq, L, D] (float16/bfloat16, CUDA); q_keys, q_values: (codes uint32
+    [B, Hkv, S, D*bits/32], scales, biases [B, Hkv, S, D/group_size]) in the queries' dtype.
+    Query head h reads KV head h // (Hq / Hkv) (:47-53). Returns [B, Hq, L, D] in the queries'
+    dtype. Rows that see no key return 0, as the reference's blocked path does.
+    """
+    B, n_q_heads, L, D = queries.shape
+    S = q_keys[0].shape[-2]
+    causal, mwin, mseq = mask_structure(mask, B, n_q_heads, L, S)
+    if window and mwin and window != mwin:
+        raise ValueError(f"window={window} disagrees with the mask's window {mwin}")
+    window = window or mwin
+    if seq_lens is None:
+        seq_lens = mseq
+    if window and not causal:
+        causal = True
+    return kernels.attention(queries, tuple(q_keys), tuple(q_values), scale, causal=causal, window=window,
+                             seq_lens=seq_lens, group_size=group_size, bits=bits)
+
+
+def quantized_scaled_dot_product_attention(queries, q_keys, q_values, scale, mask, group_size: int = 64,
+                                           bits: int = 8):
+    """The entry mlx-lm's models call for quantized caches; same kernels as the blocked path."""
+    return blocked_quantized_sdpa(queries, q_keys, q_values, scale, mask, group_size, bits)
+
+
+def safe_maybe_quantize_kv_cache(prompt_cache, quantized_kv_start, kv_group_size, kv_bits) -> None:
+    """Quantize only plain KV caches; sliding-window and recurrent caches stay as-is
+    (m5engine/attention.py:106-112). Mutates `prompt_cache` in place."""
+    if kv_bits is None:
+        return
+    for i, c in enumerate(prompt_cache):
+        if type(c) is KVCache and c.offset >= quantized_kv_start:
+            prompt_cache[i] = c.to_quantized(group_size=kv_group_size, bits=kv_bits)
+
+
+_installed = False
+
+
+def install(base_module=None, generate_module=None) -> None:
+    """Route a host framework's quantized attention and cache quantization to this module
+    (m5engine/attention.py:118-126): sets `quantized_scaled_dot_product_attention` on
+    `base_module` and `maybe_quantize_kv_cache` on `generate_module` when given. Idempotent."""
+    global _installed
+    if _installed:
+        return
+    if base_module is not None:
+        base_module.quantized_scaled_dot_product_attention = blocked_quantized_sdpa
+    if generate_module is not None:
+        generate_module.maybe_quantize_kv_cache = safe_maybe_quantize_kv_cache
+    _installed = True

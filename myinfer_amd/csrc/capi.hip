@@ -1,0 +1,168 @@
+// C ABI of libkvq.so: argument validation, error reporting, dispatch to the kernel launchers.
+// Every check runs on the host before any HIP call, so a rejected call touches no device state.
+
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "launch.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int ok() {
+  g_err[0] = '\0';
+  return KVQ_OK;
+}
+
+int hip_status(hipError_t e, const char* what) {
+  if (e == hipSuccess) return ok();
+  return fail(KVQ_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }
+
+int check_dtype(int dtype) {
+  if (dtype != KVQ_DTYPE_F16 && dtype != KVQ_DTYPE_BF16) return fail(KVQ_ERR_INVALID, "dtype %d is not f16 (0) or bf16 (1)", dtype);
+  return KVQ_OK;
+}
+
+int check_qtensor(const kvq_qtensor* t, const char* name) {
+  if (!t) return fail(KVQ_ERR_INVALID, "%s descriptor is NULL", name);
+  if (!t->codes || !t->scales || !t->biases) return fail(KVQ_ERR_INVALID, "%s has a NULL codes/scales/biases pointer", name);
+  if (t->codes_stride_b < 0 || t->codes_stride_h < 0 || t->codes_stride_s <= 0 || t->sb_stride_b < 0 ||
+      t->sb_stride_h < 0 || t->sb_stride_s <= 0)
+    return fail(KVQ_ERR_INVALID, "%s has a negative or zero stride", name);
+  if (!aligned(t->scales, 2) || !aligned(t->biases, 2)) return fail(KVQ_ERR_INVALID, "%s scales/biases are not 2-byte aligned", name);
+  return KVQ_OK;
+}
+
+int check_rows(const kvq_rows* r, const char* name, int D, bool vec16) {
+  if (!r || !r->data) return fail(KVQ_ERR_INVALID, "%s is NULL", name);
+  if (r->stride_b < 0 || r->stride_h < 0 || r->stride_l < 0) return fail(KVQ_ERR_INVALID, "%s has a negative stride", name);
+  if (vec16) {
+    if (!aligned(r->data, 16) || r->stride_b % 8 || r->stride_h % 8 || r->stride_l % 8 || D % 8)
+      return fail(KVQ_ERR_INVALID, "%s must be 16-byte aligned with strides that are multiples of 8 elements", name);
+  } else if (!aligned(r->data, 2)) {
+    return fail(KVQ_ERR_INVALID, "%s is not 2-byte aligned", name);
+  }
+  return KVQ_OK;
+}
+
+int check_attn(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v, const kvq_rows* out, int B, int Hq,
+               int Hkv, int L, int D, int S, int bits, int group_size, int dtype, float scale, int window,
+               size_t ws_needed, void* workspace, size_t workspace_bytes) {
+  int rc;
+  if ((rc = check_dtype(dtype))) return rc;
+  if (B <= 0 || Hq <= 0 || Hkv <= 0 || L <= 0 || S <= 0) return fail(KVQ_ERR_INVALID, "B, Hq, Hkv, L and S must be positive (got %d, %d, %d, %d, %d)", B, Hq, Hkv, L, S);
+  if (Hq % Hkv) return fail(KVQ_ERR_INVALID, "Hq=%d is not a multiple of Hkv=%d", Hq, Hkv);
+  if (bits != 4 && bits != 8) return fail(KVQ_ERR_UNSUPPORTED, "attention supports 4- and 8-bit caches, got bits=%d", bits);
+  if (group_size != 64) return fail(KVQ_ERR_UNSUPPORTED, "attention supports group_size 64, got %d", group_size);
+  if (window < 0) return fail(KVQ_ERR_INVALID, "window must be >= 0, got %d", window);
+  if (!isfinite(scale)) return fail(KVQ_ERR_INVALID, "scale is not finite");
+  if ((rc = check_rows(q, "queries", D, true))) return rc;
+  if ((rc = check_rows(out, "out", D, false))) return rc;
+  if ((rc = check_qtensor(k, "keys"))) return rc;
+  if ((rc = check_qtensor(v, "values"))) return rc;
+  const int64_t row_words = (int64_t)D * bits / 32;
+  for (const kvq_qtensor* t : {k, v}) {
+    if (!aligned(t->codes, 16) || (t->codes_stride_s * 4) % 16 || (t->codes_stride_h * 4) % 16 || (t->codes_stride_b * 4) % 16)
+      return fail(KVQ_ERR_INVALID, "codes must be 16-byte aligned with 16-byte-multiple row, head and batch strides");
+    if (t->codes_stride_s < row_words) return fail(KVQ_ERR_INVALID, "codes row stride %lld is smaller than D*bits/32=%lld", (long long)t->codes_stride_s, (long long)row_words);
+    if (t->sb_stride_s < D / 64) return fail(KVQ_ERR_INVALID, "scales row stride %lld is smaller than D/group=%d", (long long)t->sb_stride_s, D / 64);
+  }
+  if (!workspace || workspace_bytes < ws_needed)
+    return fail(KVQ_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", ws_needed, workspace ? workspace_bytes : (size_t)0);
+  if (!aligned(workspace, 256)) return fail(KVQ_ERR_WORKSPACE, "workspace must be 256-byte aligned");
+  return KVQ_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int kvq_abi_version(void) { return KVQ_ABI_VERSION; }
+
+const char* kvq_last_error(void) { return g_err; }
+
+int kvq_quantize_append(const kvq_rows* k_src, const kvq_qtensor* k_dst, const kvq_rows* v_src,
+                        const kvq_qtensor* v_dst, int64_t row_offset, int B, int H, int L, int D, int bits,
+                        int group_size, int dtype, void* stream) {
+  int rc;
+  if ((rc = check_dtype(dtype))) return rc;
+  if (bits != 2 && bits != 4 && bits != 8) return fail(KVQ_ERR_UNSUPPORTED, "bits must be 2, 4 or 8, got %d", bits);
+  if (group_size != 32 && group_size != 64 && group_size != 128)
+    return fail(KVQ_ERR_UNSUPPORTED, "group_size must be 32, 64 or 128, got %d", group_size);
+  if (B < 0 || H < 0 || L < 0 || D <= 0) return fail(KVQ_ERR_INVALID, "negative shape (B=%d H=%d L=%d D=%d)", B, H, L, D);
+  if (D % group_size) return fail(KVQ_ERR_INVALID, "D=%d is not a multiple of group_size=%d", D, group_size);
+  if (row_offset < 0) return fail(KVQ_ERR_INVALID, "row_offset must be >= 0");
+  if ((v_src == nullptr) != (v_dst == nullptr)) return fail(KVQ_ERR_INVALID, "v_src and v_dst must both be given or both be NULL");
+  if ((rc = check_rows(k_src, "k_src", D, true))) return rc;
+  if ((rc = check_qtensor(k_dst, "k_dst"))) return rc;
+  if (v_src) {
+    if ((rc = check_rows(v_src, "v_src", D, true))) return rc;
+    if ((rc = check_qtensor(v_dst, "v_dst"))) return rc;
+  }
+  const int64_t row_words = (int64_t)D * bits / 32;
+  for (const kvq_qtensor* t : {k_dst, v_dst}) {
+    if (!t) continue;
+    if (t->codes_stride_s < row_words) return fail(KVQ_ERR_INVALID, "codes row stride is smaller than D*bits/32");
+    if (bits == 8 && (!aligned(t->codes, 8) || t->codes_stride_s % 2 || t->codes_stride_h % 2 || t->codes_stride_b % 2))
+      return fail(KVQ_ERR_INVALID, "8-bit codes must be 8-byte aligned with even word strides");
+    if (t->sb_stride_s < D / group_size) return fail(KVQ_ERR_INVALID, "scales row stride is smaller than D/group_size");
+  }
+  if (B == 0 || H == 0 || L == 0) return ok();
+  return hip_status(kvq::launch_quantize_append(k_src, k_dst, v_src, v_dst, row_offset, B, H, L, D, bits, group_size,
+                                                dtype, (hipStream_t)stream),
+                    "quantize_append launch");
+}
+
+size_t kvq_decode_workspace_size(int B, int Hq, int Hkv, int L, int D, int S, int window) {
+  if (B <= 0 || Hq <= 0 || Hkv <= 0 || L <= 0 || S <= 0 || (D != 64 && D != 128) || window < 0) return 0;
+  // the plan depends on bits only through the chunk length; size for the larger split count
+  const size_t a = kvq::decode_workspace_bytes(B, Hq, Hkv, L, D, S, window, 8);
+  const size_t b = kvq::decode_workspace_bytes(B, Hq, Hkv, L, D, S, window, 4);
+  return a > b ? a : b;
+}
+
+int kvq_decode_attn(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v, const int32_t* seq_lens,
+                    const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int bits, int group_size,
+                    int dtype, float scale, int causal, int window, void* workspace, size_t workspace_bytes,
+                    void* stream) {
+  if (D != 64 && D != 128) return fail(KVQ_ERR_UNSUPPORTED, "decode supports head_dim 64 and 128, got %d", D);
+  int rc = check_attn(q, k, v, out, B, Hq, Hkv, L, D, S, bits, group_size, dtype, scale, window,
+                      kvq_decode_workspace_size(B, Hq, Hkv, L, D, S, window), workspace, workspace_bytes);
+  if (rc) return rc;
+  return hip_status(kvq::launch_decode(q, k, v, seq_lens, out, B, Hq, Hkv, L, D, S, bits, dtype, scale, causal,
+                                       window, workspace, (hipStream_t)stream),
+                    "decode_attn launch");
+}
+
+size_t kvq_prefill_workspace_size(int B, int Hq, int Hkv, int L, int D, int S, int window) {
+  if (B <= 0 || Hq <= 0 || Hkv <= 0 || L <= 0 || S <= 0 || D != 128 || window < 0 || Hq % Hkv) return 0;
+  return kvq::prefill_workspace_bytes(B, Hq, Hkv, L, D, S, window, 8);
+}
+
+int kvq_prefill_attn(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v, const int32_t* seq_lens,
+                     const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int bits, int group_size,
+                     int dtype, float scale, int causal, int window, void* workspace, size_t workspace_bytes,
+                     void* stream) {
+  if (D != 128) return fail(KVQ_ERR_UNSUPPORTED, "prefill supports head_dim 128, got %d", D);
+  int rc = check_attn(q, k, v, out, B, Hq, Hkv, L, D, S, bits, group_size, dtype, scale, window,
+                      kvq_prefill_workspace_size(B, Hq, Hkv, L, D, S, window), workspace, workspace_bytes);
+  if (rc) return rc;
+  return hip_status(kvq::launch_prefill(q, k, v, seq_lens, out, B, Hq, Hkv, L, D, S, bits, dtype, scale, causal,
+                                        window, workspace, (hipStream_t)stream),
+                    "prefill_attn launch");
+}
+
+}  // extern "C"

@@ -1,0 +1,129 @@
+// Shared device helpers for the gfx950 kernels of libkvq.so.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/kvq.h"
+
+namespace kvq {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef float f16v __attribute__((ext_vector_type(16)));
+typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+
+// Element-type tags. Raw storage is always a 16-bit pattern.
+struct F16 {
+  static constexpr int id = KVQ_DTYPE_F16;
+};
+struct BF16 {
+  static constexpr int id = KVQ_DTYPE_BF16;
+};
+
+__device__ __forceinline__ float to_float(uint16_t r, F16) {
+  return (float)__builtin_bit_cast(_Float16, r);
+}
+__device__ __forceinline__ float to_float(uint16_t r, BF16) {
+  return __uint_as_float((uint32_t)r << 16);
+}
+// float -> 16-bit pattern, round to nearest even (the hardware default mode for f16).
+__device__ __forceinline__ uint16_t from_float(float f, F16) {
+  return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+__device__ __forceinline__ uint16_t from_float(float f, BF16) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);  // quiet NaN
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+// Two f16 values packed in a u32 (low half first), rounded to nearest even.
+__device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
+  h2 v = {(_Float16)lo, (_Float16)hi};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Cross-lane helpers (wave64).
+__device__ __forceinline__ float shfl_xor(float v, int mask) {
+  const int lane = __lane_id();
+  return __int_as_float(__builtin_amdgcn_ds_bpermute((lane ^ mask) << 2, __float_as_int(v)));
+}
+__device__ __forceinline__ float shfl(float v, int src_lane) {
+  return __int_as_float(__builtin_amdgcn_ds_bpermute(src_lane << 2, __float_as_int(v)));
+}
+// Rotate within each row of 16 lanes: lane c receives lane (c + n) % 16 of its row.
+template <int N>
+__device__ __forceinline__ float row_rotate(float v) {
+  static_assert(N > 0 && N < 16, "rotation within a DPP row");
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x120 + (16 - N) % 16, 0xF, 0xF, false));
+}
+
+// Byte selection: bytes 0..3 come from `lo`, 4..7 from `hi`; selector byte 0x0C yields 0.
+__device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) {
+  return __builtin_amdgcn_perm(hi, lo, sel);
+}
+
+template <int NBYTES>
+struct Bytes;
+template <>
+struct Bytes<2> {
+  uint32_t w[1];
+  __device__ __forceinline__ void load(const uint8_t* p) { w[0] = *(const uint16_t*)p; }
+};
+template <>
+struct Bytes<4> {
+  uint32_t w[1];
+  __device__ __forceinline__ void load(const uint8_t* p) { w[0] = *(const uint32_t*)p; }
+};
+template <>
+struct Bytes<8> {
+  uint32_t w[2];
+  __device__ __forceinline__ void load(const uint8_t* p) {
+    u2 v = *(const u2*)p;
+    w[0] = v[0];
+    w[1] = v[1];
+  }
+};
+template <>
+struct Bytes<16> {
+  uint32_t w[4];
+  __device__ __forceinline__ void load(const uint8_t* p) {
+    u4 v = *(const u4*)p;
+    w[0] = v[0];
+    w[1] = v[1];
+    w[2] = v[2];
+    w[3] = v[3];
+  }
+};
+template <>
+struct Bytes<32> {
+  uint32_t w[8];
+  __device__ __forceinline__ void load(const uint8_t* p) {
+    u4 a = *(const u4*)p;
+    u4 b = *(const u4*)(p + 16);
+    w[0] = a[0];
+    w[1] = a[1];
+    w[2] = a[2];
+    w[3] = a[3];
+    w[4] = b[0];
+    w[5] = b[1];
+    w[6] = b[2];
+    w[7] = b[3];
+  }
+};
+
+}  // namespace kvq
+
+// Host-side launch plumbing shared by the C-ABI layer.
+namespace kvq_host {
+struct Status {
+  int code;
+  const char* msg;
+};
+void set_error(const char* fmt, ...);
+}  // namespace kvq_host

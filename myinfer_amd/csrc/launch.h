@@ -1,0 +1,26 @@
+// Internal launchers shared between the kernels' translation units and the C-ABI layer.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/kvq.h"
+
+namespace kvq {
+
+hipError_t launch_quantize_append(const kvq_rows* k_src, const kvq_qtensor* k_dst, const kvq_rows* v_src,
+                                  const kvq_qtensor* v_dst, int64_t row_offset, int B, int H, int L, int D, int bits,
+                                  int group_size, int dtype, hipStream_t stream);
+
+size_t decode_workspace_bytes(int B, int Hq, int Hkv, int L, int D, int S, int window, int bits);
+hipError_t launch_decode(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v, const int32_t* seq_lens,
+                         const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int bits, int dtype,
+                         float scale, int causal, int window, void* workspace, hipStream_t stream);
+
+size_t prefill_workspace_bytes(int B, int Hq, int Hkv, int L, int D, int S, int window, int bits);
+hipError_t launch_prefill(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v, const int32_t* seq_lens,
+                          const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int bits, int dtype,
+                          float scale, int causal, int window, void* workspace, hipStream_t stream);
+
+}  // namespace kvq

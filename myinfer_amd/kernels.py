@@ -1,0 +1,157 @@
+"""Typed wrappers around libkvq.so's entry points (torch tensors in, torch tensors out).
+
+Every wrapper validates shapes on the host, passes raw pointers and strides through the C ABI
+and launches on the tensors' current HIP stream. Scratch memory (the attention workspace) is a
+torch allocation cached per (device, stream); the library itself allocates nothing.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from typing import Optional, Sequence, Tuple
+
+import torch
+
+from . import _lib
+
+Triple = Tuple[torch.Tensor, torch.Tensor, torch.Tensor]
+
+_workspaces: dict = {}
+
+
+def _workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
+    key = (device.index, stream)
+    buf = _workspaces.get(key)
+    if buf is None or buf.numel() < nbytes:
+        buf = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        _workspaces[key] = buf
+    return buf
+
+
+def _require_cuda(*tensors: torch.Tensor) -> torch.device:
+    dev = tensors[0].device
+    if dev.type != "cuda":
+        raise ValueError(f"libkvq operates on GPU tensors; got a tensor on {dev}")
+    for t in tensors[1:]:
+        if t.device != dev:
+            raise ValueError(f"all tensors must be on {dev}; got {t.device}")
+    return dev
+
+
+def _check_triple(tr: Sequence[torch.Tensor], name: str) -> None:
+    if len(tr) != 3:
+        raise ValueError(f"{name} must be a (codes, scales, biases) triple")
+
+
+def quantize_append(k: torch.Tensor, k_dst: Triple, v: Optional[torch.Tensor] = None, v_dst: Optional[Triple] = None,
+                    row_offset: int = 0, group_size: int = 64, bits: int = 8) -> None:
+    """Quantize k (and v) [B, H, L, D] and store them at rows [row_offset, row_offset + L) of the
+    (codes, scales, biases) buffers k_dst (and v_dst), in one kernel launch."""
+    _check_triple(k_dst, "k_dst")
+    tens = [k, *k_dst]
+    if v is not None:
+        if v_dst is None:
+            raise ValueError("v_dst is required with v")
+        _check_triple(v_dst, "v_dst")
+        if v.shape != k.shape or v.dtype != k.dtype:
+            raise ValueError("k and v must have the same shape and dtype")
+        tens += [v, *v_dst]
+    dev = _require_cuda(*tens)
+    B, H, L, D = k.shape
+    for tr in [k_dst] + ([v_dst] if v is not None else []):
+        codes, scales, _ = tr
+        if codes.shape[:2] != (B, H) or scales.shape[:2] != (B, H):
+            raise ValueError(f"destination leads {tuple(codes.shape[:2])} do not match source {(B, H)}")
+        if row_offset + L > codes.shape[2] or row_offset + L > scales.shape[2]:
+            raise ValueError(f"rows [{row_offset}, {row_offset + L}) exceed the destination's {codes.shape[2]} rows")
+        if codes.shape[3] != D * bits // 32 or scales.shape[3] != D // group_size:
+            raise ValueError("destination row widths do not match D, bits and group_size")
+        if scales.dtype != k.dtype:
+            raise ValueError("scales/biases must have the dtype of the rows (MLX stores them in T)")
+    L_ = _lib.lib()
+    kr, kq = _lib.rows(k), _lib.qtensor(*k_dst)
+    if v is not None:
+        vr, vq = _lib.rows(v), _lib.qtensor(*v_dst)
+        vr_p, vq_p = ctypes.byref(vr), ctypes.byref(vq)
+    else:
+        vr_p = vq_p = None
+    rc = L_.kvq_quantize_append(ctypes.byref(kr), ctypes.byref(kq), vr_p, vq_p, int(row_offset), B, H, L, D, int(bits),
+                                int(group_size), _lib.dtype_code(k.dtype), _lib.stream_ptr(dev))
+    _lib.check(rc, "kvq_quantize_append")
+
+
+def quantize(x: torch.Tensor, group_size: int = 64, bits: int = 8) -> Triple:
+    """Counterpart of mx.quantize(x, group_size, bits) for x [..., D] on the GPU:
+    returns (codes uint32 [..., D*bits/32], scales [..., D/G], biases [..., D/G])."""
+    _require_cuda(x)
+    lead = x.shape[:-1]
+    D = x.shape[-1]
+    x4 = x.reshape(1, 1, -1, D)
+    if x4.stride(-1) != 1:
+        x4 = x4.contiguous()
+    n = x4.shape[2]
+    codes = torch.empty((1, 1, n, D * bits // 32), dtype=torch.uint32, device=x.device)
+    scales = torch.empty((1, 1, n, D // group_size), dtype=x.dtype, device=x.device)
+    biases = torch.empty_like(scales)
+    quantize_append(x4, (codes, scales, biases), row_offset=0, group_size=group_size, bits=bits)
+    return (codes.reshape(*lead, -1), scales.reshape(*lead, -1), biases.reshape(*lead, -1))
+
+
+def decode_rows_per_pass(D: int) -> int:
+    """Query rows (heads of a GQA group x query positions) one decode pass serves."""
+    return 16 * 64 // D
+
+
+def attention(queries: torch.Tensor, keys: Triple, values: Triple, scale: float, *, causal: bool = False,
+              window: int = 0, seq_lens: Optional[torch.Tensor] = None, group_size: int = 64, bits: int = 8,
+              out: Optional[torch.Tensor] = None, kernel: str = "auto") -> torch.Tensor:
+    """softmax(scale * q K^T + mask) V over a quantized cache. queries [B, Hq, L, D]; keys/values
+    (codes [B, Hkv, S, D*bits/32], scales/biases [B, Hkv, S, D/G]); returns [B, Hq, L, D]
+    (or fills `out`). kernel: "decode", "prefill" or "auto" (decode while the GQA group's query
+    rows fit one MFMA column block, prefill otherwise)."""
+    _check_triple(keys, "keys")
+    _check_triple(values, "values")
+    dev = _require_cuda(queries, *keys, *values)
+    if queries.dim() != 4:
+        raise ValueError(f"queries must be [B, Hq, L, D], got {tuple(queries.shape)}")
+    B, Hq, L, D = queries.shape
+    Hkv, S = keys[0].shape[1], keys[0].shape[2]
+    for name, tr in (("keys", keys), ("values", values)):
+        c, s, b = tr
+        if c.shape[0] != B or c.shape[1] != Hkv or c.shape[2] != S or s.shape[:3] != c.shape[:3]:
+            raise ValueError(f"{name} triple shapes {tuple(c.shape)}, {tuple(s.shape)} do not match B={B}, Hkv={Hkv}, S={S}")
+        if c.shape[3] * 32 // bits != D:
+            raise ValueError(f"{name} codes hold {c.shape[3] * 32 // bits} dims at {bits} bits, queries have {D}")
+        if s.shape[3] * group_size != D:
+            raise ValueError(f"{name} scales hold {s.shape[3]} groups, expected D/group_size = {D // group_size}")
+        if s.dtype != queries.dtype:
+            raise ValueError(f"{name} scales are {s.dtype}, queries are {queries.dtype}")
+    if Hq % Hkv:
+        raise ValueError(f"Hq={Hq} is not a multiple of Hkv={Hkv}")
+    if queries.stride(-1) != 1 or any(st % 8 for st in queries.stride()[:3]) or queries.data_ptr() % 16:
+        queries = queries.contiguous()
+    if out is None:
+        out = torch.empty((B, Hq, L, D), dtype=queries.dtype, device=dev)
+    sl_ptr = None
+    if seq_lens is not None:
+        if seq_lens.dtype != torch.int32 or seq_lens.device != dev or seq_lens.numel() != B:
+            raise ValueError("seq_lens must be an int32 tensor of B entries on the queries' device")
+        sl_ptr = seq_lens.data_ptr()
+    rep = Hq // Hkv
+    if kernel == "auto":
+        kernel = "decode" if (rep * L <= decode_rows_per_pass(D) or D != 128) else "prefill"
+    lib = _lib.lib()
+    ws_fn = lib.kvq_decode_workspace_size if kernel == "decode" else lib.kvq_prefill_workspace_size
+    fn = lib.kvq_decode_attn if kernel == "decode" else lib.kvq_prefill_attn
+    nbytes = ws_fn(B, Hq, Hkv, L, D, S, int(window))
+    if nbytes == 0:
+        raise NotImplementedError(f"{kernel} attention does not support B={B} Hq={Hq} Hkv={Hkv} L={L} D={D} S={S}")
+    stream = _lib.stream_ptr(dev)
+    ws = _workspace(dev, stream, nbytes)
+    qr, orr = _lib.rows(queries), _lib.rows(out)
+    kq, vq = _lib.qtensor(*keys), _lib.qtensor(*values)
+    rc = fn(ctypes.byref(qr), ctypes.byref(kq), ctypes.byref(vq), sl_ptr, ctypes.byref(orr), B, Hq, Hkv, L, D, S,
+            int(bits), int(group_size), _lib.dtype_code(queries.dtype), float(scale), int(bool(causal)), int(window),
+            ws.data_ptr(), ws.numel(), stream)
+    _lib.check(rc, f"kvq_{kernel}_attn")
+    return out
