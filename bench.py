@@ -1,0 +1,367 @@
+#!/usr/bin/env python3
+"""Throughput of the quantized-KV attention hot path on one MI355X.
+
+Headline (BASELINE.json `metric`, config C2): decode attention of Qwen3-32B shapes -- 64 query
+heads / 8 KV heads, head_dim 128, 8-bit affine KV cache with group 64, 32768 cached tokens,
+batch 1, one fp16 query token -- reported as algorithmic HBM GB/s and as a fraction of the
+8 TB/s HBM3E peak.
+
+A step is one attention call (the decode kernel launch(es) of libkvq.so) over one 32K-token
+cache. Inputs are resident in HBM before the timed region starts. Steps rotate over enough
+distinct caches (>= 3, and more than 2.5x the 256 MB Infinity Cache in total) that every step
+streams its cache from HBM rather than from the MALL.
+
+Timing:
+  * value / ms_per_step: the K steps are captured once in a HIP graph and replayed; HIP events
+    on the launch stream bracket the replay (after a device synchronize on both sides).
+  * roofline.achieved: the average duration of one call, from HIP event pairs around each call
+    in an eager run whose launches are queued behind a spin kernel, so the GPU runs them back to
+    back and each event pair brackets the kernels alone.
+  * cpu_baseline: the CPU restatement of the reference algorithm (a torch-CPU port of
+    m5engine/attention.py with the reference's dtype casts) timed on the host's cores on one
+    cache of the same workload, for a bounded number of calls.
+
+Algorithmic bytes of one decode call:
+  sum_b S_b * Hkv * 2 * (D*bits/8 + 2*(D/G)*2)   (K and V codes, scales, biases)
+  + 2 * B * Hq * D * 2                           (the query in, the output out)
+= 272 B per cached token and KV head at 8 bits, 144 B at 4 bits (D = 128, G = 64).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+METRIC = "decode-attn HBM GB/s (% of peak) @32K 8-bit KV; prefill TFLOP/s (% MFMA)"
+PEAK_HBM_GBS = 8000.0  # MI355X HBM3E, published
+MALL_BYTES = 256 << 20  # Infinity Cache
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def decode_bytes(seq_lens, Hq, Hkv, D, bits, G=64, elem=2, window=0):
+    """Algorithmic HBM bytes of one decode call (see the module docstring). With a sliding
+    window only the keys the query can see count: min(S_b, window) per sequence."""
+    row = D * bits // 8 + 2 * (D // G) * elem
+    keys = sum(min(s, window) if window > 0 else s for s in seq_lens)
+    return keys * Hkv * 2 * row + 2 * len(seq_lens) * Hq * D * elem
+
+
+# Decode workloads (seed = 1000 + config number). The headline is C2 at batch 1.
+DECODE = {
+    "C2-b1": dict(desc="Qwen3-32B decode attention, 8-bit KV, 32K context, batch 1", B=1, Hq=64, Hkv=8, D=128,
+                  S=32768, bits=8, dtype="float16", seed=1002),
+    "C1": dict(desc="Qwen3-0.6B decode attention, 8-bit KV, 4096+1 context", B=1, Hq=16, Hkv=8, D=128, S=4097,
+               bits=8, dtype="float16", seed=1001),
+    "C2-b8": dict(desc="Qwen3-32B decode attention, 8-bit KV, batch 8, S_b ~ U[16384, 32768]", B=8, Hq=64, Hkv=8,
+                  D=128, S=32768, bits=8, dtype="float16", seed=1002, varlen=(16384, 32768)),
+    "C4": dict(desc="Qwen3-32B decode attention, 4-bit KV, 131072 context, 1% K outlier channels x8", B=1, Hq=64,
+               Hkv=8, D=128, S=131072, bits=4, dtype="float16", seed=1004, outliers=True),
+    "C5-global": dict(desc="Gemma-3-27B decode step after 8192 prefill, global causal layer, batch 4", B=4, Hq=32,
+                      Hkv=16, D=128, S=8193, bits=8, dtype="bfloat16", seed=1005, causal=True),
+    "C5-window": dict(desc="Gemma-3-27B decode step after 8192 prefill, window-1024 layer, batch 4", B=4, Hq=32,
+                      Hkv=16, D=128, S=8193, bits=8, dtype="bfloat16", seed=1006, causal=True, window=1024),
+}
+
+
+def seq_lens_of(cfg):
+    import torch
+
+    if "varlen" not in cfg:
+        return [cfg["S"]] * cfg["B"]
+    lo, hi = cfg["varlen"]
+    g = torch.Generator().manual_seed(cfg["seed"])
+    return torch.randint(lo, hi + 1, (cfg["B"],), generator=g).tolist()
+
+
+def make_cache(cfg, seed, device):
+    """One seeded cache: K/V ~ N(0,1) in T, quantized by the append kernel into MLX-layout triples."""
+    import torch
+
+    from myinfer_amd import kernels
+
+    B, Hkv, S, D, bits = cfg["B"], cfg["Hkv"], cfg["S"], cfg["D"], cfg["bits"]
+    T = getattr(torch, cfg["dtype"])
+    g = torch.Generator(device=device).manual_seed(seed)
+    trip = []
+    for which in ("k", "v"):
+        x = torch.randn((B, Hkv, S, D), generator=g, device=device, dtype=torch.float32)
+        if which == "k" and cfg.get("outliers"):
+            gc = torch.Generator().manual_seed(seed + 7)
+            nch = max(1, round(0.01 * D))
+            for h in range(Hkv):
+                ch = torch.randperm(D, generator=gc)[:nch].to(device)
+                x[:, h, :, ch] *= 8.0
+        x = x.to(T)
+        codes = torch.empty((B, Hkv, S, D * bits // 32), dtype=torch.int32, device=device).view(torch.uint32)
+        scales = torch.empty((B, Hkv, S, D // 64), dtype=T, device=device)
+        biases = torch.empty_like(scales)
+        kernels.quantize_append(x, (codes, scales, biases), row_offset=0, group_size=64, bits=bits)
+        del x
+        trip.append((codes, scales, biases))
+    return trip[0], trip[1]
+
+
+def calibrate_spin(torch, target_ms):
+    """Cycles of torch.cuda._sleep that keep the GPU busy for about target_ms."""
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    n = 1 << 20
+    torch.cuda.synchronize()
+    s.record()
+    torch.cuda._sleep(n)
+    e.record()
+    torch.cuda.synchronize()
+    ms = max(s.elapsed_time(e), 1e-3)
+    return int(min(n * target_ms / ms, 1 << 34))
+
+
+def time_decode(cfg, steps, warmup, device, want_parity=False):
+    """Run one decode workload; returns a dict of timings (and the caches for the CPU leg)."""
+    import torch
+
+    from myinfer_amd import kernels
+
+    lens = seq_lens_of(cfg)
+    nbytes = decode_bytes(lens, cfg["Hq"], cfg["Hkv"], cfg["D"], cfg["bits"], window=cfg.get("window", 0))
+    ncache = max(3, math.ceil(2.5 * MALL_BYTES / nbytes))  # the bytes a call reads must miss the MALL
+    T = getattr(torch, cfg["dtype"])
+    log(f"[bench] {cfg['desc']}: {nbytes / 1e6:.2f} MB per call, rotating {ncache} caches")
+    caches = [make_cache(cfg, cfg["seed"] * 100 + i, device) for i in range(ncache)]
+    gq = torch.Generator(device=device).manual_seed(cfg["seed"] + 2)
+    q = torch.randn((cfg["B"], cfg["Hq"], 1, cfg["D"]), generator=gq, device=device).to(T)
+    out = torch.empty_like(q)
+    sl = None if "varlen" not in cfg else torch.tensor(lens, dtype=torch.int32, device=device)
+    scale = 1.0 / math.sqrt(cfg["D"])
+    calls = [kernels.prepare_attention(q, kt, vt, scale, causal=cfg.get("causal", False),
+                                       window=cfg.get("window", 0), seq_lens=sl, bits=cfg["bits"], out=out,
+                                       kernel="decode") for kt, vt in caches]
+    for i in range(warmup):
+        calls[i % ncache]()
+    torch.cuda.synchronize()
+
+    # per-call durations: event pairs around eager calls queued behind a spin kernel
+    nev = min(steps, 100)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(nev)]
+    cycles = calibrate_spin(torch, 20.0 + 0.05 * nev)
+    torch.cuda.synchronize()
+    torch.cuda._sleep(cycles)
+    for i in range(nev):
+        ev[i][0].record()
+        calls[i % ncache]()
+        ev[i][1].record()
+    torch.cuda.synchronize()
+    per_call_ms = [a.elapsed_time(b) for a, b in ev]
+    per_call_ms.sort()
+    call_us_mean = 1e3 * sum(per_call_ms) / len(per_call_ms)
+    call_us_median = 1e3 * per_call_ms[len(per_call_ms) // 2]
+
+    # the timed region: K steps captured in one HIP graph, replayed
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        # the prepared calls launch on the stream that was current when they were built; rebuild
+        # them on the capture stream
+        gcalls = [kernels.prepare_attention(q, kt, vt, scale, causal=cfg.get("causal", False),
+                                            window=cfg.get("window", 0), seq_lens=sl, bits=cfg["bits"], out=out,
+                                            kernel="decode") for kt, vt in caches]
+    with torch.cuda.graph(graph, stream=side):
+        for i in range(steps):
+            gcalls[i % ncache]()
+    graph.replay()  # untimed graph warm-up
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    s.record()
+    graph.replay()
+    e.record()
+    torch.cuda.synchronize()
+    total_ms = s.elapsed_time(e)
+    ms_per_step = total_ms / steps
+
+    res = dict(bytes=nbytes, ncache=ncache, ms_per_step=ms_per_step, gbs=nbytes / (ms_per_step * 1e-3) / 1e9,
+               call_us_mean=call_us_mean, call_us_median=call_us_median,
+               kernel_gbs=nbytes / (call_us_mean * 1e-6) / 1e9, seq_lens=lens)
+    if want_parity:
+        res["parity"] = parity_check(cfg, q, caches[0], sl, scale)
+        res["cpu_inputs"] = (q, caches[0], scale)
+    del graph, calls, gcalls
+    return res
+
+
+def parity_check(cfg, q, cache, sl, scale):
+    """One call against the exact fp64 oracle (the bench's own sanity check of what it times)."""
+    import numpy as np
+    import torch
+
+    from myinfer_amd import kernels
+    from oracle import attention as OA
+    from oracle import quantize as OQ
+
+    out = kernels.attention(q, cache[0], cache[1], scale, causal=cfg.get("causal", False),
+                            window=cfg.get("window", 0), seq_lens=sl, bits=cfg["bits"], kernel="decode")
+    torch.cuda.synchronize()
+    dt = cfg["dtype"]
+
+    def trip(tr):
+        c, s, b = tr
+        return (c.cpu().view(torch.int32).numpy().view(np.uint32), s.cpu().view(torch.int16).numpy().view(np.uint16),
+                b.cpu().view(torch.int16).numpy().view(np.uint16))
+
+    kdq = OQ.dequantize(*trip(cache[0]), dt, 64, cfg["bits"])
+    vdq = OQ.dequantize(*trip(cache[1]), dt, 64, cfg["bits"])
+    ref = OA.exact_attention(q.cpu().double().numpy(), kdq, vdq, scale, causal=cfg.get("causal", False),
+                             window=cfg.get("window", 0), seq_lens=None if sl is None else sl.cpu().tolist())
+    st = OA.error_stats(out.cpu().double().numpy(), ref)
+    return {"vs": "exact fp64 oracle", "max_abs": st["max_abs"], "rel_l2": st["rel_l2"]}
+
+
+def cpu_baseline(cfg, q, cache, scale, budget_s=15.0, max_calls=8):
+    """The reference algorithm restated for the CPU (oracle.attention.reference_sdpa: mlx-lm's
+    quantized SDPA for L == 1 with the reference's dtype casts), timed on the host's cores."""
+    import torch
+
+    from oracle import attention as OA
+
+    ncores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(ncores)
+
+    def cpu_trip(tr):
+        c, s, b = tr
+        return (c.cpu().view(torch.int32).to(torch.int64) & 0xFFFFFFFF, s.cpu(), b.cpu())
+
+    qc = q.cpu()
+    kt, vt = cpu_trip(cache[0]), cpu_trip(cache[1])
+    OA.reference_sdpa(qc, kt, vt, scale, None, 64, cfg["bits"])  # warm-up (allocator, threads)
+    times = []
+    t_all = time.perf_counter()
+    while len(times) < max_calls and (time.perf_counter() - t_all) < budget_s:
+        t0 = time.perf_counter()
+        OA.reference_sdpa(qc, kt, vt, scale, None, 64, cfg["bits"])
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    med = times[len(times) // 2]
+    lens = [cfg["S"]] * cfg["B"]
+    nbytes = decode_bytes(lens, cfg["Hq"], cfg["Hkv"], cfg["D"], cfg["bits"])
+    cpu_model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {
+        "value": round(nbytes / med / 1e9, 3),
+        "unit": "GB/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"{len(times)} calls of the headline workload (one 32K-token cache, B=1) through "
+                   f"oracle.attention.reference_sdpa on the host CPU ({cpu_model}); median {med * 1e3:.1f} ms/call"),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-extra", action="store_true", help="time only the headline workload")
+    ap.add_argument("--no-parity", action="store_true", help="skip the oracle check of the headline output")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        log("bench.py measures one GPU: the attention path here runs on a single MI355X (multi-GPU sharding "
+            "is a design note only). Run with --gpus 1.")
+        sys.exit(2)
+    if args.steps < 1 or args.warmup < 0:
+        ap.error("--steps must be >= 1 and --warmup >= 0")
+
+    import torch
+
+    from myinfer_amd import _lib
+
+    if not torch.cuda.is_available():
+        log("bench.py needs a GPU (torch.cuda.is_available() is False)")
+        sys.exit(1)
+    _lib.lib()  # the HIP library must be built; there is no fallback
+    device = torch.device("cuda:0")
+    torch.cuda.set_device(device)
+    log(f"[bench] device: {torch.cuda.get_device_name(device)}")
+
+    head = DECODE["C2-b1"]
+    res = time_decode(head, args.steps, args.warmup, device, want_parity=not args.no_parity)
+    log(f"[bench] C2-b1: {res['gbs']:.1f} GB/s (graph, {res['ms_per_step'] * 1e3:.2f} us/step); "
+        f"per call {res['call_us_mean']:.2f} us mean -> {res['kernel_gbs']:.1f} GB/s")
+    extra = {}
+    if not args.no_extra:
+        for name in ("C1", "C2-b8", "C4", "C5-global", "C5-window"):
+            r = time_decode(DECODE[name], args.steps, args.warmup, device)
+            extra[name] = {"gbs": round(r["gbs"], 1), "frac": round(r["gbs"] / PEAK_HBM_GBS, 4),
+                           "us_per_step": round(r["ms_per_step"] * 1e3, 3), "bytes": r["bytes"],
+                           "kernel_us": round(r["call_us_mean"], 3)}
+            log(f"[bench] {name}: {r['gbs']:.1f} GB/s ({r['ms_per_step'] * 1e3:.2f} us/step)")
+            torch.cuda.empty_cache()
+
+    cpu = None
+    if not args.no_cpu:
+        q, cache, scale = res["cpu_inputs"] if "cpu_inputs" in res else (None, None, None)
+        if q is None:
+            r2 = time_decode(head, 1, 0, device, want_parity=True)
+            q, cache, scale = r2["cpu_inputs"]
+        cpu = cpu_baseline(head, q, cache, scale)
+        log(f"[bench] CPU baseline: {cpu['value']} GB/s on {cpu['cores']} cores")
+
+    achieved = res["kernel_gbs"]
+    line = {
+        "metric": METRIC,
+        "value": round(res["gbs"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(res["ms_per_step"], 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic: seeded N(0,1) fp16 Q/K/V; K/V quantized to 8-bit affine (G=64) by the append kernel",
+        "config": {
+            "workload": "C2 decode attention (Qwen3-32B shapes): B=1, Hq=64, Hkv=8, D=128, S=32768, "
+                        "8-bit affine KV, group 64, fp16 query/scales/output, 1 query token",
+            "B": 1, "Hq": 64, "Hkv": 8, "head_dim": 128, "context": 32768, "kv_bits": 8, "group_size": 64,
+            "bytes_per_step": res["bytes"], "caches_rotated": res["ncache"],
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": PEAK_HBM_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / PEAK_HBM_GBS, 4),
+            "traffic": None,
+            "kernel_us": round(res["call_us_mean"], 3),
+            "kernel": "decode_attn_kernel + combine_kernel (one kvq_decode_attn call)",
+        },
+        "cpu_baseline": cpu,
+        "parity": res.get("parity"),
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -25,7 +25,10 @@
  *     themselves, which are read on the host during the call.
  *   - Launches are asynchronous on `stream` (a hipStream_t; NULL = the default stream).
  *   - The library allocates no device memory: scratch space (the attention workspace) is
- *     owned by the caller; its size comes from the *_workspace_size functions.
+ *     owned by the caller; its size comes from the *_workspace_size functions. A workspace must
+ *     be zero-filled once, when it is allocated (hipMemset): the kernels keep per-call split
+ *     counters in it and reset them before they finish, so it stays valid for later calls of any
+ *     shape. Calls that share one workspace must be ordered (same stream, or synchronized).
  *   - Strides are in elements of the pointed-to type.
  */
 #ifndef KVQ_H
@@ -95,7 +98,10 @@ int kvq_quantize_append(const kvq_rows* k_src, const kvq_qtensor* k_dst,
  *   seq_lens: NULL (every sequence has S keys) or device int32[B] with 1 <= seq_lens[b] <= S.
  *   causal:   query l of sequence b sits at position seq_len_b - L + l and sees keys <= it.
  *   window:   0 = none; otherwise keys k > position - window only (sliding window).
- *   workspace: device buffer of at least kvq_decode_workspace_size(...) bytes.
+ *   workspace: device buffer of at least kvq_decode_workspace_size(...) bytes, 256-byte aligned,
+ *              zero-filled at allocation (see the conventions above).
+ * One launch: the key range is split over workgroups, and the last workgroup of each
+ * (sequence, KV head) merges the splits' log-sum-exp partials and writes the output.
  */
 int kvq_decode_attn(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v,
                     const int32_t* seq_lens, const kvq_rows* out,

