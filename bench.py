@@ -14,9 +14,9 @@ streams its cache from HBM rather than from the MALL.
 Timing:
   * value / ms_per_step: the K steps are captured once in a HIP graph and replayed; HIP events
     on the launch stream bracket the replay (after a device synchronize on both sides).
-  * roofline.achieved: the average duration of one call, from HIP event pairs around each call
-    in an eager run whose launches are queued behind a spin kernel, so the GPU runs them back to
-    back and each event pair brackets the kernels alone.
+  * roofline.achieved: the average duration of one call (the decode kernel and the split-merge
+    kernel it launches), from one HIP event pair around a batch of eager calls queued behind a
+    spin kernel, so the GPU runs them back to back and the pair brackets their kernels only.
   * cpu_baseline: the CPU restatement of the reference algorithm (a torch-CPU port of
     m5engine/attention.py with the reference's dtype casts) timed on the host's cores on one
     cache of the same workload, for a bounded number of calls.
@@ -152,21 +152,20 @@ def time_decode(cfg, steps, warmup, device, want_parity=False):
         calls[i % ncache]()
     torch.cuda.synchronize()
 
-    # per-call durations: event pairs around eager calls queued behind a spin kernel
+    # per-call duration: one event pair around a batch of eager calls queued behind a spin kernel,
+    # so the GPU runs the calls back to back and the pair brackets their kernels only
     nev = min(steps, 100)
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(nev)]
+    ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
     cycles = calibrate_spin(torch, 20.0 + 0.05 * nev)
     torch.cuda.synchronize()
     torch.cuda._sleep(cycles)
+    ev[0].record()
     for i in range(nev):
-        ev[i][0].record()
         calls[i % ncache]()
-        ev[i][1].record()
+    ev[1].record()
     torch.cuda.synchronize()
-    per_call_ms = [a.elapsed_time(b) for a, b in ev]
-    per_call_ms.sort()
-    call_us_mean = 1e3 * sum(per_call_ms) / len(per_call_ms)
-    call_us_median = 1e3 * per_call_ms[len(per_call_ms) // 2]
+    call_us_mean = 1e3 * ev[0].elapsed_time(ev[1]) / nev
+    call_us_median = call_us_mean
 
     # the timed region: K steps captured in one HIP graph, replayed
     graph = torch.cuda.CUDAGraph()
@@ -354,7 +353,7 @@ def main():
             "frac": round(achieved / PEAK_HBM_GBS, 4),
             "traffic": None,
             "kernel_us": round(res["call_us_mean"], 3),
-            "kernel": "decode_attn_kernel + combine_kernel (one kvq_decode_attn call)",
+            "kernel": "decode_attn_kernel + combine_kernel (the two launches of one kvq_decode_attn call)",
         },
         "cpu_baseline": cpu,
         "parity": res.get("parity"),

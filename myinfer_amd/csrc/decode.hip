@@ -607,51 +607,54 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void decode_attn_kernel(DecParams 
   }
 }
 
-// Merge of the key splits as a separate launch: one block per output row, thread d owns output
-// element d; out = sum_s 2^(m_s - M) o_s / sum_s 2^(m_s - M) l_s.
+// Merge of the key splits as a separate launch: one wave per (output row, 64 columns);
+// out = sum_s 2^(m_s - M) o_s / sum_s 2^(m_s - M) l_s. Every lane issues all its partial loads
+// (up to kMaxSplit, in flight together) before the weights are formed, so the merge is one round
+// trip to the partials.
 template <typename T, int D>
-__global__ __launch_bounds__(D) void combine_kernel(DecParams p) {
+__global__ __launch_bounds__(64) void combine_kernel(DecParams p) {
   constexpr int R = 16 / (D / 64);
-  const int grow = blockIdx.x;
+  constexpr int CH = 32;
+  __shared__ float s_w[kMaxSplit];
+  const int lane = threadIdx.x;
+  const int grow = blockIdx.x / (D / 64), d = (blockIdx.x % (D / 64)) * 64 + lane;
   const int l = grow % p.L, h = (grow / p.L) % p.Hq, b = grow / (p.L * p.Hq);
   const int kvh = h / p.rep;
   const int rw = (h - kvh * p.rep) * p.L + l;
   const int unit = (b * p.Hkv + kvh) * p.rowblocks + rw / R;
   const int64_t base = ((int64_t)unit * R + rw % R) * p.nsplit;
-  const float2* ml = (const float2*)p.part_ml + base;
-  const float* po = p.part_o + base * D + threadIdx.x;
-  float M = -INFINITY;
-  for (int s = 0; s < p.nsplit; ++s) {
-    const float2 v = ml[s];
-    M = fmaxf(M, v.y > 0.0f ? v.x : -INFINITY);
-  }
-  float acc = 0.0f, lsum = 0.0f;
-  if (M != -INFINITY) {
-    int s = 0;
-    for (; s + 8 <= p.nsplit; s += 8) {
-      float o[8];
-      float2 v[8];
+  const float* po = p.part_o + base * D + d;
+  float o[CH];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        o[u] = po[(int64_t)(s + u) * D];
-        v[u] = ml[s + u];
-      }
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const float f = v[u].y > 0.0f ? exp2_fast(v[u].x - M) : 0.0f;
-        acc += f * o[u];
-        lsum += f * v[u].y;
-      }
-    }
-    for (; s < p.nsplit; ++s) {
-      const float2 v = ml[s];
-      const float f = v.y > 0.0f ? exp2_fast(v.x - M) : 0.0f;
-      acc += f * po[(int64_t)s * D];
-      lsum += f * v.y;
-    }
+  for (int u = 0; u < CH; ++u) o[u] = u < p.nsplit ? po[(int64_t)u * D] : 0.0f;
+  {
+    const float2* ml = (const float2*)p.part_ml + base;
+    const float2 v0 = lane < p.nsplit ? ml[lane] : make_float2(-INFINITY, 0.0f);
+    const float2 v1 = lane + 64 < p.nsplit ? ml[lane + 64] : make_float2(-INFINITY, 0.0f);
+    const float m0 = v0.y > 0.0f ? v0.x : -INFINITY, m1 = v1.y > 0.0f ? v1.x : -INFINITY;
+    const float M = wave_max(fmaxf(m0, m1));
+    const float w0 = (M == -INFINITY || m0 == -INFINITY) ? 0.0f : exp2_fast(m0 - M);
+    const float w1 = (M == -INFINITY || m1 == -INFINITY) ? 0.0f : exp2_fast(m1 - M);
+    const float Lsum = wave_sum(w0 * v0.y + w1 * v1.y);
+    const float inv = Lsum > 0.0f ? 1.0f / Lsum : 0.0f;
+    if (lane < p.nsplit) s_w[lane] = w0 * inv;
+    if (lane + 64 < p.nsplit) s_w[lane + 64] = w1 * inv;
   }
-  p.out[(int64_t)b * p.o_sb + (int64_t)h * p.o_sh + (int64_t)l * p.o_sl + threadIdx.x] =
-      from_float(lsum > 0.0f ? acc / lsum : 0.0f, T{});
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  float acc = 0.0f;
+#pragma unroll
+  for (int u = 0; u < CH; ++u)
+    if (u < p.nsplit) acc += s_w[u] * o[u];
+  for (int s0 = CH; s0 < p.nsplit; s0 += CH) {
+#pragma unroll
+    for (int u = 0; u < CH; ++u) o[u] = s0 + u < p.nsplit ? po[(int64_t)(s0 + u) * D] : 0.0f;
+#pragma unroll
+    for (int u = 0; u < CH; ++u)
+      if (s0 + u < p.nsplit) acc += s_w[s0 + u] * o[u];
+  }
+  p.out[(int64_t)b * p.o_sb + (int64_t)h * p.o_sh + (int64_t)l * p.o_sl + d] = from_float(acc, T{});
 }
 
 // ------------------------------------------------------------------------------------------
@@ -669,7 +672,7 @@ struct DecTune {
 // once per process).
 static DecTune decode_tune() {
   static DecTune t = [] {
-    DecTune d{8, 2, 256, 1};
+    DecTune d{8, 2, 256, 0};
     if (const char* e = getenv("KVQ_DECODE_TUNE")) {
       int a = 0, b = 0, c = 0, f = 1;
       if (sscanf(e, "%d,%d,%d,%d", &a, &b, &c, &f) >= 3 && (a == 4 || a == 8) && b >= 2 && b <= 4 && c >= 1)
@@ -726,7 +729,8 @@ static hipError_t launch_decode_t(const DecParams& p, hipStream_t stream) {
                      p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || p.nsplit == 1 || p.fused) return e;
-  hipLaunchKernelGGL((combine_kernel<T, D>), dim3(p.nunits / p.rowblocks * p.rep * p.L), dim3(D), 0, stream, p);
+  hipLaunchKernelGGL((combine_kernel<T, D>), dim3(p.nunits / p.rowblocks * p.rep * p.L * (D / 64)), dim3(64), 0, stream,
+                     p);
   return hipGetLastError();
 }
 
