@@ -160,6 +160,7 @@ int kvq_prefill_attn(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor*
   int rc = check_attn(q, k, v, out, B, Hq, Hkv, L, D, S, bits, group_size, dtype, scale, window,
                       kvq_prefill_workspace_size(B, Hq, Hkv, L, D, S, window), workspace, workspace_bytes);
   if (rc) return rc;
+  if ((rc = check_rows(out, "out", D, true))) return rc;  // rows are written 8 bytes at a time
   return hip_status(kvq::launch_prefill(q, k, v, seq_lens, out, B, Hq, Hkv, L, D, S, bits, dtype, scale, causal,
                                         window, workspace, (hipStream_t)stream),
                     "prefill_attn launch");

@@ -36,11 +36,11 @@
 
 #include "common.h"
 #include "launch.h"
+#include "merge.h"
 
 namespace kvq {
 
 constexpr int kTile = 32;
-constexpr int kMaxSplit = 128;
 constexpr int kXcds = 8;
 
 template <int D, int BITS>
@@ -190,17 +190,6 @@ __device__ __forceinline__ void st_agent(float* ptr, float v) {
 }
 __device__ __forceinline__ float ld_agent(const float* ptr) {
   return __hip_atomic_load(const_cast<float*>(ptr), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int m = 1; m < 16; m <<= 1) v = fmaxf(v, shfl_xor(v, m));
-  return max_xor32(max_xor16(v));
-}
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int m = 1; m < 16; m <<= 1) v += shfl_xor(v, m);
-  return add_xor32(add_xor16(v));
 }
 
 // Per-lane byte offsets of a tile's code loads, relative to the tile's first key row.
@@ -607,56 +596,6 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void decode_attn_kernel(DecParams 
   }
 }
 
-// Merge of the key splits as a separate launch: one wave per (output row, 64 columns);
-// out = sum_s 2^(m_s - M) o_s / sum_s 2^(m_s - M) l_s. Every lane issues all its partial loads
-// (up to kMaxSplit, in flight together) before the weights are formed, so the merge is one round
-// trip to the partials.
-template <typename T, int D>
-__global__ __launch_bounds__(64) void combine_kernel(DecParams p) {
-  constexpr int R = 16 / (D / 64);
-  constexpr int CH = 32;
-  __shared__ float s_w[kMaxSplit];
-  const int lane = threadIdx.x;
-  const int grow = blockIdx.x / (D / 64), d = (blockIdx.x % (D / 64)) * 64 + lane;
-  const int l = grow % p.L, h = (grow / p.L) % p.Hq, b = grow / (p.L * p.Hq);
-  const int kvh = h / p.rep;
-  const int rw = (h - kvh * p.rep) * p.L + l;
-  const int unit = (b * p.Hkv + kvh) * p.rowblocks + rw / R;
-  const int64_t base = ((int64_t)unit * R + rw % R) * p.nsplit;
-  const float* po = p.part_o + base * D + d;
-  float o[CH];
-#pragma unroll
-  for (int u = 0; u < CH; ++u) o[u] = u < p.nsplit ? po[(int64_t)u * D] : 0.0f;
-  {
-    const float2* ml = (const float2*)p.part_ml + base;
-    const float2 v0 = lane < p.nsplit ? ml[lane] : make_float2(-INFINITY, 0.0f);
-    const float2 v1 = lane + 64 < p.nsplit ? ml[lane + 64] : make_float2(-INFINITY, 0.0f);
-    const float m0 = v0.y > 0.0f ? v0.x : -INFINITY, m1 = v1.y > 0.0f ? v1.x : -INFINITY;
-    const float M = wave_max(fmaxf(m0, m1));
-    const float w0 = (M == -INFINITY || m0 == -INFINITY) ? 0.0f : exp2_fast(m0 - M);
-    const float w1 = (M == -INFINITY || m1 == -INFINITY) ? 0.0f : exp2_fast(m1 - M);
-    const float Lsum = wave_sum(w0 * v0.y + w1 * v1.y);
-    const float inv = Lsum > 0.0f ? 1.0f / Lsum : 0.0f;
-    if (lane < p.nsplit) s_w[lane] = w0 * inv;
-    if (lane + 64 < p.nsplit) s_w[lane + 64] = w1 * inv;
-  }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-  float acc = 0.0f;
-#pragma unroll
-  for (int u = 0; u < CH; ++u)
-    if (u < p.nsplit) acc += s_w[u] * o[u];
-  for (int s0 = CH; s0 < p.nsplit; s0 += CH) {
-#pragma unroll
-    for (int u = 0; u < CH; ++u) o[u] = s0 + u < p.nsplit ? po[(int64_t)(s0 + u) * D] : 0.0f;
-#pragma unroll
-    for (int u = 0; u < CH; ++u)
-      if (s0 + u < p.nsplit) acc += s_w[s0 + u] * o[u];
-  }
-  p.out[(int64_t)b * p.o_sb + (int64_t)h * p.o_sh + (int64_t)l * p.o_sl + d] = from_float(acc, T{});
-}
-
 // ------------------------------------------------------------------------------------------
 // Host side: plan, workspace, launch.
 
@@ -729,9 +668,22 @@ static hipError_t launch_decode_t(const DecParams& p, hipStream_t stream) {
                      p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || p.nsplit == 1 || p.fused) return e;
-  hipLaunchKernelGGL((combine_kernel<T, D>), dim3(p.nunits / p.rowblocks * p.rep * p.L * (D / 64)), dim3(64), 0, stream,
-                     p);
-  return hipGetLastError();
+  MergeParams m;
+  m.part_o = p.part_o;
+  m.part_ml = p.part_ml;
+  m.out = p.out;
+  m.o_sb = p.o_sb;
+  m.o_sh = p.o_sh;
+  m.o_sl = p.o_sl;
+  m.Hq = p.Hq;
+  m.Hkv = p.Hkv;
+  m.L = p.L;
+  m.rep = p.rep;
+  m.R = DecCfg<D, BITS>::R;
+  m.rowblocks = p.rowblocks;
+  m.nsplit = p.nsplit;
+  m.position_major = 0;
+  return launch_combine<T, D>(m, p.nunits / (p.Hkv * p.rowblocks), stream);
 }
 
 template <typename T, int D, int BITS>

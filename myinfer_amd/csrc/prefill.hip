@@ -1,16 +1,498 @@
-// Causal chunked-prefill attention over the quantized cache (MFMA). Placeholder until the
-// kernel lands: reports "not supported" so callers fail loudly.
+// Causal chunked-prefill attention over an MLX-layout affine-quantized KV cache, on MFMA.
+//
+// Computes, per (sequence b, query head h, query row l), the quantity m5engine/attention.py:29-103
+// evaluates for L > 1 (blocked online softmax over key blocks, :64-100, causal when the mask is a
+// string, :55-58/:70-73):
+//   out = softmax(scale * q K^T + mask) V,  K = sK * codesK + bK,  V = sV * codesV + bV
+// with query l at position S_b - L + l, keys <= position when causal, keys > position - window
+// when a sliding window is set.
+//
+// Design (head_dim 128, 64-key tiles, a workgroup = 4 waves = 128 query rows):
+//  * A workgroup serves 128 consecutive rows of one (sequence, KV head) in position-major order
+//    (row = position * rep + local head), so all rep query heads of a position share each K/V
+//    tile and a causal boundary cuts only a few positions.
+//  * Each 64-key tile is dequantized once per workgroup into LDS as fp16: K row-major, V
+//    transposed (V^T[d][slot]) with its key slots permuted to match the score layout below.
+//    Double-buffered: the codes of tile t+1 are in flight while tile t is computed.
+//  * Per wave (32 rows = the columns of a 32x32 MFMA): S^T = K Q^T (v_mfma_f32_32x32x16_f16;
+//    A = K rows from LDS, B = Q^T held in registers). In the MFMA result layout every lane holds
+//    16 keys of one query column, so the row max / sum are lane-local plus one permlane swap, and
+//    the probabilities converted to fp16 are already the B operand of O^T = V^T P^T: no shuffle.
+//  * Q carries the softmax scale in log2 units and a per-row power of two that keeps it inside
+//    the fp16 range; scores are fp32 and are corrected by that power before the softmax.
+//  * Online softmax with threshold rescaling (a row's running maximum moves only when a tile's
+//    maximum exceeds it by more than 2^6), fp32 accumulators.
+//  * Long key ranges are split over several workgroups; their (m, l, o) partials are merged by
+//    the log-sum-exp combine kernel of merge.h.
+
+#include <math.h>
 
 #include "common.h"
 #include "launch.h"
+#include "merge.h"
 
 namespace kvq {
 
-size_t prefill_workspace_bytes(int, int, int, int, int, int, int, int) { return 256; }
+constexpr int kPT = 64;       // keys per tile
+constexpr int kPRows = 128;   // query rows per workgroup (4 waves x 32 MFMA columns)
+constexpr int kPW = 4;        // waves per workgroup
+constexpr int kKS = 136;      // fp16 per K row in LDS: 128 + 8 (rows shift by 4 banks)
+constexpr int kVS = 72;       // fp16 per V^T row in LDS: 64 + 8
+constexpr float kPSlack = 6.0f;
+constexpr int kPTargetWgs = 512;
 
-hipError_t launch_prefill(const kvq_rows*, const kvq_qtensor*, const kvq_qtensor*, const int32_t*, const kvq_rows*,
-                          int, int, int, int, int, int, int, int, float, int, int, void*, hipStream_t) {
-  return hipErrorNotSupported;
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+
+struct PreParams {
+  const uint16_t* q;
+  int64_t q_sb, q_sh, q_sl;
+  const uint8_t* kc;
+  const uint8_t* vc;
+  int64_t kc_sb, kc_sh, kc_ss;  // bytes
+  int64_t vc_sb, vc_sh, vc_ss;  // bytes
+  const uint16_t* ks;
+  const uint16_t* kb;
+  const uint16_t* vs;
+  const uint16_t* vb;
+  int64_t ksb_sb, ksb_sh, ksb_ss;  // elements
+  int64_t vsb_sb, vsb_sh, vsb_ss;
+  const int32_t* seq_lens;
+  uint16_t* out;
+  int64_t o_sb, o_sh, o_sl;
+  float* part_o;
+  float* part_ml;
+  int Hq, Hkv, L, S, rep, nrows, rowblocks, nsplit, nunits;
+  int sb_vec;  // K and V scale/bias rows are [.., 2] contiguous and 16-byte aligned
+  float scale_log2;
+  int causal, window;
+};
+
+// V^T slot of key `kk` (0..63) inside a tile: the 16 keys of PV k-step j = kk / 16 are stored so
+// that slots 16j + 8h + i hold the keys the score layout gives lane half h at i.
+__device__ __forceinline__ int v_slot_key(int slot) {
+  const int j = slot >> 4, h = (slot >> 3) & 1, i = slot & 7;
+  return 16 * j + (i < 4 ? 4 * h + i : 8 + 4 * h + (i - 4));
+}
+
+// Codes and scales of one tile, as staged by one thread (K: 32 dims of one key, key = lane and
+// dims chosen by the wave; V: 4 dims of the 8 keys of one V^T slot chunk).
+template <int BITS>
+struct PreStage {
+  uint32_t kc[BITS];     // 32 codes of one K row
+  uint32_t vc[8];        // for each of 8 keys, the codes of 4 dims (8-bit: a word; 4-bit: 16 bits)
+  uint16_t ks, kbias;    // K scale / bias of (key, group)
+  uint16_t vs[8], vbias[8];
+};
+
+template <typename T, int BITS>
+__device__ __forceinline__ void stage_load(PreStage<BITS>& st, const PreParams& p, const uint8_t* kbase,
+                                           const uint8_t* vbase, const uint16_t* ksb, const uint16_t* kbb,
+                                           const uint16_t* vsb, const uint16_t* vbb, int k0, int S_b, int tid) {
+  // K: key = lane, dims [32 * wave, +32)
+  {
+    const int key = tid & 63, dch = (tid >> 6) * 32;
+    const int row = min(k0 + key, S_b - 1);
+    const uint8_t* src = kbase + (int64_t)row * p.kc_ss + dch * BITS / 8;
+    if constexpr (BITS == 8) {
+      const u4 a = *(const u4*)src, c = *(const u4*)(src + 16);
+      st.kc[0] = a[0]; st.kc[1] = a[1]; st.kc[2] = a[2]; st.kc[3] = a[3];
+      st.kc[4] = c[0]; st.kc[5] = c[1]; st.kc[6] = c[2]; st.kc[7] = c[3];
+    } else {
+      const u4 a = *(const u4*)src;
+      st.kc[0] = a[0]; st.kc[1] = a[1]; st.kc[2] = a[2]; st.kc[3] = a[3];
+    }
+    const int64_t gi = (int64_t)row * p.ksb_ss + dch / 64;
+    st.ks = ksb[gi];
+    st.kbias = kbb[gi];
+  }
+  // V: slot chunk c8 = tid / 32 (8 keys), dims [4 * (tid % 32), +4)
+  {
+    const int c8 = tid >> 5, q4 = tid & 31, g = (4 * q4) / 64;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int row = min(k0 + v_slot_key(8 * c8 + i), S_b - 1);
+      const uint8_t* src = vbase + (int64_t)row * p.vc_ss;
+      if constexpr (BITS == 8) st.vc[i] = *(const uint32_t*)(src + 4 * q4);
+      else st.vc[i] = *(const uint16_t*)(src + 2 * q4);
+    }
+    const bool full = k0 + kPT <= S_b;
+    if (p.sb_vec && full) {
+      // the 8 keys are two runs of 4 consecutive keys; a run's [key][2] scales are 16 bytes
+#pragma unroll
+      for (int run = 0; run < 2; ++run) {
+        const int key0 = k0 + v_slot_key(8 * c8 + 4 * run);
+        const u4 s4 = *(const u4*)(vsb + (int64_t)key0 * 2);
+        const u4 b4 = *(const u4*)(vbb + (int64_t)key0 * 2);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          st.vs[4 * run + i] = (uint16_t)(g ? (s4[i] >> 16) : (s4[i] & 0xffffu));
+          st.vbias[4 * run + i] = (uint16_t)(g ? (b4[i] >> 16) : (b4[i] & 0xffffu));
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int row = min(k0 + v_slot_key(8 * c8 + i), S_b - 1);
+        st.vs[i] = vsb[(int64_t)row * p.vsb_ss + g];
+        st.vbias[i] = vbb[(int64_t)row * p.vsb_ss + g];
+      }
+    }
+  }
+}
+
+template <int BITS>
+__device__ __forceinline__ float code_at(const uint32_t* w, int idx) {
+  if constexpr (BITS == 8) return (float)((w[idx >> 2] >> (8 * (idx & 3))) & 0xffu);
+  else return (float)((w[idx >> 3] >> (4 * (idx & 7))) & 0xfu);
+}
+
+template <typename T, int BITS>
+__device__ __forceinline__ void stage_store(const PreStage<BITS>& st, _Float16* klds, _Float16* vlds, int tid) {
+  {
+    // lane = key row: a row is 68 dwords, so 8 consecutive lanes write 8 disjoint 4-bank groups
+    const int key = tid & 63, dch = (tid >> 6) * 32;
+    const float s = to_float(st.ks, T{}), bb = to_float(st.kbias, T{});
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      u4 w;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float x0 = fmaf(code_at<BITS>(st.kc, 8 * c + 2 * e), s, bb);
+        const float x1 = fmaf(code_at<BITS>(st.kc, 8 * c + 2 * e + 1), s, bb);
+        w[e] = pack_f16x2(x0, x1);
+      }
+      *(u4*)&klds[key * kKS + dch + 8 * c] = w;
+    }
+  }
+  {
+    const int c8 = tid >> 5, q4 = tid & 31;
+    float s[8], bb[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      s[i] = to_float(st.vs[i], T{});
+      bb[i] = to_float(st.vbias[i], T{});
+    }
+#pragma unroll
+    for (int e0 = 0; e0 < 4; ++e0) {
+      const int e = (e0 + (q4 >> 1)) & 3;  // rotate the column order across lanes
+      u4 w;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float x0 = fmaf(code_at<BITS>(&st.vc[2 * i], e), s[2 * i], bb[2 * i]);
+        const float x1 = fmaf(code_at<BITS>(&st.vc[2 * i + 1], e), s[2 * i + 1], bb[2 * i + 1]);
+        w[i] = pack_f16x2(x0, x1);
+      }
+      *(u4*)&vlds[(4 * q4 + e) * kVS + 8 * c8] = w;
+    }
+  }
+}
+
+template <typename T, int BITS>
+__global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PreParams p) {
+  __shared__ __align__(16) _Float16 k_lds[2][kPT * kKS];
+  __shared__ __align__(16) _Float16 v_lds[2][128 * kVS];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int qc = lane & 31, hh = lane >> 5;
+
+  const int unit = blockIdx.x / p.nsplit, split = blockIdx.x % p.nsplit;
+  const int b = unit / (p.Hkv * p.rowblocks);
+  const int kvh = (unit / p.rowblocks) % p.Hkv;
+  const int rb = unit % p.rowblocks;
+  const int S_b = p.seq_lens ? min(max(p.seq_lens[b], 0), p.S) : p.S;
+
+  // ---- the workgroup's rows, their positions, and the key range they see
+  const int fr0 = rb * kPRows;
+  const int frl = min(fr0 + kPRows, p.nrows) - 1;
+  const int pos_min = S_b - p.L + fr0 / p.rep, pos_max = S_b - p.L + frl / p.rep;
+  const int hi_wg = p.causal ? min(S_b, pos_max + 1) : S_b;
+  const int lo_wg = p.window > 0 ? max(0, pos_min - p.window + 1) : 0;
+  // keys every row of the workgroup sees: tiles inside need no mask
+  const int hi_all = p.causal ? min(S_b, pos_min + 1) : S_b;
+  const int lo_all = p.window > 0 ? max(0, pos_max - p.window + 1) : 0;
+  // splits cover [lo_wg rounded down to a tile, hi_wg) in whole tiles (tile starts stay 64-aligned)
+  const int lo_al = lo_wg & ~(kPT - 1);
+  const int span = max(hi_wg - lo_al, 0);
+  const int chunk = ((span + p.nsplit - 1) / p.nsplit + kPT - 1) / kPT * kPT;
+  const int k_begin = lo_al + split * chunk;
+  const int k_end = min(k_begin + chunk, hi_wg);
+  const int ntile = k_end > k_begin ? (k_end - k_begin + kPT - 1) / kPT : 0;
+
+  // ---- this lane's query row (MFMA column qc of this wave)
+  const int fr = fr0 + wave * 32 + qc;
+  const bool row_ok = fr < p.nrows;
+  const int lq = row_ok ? fr / p.rep : 0;
+  const int head = kvh * p.rep + (row_ok ? fr % p.rep : 0);
+  const int pos = S_b - p.L + lq;
+  const int lo_r = p.window > 0 ? max(0, pos - p.window + 1) : 0;
+  const int hi_r = p.causal ? min(S_b, pos + 1) : S_b;
+
+  // ---- Q^T operand: k-step j holds dims 16j + 8hh .. +7, times scale*log2(e)*2^qe in fp16
+  h8 qop[8];
+  float inv2;
+  {
+    const uint16_t* qrow = p.q + (int64_t)b * p.q_sb + (int64_t)head * p.q_sh + (int64_t)lq * p.q_sl + 8 * hh;
+    float qv[8][8];
+    float qmax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const u4 raw = row_ok ? *(const u4*)(qrow + 16 * j) : u4{0, 0, 0, 0};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        qv[j][2 * i] = to_float((uint16_t)(raw[i] & 0xffffu), T{});
+        qv[j][2 * i + 1] = to_float((uint16_t)(raw[i] >> 16), T{});
+        qmax = fmaxf(qmax, fmaxf(fabsf(qv[j][2 * i]), fabsf(qv[j][2 * i + 1])));
+      }
+    }
+    qmax = max_xor32(qmax) * p.scale_log2;
+    int e = 0;
+    if (qmax > 0.0f) frexpf(qmax, &e);
+    const int qe = 14 - e;  // |q * scale * log2(e)| * 2^qe < 2^14
+    const float qmul = ldexpf(p.scale_log2, qe);
+    inv2 = ldexpf(1.0f, -qe);
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) qop[j][i] = (_Float16)(qv[j][i] * qmul);
+  }
+
+  const uint8_t* kbase = p.kc + (int64_t)b * p.kc_sb + (int64_t)kvh * p.kc_sh;
+  const uint8_t* vbase = p.vc + (int64_t)b * p.vc_sb + (int64_t)kvh * p.vc_sh;
+  const uint16_t* ksb = p.ks + (int64_t)b * p.ksb_sb + (int64_t)kvh * p.ksb_sh;
+  const uint16_t* kbb = p.kb + (int64_t)b * p.ksb_sb + (int64_t)kvh * p.ksb_sh;
+  const uint16_t* vsb = p.vs + (int64_t)b * p.vsb_sb + (int64_t)kvh * p.vsb_sh;
+  const uint16_t* vbb = p.vb + (int64_t)b * p.vsb_sb + (int64_t)kvh * p.vsb_sh;
+
+  float m_run = -INFINITY, l_run = 0.0f;
+  f16v oacc[4];
+#pragma unroll
+  for (int db = 0; db < 4; ++db) oacc[db] = f16v{};
+
+  PreStage<BITS> st;
+  if (ntile > 0) {
+    stage_load<T, BITS>(st, p, kbase, vbase, ksb, kbb, vsb, vbb, k_begin, S_b, tid);
+    stage_store<T, BITS>(st, k_lds[0], v_lds[0], tid);
+  }
+  __syncthreads();
+
+  for (int t = 0; t < ntile; ++t) {
+    const int cur = t & 1;
+    const int k0 = k_begin + kPT * t;
+    const bool has_next = t + 1 < ntile;
+    if (has_next) stage_load<T, BITS>(st, p, kbase, vbase, ksb, kbb, vsb, vbb, k0 + kPT, S_b, tid);
+
+    // S^T = K Q^T for the two 32-key blocks of the tile
+    f16v sacc[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      sacc[kb] = f16v{};
+      const _Float16* krow = &k_lds[cur][(32 * kb + qc) * kKS + 8 * hh];
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const h8*)(krow + 16 * j), qop[j], sacc[kb], 0, 0, 0);
+    }
+    // scores (log2 units) of this lane's query at keys k0 + 32kb + 8(i/4) + 4hh + i%4
+    float sc[2][16];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) sc[kb][i] = sacc[kb][i] * inv2;
+    const bool need_mask = !(k0 >= lo_all && k0 + kPT <= hi_all);
+    if (need_mask) {
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int key = k0 + 32 * kb + 8 * (i >> 2) + 4 * hh + (i & 3);
+          if (key < lo_r || key >= hi_r) sc[kb][i] = -INFINITY;
+        }
+    }
+    float tm = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) tm = fmaxf(tm, sc[kb][i]);
+    tm = max_xor32(tm);
+    if (__builtin_amdgcn_ballot_w64(tm > m_run + kPSlack) != 0) {
+      const float m_new = tm > m_run + kPSlack ? fmaxf(m_run, tm) : m_run;
+      const float corr = m_new == m_run ? 1.0f : exp2_fast(m_run - m_new);
+      l_run *= corr;
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) oacc[db][i] *= corr;
+      m_run = m_new;
+    }
+    const float msub = m_run == -INFINITY ? 0.0f : m_run;
+    h8 pop[4];
+    float psum = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      u4 w;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float p0 = exp2_fast(sc[j >> 1][8 * (j & 1) + 2 * e] - msub);
+        const float p1 = exp2_fast(sc[j >> 1][8 * (j & 1) + 2 * e + 1] - msub);
+        psum += p0 + p1;
+        w[e] = pack_f16x2(p0, p1);
+      }
+      pop[j] = __builtin_bit_cast(h8, w);
+    }
+    l_run += psum;
+    // O^T += V^T P^T
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      const _Float16* vrow = &v_lds[cur][(32 * db + qc) * kVS + 8 * hh];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const h8*)(vrow + 16 * j), pop[j], oacc[db], 0, 0, 0);
+    }
+
+    if (has_next) stage_store<T, BITS>(st, k_lds[cur ^ 1], v_lds[cur ^ 1], tid);
+    __syncthreads();
+  }
+
+  // ---- epilogue: this lane holds O^T[d][row] for d = 32db + 8(i/4) + 4hh + i%4
+  const float l_tot = add_xor32(l_run);
+  if (!row_ok) return;
+  if (p.nsplit == 1) {
+    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+    uint16_t* orow = p.out + (int64_t)b * p.o_sb + (int64_t)head * p.o_sh + (int64_t)lq * p.o_sl;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int d = 32 * db + 8 * c + 4 * hh;
+        u2 w;
+        w[0] = (uint32_t)from_float(oacc[db][4 * c] * inv, T{}) | ((uint32_t)from_float(oacc[db][4 * c + 1] * inv, T{}) << 16);
+        w[1] = (uint32_t)from_float(oacc[db][4 * c + 2] * inv, T{}) | ((uint32_t)from_float(oacc[db][4 * c + 3] * inv, T{}) << 16);
+        *(u2*)(orow + d) = w;
+      }
+  } else {
+    const int64_t slot = ((int64_t)unit * kPRows + (fr - fr0)) * p.nsplit + split;
+    float* po = p.part_o + slot * 128;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        *(f4*)(po + 32 * db + 8 * c + 4 * hh) =
+            f4{oacc[db][4 * c], oacc[db][4 * c + 1], oacc[db][4 * c + 2], oacc[db][4 * c + 3]};
+    if (hh == 0) *(float2*)(p.part_ml + 2 * slot) = make_float2(m_run, l_tot);
+  }
+}
+
+// ------------------------------------------------------------------------------------------
+// Host side: plan, workspace, launch.
+
+struct PrePlan {
+  int rowblocks, nunits, nsplit;
+};
+
+static PrePlan prefill_plan(int B, int Hq, int Hkv, int L, int S, int window) {
+  PrePlan pl;
+  const int nrows = (Hq / Hkv) * L;
+  pl.rowblocks = (nrows + kPRows - 1) / kPRows;
+  pl.nunits = B * Hkv * pl.rowblocks;
+  // keys a row block sees: the whole context, or about a window
+  const int span = window > 0 ? std::min(S, window + kPRows) : S;
+  const int tiles = (span + kPT - 1) / kPT;
+  int ns = (kPTargetWgs + pl.nunits - 1) / pl.nunits;
+  ns = std::min(ns, std::max(1, tiles / 4));  // at least about 4 tiles per split
+  pl.nsplit = std::max(1, std::min(ns, kMaxSplit));
+  return pl;
+}
+
+size_t prefill_workspace_bytes(int B, int Hq, int Hkv, int L, int D, int S, int window, int) {
+  const PrePlan pl = prefill_plan(B, Hq, Hkv, L, S, window);
+  if (pl.nsplit == 1) return 256;
+  const size_t slots = (size_t)pl.nunits * kPRows * pl.nsplit;
+  return slots * D * sizeof(float) + ((slots * 2 * sizeof(float) + 255) / 256) * 256 + 256;
+}
+
+template <typename T, int BITS>
+static hipError_t launch_prefill_t(const PreParams& p, hipStream_t stream) {
+  hipLaunchKernelGGL((prefill_attn_kernel<T, BITS>), dim3(p.nunits * p.nsplit), dim3(kPW * 64), 0, stream, p);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || p.nsplit == 1) return e;
+  MergeParams m;
+  m.part_o = p.part_o;
+  m.part_ml = p.part_ml;
+  m.out = p.out;
+  m.o_sb = p.o_sb;
+  m.o_sh = p.o_sh;
+  m.o_sl = p.o_sl;
+  m.Hq = p.Hq;
+  m.Hkv = p.Hkv;
+  m.L = p.L;
+  m.rep = p.rep;
+  m.R = kPRows;
+  m.rowblocks = p.rowblocks;
+  m.nsplit = p.nsplit;
+  m.position_major = 1;
+  return launch_combine<T, 128>(m, p.nunits / (p.Hkv * p.rowblocks), stream);
+}
+
+hipError_t launch_prefill(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v, const int32_t* seq_lens,
+                          const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int bits, int dtype,
+                          float scale, int causal, int window, void* workspace, hipStream_t stream) {
+  const PrePlan pl = prefill_plan(B, Hq, Hkv, L, S, window);
+  PreParams p;
+  p.q = (const uint16_t*)q->data;
+  p.q_sb = q->stride_b;
+  p.q_sh = q->stride_h;
+  p.q_sl = q->stride_l;
+  p.kc = (const uint8_t*)k->codes;
+  p.vc = (const uint8_t*)v->codes;
+  p.kc_sb = k->codes_stride_b * 4;
+  p.kc_sh = k->codes_stride_h * 4;
+  p.kc_ss = k->codes_stride_s * 4;
+  p.vc_sb = v->codes_stride_b * 4;
+  p.vc_sh = v->codes_stride_h * 4;
+  p.vc_ss = v->codes_stride_s * 4;
+  p.ks = (const uint16_t*)k->scales;
+  p.kb = (const uint16_t*)k->biases;
+  p.vs = (const uint16_t*)v->scales;
+  p.vb = (const uint16_t*)v->biases;
+  p.ksb_sb = k->sb_stride_b;
+  p.ksb_sh = k->sb_stride_h;
+  p.ksb_ss = k->sb_stride_s;
+  p.vsb_sb = v->sb_stride_b;
+  p.vsb_sh = v->sb_stride_h;
+  p.vsb_ss = v->sb_stride_s;
+  p.seq_lens = seq_lens;
+  p.out = (uint16_t*)out->data;
+  p.o_sb = out->stride_b;
+  p.o_sh = out->stride_h;
+  p.o_sl = out->stride_l;
+  const size_t slots = (size_t)pl.nunits * kPRows * pl.nsplit;
+  p.part_o = (float*)workspace;
+  p.part_ml = (float*)((char*)workspace + slots * D * sizeof(float));
+  p.Hq = Hq;
+  p.Hkv = Hkv;
+  p.L = L;
+  p.S = S;
+  p.rep = Hq / Hkv;
+  p.nrows = p.rep * L;
+  p.rowblocks = pl.rowblocks;
+  p.nsplit = pl.nsplit;
+  p.nunits = pl.nunits;
+  auto vec_ok = [](const void* base, int64_t sbb, int64_t sbh, int64_t sbs) {
+    return sbs == 2 && ((uintptr_t)base % 16) == 0 && (sbb * 2) % 16 == 0 && (sbh * 2) % 16 == 0;
+  };
+  p.sb_vec = vec_ok(v->scales, v->sb_stride_b, v->sb_stride_h, v->sb_stride_s) &&
+             vec_ok(v->biases, v->sb_stride_b, v->sb_stride_h, v->sb_stride_s);
+  p.scale_log2 = scale * 1.4426950408889634f;
+  p.causal = causal;
+  p.window = window;
+  (void)D;
+  if (dtype == KVQ_DTYPE_BF16) {
+    if (bits == 8) return launch_prefill_t<BF16, 8>(p, stream);
+    return launch_prefill_t<BF16, 4>(p, stream);
+  }
+  if (bits == 8) return launch_prefill_t<F16, 8>(p, stream);
+  return launch_prefill_t<F16, 4>(p, stream);
 }
 
 }  // namespace kvq

@@ -1,0 +1,93 @@
+"""GPU chunked-prefill attention (MFMA kernel) vs the exact fp64 oracle over the dequantized cache.
+
+Caches are filled by the quantize kernel (bit-exact with the oracle); the oracle dequantizes the
+very triples the kernel reads. Covers GQA ratios 1..8, 4- and 8-bit, fp16/bf16, causal and full
+masks, sliding windows, variable-length batches, ragged L and S (partial tiles and row blocks),
+capacity-padded cache views, split key ranges (long contexts), and the C3 / C5 prefill shapes.
+"""
+
+import math
+
+import pytest
+import torch
+
+from myinfer_amd import attention as A
+from myinfer_amd import kernels
+from tests.helpers import assert_close, exact_reference, seeded_normal
+from tests.test_gpu_decode import make_cache
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def run_case(B, Hq, Hkv, L, S, bits, dtype, *, causal=True, window=0, seq_lens=None, seed=0, cap=None, what=""):
+    print(f"prefill case {what} B={B} Hq={Hq} Hkv={Hkv} L={L} S={S} bits={bits} {dtype} causal={causal} "
+          f"window={window} var={seq_lens is not None}", flush=True)
+    D = 128
+    kt, vt = make_cache(B, Hkv, S, D, bits, dtype, seed, cap=cap)
+    q = seeded_normal((B, Hq, L, D), seed + 2, dtype, DEV)
+    sl = None if seq_lens is None else torch.tensor(seq_lens, dtype=torch.int32, device=DEV)
+    scale = 1.0 / math.sqrt(D)
+    out = kernels.attention(q, kt, vt, scale, causal=causal, window=window, seq_lens=sl, bits=bits, kernel="prefill")
+    torch.cuda.synchronize()
+    ref = exact_reference(q, kt, vt, scale, bits=bits, causal=causal, window=window, seq_lens=sl)
+    return assert_close(out, ref, what)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("bits", [8, 4])
+@pytest.mark.parametrize("Hq,Hkv", [(8, 8), (16, 8), (16, 4), (32, 4)])
+def test_gqa_ratios(dtype, bits, Hq, Hkv):
+    run_case(1, Hq, Hkv, 96, 700, bits, dtype, seed=20 + Hq + Hkv, what="gqa")
+
+
+@pytest.mark.parametrize("L,S", [(1, 1), (2, 2), (5, 5), (17, 40), (64, 64), (65, 300), (128, 1000), (200, 2048)])
+def test_ragged_shapes(L, S):
+    run_case(1, 8, 2, L, S, 8, torch.float16, seed=L + S, what="ragged")
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_full_and_causal(causal):
+    run_case(2, 16, 4, 77, 1500, 8, torch.bfloat16, causal=causal, seed=3, what="mask")
+
+
+def test_windows_and_varlen():
+    run_case(2, 16, 8, 300, 3000, 8, torch.bfloat16, window=1024, seed=5, what="window")
+    run_case(2, 16, 8, 300, 3000, 8, torch.float16, window=100, seed=6, what="small-window")
+    run_case(3, 16, 4, 64, 2500, 8, torch.float16, seq_lens=[2500, 900, 64], seed=7, what="varlen")
+    run_case(2, 8, 2, 40, 1200, 4, torch.bfloat16, window=200, seq_lens=[1200, 333], seed=8, what="window-varlen")
+
+
+def test_capacity_padded_views():
+    run_case(1, 16, 4, 100, 1000, 8, torch.bfloat16, cap=1280, seed=9, what="padded")
+
+
+def test_long_context_splits():
+    # key ranges long enough to be split over several workgroups and merged
+    run_case(1, 32, 4, 64, 8192, 8, torch.bfloat16, seed=10, what="split")
+    run_case(1, 8, 8, 32, 6000, 4, torch.float16, causal=False, seed=11, what="split-full")
+
+
+@pytest.mark.parametrize("chunk", [0, 1, 31])
+def test_c3_chunk(chunk):
+    # Qwen3-30B-A3B chunked prefill: 32 Q / 4 KV heads, 512-token chunks, 8-bit KV, bf16
+    L = 512
+    S = L * (chunk + 1)
+    run_case(1, 32, 4, L, S, 8, torch.bfloat16, seed=1003 + chunk, what=f"C3-chunk{chunk}")
+
+
+def test_c5_prefill_chunk():
+    # Gemma-3-27B: 32 Q / 16 KV heads, a 2048-token chunk of an 8192 prefill, global and window layers
+    run_case(1, 32, 16, 2048, 4096, 8, torch.bfloat16, seed=1005, what="C5-global")
+    run_case(1, 32, 16, 2048, 4096, 8, torch.bfloat16, window=1024, seed=1006, what="C5-window")
+
+
+def test_blocked_sdpa_string_mask_routes_to_prefill():
+    # the reference's causal string mask (m5engine/attention.py:55-58) through the public entry point
+    B, Hq, Hkv, L, S, D = 1, 16, 4, 48, 600, 128
+    kt, vt = make_cache(B, Hkv, S, D, 8, torch.float16, 21)
+    q = seeded_normal((B, Hq, L, D), 22, torch.float16, DEV)
+    out = A.blocked_quantized_sdpa(q, kt, vt, 1.0 / math.sqrt(D), "causal", 64, 8)
+    torch.cuda.synchronize()
+    ref = exact_reference(q, kt, vt, 1.0 / math.sqrt(D), bits=8, causal=True)
+    assert_close(out, ref, "string-mask")
