@@ -45,6 +45,7 @@ if str(ROOT) not in sys.path:
 
 METRIC = "decode-attn HBM GB/s (% of peak) @32K 8-bit KV; prefill TFLOP/s (% MFMA)"
 PEAK_HBM_GBS = 8000.0  # MI355X HBM3E, published
+PEAK_MFMA_TFLOPS = 2500.0  # MI355X dense fp16/bf16 MFMA, published
 MALL_BYTES = 256 << 20  # Infinity Cache
 
 
@@ -273,6 +274,165 @@ def cpu_baseline(cfg, q, cache, scale, budget_s=15.0, max_calls=8):
     }
 
 
+# Prefill workload C3 (seed 1003): Qwen3-30B-A3B shapes, a 16384-token prompt in 512-token chunks;
+# each chunk is quantize-appended to an 8-bit cache and then attends causally to all prior keys.
+PREFILL = dict(desc="Qwen3-30B-A3B chunked prefill, 16384 tokens in 512-token chunks, 8-bit KV, bf16", B=1,
+               Hq=32, Hkv=4, D=128, N=16384, chunk=512, bits=8, dtype="bfloat16", seed=1003)
+
+
+def prefill_flops(N, Hq, D, L0=0, L1=None):
+    """Algorithmic FLOPs of causal attention for query positions [L0, L1) of an N-token prompt:
+    4 * D * Hq per unmasked (query, key) pair; position p sees p + 1 keys."""
+    L1 = N if L1 is None else L1
+    pairs = (L1 * (L1 + 1) - L0 * (L0 + 1)) // 2
+    return 4 * D * Hq * pairs
+
+
+def time_prefill(cfg, steps, warmup, device, want_parity=False):
+    """One step = the whole prompt: per chunk, the fused quantize-append of its K/V rows and the
+    causal attention of its queries over the cache so far."""
+    import torch
+
+    from myinfer_amd import kernels
+
+    B, Hq, Hkv, D, N, C, bits = cfg["B"], cfg["Hq"], cfg["Hkv"], cfg["D"], cfg["N"], cfg["chunk"], cfg["bits"]
+    T = getattr(torch, cfg["dtype"])
+    g = torch.Generator(device=device).manual_seed(cfg["seed"])
+    k = torch.randn((B, Hkv, N, D), generator=g, device=device).to(T)
+    v = torch.randn((B, Hkv, N, D), generator=g, device=device).to(T)
+    q = torch.randn((B, Hq, N, D), generator=g, device=device).to(T)
+    out = torch.empty_like(q)
+    kc = torch.zeros((B, Hkv, N, D * bits // 32), dtype=torch.int32, device=device).view(torch.uint32)
+    vc = torch.zeros_like(kc)
+    ks, kb, vs, vb = (torch.zeros((B, Hkv, N, D // 64), dtype=T, device=device) for _ in range(4))
+    scale = 1.0 / math.sqrt(D)
+    nchunk = N // C
+    flops = prefill_flops(N, Hq, D)
+    log(f"[bench] {cfg['desc']}: {flops / 1e12:.3f} TFLOP of attention per step")
+
+    def make_calls():
+        appends, attns = [], []
+        for c in range(nchunk):
+            lo, hi = c * C, (c + 1) * C
+            appends.append((k[:, :, lo:hi], v[:, :, lo:hi], lo))
+            attns.append(kernels.prepare_attention(q[:, :, lo:hi], (kc[:, :, :hi], ks[:, :, :hi], kb[:, :, :hi]),
+                                                   (vc[:, :, :hi], vs[:, :, :hi], vb[:, :, :hi]), scale, causal=True,
+                                                   bits=bits, out=out[:, :, lo:hi], kernel="prefill"))
+        return appends, attns
+
+    def append(a):
+        kernels.quantize_append(a[0], (kc, ks, kb), a[1], (vc, vs, vb), row_offset=a[2], group_size=64, bits=bits)
+
+    appends, attns = make_calls()
+    for _ in range(max(1, warmup // nchunk)):
+        for a, f in zip(appends, attns):
+            append(a)
+            f()
+    torch.cuda.synchronize()
+
+    # attention-kernel time per chunk: event pairs around each attention call, all queued behind a
+    # spin kernel so the pairs bracket the kernels only
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(2 * nchunk)]
+    cycles = calibrate_spin(torch, 30.0)
+    torch.cuda.synchronize()
+    torch.cuda._sleep(cycles)
+    for c, (a, f) in enumerate(zip(appends, attns)):
+        ev[2 * c][0].record()
+        append(a)
+        ev[2 * c][1].record()
+        ev[2 * c + 1][0].record()
+        f()
+        ev[2 * c + 1][1].record()
+    torch.cuda.synchronize()
+    append_ms = [ev[2 * c][0].elapsed_time(ev[2 * c][1]) for c in range(nchunk)]
+    attn_ms = [ev[2 * c + 1][0].elapsed_time(ev[2 * c + 1][1]) for c in range(nchunk)]
+
+    # the timed region: `steps` whole prompts captured in one HIP graph and replayed
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        gappends, gattns = make_calls()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        for _ in range(steps):
+            for a, f in zip(gappends, gattns):
+                kernels.quantize_append(a[0], (kc, ks, kb), a[1], (vc, vs, vb), row_offset=a[2], group_size=64,
+                                        bits=bits)
+                f()
+    graph.replay()
+    torch.cuda.synchronize()
+    s_, e_ = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s_.record()
+    graph.replay()
+    e_.record()
+    torch.cuda.synchronize()
+    ms_per_step = s_.elapsed_time(e_) / steps
+    res = dict(flops=flops, ms_per_step=ms_per_step, tflops=flops / (ms_per_step * 1e-3) / 1e12,
+               attn_ms=sum(attn_ms), append_ms=sum(append_ms),
+               attn_tflops=flops / (sum(attn_ms) * 1e-3) / 1e12,
+               chunk_attn_us={c: round(1e3 * attn_ms[c], 2) for c in (0, nchunk // 2, nchunk - 1)})
+    if want_parity:
+        res["parity"] = prefill_parity(cfg, q, out, (kc, ks, kb), (vc, vs, vb), scale, nchunk - 1)
+        last = nchunk - 1
+        res["cpu_inputs"] = (q[:, :, last * C:], (kc, ks, kb), (vc, vs, vb), scale)
+    del graph
+    return res
+
+
+def prefill_parity(cfg, q, out, kt, vt, scale, c):
+    """Chunk c's output (as left by the timed steps) against the exact fp64 oracle."""
+    import numpy as np
+    import torch
+
+    from oracle import attention as OA
+    from oracle import quantize as OQ
+
+    C = cfg["chunk"]
+    hi = (c + 1) * C
+
+    def trip(tr):
+        cc, ss, bb = (x[:, :, :hi] for x in tr)
+        return (cc.cpu().view(torch.int32).numpy().view(np.uint32), ss.cpu().view(torch.int16).numpy().view(np.uint16),
+                bb.cpu().view(torch.int16).numpy().view(np.uint16))
+
+    kdq = OQ.dequantize(*trip(kt), cfg["dtype"], 64, cfg["bits"])
+    vdq = OQ.dequantize(*trip(vt), cfg["dtype"], 64, cfg["bits"])
+    qc = q[:, :, c * C:hi].float().cpu().double().numpy()
+    ref = OA.exact_attention(qc, kdq, vdq, scale, causal=True)
+    st = OA.error_stats(out[:, :, c * C:hi].float().cpu().double().numpy(), ref)
+    return {"vs": "exact fp64 oracle", "chunk": c, "max_abs": st["max_abs"], "rel_l2": st["rel_l2"]}
+
+
+def prefill_cpu_baseline(cfg, q_last, kt, vt, scale, budget_s=20.0):
+    """The reference algorithm (oracle.attention.reference_sdpa: m5engine/attention.py's blocked
+    loop with its dtype casts) on the last chunk of the prompt, timed on the host's cores."""
+    import torch
+
+    from oracle import attention as OA
+
+    ncores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(ncores)
+    N, C = cfg["N"], cfg["chunk"]
+
+    def cpu_trip(tr):
+        c, s, b = tr
+        return (c.cpu().view(torch.int32).to(torch.int64) & 0xFFFFFFFF, s.cpu(), b.cpu())
+
+    qc = q_last.cpu()
+    ktc, vtc = cpu_trip(kt), cpu_trip(vt)
+    times = []
+    t_all = time.perf_counter()
+    while not times or (time.perf_counter() - t_all < budget_s and len(times) < 3):
+        t0 = time.perf_counter()
+        OA.reference_sdpa(qc, ktc, vtc, scale, "causal", 64, cfg["bits"])
+        times.append(time.perf_counter() - t0)
+    med = sorted(times)[len(times) // 2]
+    fl = prefill_flops(N, cfg["Hq"], cfg["D"], N - C, N)
+    return {"value": round(fl / med / 1e12, 5), "unit": "TFLOP/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"{len(times)} run(s) of the last 512-token chunk (16384 keys) through oracle.attention."
+                      f"reference_sdpa on the host CPU; median {med:.2f} s"}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -281,6 +441,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="time only the headline workload")
     ap.add_argument("--no-parity", action="store_true", help="skip the oracle check of the headline output")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the C3 chunked-prefill leg")
+    ap.add_argument("--prefill-only", action="store_true", help="time only the C3 chunked-prefill leg")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -301,6 +463,40 @@ def main():
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)
     log(f"[bench] device: {torch.cuda.get_device_name(device)}")
+
+    prefill = None
+    if not args.no_prefill:
+        pr = time_prefill(PREFILL, max(1, min(args.steps, 3)), args.warmup, device, want_parity=not args.no_parity)
+        log(f"[bench] C3 prefill: {pr['tflops']:.1f} TFLOP/s whole step ({pr['ms_per_step']:.3f} ms incl. appends); "
+            f"attention kernels {pr['attn_ms']:.3f} ms -> {pr['attn_tflops']:.1f} TFLOP/s; appends {pr['append_ms']:.3f} ms")
+        pcpu = None
+        if not args.no_cpu and "cpu_inputs" in pr:
+            pcpu = prefill_cpu_baseline(PREFILL, *pr["cpu_inputs"])
+            log(f"[bench] C3 CPU baseline: {pcpu['value']} TFLOP/s on {pcpu['cores']} cores")
+        prefill = {
+            "metric": "prefill TFLOP/s (% MFMA)",
+            "value": round(pr["tflops"], 2),
+            "unit": "TFLOP/s",
+            "ms_per_step": round(pr["ms_per_step"], 4),
+            "config": {"workload": "C3 chunked prefill (Qwen3-30B-A3B shapes): B=1, Hq=32, Hkv=4, D=128, 16384-token "
+                                   "prompt in 32 chunks of 512, each quantize-appended (8-bit, G=64) then causal "
+                                   "attention over all prior keys, bf16",
+                       "flops_per_step": pr["flops"], "steps": max(1, min(args.steps, 3))},
+            "roofline": {"bound": "mfma", "achieved": round(pr["attn_tflops"], 2), "peak": PEAK_MFMA_TFLOPS,
+                         "unit": "TFLOP/s", "frac": round(pr["attn_tflops"] / PEAK_MFMA_TFLOPS, 4), "traffic": None,
+                         "kernel_ms": round(pr["attn_ms"], 4),
+                         "kernel": "prefill_attn_kernel (+ combine_kernel where a chunk's keys are split), summed "
+                                   "over the 32 chunks"},
+            "append_ms": round(pr["append_ms"], 4),
+            "chunk_attn_us": pr["chunk_attn_us"],
+            "cpu_baseline": pcpu,
+            "parity": pr.get("parity"),
+        }
+        torch.cuda.empty_cache()
+        if args.prefill_only:
+            print(json.dumps({"metric": prefill["metric"], "value": prefill["value"], "unit": "TFLOP/s", "n_gpus": 1,
+                              "higher_is_better": True, "prefill": prefill}), flush=True)
+            return
 
     head = DECODE["C2-b1"]
     res = time_decode(head, args.steps, args.warmup, device, want_parity=not args.no_parity)
@@ -357,6 +553,7 @@ def main():
         },
         "cpu_baseline": cpu,
         "parity": res.get("parity"),
+        "prefill": prefill,
         "extra": extra,
     }
     print(json.dumps(line), flush=True)

@@ -14,7 +14,10 @@ from pathlib import Path
 
 import torch  # noqa: F401  (binds the HIP runtime before libkvq.so is loaded)
 
-LIB_PATH = Path(__file__).resolve().parent / "libkvq.so"
+import os
+
+# The in-tree build; KVQ_LIB may name another build of the same library (A/B comparisons).
+LIB_PATH = Path(os.environ.get("KVQ_LIB") or (Path(__file__).resolve().parent / "libkvq.so"))
 ABI_VERSION = 1
 
 DTYPE_F16 = 0

@@ -62,7 +62,7 @@ struct PreParams {
   float* part_o;
   float* part_ml;
   int Hq, Hkv, L, S, rep, nrows, rowblocks, nsplit, nunits;
-  int sb_vec;  // K and V scale/bias rows are [.., 2] contiguous and 16-byte aligned
+  int fast;    // scale/bias rows [.., 2] contiguous and 16-byte aligned, byte ranges fit 32 bits
   float scale_log2;
   int causal, window;
 };
@@ -74,115 +74,188 @@ __device__ __forceinline__ int v_slot_key(int slot) {
   return 16 * j + (i < 4 ? 4 * h + i : 8 + 4 * h + (i - 4));
 }
 
-// Codes and scales of one tile, as staged by one thread (K: 32 dims of one key, key = lane and
-// dims chosen by the wave; V: 4 dims of the 8 keys of one V^T slot chunk).
+// Codes and scales of one tile as staged by one thread. Waves 0-1 stage V: thread t < 128 takes the
+// 8 keys of V^T slot chunk t % 8 at dims [8 * (t / 8), +8) -- the 8 lanes of a row group write 8
+// different slot chunks of one V^T row, and 32 consecutive rows are read per operand, both free of
+// bank conflicts with 144-byte rows. Waves 2-3 stage K: thread t takes dims
+// [64 * ((t - 128) / 64), +64) of key (t % 64), one scale group.
 template <int BITS>
 struct PreStage {
-  uint32_t kc[BITS];     // 32 codes of one K row
-  uint32_t vc[8];        // for each of 8 keys, the codes of 4 dims (8-bit: a word; 4-bit: 16 bits)
-  uint16_t ks, kbias;    // K scale / bias of (key, group)
-  uint16_t vs[8], vbias[8];
+  uint32_t c[2 * BITS];  // V: key i's 8 codes at c[i * BITS / 4 ..]; K: 64 codes
+  uint16_t s[8], b[8];   // V: per key; K: s[0], b[0]
 };
 
-template <typename T, int BITS>
-__device__ __forceinline__ void stage_load(PreStage<BITS>& st, const PreParams& p, const uint8_t* kbase,
-                                           const uint8_t* vbase, const uint16_t* ksb, const uint16_t* kbb,
-                                           const uint16_t* vsb, const uint16_t* vbb, int k0, int S_b, int tid) {
-  // K: key = lane, dims [32 * wave, +32)
-  {
-    const int key = tid & 63, dch = (tid >> 6) * 32;
-    const int row = min(k0 + key, S_b - 1);
-    const uint8_t* src = kbase + (int64_t)row * p.kc_ss + dch * BITS / 8;
-    if constexpr (BITS == 8) {
-      const u4 a = *(const u4*)src, c = *(const u4*)(src + 16);
-      st.kc[0] = a[0]; st.kc[1] = a[1]; st.kc[2] = a[2]; st.kc[3] = a[3];
-      st.kc[4] = c[0]; st.kc[5] = c[1]; st.kc[6] = c[2]; st.kc[7] = c[3];
-    } else {
-      const u4 a = *(const u4*)src;
-      st.kc[0] = a[0]; st.kc[1] = a[1]; st.kc[2] = a[2]; st.kc[3] = a[3];
-    }
-    const int64_t gi = (int64_t)row * p.ksb_ss + dch / 64;
-    st.ks = ksb[gi];
-    st.kbias = kbb[gi];
+// Per-thread constant byte offsets of the staging loads (relative to the tile's first row).
+struct PreOff {
+  uint32_t code[8];  // V: one per key; K: code[0]
+  uint32_t sb[2];    // V: the two 4-key scale runs; K: sb[0]
+};
+
+template <int BITS>
+__device__ __forceinline__ PreOff stage_offsets(const PreParams& p, int tid) {
+  PreOff o;
+  if (tid < 128) {
+    const int c8 = tid & 7, o8 = tid >> 3;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o.code[i] = (uint32_t)(v_slot_key(8 * c8 + i) * p.vc_ss + o8 * BITS);
+#pragma unroll
+    for (int r = 0; r < 2; ++r) o.sb[r] = (uint32_t)(v_slot_key(8 * c8 + 4 * r) * 4);
+  } else {
+    const int key = tid & 63, half = (tid >> 6) & 1;
+    o.code[0] = (uint32_t)(key * p.kc_ss + half * 8 * BITS);
+#pragma unroll
+    for (int i = 1; i < 8; ++i) o.code[i] = 0;
+    o.sb[0] = (uint32_t)((key * p.ksb_ss + half) * 2);
+    o.sb[1] = 0;
   }
-  // V: slot chunk c8 = tid / 32 (8 keys), dims [4 * (tid % 32), +4)
-  {
-    const int c8 = tid >> 5, q4 = tid & 31, g = (4 * q4) / 64;
+  return o;
+}
+
+// Buffer resources of one (sequence, KV head): codes and scales of the S_b valid rows.
+struct PreRsrc {
+  __amdgpu_buffer_rsrc_t kc, vc, ks, kb, vs, vb;
+};
+
+// Full tile (all 64 rows valid, scale rows [.., 2] contiguous): buffer loads, no address math.
+template <int BITS>
+__device__ __forceinline__ void stage_load_fast(PreStage<BITS>& st, const PreParams& p, const PreRsrc& rs,
+                                                const PreOff& o, int k0, int tid) {
+  if (tid < 128) {
+    const int g = ((tid >> 3) * 8) >> 6;
+    const uint32_t so = (uint32_t)(k0 * p.vc_ss);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const int row = min(k0 + v_slot_key(8 * c8 + i), S_b - 1);
-      const uint8_t* src = vbase + (int64_t)row * p.vc_ss;
-      if constexpr (BITS == 8) st.vc[i] = *(const uint32_t*)(src + 4 * q4);
-      else st.vc[i] = *(const uint16_t*)(src + 2 * q4);
-    }
-    const bool full = k0 + kPT <= S_b;
-    if (p.sb_vec && full) {
-      // the 8 keys are two runs of 4 consecutive keys; a run's [key][2] scales are 16 bytes
-#pragma unroll
-      for (int run = 0; run < 2; ++run) {
-        const int key0 = k0 + v_slot_key(8 * c8 + 4 * run);
-        const u4 s4 = *(const u4*)(vsb + (int64_t)key0 * 2);
-        const u4 b4 = *(const u4*)(vbb + (int64_t)key0 * 2);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          st.vs[4 * run + i] = (uint16_t)(g ? (s4[i] >> 16) : (s4[i] & 0xffffu));
-          st.vbias[4 * run + i] = (uint16_t)(g ? (b4[i] >> 16) : (b4[i] & 0xffffu));
-        }
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int row = min(k0 + v_slot_key(8 * c8 + i), S_b - 1);
-        st.vs[i] = vsb[(int64_t)row * p.vsb_ss + g];
-        st.vbias[i] = vbb[(int64_t)row * p.vsb_ss + g];
+      if constexpr (BITS == 8) {
+        const u2 v = __builtin_amdgcn_raw_buffer_load_b64(rs.vc, o.code[i], so, 0);
+        st.c[2 * i] = v[0];
+        st.c[2 * i + 1] = v[1];
+      } else {
+        st.c[i] = __builtin_amdgcn_raw_buffer_load_b32(rs.vc, o.code[i], so, 0);
       }
     }
+    const uint32_t ss = (uint32_t)(k0 * 4);
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const u4 s4 = __builtin_amdgcn_raw_buffer_load_b128(rs.vs, o.sb[r], ss, 0);
+      const u4 b4 = __builtin_amdgcn_raw_buffer_load_b128(rs.vb, o.sb[r], ss, 0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        st.s[4 * r + i] = (uint16_t)(g ? (s4[i] >> 16) : (s4[i] & 0xffffu));
+        st.b[4 * r + i] = (uint16_t)(g ? (b4[i] >> 16) : (b4[i] & 0xffffu));
+      }
+    }
+  } else {
+    const uint32_t so = (uint32_t)(k0 * p.kc_ss);
+#pragma unroll
+    for (int w = 0; w < 2 * BITS; w += 4) {
+      const u4 v = __builtin_amdgcn_raw_buffer_load_b128(rs.kc, o.code[0] + 4 * w, so, 0);
+      st.c[w] = v[0];
+      st.c[w + 1] = v[1];
+      st.c[w + 2] = v[2];
+      st.c[w + 3] = v[3];
+    }
+    const uint32_t ss = (uint32_t)(k0 * p.ksb_ss * 2);
+    st.s[0] = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rs.ks, o.sb[0], ss, 0);
+    st.b[0] = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rs.kb, o.sb[0], ss, 0);
   }
 }
 
+// Any tile, any scale layout: rows clamped to the last valid one (the rows past it are masked).
 template <int BITS>
-__device__ __forceinline__ float code_at(const uint32_t* w, int idx) {
-  if constexpr (BITS == 8) return (float)((w[idx >> 2] >> (8 * (idx & 3))) & 0xffu);
-  else return (float)((w[idx >> 3] >> (4 * (idx & 7))) & 0xfu);
+__device__ __forceinline__ void stage_load_clamped(PreStage<BITS>& st, const PreParams& p, const uint8_t* kbase,
+                                                   const uint8_t* vbase, const uint16_t* ksb, const uint16_t* kbb,
+                                                   const uint16_t* vsb, const uint16_t* vbb, int k0, int S_b,
+                                                   int tid) {
+  if (tid < 128) {
+    const int c8 = tid & 7, o8 = tid >> 3, g = (o8 * 8) >> 6;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int row = min(k0 + v_slot_key(8 * c8 + i), S_b - 1);
+      const uint8_t* src = vbase + (int64_t)row * p.vc_ss + o8 * BITS;
+      if constexpr (BITS == 8) {
+        const u2 v = *(const u2*)src;
+        st.c[2 * i] = v[0];
+        st.c[2 * i + 1] = v[1];
+      } else {
+        st.c[i] = *(const uint32_t*)src;
+      }
+      st.s[i] = vsb[(int64_t)row * p.vsb_ss + g];
+      st.b[i] = vbb[(int64_t)row * p.vsb_ss + g];
+    }
+  } else {
+    const int key = tid & 63, half = (tid >> 6) & 1;
+    const int row = min(k0 + key, S_b - 1);
+    const uint8_t* src = kbase + (int64_t)row * p.kc_ss + half * 8 * BITS;
+#pragma unroll
+    for (int w = 0; w < 2 * BITS; w += 4) {
+      const u4 v = *(const u4*)(src + 4 * w);
+      st.c[w] = v[0];
+      st.c[w + 1] = v[1];
+      st.c[w + 2] = v[2];
+      st.c[w + 3] = v[3];
+    }
+    st.s[0] = ksb[(int64_t)row * p.ksb_ss + half];
+    st.b[0] = kbb[(int64_t)row * p.ksb_ss + half];
+  }
+}
+
+__device__ __forceinline__ _Float16 to_half(uint16_t r, F16) { return __builtin_bit_cast(_Float16, r); }
+__device__ __forceinline__ _Float16 to_half(uint16_t r, BF16) { return (_Float16)__uint_as_float((uint32_t)r << 16); }
+
+// 1024 + c as fp16 for two codes: the code bytes selected by `sel` become the low mantissa bytes of
+// 0x64xx (= 1024 + c exactly); subtracting 1024 and one packed FMA give c * s + b in fp16.
+constexpr uint32_t kF16x1024 = 0x64646464u;
+__device__ __forceinline__ uint32_t dequant_pair(uint32_t bytes, uint32_t sel, h2 s2, h2 b2) {
+  h2 x = __builtin_bit_cast(h2, perm(kF16x1024, bytes, sel)) - h2{(_Float16)1024.0f, (_Float16)1024.0f};
+  x = x * s2 + b2;
+  return __builtin_bit_cast(uint32_t, x);
+}
+
+// The 8 codes of `n` (8-bit: two words; 4-bit: one word) dequantized to 4 fp16 pairs (dims 2m, 2m+1).
+template <int BITS>
+__device__ __forceinline__ void dequant8(const uint32_t* w, h2 s2, h2 b2, uint32_t* out) {
+  if constexpr (BITS == 8) {
+    out[0] = dequant_pair(w[0], 0x04010400u, s2, b2);
+    out[1] = dequant_pair(w[0], 0x04030402u, s2, b2);
+    out[2] = dequant_pair(w[1], 0x04010400u, s2, b2);
+    out[3] = dequant_pair(w[1], 0x04030402u, s2, b2);
+  } else {
+    const uint32_t lo = w[0] & 0x0F0F0F0Fu, hi = (w[0] >> 4) & 0x0F0F0F0Fu;
+    const uint32_t t0 = perm(hi, lo, 0x05010400u), t1 = perm(hi, lo, 0x07030602u);  // codes 0..3, 4..7 as bytes
+    out[0] = dequant_pair(t0, 0x04010400u, s2, b2);
+    out[1] = dequant_pair(t0, 0x04030402u, s2, b2);
+    out[2] = dequant_pair(t1, 0x04010400u, s2, b2);
+    out[3] = dequant_pair(t1, 0x04030402u, s2, b2);
+  }
 }
 
 template <typename T, int BITS>
 __device__ __forceinline__ void stage_store(const PreStage<BITS>& st, _Float16* klds, _Float16* vlds, int tid) {
-  {
-    // lane = key row: a row is 68 dwords, so 8 consecutive lanes write 8 disjoint 4-bank groups
-    const int key = tid & 63, dch = (tid >> 6) * 32;
-    const float s = to_float(st.ks, T{}), bb = to_float(st.kbias, T{});
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      u4 w;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float x0 = fmaf(code_at<BITS>(st.kc, 8 * c + 2 * e), s, bb);
-        const float x1 = fmaf(code_at<BITS>(st.kc, 8 * c + 2 * e + 1), s, bb);
-        w[e] = pack_f16x2(x0, x1);
-      }
-      *(u4*)&klds[key * kKS + dch + 8 * c] = w;
-    }
-  }
-  {
-    const int c8 = tid >> 5, q4 = tid & 31;
-    float s[8], bb[8];
+  constexpr int W = BITS / 4;  // words per 8 codes
+  if (tid < 128) {
+    const int c8 = tid & 7, o8 = tid >> 3;
+    uint32_t x[8][4];  // key i, dim pair m
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      s[i] = to_float(st.vs[i], T{});
-      bb[i] = to_float(st.vbias[i], T{});
+      const _Float16 sh = to_half(st.s[i], T{}), bh = to_half(st.b[i], T{});
+      dequant8<BITS>(&st.c[W * i], h2{sh, sh}, h2{bh, bh}, x[i]);
     }
 #pragma unroll
-    for (int e0 = 0; e0 < 4; ++e0) {
-      const int e = (e0 + (q4 >> 1)) & 3;  // rotate the column order across lanes
-      u4 w;
+    for (int e = 0; e < 8; ++e) {
+      const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
+      u4 v;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float x0 = fmaf(code_at<BITS>(&st.vc[2 * i], e), s[2 * i], bb[2 * i]);
-        const float x1 = fmaf(code_at<BITS>(&st.vc[2 * i + 1], e), s[2 * i + 1], bb[2 * i + 1]);
-        w[i] = pack_f16x2(x0, x1);
-      }
-      *(u4*)&vlds[(4 * q4 + e) * kVS + 8 * c8] = w;
+      for (int ip = 0; ip < 4; ++ip) v[ip] = perm(x[2 * ip + 1][e >> 1], x[2 * ip][e >> 1], sel);
+      *(u4*)&vlds[(8 * o8 + e) * kVS + 8 * c8] = v;
+    }
+  } else {
+    const int key = tid & 63, half = (tid >> 6) & 1;
+    const _Float16 sh = to_half(st.s[0], T{}), bh = to_half(st.b[0], T{});
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      uint32_t x[4];
+      dequant8<BITS>(&st.c[W * c], h2{sh, sh}, h2{bh, bh}, x);
+      *(u4*)&klds[key * kKS + 64 * half + 8 * c] = u4{x[0], x[1], x[2], x[3]};
     }
   }
 }
@@ -264,6 +337,21 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PreParams p) {
   const uint16_t* kbb = p.kb + (int64_t)b * p.ksb_sb + (int64_t)kvh * p.ksb_sh;
   const uint16_t* vsb = p.vs + (int64_t)b * p.vsb_sb + (int64_t)kvh * p.vsb_sh;
   const uint16_t* vbb = p.vb + (int64_t)b * p.vsb_sb + (int64_t)kvh * p.vsb_sh;
+  PreRsrc rs;
+  {
+    const int64_t nr = p.fast ? S_b : 0;  // the host checks these byte ranges fit 32 bits
+    rs.kc = make_rsrc(kbase, (uint32_t)(nr * p.kc_ss));
+    rs.vc = make_rsrc(vbase, (uint32_t)(nr * p.vc_ss));
+    rs.ks = make_rsrc(ksb, (uint32_t)(nr * p.ksb_ss * 2));
+    rs.kb = make_rsrc(kbb, (uint32_t)(nr * p.ksb_ss * 2));
+    rs.vs = make_rsrc(vsb, (uint32_t)(nr * p.vsb_ss * 2));
+    rs.vb = make_rsrc(vbb, (uint32_t)(nr * p.vsb_ss * 2));
+  }
+  const PreOff off = stage_offsets<BITS>(p, tid);
+  auto stage_load = [&](PreStage<BITS>& s_, int k0) {
+    if (p.fast && k0 + kPT <= S_b) stage_load_fast<BITS>(s_, p, rs, off, k0, tid);
+    else stage_load_clamped<BITS>(s_, p, kbase, vbase, ksb, kbb, vsb, vbb, k0, S_b, tid);
+  };
 
   float m_run = -INFINITY, l_run = 0.0f;
   f16v oacc[4];
@@ -272,7 +360,7 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PreParams p) {
 
   PreStage<BITS> st;
   if (ntile > 0) {
-    stage_load<T, BITS>(st, p, kbase, vbase, ksb, kbb, vsb, vbb, k_begin, S_b, tid);
+    stage_load(st, k_begin);
     stage_store<T, BITS>(st, k_lds[0], v_lds[0], tid);
   }
   __syncthreads();
@@ -281,9 +369,9 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PreParams p) {
     const int cur = t & 1;
     const int k0 = k_begin + kPT * t;
     const bool has_next = t + 1 < ntile;
-    if (has_next) stage_load<T, BITS>(st, p, kbase, vbase, ksb, kbb, vsb, vbb, k0 + kPT, S_b, tid);
+    if (has_next) stage_load(st, k0 + kPT);
 
-    // S^T = K Q^T for the two 32-key blocks of the tile
+    // S^T = K Q^T for the two 32-key blocks of the tile (scores in log2 units times 2^qe)
     f16v sacc[2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
@@ -293,12 +381,7 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PreParams p) {
       for (int j = 0; j < 8; ++j)
         sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const h8*)(krow + 16 * j), qop[j], sacc[kb], 0, 0, 0);
     }
-    // scores (log2 units) of this lane's query at keys k0 + 32kb + 8(i/4) + 4hh + i%4
-    float sc[2][16];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) sc[kb][i] = sacc[kb][i] * inv2;
+    // this lane's query sees keys k0 + 32kb + 8(i/4) + 4hh + i%4
     const bool need_mask = !(k0 >= lo_all && k0 + kPT <= hi_all);
     if (need_mask) {
 #pragma unroll
@@ -306,15 +389,15 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PreParams p) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
           const int key = k0 + 32 * kb + 8 * (i >> 2) + 4 * hh + (i & 3);
-          if (key < lo_r || key >= hi_r) sc[kb][i] = -INFINITY;
+          if (key < lo_r || key >= hi_r) sacc[kb][i] = -INFINITY;
         }
     }
     float tm = -INFINITY;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) tm = fmaxf(tm, sc[kb][i]);
-    tm = max_xor32(tm);
+      for (int i = 0; i < 16; ++i) tm = fmaxf(tm, sacc[kb][i]);
+    tm = max_xor32(tm) * inv2;
     if (__builtin_amdgcn_ballot_w64(tm > m_run + kPSlack) != 0) {
       const float m_new = tm > m_run + kPSlack ? fmaxf(m_run, tm) : m_run;
       const float corr = m_new == m_run ? 1.0f : exp2_fast(m_run - m_new);
@@ -325,22 +408,22 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PreParams p) {
         for (int i = 0; i < 16; ++i) oacc[db][i] *= corr;
       m_run = m_new;
     }
-    const float msub = m_run == -INFINITY ? 0.0f : m_run;
+    // p = 2^(acc * 2^-qe - m): rounded to fp16 it is the B operand of O^T = V^T P^T; the row sum
+    // is kept in fp32
+    const float nm = m_run == -INFINITY ? 0.0f : -m_run;
     h8 pop[4];
-    float psum = 0.0f;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       u4 w;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const float p0 = exp2_fast(sc[j >> 1][8 * (j & 1) + 2 * e] - msub);
-        const float p1 = exp2_fast(sc[j >> 1][8 * (j & 1) + 2 * e + 1] - msub);
-        psum += p0 + p1;
+        const float p0 = exp2_fast(fmaf(sacc[j >> 1][8 * (j & 1) + 2 * e], inv2, nm));
+        const float p1 = exp2_fast(fmaf(sacc[j >> 1][8 * (j & 1) + 2 * e + 1], inv2, nm));
         w[e] = pack_f16x2(p0, p1);
+        l_run += p0 + p1;
       }
       pop[j] = __builtin_bit_cast(h8, w);
     }
-    l_run += psum;
     // O^T += V^T P^T
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
@@ -481,8 +564,9 @@ hipError_t launch_prefill(const kvq_rows* q, const kvq_qtensor* k, const kvq_qte
   auto vec_ok = [](const void* base, int64_t sbb, int64_t sbh, int64_t sbs) {
     return sbs == 2 && ((uintptr_t)base % 16) == 0 && (sbb * 2) % 16 == 0 && (sbh * 2) % 16 == 0;
   };
-  p.sb_vec = vec_ok(v->scales, v->sb_stride_b, v->sb_stride_h, v->sb_stride_s) &&
-             vec_ok(v->biases, v->sb_stride_b, v->sb_stride_h, v->sb_stride_s);
+  const int64_t big = std::max(std::max(p.kc_ss, p.vc_ss), 2 * std::max(p.ksb_ss, p.vsb_ss));
+  p.fast = vec_ok(v->scales, v->sb_stride_b, v->sb_stride_h, v->sb_stride_s) &&
+           vec_ok(v->biases, v->sb_stride_b, v->sb_stride_h, v->sb_stride_s) && (int64_t)S * big < ((int64_t)1 << 31);
   p.scale_log2 = scale * 1.4426950408889634f;
   p.causal = causal;
   p.window = window;
