@@ -62,7 +62,7 @@ def _expected_mask(L: int, S: int, S_b: torch.Tensor, causal: bool, window: int,
         m = m & (k <= pos)
     if window > 0:
         m = m & (k > pos - window)
-    return m  # [B, L, S]
+    return m.expand(S_b.shape[0], L, S)
 
 
 def mask_structure(mask, B: int, n_q_heads: int, L: int, S: int):
@@ -80,9 +80,9 @@ def mask_structure(mask, B: int, n_q_heads: int, L: int, S: int):
     m = mask
     while m.dim() < 4:
         m = m.unsqueeze(0)
-    if m.shape[-2:] != (L, S):
-        raise ValueError(f"mask's last two dims {tuple(m.shape[-2:])} do not match (L, S) = {(L, S)}")
-    m = m.expand(B, m.shape[1], L, S)
+    if m.shape[-1] != S or m.shape[-2] not in (1, L):
+        raise ValueError(f"mask's last two dims {tuple(m.shape[-2:])} do not broadcast to (L, S) = {(L, S)}")
+    m = m.expand(B, m.shape[1], L, S)  # a size-1 query axis broadcasts, as in the reference's slicing
     if m.shape[1] > 1 and not bool((m == m[:, :1]).all()):
         raise NotImplementedError("per-head masks are not supported by the GPU kernels")
     m = m[:, 0]  # [B, L, S]

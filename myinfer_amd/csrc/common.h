@@ -95,6 +95,24 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
 }
 
+// Device-coherent vector accesses through a buffer resource, for data one workgroup publishes and
+// a workgroup on another XCD reads in the same launch: cache policy sc1 is the agent-scope form of
+// the gfx94x/gfx950 memory model (stores write through the XCD's L2, loads do not hit a stale copy
+// in it), the same bits an agent-scope atomic store or load carries.
+constexpr int kCpolAgent = 16;  // sc1
+__device__ __forceinline__ void store_agent_b128(__amdgpu_buffer_rsrc_t r, uint32_t vo, f4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, v), r, vo, 0, kCpolAgent);
+}
+__device__ __forceinline__ void store_agent_b64(__amdgpu_buffer_rsrc_t r, uint32_t vo, float2 v) {
+  __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u2, v), r, vo, 0, kCpolAgent);
+}
+__device__ __forceinline__ f4 load_agent_b128(__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so) {
+  return __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(r, vo, so, kCpolAgent));
+}
+__device__ __forceinline__ float2 load_agent_b64(__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so) {
+  return __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(r, vo, so, kCpolAgent));
+}
+
 // NBYTES consecutive bytes held as 32-bit words; load() from a generic pointer, load_buf() through
 // a buffer resource (lane offset `vo`, uniform offset `so`).
 template <int NBYTES>

@@ -638,11 +638,12 @@ DecPlan decode_plan(int B, int Hq, int Hkv, int L, int D, int S, int window, int
   tpw = std::max<int64_t>(pl.nw, (tpw + pl.nw - 1) / pl.nw * pl.nw);
   pl.chunk = (int)(tpw * kTile);
   pl.nsplit = (pl.span + pl.chunk - 1) / pl.chunk;
-  pl.fused = tune.fused;
+  pl.fused = tune.fused && pl.nunits <= kMaxCountedUnits;
   return pl;
 }
 
-// Workspace: [split counters, zero between calls][(m, l) per row and split][o per row and split]
+// Workspace: [split counters (the shared block), zero between calls][(m, l) per row and split]
+// [o per row and split]
 struct DecLayout {
   size_t counters, ml, o, total;
 };
@@ -651,7 +652,7 @@ static DecLayout decode_layout(const DecPlan& pl, int D) {
   DecLayout l;
   const size_t prow = (size_t)pl.nunits * pl.R * pl.nsplit;
   l.counters = 0;
-  l.ml = up((size_t)pl.nunits * sizeof(unsigned));
+  l.ml = kCounterBytes;
   l.o = l.ml + up(prow * sizeof(float2));
   l.total = l.o + up(prow * D * sizeof(float));
   return l;

@@ -61,6 +61,7 @@ struct PreParams {
   int64_t o_sb, o_sh, o_sl;
   float* part_o;
   float* part_ml;
+  unsigned* counters;  // arrivals per unit, zero between launches
   int Hq, Hkv, L, S, rep, nrows, rowblocks, nsplit, nunits;
   int fast;    // scale/bias rows [.., 2] contiguous and 16-byte aligned, byte ranges fit 32 bits
   float scale_log2;
@@ -264,6 +265,7 @@ template <typename T, int BITS>
 __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PreParams p) {
   __shared__ __align__(16) _Float16 k_lds[2][kPT * kKS];
   __shared__ __align__(16) _Float16 v_lds[2][128 * kVS];
+  __shared__ unsigned s_arrived;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -438,32 +440,78 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PreParams p) {
   }
 
   // ---- epilogue: this lane holds O^T[d][row] for d = 32db + 8(i/4) + 4hh + i%4
-  const float l_tot = add_xor32(l_run);
-  if (!row_ok) return;
-  if (p.nsplit == 1) {
-    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-    uint16_t* orow = p.out + (int64_t)b * p.o_sb + (int64_t)head * p.o_sh + (int64_t)lq * p.o_sl;
-#pragma unroll
-    for (int db = 0; db < 4; ++db)
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const int d = 32 * db + 8 * c + 4 * hh;
-        u2 w;
-        w[0] = (uint32_t)from_float(oacc[db][4 * c] * inv, T{}) | ((uint32_t)from_float(oacc[db][4 * c + 1] * inv, T{}) << 16);
-        w[1] = (uint32_t)from_float(oacc[db][4 * c + 2] * inv, T{}) | ((uint32_t)from_float(oacc[db][4 * c + 3] * inv, T{}) << 16);
-        *(u2*)(orow + d) = w;
-      }
-  } else {
-    const int64_t slot = ((int64_t)unit * kPRows + (fr - fr0)) * p.nsplit + split;
-    float* po = p.part_o + slot * 128;
+  float l_tot = add_xor32(l_run);
+  if (p.nsplit > 1) {
+    // Key split: publish this split's partials, count the arrival, and let the unit's last split to
+    // arrive merge them into its own registers. Partials keep the register image, so every access
+    // is a coalesced 1 KiB per wave: o word (4 db + c) of lane `lane` of wave `wave` of split s at
+    // byte ((s * kPW + wave) * 16 + 4 db + c) * 1024 + 16 lane of the unit's o block; (m, l) of
+    // row r at byte 8 (s * kPRows + r) of the unit's (m, l) block.
+    const __amdgpu_buffer_rsrc_t ro = make_rsrc(p.part_o + (int64_t)unit * p.nsplit * (kPRows * 128),
+                                                (uint32_t)p.nsplit * (kPRows * 128 * 4));
+    const __amdgpu_buffer_rsrc_t rm = make_rsrc(p.part_ml + (int64_t)unit * p.nsplit * (kPRows * 2),
+                                                (uint32_t)p.nsplit * (kPRows * 8));
+    const uint32_t lo = (uint32_t)wave * (16 * 1024) + 16 * lane;
+    const uint32_t split_o = kPW * 16 * 1024;
+    const uint32_t row_ml = 8 * (wave * 32 + qc);
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
       for (int c = 0; c < 4; ++c)
-        *(f4*)(po + 32 * db + 8 * c + 4 * hh) =
-            f4{oacc[db][4 * c], oacc[db][4 * c + 1], oacc[db][4 * c + 2], oacc[db][4 * c + 3]};
-    if (hh == 0) *(float2*)(p.part_ml + 2 * slot) = make_float2(m_run, l_tot);
+        store_agent_b128(ro, lo + (4 * db + c) * 1024 + split * split_o,
+                         f4{oacc[db][4 * c], oacc[db][4 * c + 1], oacc[db][4 * c + 2], oacc[db][4 * c + 3]});
+    if (hh == 0) store_agent_b64(rm, row_ml + split * (kPRows * 8), make_float2(m_run, l_tot));
+    // The stores are acknowledged (written through to the device's coherence point) before the
+    // arrival is counted, so the last arrival sees every split's partials.
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0) s_arrived = __hip_atomic_fetch_add(&p.counters[unit], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (s_arrived != (unsigned)(p.nsplit - 1)) return;
+    if (tid == 0) __hip_atomic_store(&p.counters[unit], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+    // M = max over the splits that saw a key; weights 2^(m_s - M)
+    float M = l_tot > 0.0f ? m_run : -INFINITY;
+    for (int s2 = 0; s2 < p.nsplit; ++s2) {
+      if (s2 == split) continue;
+      const float2 ml = load_agent_b64(rm, row_ml, s2 * (kPRows * 8));
+      if (ml.y > 0.0f) M = fmaxf(M, ml.x);
+    }
+    const float w_own = (M == -INFINITY || l_tot <= 0.0f) ? 0.0f : exp2_fast(m_run - M);
+    l_tot *= w_own;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) oacc[db][i] *= w_own;
+    for (int s2 = 0; s2 < p.nsplit; ++s2) {
+      if (s2 == split) continue;
+      const float2 ml = load_agent_b64(rm, row_ml, s2 * (kPRows * 8));
+      f4 po[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) po[u] = load_agent_b128(ro, lo + u * 1024, s2 * split_o);
+      const float w = (M == -INFINITY || ml.y <= 0.0f) ? 0.0f : exp2_fast(ml.x - M);
+      l_tot += w * ml.y;
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) oacc[db][4 * c + e] += w * po[4 * db + c][e];
+    }
   }
+  if (!row_ok) return;
+  const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+  uint16_t* orow = p.out + (int64_t)b * p.o_sb + (int64_t)head * p.o_sh + (int64_t)lq * p.o_sl;
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int d = 32 * db + 8 * c + 4 * hh;
+      u2 w;
+      w[0] = (uint32_t)from_float(oacc[db][4 * c] * inv, T{}) | ((uint32_t)from_float(oacc[db][4 * c + 1] * inv, T{}) << 16);
+      w[1] = (uint32_t)from_float(oacc[db][4 * c + 2] * inv, T{}) | ((uint32_t)from_float(oacc[db][4 * c + 3] * inv, T{}) << 16);
+      *(u2*)(orow + d) = w;
+    }
 }
 
 // ------------------------------------------------------------------------------------------
@@ -483,38 +531,33 @@ static PrePlan prefill_plan(int B, int Hq, int Hkv, int L, int S, int window) {
   const int tiles = (span + kPT - 1) / kPT;
   int ns = (kPTargetWgs + pl.nunits - 1) / pl.nunits;
   ns = std::min(ns, std::max(1, tiles / 4));  // at least about 4 tiles per split
-  pl.nsplit = std::max(1, std::min(ns, kMaxSplit));
+  pl.nsplit = pl.nunits > kMaxCountedUnits ? 1 : std::max(1, std::min(ns, kMaxSplit));
   return pl;
+}
+
+// Workspace: [arrival counters (the block shared with decode)][o partials][(m, l) partials]
+struct PreLayout {
+  size_t o, ml, total;
+};
+static PreLayout prefill_layout(const PrePlan& pl) {
+  PreLayout l;
+  const size_t slots = (size_t)pl.nunits * pl.nsplit * kPRows;
+  l.o = kCounterBytes;
+  l.ml = l.o + slots * 128 * sizeof(float);
+  l.total = l.ml + (slots * 2 * sizeof(float) + 255) / 256 * 256;
+  return l;
 }
 
 size_t prefill_workspace_bytes(int B, int Hq, int Hkv, int L, int D, int S, int window, int) {
   const PrePlan pl = prefill_plan(B, Hq, Hkv, L, S, window);
   if (pl.nsplit == 1) return 256;
-  const size_t slots = (size_t)pl.nunits * kPRows * pl.nsplit;
-  return slots * D * sizeof(float) + ((slots * 2 * sizeof(float) + 255) / 256) * 256 + 256;
+  return prefill_layout(pl).total;
 }
 
 template <typename T, int BITS>
 static hipError_t launch_prefill_t(const PreParams& p, hipStream_t stream) {
   hipLaunchKernelGGL((prefill_attn_kernel<T, BITS>), dim3(p.nunits * p.nsplit), dim3(kPW * 64), 0, stream, p);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess || p.nsplit == 1) return e;
-  MergeParams m;
-  m.part_o = p.part_o;
-  m.part_ml = p.part_ml;
-  m.out = p.out;
-  m.o_sb = p.o_sb;
-  m.o_sh = p.o_sh;
-  m.o_sl = p.o_sl;
-  m.Hq = p.Hq;
-  m.Hkv = p.Hkv;
-  m.L = p.L;
-  m.rep = p.rep;
-  m.R = kPRows;
-  m.rowblocks = p.rowblocks;
-  m.nsplit = p.nsplit;
-  m.position_major = 1;
-  return launch_combine<T, 128>(m, p.nunits / (p.Hkv * p.rowblocks), stream);
+  return hipGetLastError();
 }
 
 hipError_t launch_prefill(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v, const int32_t* seq_lens,
@@ -549,9 +592,10 @@ hipError_t launch_prefill(const kvq_rows* q, const kvq_qtensor* k, const kvq_qte
   p.o_sb = out->stride_b;
   p.o_sh = out->stride_h;
   p.o_sl = out->stride_l;
-  const size_t slots = (size_t)pl.nunits * kPRows * pl.nsplit;
-  p.part_o = (float*)workspace;
-  p.part_ml = (float*)((char*)workspace + slots * D * sizeof(float));
+  const PreLayout lay = prefill_layout(pl);
+  p.counters = (unsigned*)workspace;
+  p.part_o = (float*)((char*)workspace + lay.o);
+  p.part_ml = (float*)((char*)workspace + lay.ml);
   p.Hq = Hq;
   p.Hkv = Hkv;
   p.L = L;

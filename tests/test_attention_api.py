@@ -1,0 +1,80 @@
+"""Host-side logic of the reference-named API (myinfer_amd/attention.py) without a GPU: the block
+rule and module globals of m5engine/attention.py:21-22, :40-41 (patched by tests/test_core.py:36-37),
+the translation of reference-style masks into (causal, window, seq_lens), _slice_keys, install()."""
+
+import types
+
+import pytest
+import torch
+
+from myinfer_amd import attention as A
+from oracle import attention as OA
+
+
+def test_block_rule_reads_module_globals(monkeypatch):
+    assert A.block_size(1, 32, 512) == OA.block_size(1, 32, 512)
+    monkeypatch.setattr(A, "score_budget_bytes", 1)
+    monkeypatch.setattr(A, "MIN_BLOCK", 128)
+    assert A.block_size(1, 4, 6) == 128
+
+
+def test_slice_keys():
+    t = tuple(torch.arange(2 * 3 * 10 * 4).reshape(2, 3, 10, 4) for _ in range(3))
+    s = A._slice_keys(t, 2, 7)
+    assert all(x.shape == (2, 3, 5, 4) for x in s)
+    assert torch.equal(s[0], t[0][..., 2:7, :])
+
+
+def test_mask_none_and_string():
+    assert A.mask_structure(None, 1, 8, 4, 100) == (False, 0, None)
+    assert A.mask_structure("causal", 1, 8, 4, 100) == (True, 0, None)
+
+
+def _mask(B, L, S, S_b, causal, window):
+    k = torch.arange(S)[None, None, :]
+    pos = (torch.tensor(S_b)[:, None] - L + torch.arange(L)[None, :])[:, :, None]
+    m = k < torch.tensor(S_b)[:, None, None]
+    if causal:
+        m = m & (k <= pos)
+    if window:
+        m = m & (k > pos - window)
+    return m[:, None]  # [B, 1, L, S]
+
+
+@pytest.mark.parametrize("causal,window,lens", [(True, 0, [50, 50]), (True, 16, [50, 50]), (True, 0, [50, 21]),
+                                                (False, 0, [50, 30]), (True, 8, [50, 33])])
+def test_bool_masks_are_recognised(causal, window, lens):
+    B, L, S = 2, 4, 50
+    m = _mask(B, L, S, lens, causal, window)
+    c, w, sl = A.mask_structure(m, B, 8, L, S)
+    assert w == window
+    if window:
+        assert c
+    elif L > 1:
+        assert c == causal
+    if all(x == S for x in lens):
+        assert sl is None
+    else:
+        assert sl.tolist() == lens
+
+
+def test_additive_and_unsupported_masks():
+    assert A.mask_structure(torch.zeros(1, 1, 4, 50), 1, 8, 4, 50) == (False, 0, None)
+    with pytest.raises(NotImplementedError):
+        A.mask_structure(torch.full((1, 1, 4, 50), -1.0), 1, 8, 4, 50)
+    random = torch.rand(1, 1, 4, 50) > 0.5
+    with pytest.raises(NotImplementedError):
+        A.mask_structure(random, 1, 8, 4, 50)
+    with pytest.raises(ValueError):
+        A.mask_structure(torch.ones(1, 1, 3, 50, dtype=torch.bool), 1, 8, 4, 50)
+
+
+def test_install_is_idempotent(monkeypatch):
+    monkeypatch.setattr(A, "_installed", False)
+    base, gen = types.SimpleNamespace(), types.SimpleNamespace()
+    A.install(base, gen)
+    assert base.quantized_scaled_dot_product_attention is A.blocked_quantized_sdpa
+    assert gen.maybe_quantize_kv_cache is A.safe_maybe_quantize_kv_cache
+    other = types.SimpleNamespace()
+    A.install(other, None)  # second call is a no-op
+    assert not hasattr(other, "quantized_scaled_dot_product_attention")
