@@ -17,6 +17,9 @@ Timing:
   * roofline.achieved: the average duration of one call (the decode kernel and the split-merge
     kernel it launches), from one HIP event pair around a batch of eager calls queued behind a
     spin kernel, so the GPU runs them back to back and the pair brackets their kernels only.
+  * roofline.traffic: HBM bytes per call (decode) / per chunk launch (prefill), read from the
+    committed rocprofv3 FETCH_SIZE and WRITE_SIZE summary in profiles/, whose counters are scaled
+    by what they read for a plain 256 MiB device copy (`bench.py --calibrate-copy`).
   * cpu_baseline: the CPU restatement of the reference algorithm (a torch-CPU port of
     m5engine/attention.py with the reference's dtype casts) timed on the host's cores on one
     cache of the same workload, for a bounded number of calls.
@@ -26,7 +29,8 @@ Algorithmic bytes of one decode call:
   + 2 * B * Hq * D * 2                           (the query in, the output out)
 = 272 B per cached token and KV head at 8 bits, 144 B at 4 bits (D = 128, G = 64).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra] [--no-parity]
+                       [--no-prefill | --prefill-only] [--calibrate-copy]
 """
 
 from __future__ import annotations
@@ -35,6 +39,7 @@ import argparse
 import json
 import math
 import os
+import re
 import sys
 import time
 from pathlib import Path
@@ -433,6 +438,20 @@ def prefill_cpu_baseline(cfg, q_last, kt, vt, scale, budget_s=20.0):
                       f"reference_sdpa on the host CPU; median {med:.2f} s"}
 
 
+TRAFFIC_FILE = Path(__file__).resolve().parent / "profiles" / "hbm_traffic_decode_c2_b1_prefill_c3.md"
+
+
+def measured_traffic(key: str):
+    """HBM bytes per launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary (scaled by
+    the copy-kernel calibration recorded there), or None when the summary has no such line."""
+    try:
+        text = TRAFFIC_FILE.read_text()
+    except OSError:
+        return None
+    m = re.search(rf"^bytes_per_(?:call|launch) {re.escape(key)}: (\d+)$", text, re.M)
+    return int(m.group(1)) if m else None
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -443,6 +462,8 @@ def main():
     ap.add_argument("--no-parity", action="store_true", help="skip the oracle check of the headline output")
     ap.add_argument("--no-prefill", action="store_true", help="skip the C3 chunked-prefill leg")
     ap.add_argument("--prefill-only", action="store_true", help="time only the C3 chunked-prefill leg")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run 10 device copies of 256 MiB (reference for rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -463,6 +484,17 @@ def main():
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)
     log(f"[bench] device: {torch.cuda.get_device_name(device)}")
+    if args.calibrate_copy:
+        # A plain copy whose HBM traffic is known (256 MiB read, 256 MiB written per dispatch): the
+        # FETCH_SIZE / WRITE_SIZE counters of these dispatches give the counters' scale.
+        n = 256 * 1024**2
+        src = torch.empty(n // 4, dtype=torch.int32, device=device).random_()
+        dst = torch.empty_like(src)
+        for _ in range(10):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"[bench] calibrate-copy: 10 copies of {n} bytes")
+        return
 
     prefill = None
     if not args.no_prefill:
@@ -483,7 +515,8 @@ def main():
                                    "attention over all prior keys, bf16",
                        "flops_per_step": pr["flops"], "steps": max(1, min(args.steps, 3))},
             "roofline": {"bound": "mfma", "achieved": round(pr["attn_tflops"], 2), "peak": PEAK_MFMA_TFLOPS,
-                         "unit": "TFLOP/s", "frac": round(pr["attn_tflops"] / PEAK_MFMA_TFLOPS, 4), "traffic": None,
+                         "unit": "TFLOP/s", "frac": round(pr["attn_tflops"] / PEAK_MFMA_TFLOPS, 4),
+                         "traffic": measured_traffic("prefill_c3_chunk"),
                          "kernel_ms": round(pr["attn_ms"], 4),
                          "kernel": "prefill_attn_kernel (+ combine_kernel where a chunk's keys are split), summed "
                                    "over the 32 chunks"},
@@ -547,7 +580,7 @@ def main():
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic("decode_c2_b1"),
             "kernel_us": round(res["call_us_mean"], 3),
             "kernel": "decode_attn_kernel + combine_kernel (the two launches of one kvq_decode_attn call)",
         },
