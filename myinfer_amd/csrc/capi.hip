@@ -142,6 +142,10 @@ int kvq_decode_attn(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* 
   int rc = check_attn(q, k, v, out, B, Hq, Hkv, L, D, S, bits, group_size, dtype, scale, window,
                       kvq_decode_workspace_size(B, Hq, Hkv, L, D, S, window), workspace, workspace_bytes);
   if (rc) return rc;
+  // the kernel addresses each (sequence, KV head)'s rows with 32-bit byte offsets
+  for (const kvq_qtensor* t : {k, v})
+    if ((int64_t)S * t->codes_stride_s * 4 > (int64_t)UINT32_MAX || (int64_t)S * t->sb_stride_s * 2 > (int64_t)UINT32_MAX)
+      return fail(KVQ_ERR_UNSUPPORTED, "decode needs S times each row stride within 4 GiB (S=%d)", S);
   return hip_status(kvq::launch_decode(q, k, v, seq_lens, out, B, Hq, Hkv, L, D, S, bits, dtype, scale, causal,
                                        window, workspace, (hipStream_t)stream),
                     "decode_attn launch");

@@ -19,11 +19,12 @@
 //  * The score tile is computed transposed (keys are MFMA rows), which leaves each lane with
 //    the probabilities of its own query row at 8 keys: exactly the A operand of the PV MFMA,
 //    with no shuffle and no LDS round trip.
-//  * K codes: each lane loads 16-32 contiguous bytes of one key row (128-bit loads). V codes:
-//    each lane loads its 4-16 byte column slice of 8 key rows. Scales/biases of a 32-key tile
-//    are fetched with one coalesced load per lane and redistributed through a per-wave LDS slab.
-//  * Each wave streams its tiles through a ring of NBUF register buffers, so NBUF - 1 tiles are
-//    in flight while one is computed.
+//  * Each wave streams its 32-key tiles through a ring of NSLOT LDS slots filled by buffer->LDS
+//    DMA: every code load is one contiguous KiB (16 bytes a lane), scales and biases arrive as
+//    16-bit loads, and no VGPR holds data in flight, so NSLOT - 1 tiles stream while one is
+//    computed. Rows past the sequence end read as zero through the buffer range check. K rows
+//    are stored with their 16-byte chunks XOR-swizzled by row, so the MFMA operand reads (one
+//    key row per lane) are free of LDS bank conflicts.
 //  * Online softmax in the log2 domain; rescaling of the output accumulators is lazy (only when a
 //    row maximum grows). The waves of a workgroup merge in LDS into one (m, l, o[D]) partial per
 //    query row. The last workgroup of each (sequence, KV head, row block) to finish -- found with
@@ -52,7 +53,14 @@ struct DecCfg {
   static constexpr int ROWB = D * BITS / 8;    // code bytes per key row
   static constexpr int KLB = ROWB / 4;         // K code bytes per lane per key (4 lane groups)
   static constexpr int VLB = ROWB / 16;        // V code bytes per lane per key (16 columns)
-  static constexpr int SBB = 4 * NG;           // bytes of one cooperative scale/bias load (2 keys)
+  static constexpr int CPR = ROWB / 16;        // 16-byte chunks per code row
+  static constexpr int RPI = 64 / CPR;         // code rows per 1 KiB DMA instruction
+  static constexpr int CI = kTile / RPI;       // DMA instructions per K (or V) tile
+  static constexpr int TB = kTile * ROWB;      // bytes of a K (or V) tile
+  // a ring slot: [K tile][V tile][sK, bK, sV, bV: 64 4-byte cells each, value in the low half;
+  // cell 32 g + k holds group g of key k]
+  static constexpr int SLOT = 2 * TB + 4 * 256;
+  static constexpr int IPT = 2 * CI + 4;       // DMA instructions per tile
 };
 
 struct DecParams {
@@ -77,61 +85,150 @@ struct DecParams {
   int Hq, Hkv, L, S, rep, nrows, rowblocks, nsplit, chunk, nunits;
   int xcd_remap;  // 1: number workgroups so that consecutive splits share an XCD
   int fused;      // 1: the last workgroup of a unit merges the splits; 0: combine_kernel does
-  int sb_vec;     // scale/bias rows adjacent and aligned for one vector load per key pair
-  int fast;       // sb_vec, and a tile's row offsets fit in 32 bits: full tiles use load_tile_fast
   float scale_log2;
   int causal, window;
-};
-
-template <int D, int BITS>
-struct TileRegs {
-  using C = DecCfg<D, BITS>;
-  Bytes<C::KLB> kc[2];
-  Bytes<(C::VLB < 2 ? 2 : C::VLB)> vc[8];
-  Bytes<C::SBB> sb;
 };
 
 // Token (relative to the tile) of V slot i' (the MFMA k index 8*lg + i') for lane group lg.
 __device__ __forceinline__ int v_token(int lg, int i) { return (i < 4) ? 4 * lg + i : 16 + 4 * lg + (i - 4); }
 
-template <int D, int BITS>
-__device__ __forceinline__ void load_tile(TileRegs<D, BITS>& R, const DecParams& p, const uint8_t* kbase,
-                                          const uint8_t* vbase, const uint8_t* sbase, int64_t sb_row_bytes, int k0,
-                                          int S_b, int n, int lg) {
-  using C = DecCfg<D, BITS>;
-  const bool partial = k0 + kTile > S_b;
-#pragma unroll
-  for (int beta = 0; beta < 2; ++beta) {
-    int t = k0 + 16 * beta + n;
-    if (partial) t = min(t, S_b - 1);
-    R.kc[beta].load(kbase + (int64_t)t * p.kc_ss + lg * C::KLB);
-  }
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    int t = k0 + v_token(lg, i);
-    if (partial) t = min(t, S_b - 1);
-    R.vc[i].load(vbase + (int64_t)t * p.vc_ss + n * C::VLB);
-  }
-  // cooperative scale/bias load: lane -> (array a = lane/16, key pair tp = lane%16)
-  const int tp = __lane_id() & 15;
-  const int t0 = k0 + 2 * tp;
-  if (!partial && p.sb_vec) {
-    R.sb.load(sbase + (int64_t)t0 * sb_row_bytes);
-  } else {
-    const int ta = min(t0, S_b - 1), tb = min(t0 + 1, S_b - 1);
-    if constexpr (C::NG == 1) {
-      const uint32_t lo = *(const uint16_t*)(sbase + (int64_t)ta * sb_row_bytes);
-      const uint32_t hi = *(const uint16_t*)(sbase + (int64_t)tb * sb_row_bytes);
-      R.sb.w[0] = lo | (hi << 16);
-    } else {
-#pragma unroll
-      for (int w = 0; w < C::NG / 2; ++w) {
-        R.sb.w[w] = *(const uint32_t*)(sbase + (int64_t)ta * sb_row_bytes + 4 * w);
-        R.sb.w[C::NG / 2 + w] = *(const uint32_t*)(sbase + (int64_t)tb * sb_row_bytes + 4 * w);
-      }
-    }
-  }
+// Buffer->LDS DMA: lane i's 16 bytes (dma16) or 2 bytes (dma2, in the low half of a 4-byte cell)
+// land at lds + 16 i (+ 4 i); `lds` is wave-uniform. Device-only wrappers keep the target builtin
+// out of the host pass.
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint8_t* lds, uint32_t vo, uint32_t so) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, vo, so, 0, 0);
 }
+__device__ __forceinline__ void dma2(__amdgpu_buffer_rsrc_t r, uint8_t* lds, uint32_t vo, uint32_t so) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 2, vo, so, 0, 0);
+}
+
+// 32-bit LDS address of a pointer into shared memory.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// The LDS operands of one 32-key tile, read by one asm block that also waits for them. The reads
+// are asm so that the compiler does not tie them to the buffer->LDS loads still in flight into
+// other ring slots (it would otherwise wait for every outstanding load before any LDS read); the
+// ring's own vmcnt waits order each slot's fill before its read.
+//   k[beta]  : the lane's KLB bytes of key 16 beta + n (XOR-swizzled chunks)
+//   sb[a][b] : 4 cells of array a (sK, bK, sV, bV) for the lane's group at keys 16 b + 4 lg .. +3
+//   v[i]     : the lane's VLB-byte column slice of key v_token(lg, i)
+template <int ROWB>
+struct TileOps;
+template <>
+struct TileOps<128> {
+  u4 k[2][2];
+  u4 sb[4][2];
+  u2 v[8];
+};
+template <>
+struct TileOps<64> {
+  u4 k[2];
+  u4 sb[4][2];
+  uint32_t v[8];
+};
+template <>
+struct TileOps<32> {
+  u2 k[2];
+  u4 sb[4][2];
+  uint32_t v[8];
+};
+
+// ka0/ka1: the two K chunk addresses of key n (ka1 unused below 128-byte rows); sa: the sb base;
+// va: the V slice address of key 4 lg.
+__device__ __forceinline__ void read_tile(TileOps<128>& t, uint32_t ka0, uint32_t ka1, uint32_t sa, uint32_t va) {
+  asm volatile(
+      "ds_read_b128 %0, %20\n"
+      "ds_read_b128 %1, %21\n"
+      "ds_read_b128 %2, %20 offset:2048\n"
+      "ds_read_b128 %3, %21 offset:2048\n"
+      "ds_read_b128 %4, %22\n"
+      "ds_read_b128 %5, %22 offset:64\n"
+      "ds_read_b128 %6, %22 offset:256\n"
+      "ds_read_b128 %7, %22 offset:320\n"
+      "ds_read_b128 %8, %22 offset:512\n"
+      "ds_read_b128 %9, %22 offset:576\n"
+      "ds_read_b128 %10, %22 offset:768\n"
+      "ds_read_b128 %11, %22 offset:832\n"
+      "ds_read_b64 %12, %23\n"
+      "ds_read_b64 %13, %23 offset:128\n"
+      "ds_read_b64 %14, %23 offset:256\n"
+      "ds_read_b64 %15, %23 offset:384\n"
+      "ds_read_b64 %16, %23 offset:2048\n"
+      "ds_read_b64 %17, %23 offset:2176\n"
+      "ds_read_b64 %18, %23 offset:2304\n"
+      "ds_read_b64 %19, %23 offset:2432\n"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(t.k[0][0]), "=&v"(t.k[0][1]), "=&v"(t.k[1][0]), "=&v"(t.k[1][1]), "=&v"(t.sb[0][0]), "=&v"(t.sb[0][1]),
+        "=&v"(t.sb[1][0]), "=&v"(t.sb[1][1]), "=&v"(t.sb[2][0]), "=&v"(t.sb[2][1]), "=&v"(t.sb[3][0]),
+        "=&v"(t.sb[3][1]), "=&v"(t.v[0]), "=&v"(t.v[1]), "=&v"(t.v[2]), "=&v"(t.v[3]), "=&v"(t.v[4]), "=&v"(t.v[5]),
+        "=&v"(t.v[6]), "=&v"(t.v[7])
+      : "v"(ka0), "v"(ka1), "v"(sa), "v"(va)
+      : "memory");
+}
+__device__ __forceinline__ void read_tile(TileOps<64>& t, uint32_t ka0, uint32_t, uint32_t sa, uint32_t va) {
+  asm volatile(
+      "ds_read_b128 %0, %18\n"
+      "ds_read_b128 %1, %18 offset:1024\n"
+      "ds_read_b128 %2, %19\n"
+      "ds_read_b128 %3, %19 offset:64\n"
+      "ds_read_b128 %4, %19 offset:256\n"
+      "ds_read_b128 %5, %19 offset:320\n"
+      "ds_read_b128 %6, %19 offset:512\n"
+      "ds_read_b128 %7, %19 offset:576\n"
+      "ds_read_b128 %8, %19 offset:768\n"
+      "ds_read_b128 %9, %19 offset:832\n"
+      "ds_read_b32 %10, %20\n"
+      "ds_read_b32 %11, %20 offset:64\n"
+      "ds_read_b32 %12, %20 offset:128\n"
+      "ds_read_b32 %13, %20 offset:192\n"
+      "ds_read_b32 %14, %20 offset:1024\n"
+      "ds_read_b32 %15, %20 offset:1088\n"
+      "ds_read_b32 %16, %20 offset:1152\n"
+      "ds_read_b32 %17, %20 offset:1216\n"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(t.k[0]), "=&v"(t.k[1]), "=&v"(t.sb[0][0]), "=&v"(t.sb[0][1]), "=&v"(t.sb[1][0]), "=&v"(t.sb[1][1]),
+        "=&v"(t.sb[2][0]), "=&v"(t.sb[2][1]), "=&v"(t.sb[3][0]), "=&v"(t.sb[3][1]), "=&v"(t.v[0]), "=&v"(t.v[1]),
+        "=&v"(t.v[2]), "=&v"(t.v[3]), "=&v"(t.v[4]), "=&v"(t.v[5]), "=&v"(t.v[6]), "=&v"(t.v[7])
+      : "v"(ka0), "v"(sa), "v"(va)
+      : "memory");
+}
+__device__ __forceinline__ void read_tile(TileOps<32>& t, uint32_t ka0, uint32_t, uint32_t sa, uint32_t va) {
+  asm volatile(
+      "ds_read_b64 %0, %18\n"
+      "ds_read_b64 %1, %18 offset:512\n"
+      "ds_read_b128 %2, %19\n"
+      "ds_read_b128 %3, %19 offset:64\n"
+      "ds_read_b128 %4, %19 offset:256\n"
+      "ds_read_b128 %5, %19 offset:320\n"
+      "ds_read_b128 %6, %19 offset:512\n"
+      "ds_read_b128 %7, %19 offset:576\n"
+      "ds_read_b128 %8, %19 offset:768\n"
+      "ds_read_b128 %9, %19 offset:832\n"
+      "ds_read_u16 %10, %20\n"
+      "ds_read_u16 %11, %20 offset:32\n"
+      "ds_read_u16 %12, %20 offset:64\n"
+      "ds_read_u16 %13, %20 offset:96\n"
+      "ds_read_u16 %14, %20 offset:512\n"
+      "ds_read_u16 %15, %20 offset:544\n"
+      "ds_read_u16 %16, %20 offset:576\n"
+      "ds_read_u16 %17, %20 offset:608\n"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(t.k[0]), "=&v"(t.k[1]), "=&v"(t.sb[0][0]), "=&v"(t.sb[0][1]), "=&v"(t.sb[1][0]), "=&v"(t.sb[1][1]),
+        "=&v"(t.sb[2][0]), "=&v"(t.sb[2][1]), "=&v"(t.sb[3][0]), "=&v"(t.sb[3][1]), "=&v"(t.v[0]), "=&v"(t.v[1]),
+        "=&v"(t.v[2]), "=&v"(t.v[3]), "=&v"(t.v[4]), "=&v"(t.v[5]), "=&v"(t.v[6]), "=&v"(t.v[7])
+      : "v"(ka0), "v"(sa), "v"(va)
+      : "memory");
+}
+
+// s_waitcnt vmcnt(N) (N < 64), other counters left alone.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+__device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
 
 // K operand (A of S^T = K Q^T) for k-step j: 8 codes of the lane's key as f16 subnormals.
 template <int D, int BITS>
@@ -168,8 +265,8 @@ __device__ __forceinline__ float k_slot_weight(int i) {
 }
 
 // V operand (B of O = P' V) for column block jN: codes of 8 keys at the lane's column.
-template <int D, int BITS>
-__device__ __forceinline__ h8 v_operand(const TileRegs<D, BITS>& R, int jN) {
+template <int D, int BITS, int VB>
+__device__ __forceinline__ h8 v_operand(const Bytes<VB> (&vc)[8], int jN) {
   const int byte_off = (jN * BITS) / 8;  // byte of the lane's slice holding code jN
   const int wi = byte_off / 4;
   const uint32_t jb = (uint32_t)(byte_off % 4);
@@ -177,40 +274,11 @@ __device__ __forceinline__ h8 v_operand(const TileRegs<D, BITS>& R, int jN) {
   u4 r;
 #pragma unroll
   for (int a = 0; a < 4; ++a) {
-    uint32_t y = perm(R.vc[2 * a + 1].w[wi], R.vc[2 * a].w[wi], sel);
+    uint32_t y = perm(vc[2 * a + 1].w[wi], vc[2 * a].w[wi], sel);
     if constexpr (BITS == 4) y &= (jN & 1) ? 0x00F000F0u : 0x000F000Fu;
     r[a] = y;
   }
   return __builtin_bit_cast(h8, r);
-}
-
-// Agent-scope (device-coherent) accesses to the split partials.
-__device__ __forceinline__ void st_agent(float* ptr, float v) {
-  __hip_atomic_store(ptr, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float ld_agent(const float* ptr) {
-  return __hip_atomic_load(const_cast<float*>(ptr), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Per-lane byte offsets of a tile's code loads, relative to the tile's first key row.
-template <int D, int BITS>
-struct LaneOff {
-  uint32_t k[2];
-  uint32_t v[8];
-};
-
-// Full-tile load: buffer loads with the tile's byte offset as the wave-uniform offset and fixed
-// 32-bit lane offsets, so the code loads need no per-tile address arithmetic; `st` is this lane's
-// scale/bias pointer for the tile.
-template <int D, int BITS>
-__device__ __forceinline__ void load_tile_fast(TileRegs<D, BITS>& R, __amdgpu_buffer_rsrc_t kr, uint32_t ks,
-                                               __amdgpu_buffer_rsrc_t vr, uint32_t vs, const uint8_t* st,
-                                               const LaneOff<D, BITS>& o) {
-#pragma unroll
-  for (int beta = 0; beta < 2; ++beta) R.kc[beta].load_buf(kr, o.k[beta], ks);
-#pragma unroll
-  for (int i = 0; i < 8; ++i) R.vc[i].load_buf(vr, o.v[i], vs);
-  R.sb.load(st);
 }
 
 // Rescaling slack, log2 units: a row's running maximum is raised only when a tile's maximum
@@ -218,15 +286,22 @@ __device__ __forceinline__ void load_tile_fast(TileRegs<D, BITS>& R, __amdgpu_bu
 // below 2^kSlack; with fp16 scales (|s| <= 514) the fp16 PV operand p*s stays finite.
 constexpr float kSlack = 6.0f;
 
-template <typename T, int D, int BITS, int NW, int NBUF>
-__global__ __launch_bounds__(NW * 64, 8 / NW) void decode_attn_kernel(DecParams p) {
+// Workgroups per CU the launch bounds ask for: two 4-wave workgroups when their rings fit in LDS
+// together, else one.
+template <int D, int BITS, int NW, int NSLOT>
+constexpr int dec_min_wgs() {
+  return (NW == 4 && 2 * NW * NSLOT * DecCfg<D, BITS>::SLOT <= 160 * 1024) ? 2 : 1;
+}
+
+template <typename T, int D, int BITS, int NW, int NSLOT>
+__global__ __launch_bounds__(NW * 64, (dec_min_wgs<D, BITS, NW, NSLOT>())) void decode_attn_kernel(DecParams p) {
   using C = DecCfg<D, BITS>;
   constexpr int R = C::R;
   constexpr int NT = NW * 64;
-  __shared__ __align__(16) uint16_t sb_lds[NW][4][C::NG][kTile];
-  __shared__ float w_m[NW][R], w_l[NW][R];
-  __shared__ __align__(16) float w_o[NW][R][D];
-  __shared__ float s_w[R][kMaxSplit];
+  // the tile ring while streaming; the waves' (m, l, o) and the split weights afterwards
+  constexpr int kRing = NW * NSLOT * C::SLOT;
+  constexpr int kEpi = (2 * NW * R + NW * R * D + R * kMaxSplit) * 4;
+  __shared__ __align__(16) uint8_t smem[kRing > kEpi ? kRing : kEpi];
   __shared__ unsigned s_prev;
 
   const int lane = __lane_id();
@@ -250,56 +325,77 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void decode_attn_kernel(DecParams 
   const int k_begin = key_base + split * p.chunk;
   const int k_end = min(k_begin + p.chunk, S_b);
   const int ntile = k_end > k_begin ? (k_end - k_begin + kTile - 1) / kTile : 0;
-  // full tiles run through the register ring; a ragged last tile (and every tile of a cache
-  // whose layout the fast loads do not cover) takes the clamped path afterwards
-  const bool ragged = ntile > 0 && (k_end - k_begin) % kTile != 0;
-  const int nfull = p.fast ? ntile - (ragged ? 1 : 0) : 0;
-  const int nring = nfull > wave ? (nfull - wave + NW - 1) / NW : 0;  // ring tiles of this wave
+  const int nmine = ntile > wave ? (ntile - wave + NW - 1) / NW : 0;  // tiles wave, wave + NW, ...
 
-  // ---- per-(b, kv head) bases
-  const uint8_t* kbase = p.kc + (int64_t)b * p.kc_sb + (int64_t)kvh * p.kc_sh;
-  const uint8_t* vbase = p.vc + (int64_t)b * p.vc_sb + (int64_t)kvh * p.vc_sh;
-  const int arr = lane >> 4;  // cooperative scale/bias array of this lane: sK, bK, sV, bV
-  const uint16_t* sbp;
-  {
-    const int64_t ko = (int64_t)b * p.ksb_sb + (int64_t)kvh * p.ksb_sh;
-    const int64_t vo = (int64_t)b * p.vsb_sb + (int64_t)kvh * p.vsb_sh;
-    sbp = arr == 0 ? p.ks + ko : arr == 1 ? p.kb + ko : arr == 2 ? p.vs + vo : p.vb + vo;
-  }
-  const int64_t sb_row_bytes = (arr < 2 ? p.ksb_ss : p.vsb_ss) * 2;
-  const uint8_t* sbase = (const uint8_t*)sbp;
-
-  LaneOff<D, BITS> off;
-#pragma unroll
-  for (int beta = 0; beta < 2; ++beta) off.k[beta] = (uint32_t)((16 * beta + n) * p.kc_ss + lg * C::KLB);
-#pragma unroll
-  for (int i = 0; i < 8; ++i) off.v[i] = (uint32_t)(v_token(lg, i) * p.vc_ss + n * C::VLB);
-  const uint8_t* sb_lane = sbase + (int64_t)(2 * (lane & 15)) * sb_row_bytes;
-  // ring tile i of this wave (clamped to the wave's last ring tile: look-ahead loads past the end
-  // re-read a tile the wave already holds)
-  auto ring_k0 = [&](int i) { return k_begin + kTile * (wave + NW * min(i, nring - 1)); };
-  // code buffers of this (sequence, KV head): the S_b valid rows (the host checks the byte range
-  // fits 32 bits before it enables the fast path)
-  const __amdgpu_buffer_rsrc_t krs = make_rsrc(kbase, (uint32_t)(p.fast ? (int64_t)S_b * p.kc_ss : 0));
-  const __amdgpu_buffer_rsrc_t vrs = make_rsrc(vbase, (uint32_t)(p.fast ? (int64_t)S_b * p.vc_ss : 0));
-  auto ring_load = [&](TileRegs<D, BITS>& buf, int i) {
-    const int k0 = ring_k0(i);
-    load_tile_fast<D, BITS>(buf, krs, (uint32_t)(k0 * p.kc_ss), vrs, (uint32_t)(k0 * p.vc_ss),
-                            sb_lane + (int64_t)k0 * sb_row_bytes, off);
-  };
-
-  TileRegs<D, BITS> buf[NBUF];
-  if (nring > 0) {
-#pragma unroll
-    for (int j = 0; j < NBUF - 1; ++j) ring_load(buf[j], j);
-  }
-
-  // ---- this lane's query row / group
+  // ---- this lane's query row / group, and its raw query slice (loaded before the tile stream
+  // so that waiting for it does not wait for the tiles)
   const int r = n % R, g = n / R;
   const int row = rb * R + r;
   const bool row_ok = row < p.nrows;
   const int hq = kvh * p.rep + (row_ok ? row / p.L : 0);
   const int lq = row_ok ? row % p.L : 0;
+  const bool in_group = (lg * (D / 4)) / 64 == g;
+  u4 qraw[C::KSTEPS];
+  {
+    const uint16_t* qrow = p.q + (int64_t)b * p.q_sb + (int64_t)hq * p.q_sh + (int64_t)lq * p.q_sl + lg * (D / 4);
+#pragma unroll
+    for (int j = 0; j < C::KSTEPS; ++j) qraw[j] = *(const u4*)(qrow + 8 * j);  // in bounds: row and head are clamped
+  }
+
+  // ---- tile stream: buffer resources over the S_b valid rows of this (sequence, KV head); the
+  // host checks that S * row stride fits 32 bits for every array
+  const uint8_t* kbase = p.kc + (int64_t)b * p.kc_sb + (int64_t)kvh * p.kc_sh;
+  const uint8_t* vbase = p.vc + (int64_t)b * p.vc_sb + (int64_t)kvh * p.vc_sh;
+  const __amdgpu_buffer_rsrc_t krs = make_rsrc(kbase, (uint32_t)((int64_t)S_b * p.kc_ss));
+  const __amdgpu_buffer_rsrc_t vrs = make_rsrc(vbase, (uint32_t)((int64_t)S_b * p.vc_ss));
+  __amdgpu_buffer_rsrc_t srs[4];
+  {
+    const int64_t ko = (int64_t)b * p.ksb_sb + (int64_t)kvh * p.ksb_sh;
+    const int64_t vo = (int64_t)b * p.vsb_sb + (int64_t)kvh * p.vsb_sh;
+    const uint32_t kn = (uint32_t)((int64_t)S_b * p.ksb_ss * 2), vn = (uint32_t)((int64_t)S_b * p.vsb_ss * 2);
+    srs[0] = make_rsrc(p.ks + ko, kn);
+    srs[1] = make_rsrc(p.kb + ko, kn);
+    srs[2] = make_rsrc(p.vs + vo, vn);
+    srs[3] = make_rsrc(p.vb + vo, vn);
+  }
+  // lane offsets: code lane l fills 16-byte cell l of each KiB, i.e. row l / CPR and -- for K,
+  // swizzled -- chunk (l % CPR) ^ (row % CPR); scale/bias lane l reads group l / 32 of key l % 32
+  // (for NG == 1 the upper half re-reads the lower half's keys)
+  uint32_t dk[C::CI], dv[C::CI], dsb[4];
+  {
+    const int rr = lane / C::CPR, cc = lane % C::CPR;
+#pragma unroll
+    for (int c = 0; c < C::CI; ++c) {
+      dk[c] = (uint32_t)((int64_t)(c * C::RPI + rr) * p.kc_ss + 16 * (cc ^ (rr % C::CPR)));
+      dv[c] = (uint32_t)((int64_t)(c * C::RPI + rr) * p.vc_ss + 16 * cc);
+    }
+    const int sk = lane & 31, sg = C::NG == 2 ? lane >> 5 : 0;
+    dsb[0] = dsb[1] = (uint32_t)(sk * p.ksb_ss * 2 + 2 * sg);
+    dsb[2] = dsb[3] = (uint32_t)(sk * p.vsb_ss * 2 + 2 * sg);
+  }
+  uint8_t* const ring = smem + wave * (NSLOT * C::SLOT);
+  auto tile_k0 = [&](int i) { return k_begin + kTile * (wave + NW * i); };
+  // tile i of this wave -> slot `slot`; past the wave's last tile it re-reads that tile, so the
+  // number of loads in flight behind any tile is always (NSLOT - 1) * IPT
+  const int last = max(nmine - 1, 0);
+  auto issue = [&](int i, int slot) {
+    const int k0 = tile_k0(min(i, last));
+    uint8_t* sl = ring + slot * C::SLOT;
+    const uint32_t ko = (uint32_t)((int64_t)k0 * p.kc_ss), vo = (uint32_t)((int64_t)k0 * p.vc_ss);
+#pragma unroll
+    for (int c = 0; c < C::CI; ++c) dma16(krs, sl + 1024 * c, dk[c], ko);
+#pragma unroll
+    for (int c = 0; c < C::CI; ++c) dma16(vrs, sl + C::TB + 1024 * c, dv[c], vo);
+    const uint32_t kso = (uint32_t)((int64_t)k0 * p.ksb_ss * 2), vso = (uint32_t)((int64_t)k0 * p.vsb_ss * 2);
+#pragma unroll
+    for (int a = 0; a < 4; ++a) dma2(srs[a], sl + 2 * C::TB + 256 * a, dsb[a], a < 2 ? kso : vso);
+  };
+  // nothing that waits for the query loads may be scheduled into (or before) the first tile loads
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int j = 0; j < NSLOT; ++j) issue(j, j);
+  __builtin_amdgcn_sched_barrier(0);
+
   const int qpos = S_b - p.L + lq;
   const int lo_r = p.window > 0 ? max(0, qpos - p.window + 1) : 0;
   const int hi_r = p.causal ? min(S_b, qpos + 1) : S_b;
@@ -307,26 +403,23 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void decode_attn_kernel(DecParams 
   const int hi_all = p.causal ? S_b - p.L + 1 : S_b;
 
   // ---- Q operand: slot i of k-step j is q[row][lg*D/4 + 8j + dim(i)] if that dim is in group g
-  const bool in_group = (lg * (D / 4)) / 64 == g;
   float qv[C::KSTEPS][8];
   float qmax = 0.0f, qsum = 0.0f;
-  {
-    const uint16_t* qrow = p.q + (int64_t)b * p.q_sb + (int64_t)hq * p.q_sh + (int64_t)lq * p.q_sl + lg * (D / 4);
+  const bool q_on = row_ok && in_group;
 #pragma unroll
-    for (int j = 0; j < C::KSTEPS; ++j) {
-      u4 raw = (row_ok && in_group) ? *(const u4*)(qrow + 8 * j) : u4{0, 0, 0, 0};
-      float e[8];
+  for (int j = 0; j < C::KSTEPS; ++j) {
+    if (!q_on) qraw[j] = u4{0, 0, 0, 0};
+    float e[8];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        e[2 * i] = to_float((uint16_t)(raw[i] & 0xffffu), T{});
-        e[2 * i + 1] = to_float((uint16_t)(raw[i] >> 16), T{});
-      }
+    for (int i = 0; i < 4; ++i) {
+      e[2 * i] = to_float((uint16_t)(qraw[j][i] & 0xffffu), T{});
+      e[2 * i + 1] = to_float((uint16_t)(qraw[j][i] >> 16), T{});
+    }
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        qv[j][i] = e[k_slot_dim<BITS>(i)];
-        qmax = fmaxf(qmax, fabsf(qv[j][i]));
-        qsum += qv[j][i];
-      }
+    for (int i = 0; i < 8; ++i) {
+      qv[j][i] = e[k_slot_dim<BITS>(i)];
+      qmax = fmaxf(qmax, fabsf(qv[j][i]));
+      qsum += qv[j][i];
     }
   }
 #pragma unroll
@@ -354,48 +447,45 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void decode_attn_kernel(DecParams 
 #pragma unroll
   for (int jn = 0; jn < C::NBLK; ++jn) acc_o[jn] = f4{0, 0, 0, 0};
 
-  auto compute = [&](const TileRegs<D, BITS>& Rg, int k0) {
-    // scales/biases -> LDS as [array][group][key], then each lane reads its keys' values
-    {
-      const int tp = lane & 15;
-#pragma unroll
-      for (int gg = 0; gg < C::NG; ++gg) {
-        uint32_t v;
-        if constexpr (C::NG == 1) {
-          v = Rg.sb.w[0];
-        } else {
-          const int wlo = gg / 2;
-          const uint32_t sel = (gg & 1) ? 0x07060302u : 0x05040100u;
-          v = perm(Rg.sb.w[C::NG / 2 + wlo], Rg.sb.w[wlo], sel);
-        }
-        *(uint32_t*)&sb_lds[wave][arr][gg][2 * tp] = v;
-      }
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    u2 sbr[4][2];
-#pragma unroll
-    for (int a = 0; a < 4; ++a)
-#pragma unroll
-      for (int beta = 0; beta < 2; ++beta) sbr[a][beta] = *(const u2*)&sb_lds[wave][a][g][16 * beta + 4 * lg];
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    auto sbv = [&](int a, int beta, int i) -> float {
-      const uint32_t w = sbr[a][beta][i >> 1];
-      return to_float((uint16_t)((i & 1) ? (w >> 16) : (w & 0xffffu)), T{});
-    };
+  // per-lane LDS offsets of the tile operands, relative to a slot
+  const int sw = n % C::CPR;  // the swizzle of key n (and of key 16 + n)
+  uint32_t off_k0, off_k1;
+  if constexpr (C::KLB == 32) {
+    off_k0 = n * C::ROWB + 16 * ((2 * lg) ^ sw);
+    off_k1 = n * C::ROWB + 16 * ((2 * lg + 1) ^ sw);
+  } else if constexpr (C::KLB == 16) {
+    off_k0 = off_k1 = n * C::ROWB + 16 * (lg ^ sw);
+  } else {
+    off_k0 = off_k1 = n * C::ROWB + 16 * ((lg >> 1) ^ sw) + 8 * (lg & 1);
+  }
+  const uint32_t off_sb = 2 * C::TB + 4 * (32 * g + 4 * lg);
+  const uint32_t off_v = C::TB + 4 * lg * C::ROWB + n * C::VLB;
+
+  auto compute = [&](const TileOps<C::ROWB>& op, int k0) {
+    auto sbv = [&](int a, int beta, int i) -> float { return to_float((uint16_t)(op.sb[a][beta][i] & 0xffffu), T{}); };
 
     // S^T = K Q^T: rows = 16 keys of block beta, columns = (query row, group)
     f4 sacc[2];
 #pragma unroll
     for (int beta = 0; beta < 2; ++beta) {
+      Bytes<C::KLB> kc;
+      if constexpr (C::KLB == 32) {
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          kc.w[w] = op.k[beta][0][w];
+          kc.w[4 + w] = op.k[beta][1][w];
+        }
+      } else if constexpr (C::KLB == 16) {
+#pragma unroll
+        for (int w = 0; w < 4; ++w) kc.w[w] = op.k[beta][w];
+      } else {
+        kc.w[0] = op.k[beta][0];
+        kc.w[1] = op.k[beta][1];
+      }
       sacc[beta] = f4{0, 0, 0, 0};
 #pragma unroll
       for (int j = 0; j < C::KSTEPS; ++j)
-        sacc[beta] = __builtin_amdgcn_mfma_f32_16x16x32_f16(k_operand<D, BITS>(Rg.kc[beta], j), qop[j], sacc[beta],
-                                                            0, 0, 0);
+        sacc[beta] = __builtin_amdgcn_mfma_f32_16x16x32_f16(k_operand<D, BITS>(kc, j), qop[j], sacc[beta], 0, 0, 0);
     }
     float sc[8];
 #pragma unroll
@@ -448,34 +538,42 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void decode_attn_kernel(DecParams 
 #pragma unroll
     for (int a = 0; a < 4; ++a) aw[a] = pack_f16x2(pa[2 * a], pa[2 * a + 1]);
     const h8 aop = __builtin_bit_cast(h8, aw);
+    // V codes of the lane's column slice at its 8 keys
+    constexpr int VB = C::VLB < 2 ? 2 : C::VLB;
+    Bytes<VB> vc[8];
 #pragma unroll
-    for (int jn = 0; jn < C::NBLK; ++jn)
-      acc_o[jn] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, v_operand<D, BITS>(Rg, jn), acc_o[jn], 0, 0, 0);
-  };
-
-  // ---- main loop: a ring of NBUF tile buffers, NBUF - 1 loads ahead of the compute
-  if (nring > 0) {
-    int i = 0;
-    for (; i + NBUF <= nring; i += NBUF) {
-#pragma unroll
-      for (int j = 0; j < NBUF; ++j) {
-        ring_load(buf[(j + NBUF - 1) % NBUF], i + j + NBUF - 1);
-        compute(buf[j], ring_k0(i + j));
+    for (int i = 0; i < 8; ++i) {
+      if constexpr (C::VLB == 8) {
+        vc[i].w[0] = op.v[i][0];
+        vc[i].w[1] = op.v[i][1];
+      } else {
+        vc[i].w[0] = op.v[i];
       }
     }
-    // the fewer than NBUF tiles left are already in buf[0 .. NBUF-2]
 #pragma unroll
-    for (int j = 0; j < NBUF - 1; ++j)
-      if (i + j < nring) compute(buf[j], ring_k0(i + j));
-  }
-  // ---- clamped tiles: the ragged last tile, or every tile when the fast loads do not apply
-  for (int t = p.fast ? ntile - 1 : wave; t < ntile; t += NW) {
-    if (p.fast && (!ragged || t % NW != wave)) break;
-    const int k0 = k_begin + kTile * t;
-    load_tile<D, BITS>(buf[0], p, kbase, vbase, sbase, sb_row_bytes, k0, S_b, n, lg);
-    compute(buf[0], k0);
-  }
+    for (int jn = 0; jn < C::NBLK; ++jn)
+      acc_o[jn] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, v_operand<D, BITS, VB>(vc, jn), acc_o[jn], 0, 0, 0);
+  };
 
+  // ---- main loop: tile i is read out of its slot, the slot is refilled with tile i + NSLOT, and
+  // tile i is computed while NSLOT tiles stream
+  const uint32_t ring_lds = lds_addr(ring);
+  for (int i = 0; i < nmine; ++i) {
+    const int slot = i % NSLOT;
+    wait_vmcnt<(NSLOT - 1) * C::IPT>();  // tile i has landed
+    const uint32_t sa = ring_lds + slot * C::SLOT;
+    TileOps<C::ROWB> op;
+    read_tile(op, sa + off_k0, sa + off_k1, sa + off_sb, sa + off_v);
+    issue(i + NSLOT, slot);
+    compute(op, tile_k0(i));
+  }
+  wait_vmcnt<0>();  // the look-ahead loads past the last tile land before the ring is reused
+  __syncthreads();  // every wave is done with its ring: the space is reused below
+
+  float* const w_m = (float*)smem;     // [NW][R]
+  float* const w_l = w_m + NW * R;     // [NW][R]
+  float* const w_o = w_l + NW * R;     // [NW][R][D]
+  float* const s_w = w_o + NW * R * D;  // [R][kMaxSplit]
   // ---- wave epilogue: sums over the 4 lane groups, then stage (m, l, o) in LDS
   l_part = add_xor32(add_xor16(l_part));
   ob_part = add_xor32(add_xor16(ob_part));
@@ -483,8 +581,8 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void decode_attn_kernel(DecParams 
 #pragma unroll
   for (int i = 0; i < 4; ++i) obi[i] = shfl(ob_part, 4 * lg + i);
   if (lg == 0 && n < R) {
-    w_m[wave][n] = m_run;
-    w_l[wave][n] = l_part;
+    w_m[wave * R + n] = m_run;
+    w_l[wave * R + n] = l_part;
   }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -494,55 +592,62 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void decode_attn_kernel(DecParams 
       for (int jn = 0; jn < C::NBLK; ++jn) {
         float sc = 16777216.0f;
         if constexpr (BITS == 4) sc = (jn & 1) ? 1048576.0f : 16777216.0f;
-        w_o[wave][m % R][(D / 16) * n + jn] = acc_o[jn][i] * sc + obi[i];
+        w_o[(wave * R + m % R) * D + (D / 16) * n + jn] = acc_o[jn][i] * sc + obi[i];
       }
     }
   }
   __syncthreads();
 
-  // ---- merge the waves: this workgroup's (m, l, o) per row; a single split writes the output
+  // ---- merge the waves: this workgroup's (m, l, o) per row, one float4 of o per thread; a single
+  // split writes the output, otherwise the partial goes to the workspace split-major:
+  // o at ((unit * nsplit + split) * R + row) * D, (m, l) at the same index in pairs
+  constexpr int NV = R * D / 4;
+  static_assert(NV <= NT, "one float4 of a partial per thread");
   const bool single = p.nsplit == 1;
-  for (int idx = threadIdx.x; idx < R * D; idx += NT) {
-    const int rr = idx / D, d = idx % D;
-    const int rw = rb * R + rr;
-    if (rw >= p.nrows) continue;
+  const int i4 = threadIdx.x;
+  const int rr = (4 * i4) / D, d0 = (4 * i4) % D;
+  const int rw = rb * R + rr;
+  const bool mine = i4 < NV && rw < p.nrows;
+  const int hh = kvh * p.rep + rw / p.L, ll = rw % p.L;
+  uint16_t* const orow = p.out + (int64_t)b * p.o_sb + (int64_t)hh * p.o_sh + (int64_t)ll * p.o_sl + d0;
+  auto write_out = [&](f4 o, float inv) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) orow[e] = from_float(o[e] * inv, T{});
+  };
+  const __amdgpu_buffer_rsrc_t ro = make_rsrc(p.part_o + (int64_t)unit * p.nsplit * (R * D), (uint32_t)(p.nsplit * R * D * 4));
+  const __amdgpu_buffer_rsrc_t rm = make_rsrc(p.part_ml + (int64_t)unit * p.nsplit * (2 * R), (uint32_t)(p.nsplit * R * 8));
+  if (i4 < NV) {
     float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < NW; ++w) M = fmaxf(M, w_m[w][rr]);
-    float o = 0.0f, lsum = 0.0f;
+    for (int w = 0; w < NW; ++w) M = fmaxf(M, w_m[w * R + rr]);
+    f4 o = {0, 0, 0, 0};
+    float lsum = 0.0f;
     if (M != -INFINITY) {
 #pragma unroll
       for (int w = 0; w < NW; ++w) {
-        const float mw = w_m[w][rr];
+        const float mw = w_m[w * R + rr];
         if (mw != -INFINITY) {
           const float f = exp2_fast(mw - M);
-          o += f * w_o[w][rr][d];
-          lsum += f * w_l[w][rr];
+          o += f * *(const f4*)&w_o[(w * R + rr) * D + d0];
+          lsum += f * w_l[w * R + rr];
         }
       }
     }
     if (single) {
-      const int hh = kvh * p.rep + rw / p.L, ll = rw % p.L;
-      uint16_t* orow = p.out + (int64_t)b * p.o_sb + (int64_t)hh * p.o_sh + (int64_t)ll * p.o_sl;
-      orow[d] = from_float(lsum > 0.0f ? o / lsum : 0.0f, T{});
+      if (mine) write_out(o, lsum > 0.0f ? 1.0f / lsum : 0.0f);
+    } else if (p.fused) {
+      store_agent_b128(ro, 16 * i4 + split * (R * D * 4), o);
+      if (d0 == 0) store_agent_b64(rm, 8 * rr + split * (R * 8), make_float2(M, lsum));
     } else {
-      const int64_t slot = ((int64_t)unit * R + rr) * p.nsplit + split;
-      if (p.fused) {
-        st_agent(p.part_o + slot * D + d, o);
-        if (d == 0) {
-          st_agent(p.part_ml + 2 * slot, M);
-          st_agent(p.part_ml + 2 * slot + 1, lsum);
-        }
-      } else {
-        p.part_o[slot * D + d] = o;
-        if (d == 0) ((float2*)p.part_ml)[slot] = make_float2(M, lsum);
-      }
+      const int64_t pi = ((int64_t)unit * p.nsplit + split) * R + rr;
+      *(f4*)(p.part_o + pi * D + d0) = o;
+      if (d0 == 0) ((float2*)p.part_ml)[pi] = make_float2(M, lsum);
     }
   }
   if (single || !p.fused) return;
 
   // ---- the last workgroup of this unit to finish merges the splits. The partials were written
-  // with agent-scope stores; once they are acknowledged (s_waitcnt) the counter increment is
+  // with agent-scope (sc1) stores; once they are acknowledged (s_waitcnt) the counter increment is
   // ordered after them at the device's coherence point, and the merging workgroup reads them with
   // agent-scope loads. No device-scope fence is needed (on gfx950 one writes back the XCD's L2).
   __builtin_amdgcn_s_waitcnt(0);
@@ -553,68 +658,63 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void decode_attn_kernel(DecParams 
   if (s_prev != (unsigned)(p.nsplit - 1)) return;
   if (threadIdx.x == 0) __hip_atomic_store(&p.counters[unit], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
-  // weights w_s / sum_s w_s l_s per row, one wave per row
-  for (int rr = wave; rr < R; rr += NW) {
-    const int64_t base = ((int64_t)unit * R + rr) * p.nsplit;
-    float m0 = -INFINITY, l0 = 0.0f, m1 = -INFINITY, l1 = 0.0f;
-    if (lane < p.nsplit) {
-      m0 = ld_agent(p.part_ml + 2 * (base + lane));
-      l0 = ld_agent(p.part_ml + 2 * (base + lane) + 1);
-    }
-    if (lane + 64 < p.nsplit) {
-      m1 = ld_agent(p.part_ml + 2 * (base + lane + 64));
-      l1 = ld_agent(p.part_ml + 2 * (base + lane + 64) + 1);
-    }
-    m0 = l0 > 0.0f ? m0 : -INFINITY;
-    m1 = l1 > 0.0f ? m1 : -INFINITY;
-    const float M = wave_max(fmaxf(m0, m1));
-    const float w0 = (M == -INFINITY || m0 == -INFINITY) ? 0.0f : exp2_fast(m0 - M);
-    const float w1 = (M == -INFINITY || m1 == -INFINITY) ? 0.0f : exp2_fast(m1 - M);
-    const float Lsum = wave_sum(w0 * l0 + w1 * l1);
+  // this thread's float4 of the first 32 splits, in flight while the weights are formed
+  constexpr int CH = 32;
+  f4 po[CH];
+#pragma unroll
+  for (int u = 0; u < CH; ++u)
+    po[u] = (i4 < NV && u < p.nsplit) ? load_agent_b128(ro, 16 * i4, u * (R * D * 4)) : f4{0, 0, 0, 0};
+  // weights w_s / sum_s w_s l_s per row: one wave per row, lane = split
+  for (int r2 = wave; r2 < R; r2 += NW) {
+    float2 v0 = make_float2(-INFINITY, 0.0f), v1 = v0;
+    if (lane < p.nsplit) v0 = load_agent_b64(rm, 8 * r2, lane * (R * 8));
+    if (lane + 64 < p.nsplit) v1 = load_agent_b64(rm, 8 * r2, (lane + 64) * (R * 8));
+    const float m0 = v0.y > 0.0f ? v0.x : -INFINITY, m1 = v1.y > 0.0f ? v1.x : -INFINITY;
+    const float Mx = wave_max(fmaxf(m0, m1));
+    const float w0 = (Mx == -INFINITY || m0 == -INFINITY) ? 0.0f : exp2_fast(m0 - Mx);
+    const float w1 = (Mx == -INFINITY || m1 == -INFINITY) ? 0.0f : exp2_fast(m1 - Mx);
+    const float Lsum = wave_sum(w0 * v0.y + w1 * v1.y);
     const float inv = Lsum > 0.0f ? 1.0f / Lsum : 0.0f;
-    if (lane < p.nsplit) s_w[rr][lane] = w0 * inv;
-    if (lane + 64 < p.nsplit) s_w[rr][lane + 64] = w1 * inv;
+    if (lane < p.nsplit) s_w[r2 * kMaxSplit + lane] = w0 * inv;
+    if (lane + 64 < p.nsplit) s_w[r2 * kMaxSplit + lane + 64] = w1 * inv;
   }
   __syncthreads();
-  for (int idx = threadIdx.x; idx < R * D; idx += NT) {
-    const int rr = idx / D, d = idx % D;
-    const int rw = rb * R + rr;
-    if (rw >= p.nrows) continue;
-    const float* po = p.part_o + ((int64_t)unit * R + rr) * p.nsplit * D + d;
-    float acc = 0.0f;
-    int s = 0;
-    for (; s + 8 <= p.nsplit; s += 8) {
-      float v[8];
+  if (!mine) return;
+  const float* wrow = s_w + rr * kMaxSplit;
+  f4 acc = {0, 0, 0, 0};
 #pragma unroll
-      for (int u = 0; u < 8; ++u) v[u] = ld_agent(po + (int64_t)(s + u) * D);
+  for (int u = 0; u < CH; ++u)
+    if (u < p.nsplit) acc += wrow[u] * po[u];
+  for (int s0 = CH; s0 < p.nsplit; s0 += CH) {
 #pragma unroll
-      for (int u = 0; u < 8; ++u) acc += s_w[rr][s + u] * v[u];
-    }
-    for (; s < p.nsplit; ++s) acc += s_w[rr][s] * ld_agent(po + (int64_t)s * D);
-    const int hh = kvh * p.rep + rw / p.L, ll = rw % p.L;
-    p.out[(int64_t)b * p.o_sb + (int64_t)hh * p.o_sh + (int64_t)ll * p.o_sl + d] = from_float(acc, T{});
+    for (int u = 0; u < CH; ++u)
+      po[u] = s0 + u < p.nsplit ? load_agent_b128(ro, 16 * i4, (s0 + u) * (R * D * 4)) : f4{0, 0, 0, 0};
+#pragma unroll
+    for (int u = 0; u < CH; ++u)
+      if (s0 + u < p.nsplit) acc += wrow[s0 + u] * po[u];
   }
+  write_out(acc, 1.0f);
 }
 
 // ------------------------------------------------------------------------------------------
 // Host side: plan, workspace, launch.
 
 struct DecPlan {
-  int R, rowblocks, chunk, nsplit, span, nunits, nw, nbuf, fused;
+  int R, rowblocks, chunk, nsplit, span, nunits, nw, nslot, fused;
 };
 
 struct DecTune {
-  int nw, nbuf, target_wgs, fused;
+  int nw, nslot, target_wgs, fused;
 };
 
-// Launch-shape defaults; KVQ_DECODE_TUNE="waves,buffers,workgroups,fused" overrides them (read
-// once per process).
+// Launch-shape defaults; KVQ_DECODE_TUNE="waves,slots,workgroups,fused" overrides them (read once
+// per process). 8-wave workgroups take 2 ring slots (the ring of 3 would not fit in LDS).
 static DecTune decode_tune() {
   static DecTune t = [] {
-    DecTune d{8, 2, 256, 0};
+    DecTune d{4, 2, 256, 0};
     if (const char* e = getenv("KVQ_DECODE_TUNE")) {
       int a = 0, b = 0, c = 0, f = 1;
-      if (sscanf(e, "%d,%d,%d,%d", &a, &b, &c, &f) >= 3 && (a == 4 || a == 8) && b >= 2 && b <= 4 && c >= 1)
+      if (sscanf(e, "%d,%d,%d,%d", &a, &b, &c, &f) >= 3 && (a == 4 || (a == 8 && b == 2)) && b >= 2 && b <= 4 && c >= 1)
         d = {a, b, c, f != 0};
     }
     return d;
@@ -626,7 +726,7 @@ DecPlan decode_plan(int B, int Hq, int Hkv, int L, int D, int S, int window, int
   DecPlan pl;
   const DecTune tune = decode_tune();
   pl.nw = D == 128 ? tune.nw : 4;
-  pl.nbuf = D == 128 ? tune.nbuf : 2;
+  pl.nslot = D == 128 ? tune.nslot : 2;
   pl.R = 16 / (D / 64);
   const int nrows = (Hq / Hkv) * L;
   pl.rowblocks = (nrows + pl.R - 1) / pl.R;
@@ -663,9 +763,9 @@ size_t decode_workspace_bytes(int B, int Hq, int Hkv, int L, int D, int S, int w
   return decode_layout(pl, D).total;
 }
 
-template <typename T, int D, int BITS, int NW, int NBUF>
+template <typename T, int D, int BITS, int NW, int NSLOT>
 static hipError_t launch_decode_t(const DecParams& p, hipStream_t stream) {
-  hipLaunchKernelGGL((decode_attn_kernel<T, D, BITS, NW, NBUF>), dim3(p.nunits * p.nsplit), dim3(NW * 64), 0, stream,
+  hipLaunchKernelGGL((decode_attn_kernel<T, D, BITS, NW, NSLOT>), dim3(p.nunits * p.nsplit), dim3(NW * 64), 0, stream,
                      p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || p.nsplit == 1 || p.fused) return e;
@@ -683,19 +783,15 @@ static hipError_t launch_decode_t(const DecParams& p, hipStream_t stream) {
   m.R = DecCfg<D, BITS>::R;
   m.rowblocks = p.rowblocks;
   m.nsplit = p.nsplit;
-  m.position_major = 0;
   return launch_combine<T, D>(m, p.nunits / (p.Hkv * p.rowblocks), stream);
 }
 
 template <typename T, int D, int BITS>
 static hipError_t launch_decode_shape(const DecParams& p, const DecPlan& pl, hipStream_t stream) {
   if constexpr (D == 128) {
-    if (pl.nw == 8) {
-      if (pl.nbuf == 2) return launch_decode_t<T, D, BITS, 8, 2>(p, stream);
-      return launch_decode_t<T, D, BITS, 8, 3>(p, stream);
-    }
-    if (pl.nbuf == 2) return launch_decode_t<T, D, BITS, 4, 2>(p, stream);
-    if (pl.nbuf == 3) return launch_decode_t<T, D, BITS, 4, 3>(p, stream);
+    if (pl.nw == 8) return launch_decode_t<T, D, BITS, 8, 2>(p, stream);
+    if (pl.nslot == 2) return launch_decode_t<T, D, BITS, 4, 2>(p, stream);
+    if (pl.nslot == 3) return launch_decode_t<T, D, BITS, 4, 3>(p, stream);
     return launch_decode_t<T, D, BITS, 4, 4>(p, stream);
   } else {
     return launch_decode_t<T, D, BITS, 4, 2>(p, stream);
@@ -753,18 +849,6 @@ hipError_t launch_decode(const kvq_rows* q, const kvq_qtensor* k, const kvq_qten
   p.scale_log2 = scale * 1.4426950408889634f;
   p.causal = causal;
   p.window = window;
-  {
-    const int NG = D / 64;
-    const int64_t vb = 4 * NG;  // bytes of one 2-key vector load
-    auto ok = [&](const void* base, int64_t sbb, int64_t sbh, int64_t sbs) {
-      return sbs == NG && ((uintptr_t)base % vb) == 0 && (sbb * 2) % vb == 0 && (sbh * 2) % vb == 0;
-    };
-    p.sb_vec = ok(k->scales, k->sb_stride_b, k->sb_stride_h, k->sb_stride_s) &&
-               ok(k->biases, k->sb_stride_b, k->sb_stride_h, k->sb_stride_s) &&
-               ok(v->scales, v->sb_stride_b, v->sb_stride_h, v->sb_stride_s) &&
-               ok(v->biases, v->sb_stride_b, v->sb_stride_h, v->sb_stride_s);
-    p.fast = p.sb_vec && (int64_t)S * std::max(p.kc_ss, p.vc_ss) < ((int64_t)1 << 31);
-  }
   const bool bf = dtype == KVQ_DTYPE_BF16;
 #define KVQ_DEC(TT, DD, BB) return launch_decode_shape<TT, DD, BB>(p, pl, stream)
   if (D == 128) {

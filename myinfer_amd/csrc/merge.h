@@ -6,10 +6,9 @@
 // l_s = 0 saw no key and drop out); a row no split saw is written as 0.
 //
 // Partials are laid out by "unit" -- the (sequence, KV head, row block) a workgroup serves -- with
-// R rows per unit: slot = (unit * R + r) * nsplit + split; o at part_o[slot * D], (m, l) at
-// part_ml[2 * slot]. The row order inside a unit depends on the producing kernel:
-//   head-major     (decode)  row index = local head * L + query position
-//   position-major (prefill) row index = query position * rep + local head
+// R rows per unit, split-major: o of (unit, split, r) at part_o[((unit * nsplit + split) * R + r) * D],
+// (m, l) at part_ml[2 * ((unit * nsplit + split) * R + r)]. Row r of a unit is query position
+// r % L of local head r / L.
 #pragma once
 
 #include <math.h>
@@ -46,7 +45,6 @@ struct MergeParams {
   uint16_t* out;
   int64_t o_sb, o_sh, o_sl;
   int Hq, Hkv, L, rep, R, rowblocks, nsplit;
-  int position_major;
 };
 
 // One wave per (output row, 64 columns) item, grid-stride over the items beyond two waves of
@@ -61,17 +59,17 @@ __global__ __launch_bounds__(64) void combine_kernel(MergeParams p, int nitems) 
     const int grow = item / (D / 64), d = (item % (D / 64)) * 64 + lane;
     const int l = grow % p.L, h = (grow / p.L) % p.Hq, b = grow / (p.L * p.Hq);
     const int kvh = h / p.rep;
-    const int rw = p.position_major ? l * p.rep + (h - kvh * p.rep) : (h - kvh * p.rep) * p.L + l;
+    const int rw = (h - kvh * p.rep) * p.L + l;
     const int unit = (b * p.Hkv + kvh) * p.rowblocks + rw / p.R;
-    const int64_t base = ((int64_t)unit * p.R + rw % p.R) * p.nsplit;
+    const int64_t base = (int64_t)unit * p.nsplit * p.R + rw % p.R;  // split s at base + s * R
     const float* po = p.part_o + base * D + d;
     float o[CH];
 #pragma unroll
-    for (int u = 0; u < CH; ++u) o[u] = u < p.nsplit ? po[(int64_t)u * D] : 0.0f;
+    for (int u = 0; u < CH; ++u) o[u] = u < p.nsplit ? po[(int64_t)u * p.R * D] : 0.0f;
     {
       const float2* ml = (const float2*)p.part_ml + base;
-      const float2 v0 = lane < p.nsplit ? ml[lane] : make_float2(-INFINITY, 0.0f);
-      const float2 v1 = lane + 64 < p.nsplit ? ml[lane + 64] : make_float2(-INFINITY, 0.0f);
+      const float2 v0 = lane < p.nsplit ? ml[(int64_t)lane * p.R] : make_float2(-INFINITY, 0.0f);
+      const float2 v1 = lane + 64 < p.nsplit ? ml[(int64_t)(lane + 64) * p.R] : make_float2(-INFINITY, 0.0f);
       const float m0 = v0.y > 0.0f ? v0.x : -INFINITY, m1 = v1.y > 0.0f ? v1.x : -INFINITY;
       const float M = wave_max(fmaxf(m0, m1));
       const float w0 = (M == -INFINITY || m0 == -INFINITY) ? 0.0f : exp2_fast(m0 - M);
@@ -92,7 +90,7 @@ __global__ __launch_bounds__(64) void combine_kernel(MergeParams p, int nitems) 
       if (u < p.nsplit) acc += s_w[u] * o[u];
     for (int s0 = CH; s0 < p.nsplit; s0 += CH) {
 #pragma unroll
-      for (int u = 0; u < CH; ++u) o[u] = s0 + u < p.nsplit ? po[(int64_t)(s0 + u) * D] : 0.0f;
+      for (int u = 0; u < CH; ++u) o[u] = s0 + u < p.nsplit ? po[(int64_t)(s0 + u) * p.R * D] : 0.0f;
 #pragma unroll
       for (int u = 0; u < CH; ++u)
         if (s0 + u < p.nsplit) acc += s_w[s0 + u] * o[u];
