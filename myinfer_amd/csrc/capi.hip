@@ -79,6 +79,9 @@ int check_attn(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v, co
       return fail(KVQ_ERR_INVALID, "codes must be 16-byte aligned with 16-byte-multiple row, head and batch strides");
     if (t->codes_stride_s < row_words) return fail(KVQ_ERR_INVALID, "codes row stride %lld is smaller than D*bits/32=%lld", (long long)t->codes_stride_s, (long long)row_words);
     if (t->sb_stride_s < D / 64) return fail(KVQ_ERR_INVALID, "scales row stride %lld is smaller than D/group=%d", (long long)t->sb_stride_s, D / 64);
+    // the kernels address each (sequence, KV head)'s rows with 32-bit byte offsets
+    if ((int64_t)S * t->codes_stride_s * 4 > (int64_t)UINT32_MAX || (int64_t)S * t->sb_stride_s * 2 > (int64_t)UINT32_MAX)
+      return fail(KVQ_ERR_UNSUPPORTED, "attention needs S times each row stride within 4 GiB (S=%d)", S);
   }
   if (!workspace || workspace_bytes < ws_needed)
     return fail(KVQ_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", ws_needed, workspace ? workspace_bytes : (size_t)0);
@@ -142,10 +145,6 @@ int kvq_decode_attn(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* 
   int rc = check_attn(q, k, v, out, B, Hq, Hkv, L, D, S, bits, group_size, dtype, scale, window,
                       kvq_decode_workspace_size(B, Hq, Hkv, L, D, S, window), workspace, workspace_bytes);
   if (rc) return rc;
-  // the kernel addresses each (sequence, KV head)'s rows with 32-bit byte offsets
-  for (const kvq_qtensor* t : {k, v})
-    if ((int64_t)S * t->codes_stride_s * 4 > (int64_t)UINT32_MAX || (int64_t)S * t->sb_stride_s * 2 > (int64_t)UINT32_MAX)
-      return fail(KVQ_ERR_UNSUPPORTED, "decode needs S times each row stride within 4 GiB (S=%d)", S);
   return hip_status(kvq::launch_decode(q, k, v, seq_lens, out, B, Hq, Hkv, L, D, S, bits, dtype, scale, causal,
                                        window, workspace, (hipStream_t)stream),
                     "decode_attn launch");

@@ -7,13 +7,16 @@
 // with query l at position S_b - L + l, keys <= position when causal, keys > position - window
 // when a sliding window is set.
 //
-// Design (head_dim 128, 64-key tiles, a workgroup = 4 waves = 128 query rows):
-//  * A workgroup serves 128 consecutive rows of one (sequence, KV head) in position-major order
+// Design (head_dim 128, 64-key tiles, a workgroup = 8 waves = 256 query rows, one per CU):
+//  * A workgroup serves 256 consecutive rows of one (sequence, KV head) in position-major order
 //    (row = position * rep + local head), so all rep query heads of a position share each K/V
 //    tile and a causal boundary cuts only a few positions.
-//  * Each 64-key tile is dequantized once per workgroup into LDS as fp16: K row-major, V
-//    transposed (V^T[d][slot]) with its key slots permuted to match the score layout below.
-//    Double-buffered: the codes of tile t+1 are in flight while tile t is computed.
+//  * The raw tiles (codes, scales, biases) stream into a 3-slot LDS ring by buffer->LDS DMA, two
+//    tiles ahead of their use, with no registers held in flight; rows past the sequence end read
+//    as zero through the buffer range check (they are masked). Each 64-key tile is then
+//    dequantized once per workgroup, LDS to LDS, into fp16 operands: K row-major, V transposed
+//    (V^T[d][slot]) with its key slots permuted to match the score layout below. The fp16
+//    operands are double-buffered: tile t+1 is dequantized while tile t is computed.
 //  * Per wave (32 rows = the columns of a 32x32 MFMA): S^T = K Q^T (v_mfma_f32_32x32x16_f16;
 //    A = K rows from LDS, B = Q^T held in registers). In the MFMA result layout every lane holds
 //    16 keys of one query column, so the row max / sum are lane-local plus one permlane swap, and
@@ -22,8 +25,8 @@
 //    the fp16 range; scores are fp32 and are corrected by that power before the softmax.
 //  * Online softmax with threshold rescaling (a row's running maximum moves only when a tile's
 //    maximum exceeds it by more than 2^6), fp32 accumulators.
-//  * Long key ranges are split over several workgroups; their (m, l, o) partials are merged by
-//    the log-sum-exp combine kernel of merge.h.
+//  * Long key ranges are split over several workgroups; the last split of a row block to finish
+//    merges the (m, l, o) partials of the others (log-sum-exp) and writes the output.
 
 #include <math.h>
 
@@ -34,12 +37,30 @@
 namespace kvq {
 
 constexpr int kPT = 64;       // keys per tile
-constexpr int kPRows = 128;   // query rows per workgroup (4 waves x 32 MFMA columns)
-constexpr int kPW = 4;        // waves per workgroup
+constexpr int kPRows = 256;   // query rows per workgroup (8 waves x 32 MFMA columns)
+constexpr int kPW = 8;        // waves per workgroup
 constexpr int kKS = 136;      // fp16 per K row in LDS: 128 + 8 (rows shift by 4 banks)
 constexpr int kVS = 72;       // fp16 per V^T row in LDS: 64 + 8
 constexpr float kPSlack = 6.0f;
-constexpr int kPTargetWgs = 512;
+constexpr int kPTargetWgs = 256;  // one workgroup per CU
+constexpr int kRawSlots = 3;
+
+// The raw tile ring. A slot holds one 64-key tile as loaded: [K codes][V codes][sK, bK, sV, bV],
+// code rows with their 16-byte chunks XOR-swizzled by row (chunk c of row r at position
+// c ^ (r % CPR)), each scale/bias array as 128 4-byte cells (cell 2 key + g holds group g of the
+// key in its low half).
+template <int BITS>
+struct RawCfg {
+  static constexpr int ROWB = 128 * BITS / 8;       // code bytes per key row
+  static constexpr int CPR = ROWB / 16;             // 16-byte chunks per row
+  static constexpr int RPI = 64 / CPR;              // rows per 1 KiB DMA instruction
+  static constexpr int CI = kPT / RPI;              // DMA instructions per K (or V) code tile
+  static constexpr int KB = kPT * ROWB;             // bytes of a K (or V) code tile
+  static constexpr int SLOT = 2 * KB + 4 * 512;
+  static constexpr int CPW = 2 * CI / kPW;          // code DMA instructions per wave
+  static constexpr int IPT = CPW + 1;               // DMA instructions per wave per tile
+  static_assert(CPW * kPW == 2 * CI, "code DMAs divide evenly over the waves");
+};
 
 typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 
@@ -63,7 +84,6 @@ struct PreParams {
   float* part_ml;
   unsigned* counters;  // arrivals per unit, zero between launches
   int Hq, Hkv, L, S, rep, nrows, rowblocks, nsplit, nunits;
-  int fast;    // scale/bias rows [.., 2] contiguous and 16-byte aligned, byte ranges fit 32 bits
   float scale_log2;
   int causal, window;
 };
@@ -75,130 +95,71 @@ __device__ __forceinline__ int v_slot_key(int slot) {
   return 16 * j + (i < 4 ? 4 * h + i : 8 + 4 * h + (i - 4));
 }
 
-// Codes and scales of one tile as staged by one thread. Waves 0-1 stage V: thread t < 128 takes the
-// 8 keys of V^T slot chunk t % 8 at dims [8 * (t / 8), +8) -- the 8 lanes of a row group write 8
-// different slot chunks of one V^T row, and 32 consecutive rows are read per operand, both free of
-// bank conflicts with 144-byte rows. Waves 2-3 stage K: thread t takes dims
-// [64 * ((t - 128) / 64), +64) of key (t % 64), one scale group.
-template <int BITS>
-struct PreStage {
-  uint32_t c[2 * BITS];  // V: key i's 8 codes at c[i * BITS / 4 ..]; K: 64 codes
-  uint16_t s[8], b[8];   // V: per key; K: s[0], b[0]
-};
-
-// Per-thread constant byte offsets of the staging loads (relative to the tile's first row).
-struct PreOff {
-  uint32_t code[8];  // V: one per key; K: code[0]
-  uint32_t sb[2];    // V: the two 4-key scale runs; K: sb[0]
-};
-
-template <int BITS>
-__device__ __forceinline__ PreOff stage_offsets(const PreParams& p, int tid) {
-  PreOff o;
-  if (tid < 128) {
-    const int c8 = tid & 7, o8 = tid >> 3;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) o.code[i] = (uint32_t)(v_slot_key(8 * c8 + i) * p.vc_ss + o8 * BITS);
-#pragma unroll
-    for (int r = 0; r < 2; ++r) o.sb[r] = (uint32_t)(v_slot_key(8 * c8 + 4 * r) * 4);
-  } else {
-    const int key = tid & 63, half = (tid >> 6) & 1;
-    o.code[0] = (uint32_t)(key * p.kc_ss + half * 8 * BITS);
-#pragma unroll
-    for (int i = 1; i < 8; ++i) o.code[i] = 0;
-    o.sb[0] = (uint32_t)((key * p.ksb_ss + half) * 2);
-    o.sb[1] = 0;
-  }
-  return o;
+// Buffer->LDS DMA issued from inline asm: the compiler does not model these loads, so it adds no
+// wait for them before the kernel's LDS accesses; the tile ring orders every slot with explicit
+// vmcnt waits and barriers. M0 (the LDS base of the wave's 64 lanes) is saved and restored around
+// the load. Lane i's 16 bytes (2 bytes, in the low half of a 4-byte cell) land at lds + 16 i
+// (lds + 4 i).
+__device__ __forceinline__ void dma_b128(__amdgpu_buffer_rsrc_t r, uint32_t lds, uint32_t vo, uint32_t so) {
+  uint32_t m0;
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\tbuffer_load_dwordx4 %2, %3, %4 offen lds\n\ts_mov_b32 m0, %0"
+               : "=&s"(m0)
+               : "s"(lds), "v"(vo), "s"(r), "s"(so)
+               : "memory");
+}
+__device__ __forceinline__ void dma_b16(__amdgpu_buffer_rsrc_t r, uint32_t lds, uint32_t vo, uint32_t so) {
+  uint32_t m0;
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\tbuffer_load_ushort %2, %3, %4 offen lds\n\ts_mov_b32 m0, %0"
+               : "=&s"(m0)
+               : "s"(lds), "v"(vo), "s"(r), "s"(so)
+               : "memory");
+}
+// s_waitcnt vmcnt(N), other counters left alone.
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+__device__ __forceinline__ uint32_t lds_addr(const void* ptr) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)ptr;
 }
 
-// Buffer resources of one (sequence, KV head): codes and scales of the S_b valid rows.
-struct PreRsrc {
-  __amdgpu_buffer_rsrc_t kc, vc, ks, kb, vs, vb;
+// This wave's share of a raw tile: CPW 1 KiB code loads (K instructions first, then V) and one
+// 64-cell scale/bias load (array wave / 2, cells 64 (wave % 2) ..).
+template <int BITS>
+struct RawShare {
+  using C = RawCfg<BITS>;
+  __amdgpu_buffer_rsrc_t code_r[C::CPW], sb_r;
+  uint32_t code_vo[C::CPW], code_lds[C::CPW], sb_vo, sb_lds;
+  int64_t code_ss[C::CPW], sb_ss;  // bytes per key row
+
+  __device__ __forceinline__ void init(const PreParams& p, __amdgpu_buffer_rsrc_t kr, __amdgpu_buffer_rsrc_t vr,
+                                       const __amdgpu_buffer_rsrc_t (&sr)[4], int wave, int lane) {
+#pragma unroll
+    for (int j = 0; j < C::CPW; ++j) {
+      const int q = wave * C::CPW + j;
+      const bool is_k = q < C::CI;
+      const int i = is_k ? q : q - C::CI;
+      const int r = i * C::RPI + lane / C::CPR;
+      const int c = (lane % C::CPR) ^ (r % C::CPR);
+      code_r[j] = is_k ? kr : vr;
+      code_ss[j] = is_k ? p.kc_ss : p.vc_ss;
+      code_vo[j] = (uint32_t)(r * code_ss[j] + 16 * c);
+      code_lds[j] = (is_k ? 0 : C::KB) + 1024 * i;
+    }
+    const int a = wave >> 1, cell = 64 * (wave & 1) + lane;
+    sb_r = a == 0 ? sr[0] : a == 1 ? sr[1] : a == 2 ? sr[2] : sr[3];
+    sb_ss = 2 * (a < 2 ? p.ksb_ss : p.vsb_ss);
+    sb_vo = (uint32_t)((cell >> 1) * sb_ss + 2 * (cell & 1));
+    sb_lds = 2 * C::KB + 512 * a + 256 * (wave & 1);
+  }
+  // raw tile of keys [k0, k0 + 64) into the slot at LDS address `slot`
+  __device__ __forceinline__ void issue(uint32_t slot, int k0) const {
+#pragma unroll
+    for (int j = 0; j < C::CPW; ++j) dma_b128(code_r[j], slot + code_lds[j], code_vo[j], (uint32_t)(k0 * code_ss[j]));
+    dma_b16(sb_r, slot + sb_lds, sb_vo, (uint32_t)(k0 * sb_ss));
+  }
 };
-
-// Full tile (all 64 rows valid, scale rows [.., 2] contiguous): buffer loads, no address math.
-template <int BITS>
-__device__ __forceinline__ void stage_load_fast(PreStage<BITS>& st, const PreParams& p, const PreRsrc& rs,
-                                                const PreOff& o, int k0, int tid) {
-  if (tid < 128) {
-    const int g = ((tid >> 3) * 8) >> 6;
-    const uint32_t so = (uint32_t)(k0 * p.vc_ss);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      if constexpr (BITS == 8) {
-        const u2 v = __builtin_amdgcn_raw_buffer_load_b64(rs.vc, o.code[i], so, 0);
-        st.c[2 * i] = v[0];
-        st.c[2 * i + 1] = v[1];
-      } else {
-        st.c[i] = __builtin_amdgcn_raw_buffer_load_b32(rs.vc, o.code[i], so, 0);
-      }
-    }
-    const uint32_t ss = (uint32_t)(k0 * 4);
-#pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const u4 s4 = __builtin_amdgcn_raw_buffer_load_b128(rs.vs, o.sb[r], ss, 0);
-      const u4 b4 = __builtin_amdgcn_raw_buffer_load_b128(rs.vb, o.sb[r], ss, 0);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        st.s[4 * r + i] = (uint16_t)(g ? (s4[i] >> 16) : (s4[i] & 0xffffu));
-        st.b[4 * r + i] = (uint16_t)(g ? (b4[i] >> 16) : (b4[i] & 0xffffu));
-      }
-    }
-  } else {
-    const uint32_t so = (uint32_t)(k0 * p.kc_ss);
-#pragma unroll
-    for (int w = 0; w < 2 * BITS; w += 4) {
-      const u4 v = __builtin_amdgcn_raw_buffer_load_b128(rs.kc, o.code[0] + 4 * w, so, 0);
-      st.c[w] = v[0];
-      st.c[w + 1] = v[1];
-      st.c[w + 2] = v[2];
-      st.c[w + 3] = v[3];
-    }
-    const uint32_t ss = (uint32_t)(k0 * p.ksb_ss * 2);
-    st.s[0] = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rs.ks, o.sb[0], ss, 0);
-    st.b[0] = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rs.kb, o.sb[0], ss, 0);
-  }
-}
-
-// Any tile, any scale layout: rows clamped to the last valid one (the rows past it are masked).
-template <int BITS>
-__device__ __forceinline__ void stage_load_clamped(PreStage<BITS>& st, const PreParams& p, const uint8_t* kbase,
-                                                   const uint8_t* vbase, const uint16_t* ksb, const uint16_t* kbb,
-                                                   const uint16_t* vsb, const uint16_t* vbb, int k0, int S_b,
-                                                   int tid) {
-  if (tid < 128) {
-    const int c8 = tid & 7, o8 = tid >> 3, g = (o8 * 8) >> 6;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int row = min(k0 + v_slot_key(8 * c8 + i), S_b - 1);
-      const uint8_t* src = vbase + (int64_t)row * p.vc_ss + o8 * BITS;
-      if constexpr (BITS == 8) {
-        const u2 v = *(const u2*)src;
-        st.c[2 * i] = v[0];
-        st.c[2 * i + 1] = v[1];
-      } else {
-        st.c[i] = *(const uint32_t*)src;
-      }
-      st.s[i] = vsb[(int64_t)row * p.vsb_ss + g];
-      st.b[i] = vbb[(int64_t)row * p.vsb_ss + g];
-    }
-  } else {
-    const int key = tid & 63, half = (tid >> 6) & 1;
-    const int row = min(k0 + key, S_b - 1);
-    const uint8_t* src = kbase + (int64_t)row * p.kc_ss + half * 8 * BITS;
-#pragma unroll
-    for (int w = 0; w < 2 * BITS; w += 4) {
-      const u4 v = *(const u4*)(src + 4 * w);
-      st.c[w] = v[0];
-      st.c[w + 1] = v[1];
-      st.c[w + 2] = v[2];
-      st.c[w + 3] = v[3];
-    }
-    st.s[0] = ksb[(int64_t)row * p.ksb_ss + half];
-    st.b[0] = kbb[(int64_t)row * p.ksb_ss + half];
-  }
-}
 
 __device__ __forceinline__ _Float16 to_half(uint16_t r, F16) { return __builtin_bit_cast(_Float16, r); }
 __device__ __forceinline__ _Float16 to_half(uint16_t r, BF16) { return (_Float16)__uint_as_float((uint32_t)r << 16); }
@@ -230,41 +191,76 @@ __device__ __forceinline__ void dequant8(const uint32_t* w, h2 s2, h2 b2, uint32
   }
 }
 
+// Dequantize the raw tile at `raw` into the fp16 operands. Threads 0-255 build V^T: thread t takes
+// the 8 keys of slot chunk t % 8 at dims [4 (t / 8), +4) and writes 4 V^T rows of 8 slots. Threads
+// 256-511 build K: thread t takes dims [32 q, +32) of key t % 64, q = (t - 256) / 64.
 template <typename T, int BITS>
-__device__ __forceinline__ void stage_store(const PreStage<BITS>& st, _Float16* klds, _Float16* vlds, int tid) {
-  constexpr int W = BITS / 4;  // words per 8 codes
-  if (tid < 128) {
-    const int c8 = tid & 7, o8 = tid >> 3;
-    uint32_t x[8][4];  // key i, dim pair m
+__device__ __forceinline__ void stage_from_raw(const uint8_t* raw, _Float16* klds, _Float16* vlds, int tid) {
+  using C = RawCfg<BITS>;
+  const uint8_t* sbase = raw + 2 * C::KB;
+  auto sb_at = [&](int a, int key, int g) -> _Float16 {
+    return to_half(*(const uint16_t*)(sbase + 512 * a + 4 * (2 * key + g)), T{});
+  };
+  if (tid < 256) {
+    const int c8 = tid & 7, d4 = tid >> 3, g = d4 >> 4;
+    const uint8_t* vr = raw + C::KB;
+    uint32_t x[8][2];  // key i, dim pair m
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const _Float16 sh = to_half(st.s[i], T{}), bh = to_half(st.b[i], T{});
-      dequant8<BITS>(&st.c[W * i], h2{sh, sh}, h2{bh, bh}, x[i]);
+      const int key = v_slot_key(8 * c8 + i);
+      uint32_t bytes;  // codes of dims 4 d4 .. 4 d4 + 3 as 4 bytes
+      if constexpr (BITS == 8) {
+        bytes = *(const uint32_t*)(vr + key * C::ROWB + 16 * ((d4 >> 2) ^ (key % C::CPR)) + 4 * (d4 & 3));
+      } else {
+        const uint32_t h = *(const uint16_t*)(vr + key * C::ROWB + 16 * ((d4 >> 3) ^ (key % C::CPR)) + 2 * (d4 & 7));
+        bytes = perm((h >> 4) & 0x0F0Fu, h & 0x0F0Fu, 0x05010400u);
+      }
+      const _Float16 sh = sb_at(2, key, g), bh = sb_at(3, key, g);
+      x[i][0] = dequant_pair(bytes, 0x04010400u, h2{sh, sh}, h2{bh, bh});
+      x[i][1] = dequant_pair(bytes, 0x04030402u, h2{sh, sh}, h2{bh, bh});
     }
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
+    for (int e = 0; e < 4; ++e) {
       const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
       u4 v;
 #pragma unroll
       for (int ip = 0; ip < 4; ++ip) v[ip] = perm(x[2 * ip + 1][e >> 1], x[2 * ip][e >> 1], sel);
-      *(u4*)&vlds[(8 * o8 + e) * kVS + 8 * c8] = v;
+      *(u4*)&vlds[(4 * d4 + e) * kVS + 8 * c8] = v;
     }
   } else {
-    const int key = tid & 63, half = (tid >> 6) & 1;
-    const _Float16 sh = to_half(st.s[0], T{}), bh = to_half(st.b[0], T{});
+    constexpr int W = BITS / 4;  // words per 8 codes
+    const int key = tid & 63, q = (tid - 256) >> 6;
+    const uint8_t* kr = raw + key * C::ROWB;
+    uint32_t w[4 * W];
+    if constexpr (BITS == 8) {
+      const u4 a0 = *(const u4*)(kr + 16 * ((2 * q) ^ (key % C::CPR)));
+      const u4 a1 = *(const u4*)(kr + 16 * ((2 * q + 1) ^ (key % C::CPR)));
 #pragma unroll
-    for (int c = 0; c < 8; ++c) {
+      for (int i = 0; i < 4; ++i) {
+        w[i] = a0[i];
+        w[4 + i] = a1[i];
+      }
+    } else {
+      const u4 a0 = *(const u4*)(kr + 16 * (q ^ (key % C::CPR)));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) w[i] = a0[i];
+    }
+    const _Float16 sh = sb_at(0, key, q >> 1), bh = sb_at(1, key, q >> 1);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
       uint32_t x[4];
-      dequant8<BITS>(&st.c[W * c], h2{sh, sh}, h2{bh, bh}, x);
-      *(u4*)&klds[key * kKS + 64 * half + 8 * c] = u4{x[0], x[1], x[2], x[3]};
+      dequant8<BITS>(&w[W * c], h2{sh, sh}, h2{bh, bh}, x);
+      *(u4*)&klds[key * kKS + 32 * q + 8 * c] = u4{x[0], x[1], x[2], x[3]};
     }
   }
 }
 
 template <typename T, int BITS>
-__global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PreParams p) {
+__global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) {
+  using RC = RawCfg<BITS>;
   __shared__ __align__(16) _Float16 k_lds[2][kPT * kKS];
   __shared__ __align__(16) _Float16 v_lds[2][128 * kVS];
+  __shared__ __align__(16) uint8_t raw[kRawSlots][RC::SLOT];
   __shared__ unsigned s_arrived;
 
   const int tid = threadIdx.x;
@@ -304,20 +300,51 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PreParams p) {
   const int lo_r = p.window > 0 ? max(0, pos - p.window + 1) : 0;
   const int hi_r = p.causal ? min(S_b, pos + 1) : S_b;
 
+  // ---- the raw query slice (loaded before the tile stream; row and head are clamped, so every
+  // lane's load is in bounds)
+  u4 qraw[8];
+  {
+    const uint16_t* qrow = p.q + (int64_t)b * p.q_sb + (int64_t)head * p.q_sh + (int64_t)lq * p.q_sl + 8 * hh;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) qraw[j] = *(const u4*)(qrow + 16 * j);
+  }
+
+  // ---- raw tile stream: buffer resources over the S_b valid rows of this (sequence, KV head)
+  // (the host checks S * row stride fits 32 bits); tiles past the last re-read the last one
+  RawShare<BITS> share;
+  {
+    const __amdgpu_buffer_rsrc_t kr =
+        make_rsrc(p.kc + (int64_t)b * p.kc_sb + (int64_t)kvh * p.kc_sh, (uint32_t)((int64_t)S_b * p.kc_ss));
+    const __amdgpu_buffer_rsrc_t vr =
+        make_rsrc(p.vc + (int64_t)b * p.vc_sb + (int64_t)kvh * p.vc_sh, (uint32_t)((int64_t)S_b * p.vc_ss));
+    const int64_t ko = (int64_t)b * p.ksb_sb + (int64_t)kvh * p.ksb_sh;
+    const int64_t vo = (int64_t)b * p.vsb_sb + (int64_t)kvh * p.vsb_sh;
+    const uint32_t kn = (uint32_t)((int64_t)S_b * p.ksb_ss * 2), vn = (uint32_t)((int64_t)S_b * p.vsb_ss * 2);
+    const __amdgpu_buffer_rsrc_t sr[4] = {make_rsrc(p.ks + ko, kn), make_rsrc(p.kb + ko, kn), make_rsrc(p.vs + vo, vn),
+                                          make_rsrc(p.vb + vo, vn)};
+    share.init(p, kr, vr, sr, wave, lane);
+  }
+  const uint32_t raw_lds = lds_addr(&raw[0][0]);
+  const int last = max(ntile - 1, 0);
+  auto issue_raw = [&](int i) { share.issue(raw_lds + (i % kRawSlots) * RC::SLOT, k_begin + kPT * min(i, last)); };
+  if (ntile > 0) {
+#pragma unroll
+    for (int j = 0; j < kRawSlots; ++j) issue_raw(j);
+  }
+
   // ---- Q^T operand: k-step j holds dims 16j + 8hh .. +7, times scale*log2(e)*2^qe in fp16
   h8 qop[8];
   float inv2;
   {
-    const uint16_t* qrow = p.q + (int64_t)b * p.q_sb + (int64_t)head * p.q_sh + (int64_t)lq * p.q_sl + 8 * hh;
     float qv[8][8];
     float qmax = 0.0f;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const u4 raw = row_ok ? *(const u4*)(qrow + 16 * j) : u4{0, 0, 0, 0};
+      const u4 raw_q = row_ok ? qraw[j] : u4{0, 0, 0, 0};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        qv[j][2 * i] = to_float((uint16_t)(raw[i] & 0xffffu), T{});
-        qv[j][2 * i + 1] = to_float((uint16_t)(raw[i] >> 16), T{});
+        qv[j][2 * i] = to_float((uint16_t)(raw_q[i] & 0xffffu), T{});
+        qv[j][2 * i + 1] = to_float((uint16_t)(raw_q[i] >> 16), T{});
         qmax = fmaxf(qmax, fmaxf(fabsf(qv[j][2 * i]), fabsf(qv[j][2 * i + 1])));
       }
     }
@@ -333,45 +360,24 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PreParams p) {
       for (int i = 0; i < 8; ++i) qop[j][i] = (_Float16)(qv[j][i] * qmul);
   }
 
-  const uint8_t* kbase = p.kc + (int64_t)b * p.kc_sb + (int64_t)kvh * p.kc_sh;
-  const uint8_t* vbase = p.vc + (int64_t)b * p.vc_sb + (int64_t)kvh * p.vc_sh;
-  const uint16_t* ksb = p.ks + (int64_t)b * p.ksb_sb + (int64_t)kvh * p.ksb_sh;
-  const uint16_t* kbb = p.kb + (int64_t)b * p.ksb_sb + (int64_t)kvh * p.ksb_sh;
-  const uint16_t* vsb = p.vs + (int64_t)b * p.vsb_sb + (int64_t)kvh * p.vsb_sh;
-  const uint16_t* vbb = p.vb + (int64_t)b * p.vsb_sb + (int64_t)kvh * p.vsb_sh;
-  PreRsrc rs;
-  {
-    const int64_t nr = p.fast ? S_b : 0;  // the host checks these byte ranges fit 32 bits
-    rs.kc = make_rsrc(kbase, (uint32_t)(nr * p.kc_ss));
-    rs.vc = make_rsrc(vbase, (uint32_t)(nr * p.vc_ss));
-    rs.ks = make_rsrc(ksb, (uint32_t)(nr * p.ksb_ss * 2));
-    rs.kb = make_rsrc(kbb, (uint32_t)(nr * p.ksb_ss * 2));
-    rs.vs = make_rsrc(vsb, (uint32_t)(nr * p.vsb_ss * 2));
-    rs.vb = make_rsrc(vbb, (uint32_t)(nr * p.vsb_ss * 2));
-  }
-  const PreOff off = stage_offsets<BITS>(p, tid);
-  auto stage_load = [&](PreStage<BITS>& s_, int k0) {
-    if (p.fast && k0 + kPT <= S_b) stage_load_fast<BITS>(s_, p, rs, off, k0, tid);
-    else stage_load_clamped<BITS>(s_, p, kbase, vbase, ksb, kbb, vsb, vbb, k0, S_b, tid);
-  };
-
   float m_run = -INFINITY, l_run = 0.0f;
   f16v oacc[4];
 #pragma unroll
   for (int db = 0; db < 4; ++db) oacc[db] = f16v{};
 
-  PreStage<BITS> st;
+  // ---- prologue: tile 0 dequantized, tile 1 landed
   if (ntile > 0) {
-    stage_load(st, k_begin);
-    stage_store<T, BITS>(st, k_lds[0], v_lds[0], tid);
+    wait_vm<2 * RC::IPT>();
+    __syncthreads();
+    stage_from_raw<T, BITS>(raw[0], k_lds[0], v_lds[0], tid);
+    wait_vm<RC::IPT>();
+    __syncthreads();
   }
-  __syncthreads();
 
   for (int t = 0; t < ntile; ++t) {
     const int cur = t & 1;
     const int k0 = k_begin + kPT * t;
-    const bool has_next = t + 1 < ntile;
-    if (has_next) stage_load(st, k0 + kPT);
+    issue_raw(t + kRawSlots);  // into the slot of tile t, dequantized before the last barrier
 
     // S^T = K Q^T for the two 32-key blocks of the tile (scores in log2 units times 2^qe)
     f16v sacc[2];
@@ -435,9 +441,11 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PreParams p) {
         oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const h8*)(vrow + 16 * j), pop[j], oacc[db], 0, 0, 0);
     }
 
-    if (has_next) stage_store<T, BITS>(st, k_lds[cur ^ 1], v_lds[cur ^ 1], tid);
+    if (t + 1 < ntile) stage_from_raw<T, BITS>(raw[(t + 1) % kRawSlots], k_lds[cur ^ 1], v_lds[cur ^ 1], tid);
+    wait_vm<RC::IPT>();  // tile t + 2 has landed (tile t + 3 may be in flight)
     __syncthreads();
   }
+  wait_vm<0>();  // no load into this workgroup's LDS outlives it
 
   // ---- epilogue: this lane holds O^T[d][row] for d = 32db + 8(i/4) + 4hh + i%4
   float l_tot = add_xor32(l_run);
@@ -605,12 +613,6 @@ hipError_t launch_prefill(const kvq_rows* q, const kvq_qtensor* k, const kvq_qte
   p.rowblocks = pl.rowblocks;
   p.nsplit = pl.nsplit;
   p.nunits = pl.nunits;
-  auto vec_ok = [](const void* base, int64_t sbb, int64_t sbh, int64_t sbs) {
-    return sbs == 2 && ((uintptr_t)base % 16) == 0 && (sbb * 2) % 16 == 0 && (sbh * 2) % 16 == 0;
-  };
-  const int64_t big = std::max(std::max(p.kc_ss, p.vc_ss), 2 * std::max(p.ksb_ss, p.vsb_ss));
-  p.fast = vec_ok(v->scales, v->sb_stride_b, v->sb_stride_h, v->sb_stride_s) &&
-           vec_ok(v->biases, v->sb_stride_b, v->sb_stride_h, v->sb_stride_s) && (int64_t)S * big < ((int64_t)1 << 31);
   p.scale_log2 = scale * 1.4426950408889634f;
   p.causal = causal;
   p.window = window;
