@@ -378,16 +378,25 @@ __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) 
     const int cur = t & 1;
     const int k0 = k_begin + kPT * t;
     issue_raw(t + kRawSlots);  // into the slot of tile t, dequantized before the last barrier
+    // waves 4-7 (K) dequantize tile t + 1 before their MFMAs, waves 0-3 (V) after theirs: the two
+    // waves that share a SIMD (w and w + 4) are in opposite phases, one on the MFMA pipe while
+    // the other is on the VALU
+    if (t + 1 < ntile && wave >= kPW / 2)
+      stage_from_raw<T, BITS>(raw[(t + 1) % kRawSlots], k_lds[cur ^ 1], v_lds[cur ^ 1], tid);
 
     // S^T = K Q^T for the two 32-key blocks of the tile (scores in log2 units times 2^qe)
-    f16v sacc[2];
+    // the 16 K operands stream through a 4-deep register ring, so each MFMA's LDS read was issued
+    // four MFMAs earlier; the two 32-key blocks alternate
+    f16v sacc[2] = {f16v{}, f16v{}};
+    {
+      const _Float16* kl = &k_lds[cur][qc * kKS + 8 * hh];
+      auto kop = [&](int i) { return *(const h8*)(kl + (i & 1) * 32 * kKS + 16 * (i >> 1)); };
+      h8 ring[4] = {kop(0), kop(1), kop(2), kop(3)};
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      sacc[kb] = f16v{};
-      const _Float16* krow = &k_lds[cur][(32 * kb + qc) * kKS + 8 * hh];
-#pragma unroll
-      for (int j = 0; j < 8; ++j)
-        sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const h8*)(krow + 16 * j), qop[j], sacc[kb], 0, 0, 0);
+      for (int i = 0; i < 16; ++i) {
+        sacc[i & 1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ring[i & 3], qop[i >> 1], sacc[i & 1], 0, 0, 0);
+        if (i + 4 < 16) ring[i & 3] = kop(i + 4);
+      }
     }
     // this lane's query sees keys k0 + 32kb + 8(i/4) + 4hh + i%4
     const bool need_mask = !(k0 >= lo_all && k0 + kPT <= hi_all);
@@ -433,15 +442,20 @@ __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) 
       pop[j] = __builtin_bit_cast(h8, w);
     }
     // O^T += V^T P^T
+    {
+      // the 16 V^T operands stream through a 4-deep register ring; the 4 dim blocks alternate
+      const _Float16* vl = &v_lds[cur][qc * kVS + 8 * hh];
+      auto vop = [&](int i) { return *(const h8*)(vl + (i & 3) * 32 * kVS + 16 * (i >> 2)); };
+      h8 ring[4] = {vop(0), vop(1), vop(2), vop(3)};
 #pragma unroll
-    for (int db = 0; db < 4; ++db) {
-      const _Float16* vrow = &v_lds[cur][(32 * db + qc) * kVS + 8 * hh];
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const h8*)(vrow + 16 * j), pop[j], oacc[db], 0, 0, 0);
+      for (int i = 0; i < 16; ++i) {
+        oacc[i & 3] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ring[i & 3], pop[i >> 2], oacc[i & 3], 0, 0, 0);
+        if (i + 4 < 16) ring[i & 3] = vop(i + 4);
+      }
     }
 
-    if (t + 1 < ntile) stage_from_raw<T, BITS>(raw[(t + 1) % kRawSlots], k_lds[cur ^ 1], v_lds[cur ^ 1], tid);
+    if (t + 1 < ntile && wave < kPW / 2)
+      stage_from_raw<T, BITS>(raw[(t + 1) % kRawSlots], k_lds[cur ^ 1], v_lds[cur ^ 1], tid);
     wait_vm<RC::IPT>();  // tile t + 2 has landed (tile t + 3 may be in flight)
     __syncthreads();
   }
