@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define KVQ_ABI_VERSION 1
+#define KVQ_ABI_VERSION 2
 
 /* Element types of queries, K/V rows, outputs, scales and biases. */
 #define KVQ_DTYPE_F16 0
@@ -89,6 +89,38 @@ int kvq_quantize_append(const kvq_rows* k_src, const kvq_qtensor* k_dst,
                         int64_t row_offset, int B, int H, int L, int D,
                         int bits, int group_size, int dtype, void* stream);
 
+/* Rotary position embedding of the rows passed to kvq_rope / kvq_rope_quantize_append
+ * (the rotation mlx-lm's attention layers apply with nn.RoPE / mx.fast.rope before the cache
+ * update; fused with the KV write as in native/src/kernels.metal:106-160). Row l of a call sits
+ * at position offset + l; pair i turns by the angle (position * scale) * freq_i in fp32, with
+ * freq_i = 1 / base^(2i / dims) evaluated in double precision and rounded to fp32. */
+typedef struct kvq_rope_params {
+  int dims;        /* rotated leading dims: a multiple of 16, <= min(D, 256); the rest pass through */
+  int traditional; /* 0: pairs (i, i + dims/2) (NeoX; mlx traditional=False); 1: pairs (2i, 2i+1) */
+  float base;      /* theta                                                                        */
+  float scale;     /* position scale (1 = none; linear RoPE scaling divides positions)             */
+  int64_t offset;  /* position of row 0                                                            */
+} kvq_rope_params;
+
+/*
+ * In-place RoPE of rows [0, L) of x (T[B][H][L][D], the query rows of a step).
+ * Replaces: the query rotation mlx-lm's attention layers apply before attention.
+ * The rotation runs in fp32 and the result is rounded to T.
+ */
+int kvq_rope(const kvq_rows* x, const kvq_rope_params* rope, int B, int H, int L, int D, int dtype, void* stream);
+
+/*
+ * kvq_quantize_append with the keys rotated first: k_src is read, rotated by `rope`, rounded to
+ * T (the dtype RoPE returns) and quantized; v_src is quantized as is. k_src is not modified.
+ * Replaces: the key rotation followed by QuantizedKVCache.update_and_fetch in mlx-lm's attention
+ * layers (the fused RoPE + KV write of native/src/kernels.metal:106-160, here into the
+ * quantized cache). Same support as kvq_quantize_append, and rope->dims as in kvq_rope.
+ */
+int kvq_rope_quantize_append(const kvq_rows* k_src, const kvq_qtensor* k_dst,
+                             const kvq_rows* v_src, const kvq_qtensor* v_dst, const kvq_rope_params* rope,
+                             int64_t row_offset, int B, int H, int L, int D,
+                             int bits, int group_size, int dtype, void* stream);
+
 /*
  * Attention of L query rows per sequence against a quantized cache, for small L (decode):
  * out = softmax(scale * q K^T + mask) V over the dequantized K/V.
@@ -100,8 +132,8 @@ int kvq_quantize_append(const kvq_rows* k_src, const kvq_qtensor* k_dst,
  *   window:   0 = none; otherwise keys k > position - window only (sliding window).
  *   workspace: device buffer of at least kvq_decode_workspace_size(...) bytes, 256-byte aligned,
  *              zero-filled at allocation (see the conventions above).
- * One launch: the key range is split over workgroups, and the last workgroup of each
- * (sequence, KV head) merges the splits' log-sum-exp partials and writes the output.
+ * The key range is split over workgroups; their log-sum-exp partials are merged by a second,
+ * small launch on the same stream (both are enqueued by this call).
  */
 int kvq_decode_attn(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v,
                     const int32_t* seq_lens, const kvq_rows* out,

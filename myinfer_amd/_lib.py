@@ -18,7 +18,7 @@ import os
 
 # The in-tree build; KVQ_LIB may name another build of the same library (A/B comparisons).
 LIB_PATH = Path(os.environ.get("KVQ_LIB") or (Path(__file__).resolve().parent / "libkvq.so"))
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 DTYPE_F16 = 0
 DTYPE_BF16 = 1
@@ -54,6 +54,13 @@ class QTensor(ctypes.Structure):
     ]
 
 
+class RopeParams(ctypes.Structure):
+    """kvq_rope_params: rotary embedding of the rows of one call (row l at position offset + l)."""
+
+    _fields_ = [("dims", c_int), ("traditional", c_int), ("base", c_float), ("scale", c_float),
+                ("offset", c_int64)]
+
+
 _ATTN_ARGS = [
     POINTER(Rows), POINTER(QTensor), POINTER(QTensor), c_void_p, POINTER(Rows),
     c_int, c_int, c_int, c_int, c_int, c_int,  # B Hq Hkv L D S
@@ -69,6 +76,12 @@ SIGNATURES = {
     "kvq_quantize_append": (
         c_int,
         [POINTER(Rows), POINTER(QTensor), POINTER(Rows), POINTER(QTensor), c_int64,
+         c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_void_p],
+    ),
+    "kvq_rope": (c_int, [POINTER(Rows), POINTER(RopeParams), c_int, c_int, c_int, c_int, c_int, c_void_p]),
+    "kvq_rope_quantize_append": (
+        c_int,
+        [POINTER(Rows), POINTER(QTensor), POINTER(Rows), POINTER(QTensor), POINTER(RopeParams), c_int64,
          c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_void_p],
     ),
     "kvq_decode_attn": (c_int, _ATTN_ARGS),

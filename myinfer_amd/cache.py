@@ -163,13 +163,16 @@ class QuantizedKVCache:
         if self.keys is None or self.keys[0].shape[2] < capacity:
             self._resize(like, like, 0, capacity=capacity)
 
-    def update_and_fetch(self, keys: torch.Tensor, values: torch.Tensor):
+    def update_and_fetch(self, keys: torch.Tensor, values: torch.Tensor, rope: Optional["kernels.Rope"] = None):
+        """Append keys/values [B, H, L, D] at `offset` and return the fetched views. With `rope`,
+        the keys are rotated (positions offset .. offset + L - 1) in the same launch that
+        quantizes them: the RoPE + cache update an attention layer does, fused."""
         prev = self.offset
         L = keys.shape[2]
         if self.keys is None or prev + L > self.keys[0].shape[2]:
             self._resize(keys, values, L)
         kernels.quantize_append(keys, self.keys, values, self.values, row_offset=prev,
-                                group_size=self.group_size, bits=self.bits)
+                                group_size=self.group_size, bits=self.bits, rope=rope)
         self.offset += L
         return self.fetch()
 

@@ -89,17 +89,8 @@ int check_attn(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v, co
   return KVQ_OK;
 }
 
-}  // namespace
-
-extern "C" {
-
-int kvq_abi_version(void) { return KVQ_ABI_VERSION; }
-
-const char* kvq_last_error(void) { return g_err; }
-
-int kvq_quantize_append(const kvq_rows* k_src, const kvq_qtensor* k_dst, const kvq_rows* v_src,
-                        const kvq_qtensor* v_dst, int64_t row_offset, int B, int H, int L, int D, int bits,
-                        int group_size, int dtype, void* stream) {
+int check_quantize(const kvq_rows* k_src, const kvq_qtensor* k_dst, const kvq_rows* v_src, const kvq_qtensor* v_dst,
+                   int64_t row_offset, int B, int H, int L, int D, int bits, int group_size, int dtype) {
   int rc;
   if ((rc = check_dtype(dtype))) return rc;
   if (bits != 2 && bits != 4 && bits != 8) return fail(KVQ_ERR_UNSUPPORTED, "bits must be 2, 4 or 8, got %d", bits);
@@ -123,10 +114,59 @@ int kvq_quantize_append(const kvq_rows* k_src, const kvq_qtensor* k_dst, const k
       return fail(KVQ_ERR_INVALID, "8-bit codes must be 8-byte aligned with even word strides");
     if (t->sb_stride_s < D / group_size) return fail(KVQ_ERR_INVALID, "scales row stride is smaller than D/group_size");
   }
+  return KVQ_OK;
+}
+
+int check_rope(const kvq_rope_params* r, int D) {
+  if (!r) return fail(KVQ_ERR_INVALID, "rope descriptor is NULL");
+  if (r->dims <= 0 || r->dims > D || r->dims > 256 || r->dims % 16)
+    return fail(KVQ_ERR_UNSUPPORTED, "rope dims must be a positive multiple of 16, at most D=%d and 256, got %d", D,
+                r->dims);
+  if (!(r->base > 0.0f) || !isfinite(r->base)) return fail(KVQ_ERR_INVALID, "rope base must be positive and finite");
+  if (!isfinite(r->scale)) return fail(KVQ_ERR_INVALID, "rope scale is not finite");
+  if (r->offset < 0) return fail(KVQ_ERR_INVALID, "rope offset must be >= 0");
+  return KVQ_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int kvq_abi_version(void) { return KVQ_ABI_VERSION; }
+
+const char* kvq_last_error(void) { return g_err; }
+
+int kvq_quantize_append(const kvq_rows* k_src, const kvq_qtensor* k_dst, const kvq_rows* v_src,
+                        const kvq_qtensor* v_dst, int64_t row_offset, int B, int H, int L, int D, int bits,
+                        int group_size, int dtype, void* stream) {
+  int rc;
+  if ((rc = check_quantize(k_src, k_dst, v_src, v_dst, row_offset, B, H, L, D, bits, group_size, dtype))) return rc;
   if (B == 0 || H == 0 || L == 0) return ok();
-  return hip_status(kvq::launch_quantize_append(k_src, k_dst, v_src, v_dst, row_offset, B, H, L, D, bits, group_size,
-                                                dtype, (hipStream_t)stream),
+  return hip_status(kvq::launch_quantize_append(k_src, k_dst, v_src, v_dst, nullptr, row_offset, B, H, L, D, bits,
+                                                group_size, dtype, (hipStream_t)stream),
                     "quantize_append launch");
+}
+
+int kvq_rope(const kvq_rows* x, const kvq_rope_params* rope, int B, int H, int L, int D, int dtype, void* stream) {
+  int rc;
+  if ((rc = check_dtype(dtype))) return rc;
+  if (B < 0 || H < 0 || L < 0 || D <= 0 || D % 8) return fail(KVQ_ERR_INVALID, "bad shape (B=%d H=%d L=%d D=%d)", B, H, L, D);
+  if ((rc = check_rope(rope, D))) return rc;
+  if ((rc = check_rows(x, "x", D, true))) return rc;
+  if (B == 0 || H == 0 || L == 0) return ok();
+  return hip_status(kvq::launch_rope(x, rope, B, H, L, dtype, (hipStream_t)stream), "rope launch");
+}
+
+int kvq_rope_quantize_append(const kvq_rows* k_src, const kvq_qtensor* k_dst, const kvq_rows* v_src,
+                             const kvq_qtensor* v_dst, const kvq_rope_params* rope, int64_t row_offset, int B, int H, int L,
+                             int D, int bits, int group_size, int dtype, void* stream) {
+  int rc;
+  if ((rc = check_rope(rope, D))) return rc;
+  if ((rc = check_quantize(k_src, k_dst, v_src, v_dst, row_offset, B, H, L, D, bits, group_size, dtype))) return rc;
+  if (B == 0 || H == 0 || L == 0) return ok();
+  return hip_status(kvq::launch_quantize_append(k_src, k_dst, v_src, v_dst, rope, row_offset, B, H, L, D, bits,
+                                                group_size, dtype, (hipStream_t)stream),
+                    "rope_quantize_append launch");
 }
 
 size_t kvq_decode_workspace_size(int B, int Hq, int Hkv, int L, int D, int S, int window) {

@@ -10,8 +10,9 @@
 namespace kvq {
 
 hipError_t launch_quantize_append(const kvq_rows* k_src, const kvq_qtensor* k_dst, const kvq_rows* v_src,
-                                  const kvq_qtensor* v_dst, int64_t row_offset, int B, int H, int L, int D, int bits,
-                                  int group_size, int dtype, hipStream_t stream);
+                                  const kvq_qtensor* v_dst, const kvq_rope_params* rope, int64_t row_offset, int B, int H,
+                                  int L, int D, int bits, int group_size, int dtype, hipStream_t stream);
+hipError_t launch_rope(const kvq_rows* x, const kvq_rope_params* rope, int B, int H, int L, int dtype, hipStream_t stream);
 
 size_t decode_workspace_bytes(int B, int Hq, int Hkv, int L, int D, int S, int window, int bits);
 hipError_t launch_decode(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v, const int32_t* seq_lens,

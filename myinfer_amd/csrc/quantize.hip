@@ -14,11 +14,84 @@
 //
 // Thread mapping: one thread per 8 consecutive elements (one 16-byte load); the G/8 threads of a
 // group reduce min/max with lane permutes. Grid.y selects the K or the V job of one launch.
+//
+// RoPE (kvq_rope_quantize_append): the K job rotates its rows before quantizing, the way mlx-lm's
+// attention layers rotate keys before the cache update and the reference's native kernel fuses
+// the rotation with the KV write (native/src/kernels.metal:106-160). Pair i of a row at position
+// p turns by angle = (p * scale) * freq_i, freq_i = 1 / base^(2i / dims), in fp32; the rotated
+// value is rounded to T (what RoPE returns) before it is quantized. NeoX pairs (i, i + dims/2)
+// are read by each thread from its own chunk and the partner chunk, so no lanes exchange data.
 
 #include "common.h"
 #include "launch.h"
 
 namespace kvq {
+
+constexpr int kMaxRopePairs = 128;
+
+// freq[i] = 1 / base^(2i / dims), computed once on the host in double precision and rounded to
+// fp32, so that the angles do not depend on the device's pow (at position 1e5 one ulp of freq
+// moves the angle by about 6e-3 rad).
+struct RopeArgs {
+  int dims, traditional;
+  float scale;
+  int64_t offset;
+  float freq[kMaxRopePairs];
+};
+
+// cos and sin of the angle of pair `pair` at position `pos`
+__device__ __forceinline__ void rope_cs(const RopeArgs& r, int64_t pos, int pair, float& c, float& s) {
+#pragma clang fp contract(off)
+  const float ang = ((float)pos * r.scale) * r.freq[pair];
+  sincosf(ang, &s, &c);
+}
+
+static RopeArgs make_rope_args(const kvq_rope_params* p) {
+  RopeArgs r{};
+  r.dims = p->dims;
+  r.traditional = p->traditional;
+  r.scale = p->scale;
+  r.offset = p->offset;
+  for (int i = 0; i < p->dims / 2 && i < kMaxRopePairs; ++i)
+    r.freq[i] = (float)(1.0 / pow((double)p->base, 2.0 * i / (double)p->dims));
+  return r;
+}
+
+// Rotate the 8 values x of dims [d0, d0 + 8) of a row at position pos. For NeoX pairs, xp holds
+// the 8 values at the partner dims (d0 -+ dims/2). Dims at or past r.dims pass through.
+__device__ __forceinline__ void rope8(const RopeArgs& r, int64_t pos, int d0, float (&x)[8], const float (&xp)[8]) {
+#pragma clang fp contract(off)
+  if (d0 >= r.dims) return;
+  if (r.traditional) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float c, sn;
+      rope_cs(r, pos, d0 / 2 + i, c, sn);
+      const float a = x[2 * i], b = x[2 * i + 1];
+      x[2 * i] = a * c - b * sn;
+      x[2 * i + 1] = a * sn + b * c;
+    }
+  } else {
+    const int half = r.dims / 2;
+    const bool lo = d0 < half;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float c, sn;
+      rope_cs(r, pos, (lo ? d0 : d0 - half) + e, c, sn);
+      x[e] = lo ? x[e] * c - xp[e] * sn : x[e] * c + xp[e] * sn;
+    }
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ void load8(const uint16_t* p, float (&x)[8]) {
+  const u4 raw = *(const u4*)p;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    x[2 * i] = to_float((uint16_t)(raw[i] & 0xffffu), T{});
+    x[2 * i + 1] = to_float((uint16_t)(raw[i] >> 16), T{});
+  }
+}
 
 struct QuantJob {
   const uint16_t* src;
@@ -30,9 +103,9 @@ struct QuantJob {
   int64_t g_b, g_h, g_s;
 };
 
-template <typename T, int BITS, int G>
+template <typename T, int BITS, int G, bool ROPE>
 __global__ __launch_bounds__(256) void quantize_append_kernel(QuantJob job0, QuantJob job1, int H, int L,
-                                                              int D, int64_t total, int64_t row_offset) {
+                                                              int D, int64_t total, int64_t row_offset, RopeArgs rope) {
 #pragma clang fp contract(off)
   const QuantJob job = blockIdx.y == 0 ? job0 : job1;
   const int64_t tid = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -45,13 +118,18 @@ __global__ __launch_bounds__(256) void quantize_append_kernel(QuantJob job0, Qua
   const int h = (int)((row / L) % H);
   const int64_t b = row / ((int64_t)L * H);
 
-  const uint16_t* src = job.src + b * job.s_b + h * job.s_h + (int64_t)l * job.s_l + chunk * 8;
-  u4 raw = *(const u4*)src;
+  const uint16_t* srow = job.src + b * job.s_b + h * job.s_h + (int64_t)l * job.s_l;
   float x[8];
+  load8<T>(srow + chunk * 8, x);
+  if constexpr (ROPE) {
+    if (blockIdx.y == 0) {  // the K job
+      const int d0 = chunk * 8, half = rope.dims / 2;
+      float xp[8];
+      if (!rope.traditional && d0 < rope.dims) load8<T>(srow + (d0 < half ? d0 + half : d0 - half), xp);
+      rope8(rope, rope.offset + l, d0, x, xp);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    x[2 * i] = to_float((uint16_t)(raw[i] & 0xffffu), T{});
-    x[2 * i + 1] = to_float((uint16_t)(raw[i] >> 16), T{});
+      for (int i = 0; i < 8; ++i) x[i] = to_float(from_float(x[i], T{}), T{});
+    }
   }
   float mx = x[0], mn = x[0];
 #pragma unroll
@@ -107,31 +185,35 @@ __global__ __launch_bounds__(256) void quantize_append_kernel(QuantJob job0, Qua
 
 template <typename T, int BITS, int G>
 static hipError_t launch_quant(const QuantJob& k, const QuantJob& v, int njobs, int B, int H, int L, int D,
-                               int64_t row_offset, hipStream_t stream) {
+                               int64_t row_offset, const RopeArgs* rope, hipStream_t stream) {
   const int64_t total = (int64_t)B * H * L * (D / 8);
   const int64_t blocks = (total + 255) / 256;
-  hipLaunchKernelGGL((quantize_append_kernel<T, BITS, G>), dim3((unsigned)blocks, njobs), dim3(256), 0, stream, k,
-                     v, H, L, D, total, row_offset);
+  if (rope)
+    hipLaunchKernelGGL((quantize_append_kernel<T, BITS, G, true>), dim3((unsigned)blocks, njobs), dim3(256), 0, stream,
+                       k, v, H, L, D, total, row_offset, *rope);
+  else
+    hipLaunchKernelGGL((quantize_append_kernel<T, BITS, G, false>), dim3((unsigned)blocks, njobs), dim3(256), 0,
+                       stream, k, v, H, L, D, total, row_offset, RopeArgs{});
   return hipGetLastError();
 }
 
 template <typename T, int BITS>
 static hipError_t dispatch_group(int G, const QuantJob& k, const QuantJob& v, int njobs, int B, int H, int L, int D,
-                                 int64_t row_offset, hipStream_t stream) {
+                                 int64_t row_offset, const RopeArgs* rope, hipStream_t stream) {
   switch (G) {
-    case 32: return launch_quant<T, BITS, 32>(k, v, njobs, B, H, L, D, row_offset, stream);
-    case 64: return launch_quant<T, BITS, 64>(k, v, njobs, B, H, L, D, row_offset, stream);
-    default: return launch_quant<T, BITS, 128>(k, v, njobs, B, H, L, D, row_offset, stream);
+    case 32: return launch_quant<T, BITS, 32>(k, v, njobs, B, H, L, D, row_offset, rope, stream);
+    case 64: return launch_quant<T, BITS, 64>(k, v, njobs, B, H, L, D, row_offset, rope, stream);
+    default: return launch_quant<T, BITS, 128>(k, v, njobs, B, H, L, D, row_offset, rope, stream);
   }
 }
 
 template <typename T>
 static hipError_t dispatch_bits(int bits, int G, const QuantJob& k, const QuantJob& v, int njobs, int B, int H, int L,
-                                int D, int64_t row_offset, hipStream_t stream) {
+                                int D, int64_t row_offset, const RopeArgs* rope, hipStream_t stream) {
   switch (bits) {
-    case 2: return dispatch_group<T, 2>(G, k, v, njobs, B, H, L, D, row_offset, stream);
-    case 4: return dispatch_group<T, 4>(G, k, v, njobs, B, H, L, D, row_offset, stream);
-    default: return dispatch_group<T, 8>(G, k, v, njobs, B, H, L, D, row_offset, stream);
+    case 2: return dispatch_group<T, 2>(G, k, v, njobs, B, H, L, D, row_offset, rope, stream);
+    case 4: return dispatch_group<T, 4>(G, k, v, njobs, B, H, L, D, row_offset, rope, stream);
+    default: return dispatch_group<T, 8>(G, k, v, njobs, B, H, L, D, row_offset, rope, stream);
   }
 }
 
@@ -154,13 +236,71 @@ static QuantJob make_job(const kvq_rows* src, const kvq_qtensor* dst) {
 }
 
 hipError_t launch_quantize_append(const kvq_rows* k_src, const kvq_qtensor* k_dst, const kvq_rows* v_src,
-                                  const kvq_qtensor* v_dst, int64_t row_offset, int B, int H, int L, int D, int bits,
-                                  int group_size, int dtype, hipStream_t stream) {
+                                  const kvq_qtensor* v_dst, const kvq_rope_params* rope, int64_t row_offset, int B, int H,
+                                  int L, int D, int bits, int group_size, int dtype, hipStream_t stream) {
   QuantJob k = make_job(k_src, k_dst);
   QuantJob v = v_src ? make_job(v_src, v_dst) : k;
   const int njobs = v_src ? 2 : 1;
-  if (dtype == KVQ_DTYPE_BF16) return dispatch_bits<BF16>(bits, group_size, k, v, njobs, B, H, L, D, row_offset, stream);
-  return dispatch_bits<F16>(bits, group_size, k, v, njobs, B, H, L, D, row_offset, stream);
+  RopeArgs ra{};
+  if (rope) ra = make_rope_args(rope);
+  const RopeArgs* rp = rope ? &ra : nullptr;
+  if (dtype == KVQ_DTYPE_BF16) return dispatch_bits<BF16>(bits, group_size, k, v, njobs, B, H, L, D, row_offset, rp, stream);
+  return dispatch_bits<F16>(bits, group_size, k, v, njobs, B, H, L, D, row_offset, rp, stream);
+}
+
+// In-place RoPE: one thread per rotated pair of 8-value chunks (NeoX: dims [8j, +8) and
+// [8j + dims/2, +8); interleaved: one chunk), so no thread reads what another writes.
+template <typename T>
+__global__ __launch_bounds__(256) void rope_kernel(uint16_t* x, int64_t s_b, int64_t s_h, int64_t s_l, int H, int L,
+                                                   int64_t total, int per_row, RopeArgs r) {
+  const int64_t tid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (tid >= total) return;
+  const int j = (int)(tid % per_row);
+  const int64_t row = tid / per_row;
+  const int l = (int)(row % L), h = (int)((row / L) % H);
+  const int64_t b = row / ((int64_t)L * H);
+  uint16_t* xr = x + b * s_b + h * s_h + (int64_t)l * s_l;
+  const int64_t pos = r.offset + l;
+  auto store8 = [&](uint16_t* p, const float (&v)[8]) {
+    u4 w;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w[i] = (uint32_t)from_float(v[2 * i], T{}) | ((uint32_t)from_float(v[2 * i + 1], T{}) << 16);
+    *(u4*)p = w;
+  };
+  float a[8], c[8];
+  if (r.traditional) {
+    load8<T>(xr + 8 * j, a);
+    rope8(r, pos, 8 * j, a, c);
+    store8(xr + 8 * j, a);
+  } else {
+    const int half = r.dims / 2;
+    load8<T>(xr + 8 * j, a);
+    load8<T>(xr + 8 * j + half, c);
+    float a2[8], c2[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      a2[i] = a[i];
+      c2[i] = c[i];
+    }
+    rope8(r, pos, 8 * j, a2, c);         // first half: a * cos - c * sin
+    rope8(r, pos, 8 * j + half, c2, a);  // second half: c * cos + a * sin
+    store8(xr + 8 * j, a2);
+    store8(xr + 8 * j + half, c2);
+  }
+}
+
+hipError_t launch_rope(const kvq_rows* x, const kvq_rope_params* rope, int B, int H, int L, int dtype, hipStream_t stream) {
+  const RopeArgs r = make_rope_args(rope);
+  const int per_row = rope->traditional ? rope->dims / 8 : rope->dims / 16;
+  const int64_t total = (int64_t)B * H * L * per_row;
+  const int64_t blocks = (total + 255) / 256;
+  if (dtype == KVQ_DTYPE_BF16)
+    hipLaunchKernelGGL((rope_kernel<BF16>), dim3((unsigned)blocks), dim3(256), 0, stream, (uint16_t*)x->data,
+                       x->stride_b, x->stride_h, x->stride_l, H, L, total, per_row, r);
+  else
+    hipLaunchKernelGGL((rope_kernel<F16>), dim3((unsigned)blocks), dim3(256), 0, stream, (uint16_t*)x->data,
+                       x->stride_b, x->stride_h, x->stride_l, H, L, total, per_row, r);
+  return hipGetLastError();
 }
 
 }  // namespace kvq

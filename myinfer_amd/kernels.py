@@ -8,6 +8,7 @@ zero-filled torch allocation cached per (device, stream); the library itself all
 from __future__ import annotations
 
 import ctypes
+from dataclasses import dataclass
 from typing import Optional, Sequence, Tuple
 
 import torch
@@ -49,10 +50,42 @@ def _check_triple(tr: Sequence[torch.Tensor], name: str) -> None:
         raise ValueError(f"{name} must be a (codes, scales, biases) triple")
 
 
+@dataclass(frozen=True)
+class Rope:
+    """Rotary position embedding as mlx's nn.RoPE(dims, traditional, base, scale) applies it: row l
+    of a call at position offset + l, pair i turned by (position * scale) * base^(-2i/dims)."""
+
+    dims: int
+    traditional: bool = False
+    base: float = 10000.0
+    scale: float = 1.0
+
+    def params(self, offset: int) -> "_lib.RopeParams":
+        return _lib.RopeParams(int(self.dims), int(bool(self.traditional)), float(self.base), float(self.scale),
+                               int(offset))
+
+
+def rope(x: torch.Tensor, r: Rope, offset: int = 0) -> torch.Tensor:
+    """Rotate x [B, H, L, D] (float16/bfloat16, CUDA) in place, rows at positions offset + l, and
+    return it: the query side of a fused RoPE + cache update (kernels.metal:106-160)."""
+    dev = _require_cuda(x)
+    if x.dim() != 4:
+        raise ValueError(f"x must be [B, H, L, D], got {tuple(x.shape)}")
+    B, H, L, D = x.shape
+    xr, rp = _lib.rows(x), r.params(offset)
+    rc = _lib.lib().kvq_rope(ctypes.byref(xr), ctypes.byref(rp), B, H, L, D, _lib.dtype_code(x.dtype),
+                             _lib.stream_ptr(dev))
+    _lib.check(rc, "kvq_rope")
+    return x
+
+
 def quantize_append(k: torch.Tensor, k_dst: Triple, v: Optional[torch.Tensor] = None, v_dst: Optional[Triple] = None,
-                    row_offset: int = 0, group_size: int = 64, bits: int = 8) -> None:
+                    row_offset: int = 0, group_size: int = 64, bits: int = 8, rope: Optional[Rope] = None,
+                    rope_offset: Optional[int] = None) -> None:
     """Quantize k (and v) [B, H, L, D] and store them at rows [row_offset, row_offset + L) of the
-    (codes, scales, biases) buffers k_dst (and v_dst), in one kernel launch."""
+    (codes, scales, biases) buffers k_dst (and v_dst), in one kernel launch. With `rope`, the keys
+    are rotated first (row l at position rope_offset + l, rope_offset defaulting to row_offset) and
+    rounded to their dtype before they are quantized; k itself is not modified."""
     _check_triple(k_dst, "k_dst")
     tens = [k, *k_dst]
     if v is not None:
@@ -81,9 +114,16 @@ def quantize_append(k: torch.Tensor, k_dst: Triple, v: Optional[torch.Tensor] = 
         vr_p, vq_p = ctypes.byref(vr), ctypes.byref(vq)
     else:
         vr_p = vq_p = None
-    rc = L_.kvq_quantize_append(ctypes.byref(kr), ctypes.byref(kq), vr_p, vq_p, int(row_offset), B, H, L, D, int(bits),
-                                int(group_size), _lib.dtype_code(k.dtype), _lib.stream_ptr(dev))
-    _lib.check(rc, "kvq_quantize_append")
+    if rope is None:
+        rc = L_.kvq_quantize_append(ctypes.byref(kr), ctypes.byref(kq), vr_p, vq_p, int(row_offset), B, H, L, D,
+                                    int(bits), int(group_size), _lib.dtype_code(k.dtype), _lib.stream_ptr(dev))
+        _lib.check(rc, "kvq_quantize_append")
+    else:
+        rp = rope.params(row_offset if rope_offset is None else rope_offset)
+        rc = L_.kvq_rope_quantize_append(ctypes.byref(kr), ctypes.byref(kq), vr_p, vq_p, ctypes.byref(rp),
+                                         int(row_offset), B, H, L, D, int(bits), int(group_size),
+                                         _lib.dtype_code(k.dtype), _lib.stream_ptr(dev))
+        _lib.check(rc, "kvq_rope_quantize_append")
 
 
 def quantize(x: torch.Tensor, group_size: int = 64, bits: int = 8) -> Triple:

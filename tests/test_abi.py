@@ -117,3 +117,41 @@ def test_workspace_sizes():
     assert lib.kvq_decode_workspace_size(1, 64, 8, 1, 96, 32768, 0) == 0
     # a sliding window never needs more splits than the full context
     assert 0 < lib.kvq_decode_workspace_size(4, 32, 16, 1, 128, 8192, 1024) <= lib.kvq_decode_workspace_size(4, 32, 16, 1, 128, 8192, 0)
+
+
+def test_rope_entry_points_reject_bad_arguments():
+    lib = _lib.lib()
+    r = _fake_rows()
+    q = _fake_q()
+    byref = ctypes.byref
+
+    def rp(**kw):
+        a = dict(dims=128, traditional=0, base=10000.0, scale=1.0, offset=0)
+        a.update(kw)
+        return _lib.RopeParams(a["dims"], a["traditional"], a["base"], a["scale"], a["offset"])
+
+    for bad, code, needle in [
+        (rp(dims=24), _lib.ERR_UNSUPPORTED, "dims"),
+        (rp(dims=256), _lib.ERR_UNSUPPORTED, "dims"),  # more than D = 128
+        (rp(dims=0), _lib.ERR_UNSUPPORTED, "dims"),
+        (rp(base=0.0), _lib.ERR_INVALID, "base"),
+        (rp(base=float("inf")), _lib.ERR_INVALID, "base"),
+        (rp(scale=float("nan")), _lib.ERR_INVALID, "scale"),
+        (rp(offset=-1), _lib.ERR_INVALID, "offset"),
+    ]:
+        assert lib.kvq_rope(byref(r), byref(bad), 1, 1, 1, 128, 0, None) == code
+        assert needle in _lib.last_error()
+        assert lib.kvq_rope_quantize_append(byref(r), byref(q), None, None, byref(bad), 0, 1, 1, 1, 128, 8, 64, 0,
+                                            None) == code
+        assert needle in _lib.last_error()
+    good = rp(dims=64, traditional=1, offset=5)
+    assert lib.kvq_rope(byref(r), None, 1, 1, 1, 128, 0, None) == _lib.ERR_INVALID
+    assert lib.kvq_rope(byref(r), byref(good), 1, 1, 1, 128, 7, None) == _lib.ERR_INVALID
+    assert lib.kvq_rope(_lib.Rows(16 * 1024 + 2, 1024, 512, 128), byref(good), 1, 1, 1, 128, 0, None) == _lib.ERR_INVALID
+    assert lib.kvq_rope_quantize_append(byref(r), byref(q), None, None, byref(good), 0, 1, 1, 1, 128, 3, 64, 0,
+                                        None) == _lib.ERR_UNSUPPORTED
+    # zero rows are a successful no-op that never touches the device
+    assert lib.kvq_rope(byref(r), byref(good), 1, 1, 0, 128, 0, None) == _lib.OK
+    assert lib.kvq_rope_quantize_append(byref(r), byref(q), None, None, byref(good), 0, 1, 1, 0, 128, 8, 64, 0,
+                                        None) == _lib.OK
+    assert _lib.last_error() == ""
