@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define KVQ_ABI_VERSION 2
+#define KVQ_ABI_VERSION 3
 
 /* Element types of queries, K/V rows, outputs, scales and biases. */
 #define KVQ_DTYPE_F16 0
@@ -157,6 +157,31 @@ int kvq_prefill_attn(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor*
                      void* workspace, size_t workspace_bytes, void* stream);
 
 size_t kvq_prefill_workspace_size(int B, int Hq, int Hkv, int L, int D, int S, int window);
+
+/*
+ * Attention over an unquantized cache: K and V are T[B][Hkv][S_cap][D] rows (kvq_rows, viewed
+ * as [..., :S, :]) in the queries' dtype. Same masks, outputs, workspace and streams as the
+ * quantized entry points; the workspace sizes above cover these calls too.
+ * Replaces: mx.fast.scaled_dot_product_attention, which mlx-lm's scaled_dot_product_attention
+ * calls for every cache that is not quantized: the plain KVCache before quantized_kv_start and
+ * the RotatingKVCache (sliding-window) layers that m5engine/attention.py:106-112 leaves
+ * unquantized.
+ * The products run on MFMA in the cache's own type (fp16 or bf16, exact operands) with fp32
+ * accumulation; the probabilities enter the PV product in that type.
+ * Requirements: decode D in {64, 128}, prefill D == 128; rows 16-byte aligned with strides that are
+ * multiples of 8 elements.
+ */
+int kvq_decode_attn_dense(const kvq_rows* q, const kvq_rows* k, const kvq_rows* v,
+                          const int32_t* seq_lens, const kvq_rows* out,
+                          int B, int Hq, int Hkv, int L, int D, int S, int dtype,
+                          float scale, int causal, int window,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
+int kvq_prefill_attn_dense(const kvq_rows* q, const kvq_rows* k, const kvq_rows* v,
+                           const int32_t* seq_lens, const kvq_rows* out,
+                           int B, int Hq, int Hkv, int L, int D, int S, int dtype,
+                           float scale, int causal, int window,
+                           void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

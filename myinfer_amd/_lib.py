@@ -18,7 +18,7 @@ import os
 
 # The in-tree build; KVQ_LIB may name another build of the same library (A/B comparisons).
 LIB_PATH = Path(os.environ.get("KVQ_LIB") or (Path(__file__).resolve().parent / "libkvq.so"))
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 DTYPE_F16 = 0
 DTYPE_BF16 = 1
@@ -68,6 +68,13 @@ _ATTN_ARGS = [
     c_float, c_int, c_int,  # scale causal window
     c_void_p, c_size_t, c_void_p,  # workspace bytes stream
 ]
+_DENSE_ARGS = [
+    POINTER(Rows), POINTER(Rows), POINTER(Rows), c_void_p, POINTER(Rows),
+    c_int, c_int, c_int, c_int, c_int, c_int,  # B Hq Hkv L D S
+    c_int,  # dtype
+    c_float, c_int, c_int,  # scale causal window
+    c_void_p, c_size_t, c_void_p,  # workspace bytes stream
+]
 _WS_ARGS = [c_int, c_int, c_int, c_int, c_int, c_int, c_int]
 
 SIGNATURES = {
@@ -85,6 +92,8 @@ SIGNATURES = {
          c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_void_p],
     ),
     "kvq_decode_attn": (c_int, _ATTN_ARGS),
+    "kvq_decode_attn_dense": (c_int, _DENSE_ARGS),
+    "kvq_prefill_attn_dense": (c_int, _DENSE_ARGS),
     "kvq_decode_workspace_size": (c_size_t, _WS_ARGS),
     "kvq_prefill_attn": (c_int, _ATTN_ARGS),
     "kvq_prefill_workspace_size": (c_size_t, _WS_ARGS),

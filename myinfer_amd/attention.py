@@ -10,6 +10,12 @@ over torch tensors in MLX layout on the GPU, executed by libkvq.so's HIP kernels
   quantized_scaled_dot_product_attention(...)
       the L == 1 entry mlx-lm calls (captured at m5engine/attention.py:19, used at :42-45);
       here it is the same kernels.
+  fast_scaled_dot_product_attention(queries, keys, values, scale, mask)
+      attention over an unquantized cache (mlx's mx.fast.scaled_dot_product_attention, which
+      mlx-lm uses for the caches m5engine/attention.py:106-112 leaves unquantized: the plain
+      cache before quantized_kv_start and the sliding-window RotatingKVCache layers).
+  scaled_dot_product_attention(queries, keys, values, cache, scale, mask)
+      mlx-lm's dispatcher between the two, by the cache's type.
   safe_maybe_quantize_kv_cache(prompt_cache, quantized_kv_start, kv_group_size, kv_bits)
       reference: m5engine/attention.py:106-112.
   install(base_module=None, generate_module=None)
@@ -118,6 +124,13 @@ def blocked_quantized_sdpa(queries: torch.Tensor, q_keys, q_values, scale: float
     """
     B, n_q_heads, L, D = queries.shape
     S = q_keys[0].shape[-2]
+    causal, window, seq_lens = _resolve_mask(mask, B, n_q_heads, L, S, window, seq_lens)
+    return kernels.attention(queries, tuple(q_keys), tuple(q_values), scale, causal=causal, window=window,
+                             seq_lens=seq_lens, group_size=group_size, bits=bits)
+
+
+def _resolve_mask(mask, B: int, n_q_heads: int, L: int, S: int, window: int, seq_lens):
+    """(causal, window, seq_lens) from a reference-style mask plus the keyword extensions."""
     causal, mwin, mseq = mask_structure(mask, B, n_q_heads, L, S)
     if window and mwin and window != mwin:
         raise ValueError(f"window={window} disagrees with the mask's window {mwin}")
@@ -126,8 +139,35 @@ def blocked_quantized_sdpa(queries: torch.Tensor, q_keys, q_values, scale: float
         seq_lens = mseq
     if window and not causal:
         causal = True
-    return kernels.attention(queries, tuple(q_keys), tuple(q_values), scale, causal=causal, window=window,
-                             seq_lens=seq_lens, group_size=group_size, bits=bits)
+    return causal, window, seq_lens
+
+
+def fast_scaled_dot_product_attention(queries: torch.Tensor, keys: torch.Tensor, values: torch.Tensor, scale: float,
+                                      mask=None, *, window: int = 0,
+                                      seq_lens: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """softmax(scale * Q K^T + mask) V over an unquantized cache: the counterpart of
+    mx.fast.scaled_dot_product_attention, which mlx-lm calls for every cache that is not quantized
+    (the KVCache before quantized_kv_start, and the RotatingKVCache sliding-window layers that
+    m5engine/attention.py:106-112 leaves unquantized).
+
+    queries [B, Hq, L, D]; keys, values [B, Hkv, S, D] in the queries' dtype (float16/bfloat16,
+    CUDA). Masks as for blocked_quantized_sdpa. Returns [B, Hq, L, D].
+    """
+    B, n_q_heads, L, D = queries.shape
+    S = keys.shape[-2]
+    causal, window, seq_lens = _resolve_mask(mask, B, n_q_heads, L, S, window, seq_lens)
+    return kernels.attention(queries, keys, values, scale, causal=causal, window=window, seq_lens=seq_lens)
+
+
+def scaled_dot_product_attention(queries, keys, values, cache, scale: float, mask, sinks=None):
+    """mlx-lm's models.base.scaled_dot_product_attention: a quantized cache (one with ``bits``)
+    goes to the quantized path, any other cache to the unquantized kernels."""
+    if sinks is not None:
+        raise NotImplementedError("attention sinks are not supported by the GPU kernels")
+    if hasattr(cache, "bits"):
+        return quantized_scaled_dot_product_attention(queries, keys, values, scale, mask,
+                                                      group_size=cache.group_size, bits=cache.bits)
+    return fast_scaled_dot_product_attention(queries, keys, values, scale, mask)
 
 
 def quantized_scaled_dot_product_attention(queries, q_keys, q_values, scale, mask, group_size: int = 64,

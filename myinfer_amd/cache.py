@@ -1,8 +1,8 @@
 """KV caches in MLX layout on the GPU: the objects the reference's attention path reads and
 appends to.
 
-Counterparts of mlx-lm's ``KVCache`` / ``QuantizedKVCache`` (third-party, mlx-lm==0.31.3,
-requirements.txt:4), with the contract the reference relies on:
+Counterparts of mlx-lm's ``KVCache`` / ``QuantizedKVCache`` / ``RotatingKVCache`` (third-party,
+mlx-lm==0.31.3, requirements.txt:4), with the contract the reference relies on:
   * ``update_and_fetch(keys, values)`` appends [B, H, L, D] rows at ``offset`` and returns the
     ``[..., :offset, :]`` views (for the quantized cache: two (codes, scales, biases) triples);
   * storage grows in steps of 256 rows (cut to ``offset`` first when it is not step-aligned);
@@ -120,6 +120,135 @@ class KVCache:
         return qc
 
 
+class RotatingKVCache:
+    """Sliding-window K/V rows [B, H, rows, D]: mlx-lm's RotatingKVCache, the cache of windowed
+    attention layers. m5engine/attention.py:106-112 leaves it unquantized (its attention runs on
+    the unquantized kernels) and m5engine/context.py:65-66 sizes it by ``max_size``.
+
+    * One-token updates write in place into a ring of ``max_size`` rows (grown in steps of
+      ``step`` until full); its first ``keep`` rows are never overwritten. The fetched rows are in
+      ring order, which attention of a single query does not depend on.
+    * Multi-token updates return the rows in temporal order: the ``keep`` first tokens, the newest
+      ``max_size - 1 - keep`` earlier ones and the new tokens, so that with ``make_mask`` every new
+      token sees a full window.
+    """
+
+    def __init__(self, max_size: int, keep: int = 0, step: int = STEP) -> None:
+        if max_size <= 0 or keep < 0 or keep >= max_size:
+            raise ValueError(f"need 0 <= keep < max_size, got keep={keep}, max_size={max_size}")
+        self.max_size, self.keep, self.step = int(max_size), int(keep), int(step)
+        self.keys: Optional[torch.Tensor] = None
+        self.values: Optional[torch.Tensor] = None
+        self.offset = 0
+        self._idx = 0  # next ring row to write (one-token updates)
+
+    def _drop_oldest(self, x: torch.Tensor, n: int, append: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """x without its n oldest rows after the first `keep` (x in temporal order), plus `append`."""
+        parts = [x[..., : self.keep, :], x[..., n + self.keep:, :]] if n > 0 else [x]
+        if append is not None:
+            parts.append(append)
+        return torch.cat(parts, dim=2) if len(parts) > 1 else parts[0]
+
+    def _in_time_order(self, x: torch.Tensor) -> torch.Tensor:
+        if self._idx == x.shape[2]:
+            return x
+        if self._idx < self.offset:  # the ring has wrapped: the oldest rows follow the write point
+            return torch.cat([x[..., : self.keep, :], x[..., self._idx:, :], x[..., self.keep: self._idx, :]], dim=2)
+        return x[..., : self._idx, :]
+
+    def _append_chunk(self, keys: torch.Tensor, values: torch.Tensor):
+        if self.keys is None:
+            self.keys, self.values = keys.clone(), values.clone()
+        else:
+            k, v = self._in_time_order(self.keys), self._in_time_order(self.values)
+            self._idx = k.shape[2]
+            drop = self._idx - self.max_size + 1
+            self.keys, self.values = self._drop_oldest(k, drop, keys), self._drop_oldest(v, drop, values)
+        self.offset += keys.shape[2]
+        self._idx = self.keys.shape[2]
+        return self.keys, self.values
+
+    def _write_one(self, keys: torch.Tensor, values: torch.Tensor):
+        prev = self.offset
+        if self.keys is None or (prev >= self.keys.shape[2] and self.keys.shape[2] < self.max_size):
+            grow = min(self.step, self.max_size - prev)
+            B, H, _, Dk = keys.shape
+            nk = torch.zeros((B, H, grow, Dk), dtype=keys.dtype, device=keys.device)
+            nv = torch.zeros((B, H, grow, values.shape[3]), dtype=values.dtype, device=values.device)
+            if self.keys is None:
+                self.keys, self.values = nk, nv
+            else:
+                self.keys, self.values = torch.cat([self.keys, nk], dim=2), torch.cat([self.values, nv], dim=2)
+            self._idx = prev
+        extra = self.keys.shape[2] - self.max_size
+        if extra > 0:  # after a multi-token update: back to a ring of max_size rows
+            self.keys, self.values = self._drop_oldest(self.keys, extra), self._drop_oldest(self.values, extra)
+            self._idx = self.max_size
+        if self._idx == self.max_size:
+            self._idx = self.keep
+        self.keys[..., self._idx: self._idx + 1, :] = keys
+        self.values[..., self._idx: self._idx + 1, :] = values
+        self.offset += 1
+        self._idx += 1
+        if self.offset < self.max_size:
+            return self.keys[..., : self.offset, :], self.values[..., : self.offset, :]
+        return self.keys, self.values
+
+    def update_and_fetch(self, keys: torch.Tensor, values: torch.Tensor):
+        if keys.shape[2] == 1:
+            return self._write_one(keys, values)
+        return self._append_chunk(keys, values)
+
+    def make_mask(self, N: int, window_size: Optional[int] = None):
+        """The mask mlx-lm builds for N new queries over this cache: None or "causal" where that
+        suffices, else a bool [N, S] causal sliding-window mask (ring-rotated for one query when
+        the window is shorter than the ring)."""
+        if N > 1:
+            window_size = window_size or self.max_size
+            off = min(self.max_size - 1, self.offset)
+            if off + N > window_size:
+                q = torch.arange(off, off + N)[:, None]
+                k = torch.arange(off + N)[None, :]
+                return (k <= q) & (k > q - window_size)
+            return "causal"
+        if window_size is None:
+            return None
+        if self.offset >= window_size and self.max_size > window_size:
+            idx = self._idx if self._idx < self.max_size else 0
+            n = min(self.max_size, self.offset + 1)
+            return torch.roll(torch.arange(n) >= n - window_size, shifts=idx + 1)
+        return None
+
+    @property
+    def state(self):
+        if self.keys is None:
+            return None, None
+        if self.offset < self.keys.shape[2]:
+            return self.keys[..., : self.offset, :], self.values[..., : self.offset, :]
+        return self.keys, self.values
+
+    def is_trimmable(self) -> bool:
+        return self.offset < self.max_size
+
+    def trim(self, n: int) -> int:
+        n = min(self.offset, n)
+        self.offset -= n
+        self._idx -= n
+        return n
+
+    @property
+    def nbytes(self) -> int:
+        if self.keys is None:
+            return 0
+        return self.keys.nbytes + self.values.nbytes
+
+    def empty(self) -> bool:
+        return self.keys is None
+
+    def to_quantized(self, group_size: int = 64, bits: int = 4):
+        raise NotImplementedError("RotatingKVCache quantization is not supported (mlx-lm raises too)")
+
+
 class QuantizedKVCache:
     """Affine-quantized K/V: per head, codes uint32 [B, H, cap, D*bits/32] and scales / biases in
     the K/V dtype [B, H, cap, D/group_size] (MLX layout)."""
@@ -219,6 +348,17 @@ def trim_prompt_cache(cache: List, num_tokens: int) -> int:
     return [c.trim(num_tokens) for c in cache][0]
 
 
-def make_prompt_cache(num_layers: int) -> List[KVCache]:
-    """One unquantized cache per attention layer (mlx-lm make_prompt_cache for plain models)."""
+def make_prompt_cache(num_layers: int, max_kv_size: Optional[int] = None,
+                      layer_windows: Optional[List[Optional[int]]] = None) -> List:
+    """One cache per attention layer, as mlx-lm's make_prompt_cache builds them: a KVCache per
+    layer, or a RotatingKVCache(max_kv_size, keep=4) per layer when max_kv_size is given.
+    layer_windows gives a model's own pattern instead (a model's make_cache(): a window size for
+    each sliding-window layer, None for a global layer), e.g. five 1024-token windows then one
+    global layer."""
+    if layer_windows is not None:
+        if len(layer_windows) != num_layers:
+            raise ValueError(f"layer_windows has {len(layer_windows)} entries for {num_layers} layers")
+        return [RotatingKVCache(max_size=w, keep=0) if w else KVCache() for w in layer_windows]
+    if max_kv_size is not None:
+        return [RotatingKVCache(max_size=max_kv_size, keep=4) for _ in range(num_layers)]
     return [KVCache() for _ in range(num_layers)]

@@ -58,19 +58,35 @@ int check_rows(const kvq_rows* r, const char* name, int D, bool vec16) {
   return KVQ_OK;
 }
 
-int check_attn(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v, const kvq_rows* out, int B, int Hq,
-               int Hkv, int L, int D, int S, int bits, int group_size, int dtype, float scale, int window,
-               size_t ws_needed, void* workspace, size_t workspace_bytes) {
+
+// Shared checks of the attention entry points (shape, dtype, scale, window, queries, output).
+int check_attn_common(const kvq_rows* q, const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int dtype,
+                      float scale, int window) {
   int rc;
   if ((rc = check_dtype(dtype))) return rc;
   if (B <= 0 || Hq <= 0 || Hkv <= 0 || L <= 0 || S <= 0) return fail(KVQ_ERR_INVALID, "B, Hq, Hkv, L and S must be positive (got %d, %d, %d, %d, %d)", B, Hq, Hkv, L, S);
   if (Hq % Hkv) return fail(KVQ_ERR_INVALID, "Hq=%d is not a multiple of Hkv=%d", Hq, Hkv);
-  if (bits != 4 && bits != 8) return fail(KVQ_ERR_UNSUPPORTED, "attention supports 4- and 8-bit caches, got bits=%d", bits);
-  if (group_size != 64) return fail(KVQ_ERR_UNSUPPORTED, "attention supports group_size 64, got %d", group_size);
   if (window < 0) return fail(KVQ_ERR_INVALID, "window must be >= 0, got %d", window);
   if (!isfinite(scale)) return fail(KVQ_ERR_INVALID, "scale is not finite");
   if ((rc = check_rows(q, "queries", D, true))) return rc;
   if ((rc = check_rows(out, "out", D, false))) return rc;
+  return KVQ_OK;
+}
+
+int check_workspace(size_t ws_needed, void* workspace, size_t workspace_bytes) {
+  if (!workspace || workspace_bytes < ws_needed)
+    return fail(KVQ_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", ws_needed, workspace ? workspace_bytes : (size_t)0);
+  if (!aligned(workspace, 256)) return fail(KVQ_ERR_WORKSPACE, "workspace must be 256-byte aligned");
+  return KVQ_OK;
+}
+
+int check_attn(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v, const kvq_rows* out, int B, int Hq,
+               int Hkv, int L, int D, int S, int bits, int group_size, int dtype, float scale, int window,
+               size_t ws_needed, void* workspace, size_t workspace_bytes) {
+  int rc;
+  if ((rc = check_attn_common(q, out, B, Hq, Hkv, L, D, S, dtype, scale, window))) return rc;
+  if (bits != 4 && bits != 8) return fail(KVQ_ERR_UNSUPPORTED, "attention supports 4- and 8-bit caches, got bits=%d", bits);
+  if (group_size != 64) return fail(KVQ_ERR_UNSUPPORTED, "attention supports group_size 64, got %d", group_size);
   if ((rc = check_qtensor(k, "keys"))) return rc;
   if ((rc = check_qtensor(v, "values"))) return rc;
   const int64_t row_words = (int64_t)D * bits / 32;
@@ -83,10 +99,24 @@ int check_attn(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v, co
     if ((int64_t)S * t->codes_stride_s * 4 > (int64_t)UINT32_MAX || (int64_t)S * t->sb_stride_s * 2 > (int64_t)UINT32_MAX)
       return fail(KVQ_ERR_UNSUPPORTED, "attention needs S times each row stride within 4 GiB (S=%d)", S);
   }
-  if (!workspace || workspace_bytes < ws_needed)
-    return fail(KVQ_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", ws_needed, workspace ? workspace_bytes : (size_t)0);
-  if (!aligned(workspace, 256)) return fail(KVQ_ERR_WORKSPACE, "workspace must be 256-byte aligned");
-  return KVQ_OK;
+  return check_workspace(ws_needed, workspace, workspace_bytes);
+}
+
+// Attention over an unquantized cache: K and V are strided T rows like the queries.
+int check_attn_dense(const kvq_rows* q, const kvq_rows* k, const kvq_rows* v, const kvq_rows* out, int B, int Hq,
+                     int Hkv, int L, int D, int S, int dtype, float scale, int window, size_t ws_needed,
+                     void* workspace, size_t workspace_bytes) {
+  int rc;
+  if ((rc = check_attn_common(q, out, B, Hq, Hkv, L, D, S, dtype, scale, window))) return rc;
+  if ((rc = check_rows(k, "keys", D, true))) return rc;
+  if ((rc = check_rows(v, "values", D, true))) return rc;
+  for (const kvq_rows* t : {k, v}) {
+    if (t->stride_l < D) return fail(KVQ_ERR_INVALID, "K/V row stride %lld is smaller than D=%d", (long long)t->stride_l, D);
+    // the kernels address each (sequence, KV head)'s rows with 32-bit byte offsets
+    if ((int64_t)S * t->stride_l * 2 > (int64_t)UINT32_MAX)
+      return fail(KVQ_ERR_UNSUPPORTED, "attention needs S times the K/V row stride within 4 GiB (S=%d)", S);
+  }
+  return check_workspace(ws_needed, workspace, workspace_bytes);
 }
 
 int check_quantize(const kvq_rows* k_src, const kvq_qtensor* k_dst, const kvq_rows* v_src, const kvq_qtensor* v_dst,
@@ -171,10 +201,13 @@ int kvq_rope_quantize_append(const kvq_rows* k_src, const kvq_qtensor* k_dst, co
 
 size_t kvq_decode_workspace_size(int B, int Hq, int Hkv, int L, int D, int S, int window) {
   if (B <= 0 || Hq <= 0 || Hkv <= 0 || L <= 0 || S <= 0 || (D != 64 && D != 128) || window < 0) return 0;
-  // the plan depends on bits only through the chunk length; size for the larger split count
-  const size_t a = kvq::decode_workspace_bytes(B, Hq, Hkv, L, D, S, window, 8);
-  const size_t b = kvq::decode_workspace_bytes(B, Hq, Hkv, L, D, S, window, 4);
-  return a > b ? a : b;
+  // one size serves every cache format: the quantized (8-, 4-bit) and the unquantized (16) plans
+  size_t n = 0;
+  for (int bits : {8, 4, 16}) {
+    const size_t x = kvq::decode_workspace_bytes(B, Hq, Hkv, L, D, S, window, bits);
+    n = x > n ? x : n;
+  }
+  return n;
 }
 
 int kvq_decode_attn(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v, const int32_t* seq_lens,
@@ -207,6 +240,30 @@ int kvq_prefill_attn(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor*
   return hip_status(kvq::launch_prefill(q, k, v, seq_lens, out, B, Hq, Hkv, L, D, S, bits, dtype, scale, causal,
                                         window, workspace, (hipStream_t)stream),
                     "prefill_attn launch");
+}
+
+int kvq_decode_attn_dense(const kvq_rows* q, const kvq_rows* k, const kvq_rows* v, const int32_t* seq_lens,
+                          const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int dtype, float scale,
+                          int causal, int window, void* workspace, size_t workspace_bytes, void* stream) {
+  if (D != 64 && D != 128) return fail(KVQ_ERR_UNSUPPORTED, "decode supports head_dim 64 and 128, got %d", D);
+  int rc = check_attn_dense(q, k, v, out, B, Hq, Hkv, L, D, S, dtype, scale, window,
+                            kvq_decode_workspace_size(B, Hq, Hkv, L, D, S, window), workspace, workspace_bytes);
+  if (rc) return rc;
+  return hip_status(kvq::launch_decode_dense(q, k, v, seq_lens, out, B, Hq, Hkv, L, D, S, dtype, scale, causal, window,
+                                             workspace, (hipStream_t)stream),
+                    "decode_attn_dense launch");
+}
+
+int kvq_prefill_attn_dense(const kvq_rows* q, const kvq_rows* k, const kvq_rows* v, const int32_t* seq_lens,
+                           const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int dtype, float scale,
+                           int causal, int window, void* workspace, size_t workspace_bytes, void* stream) {
+  if (D != 128) return fail(KVQ_ERR_UNSUPPORTED, "prefill supports head_dim 128, got %d", D);
+  int rc = check_attn_dense(q, k, v, out, B, Hq, Hkv, L, D, S, dtype, scale, window,
+                            kvq_prefill_workspace_size(B, Hq, Hkv, L, D, S, window), workspace, workspace_bytes);
+  if (rc) return rc;
+  return hip_status(kvq::launch_prefill_dense(q, k, v, seq_lens, out, B, Hq, Hkv, L, D, S, dtype, scale, causal, window,
+                                              workspace, (hipStream_t)stream),
+                    "prefill_attn_dense launch");
 }
 
 }  // extern "C"

@@ -46,6 +46,32 @@ __device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
+typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+
+// Two bf16 values packed in a u32 (low half first), rounded to nearest even; lo and hi are
+// replaced by the rounded values (callers keep sums consistent with the operands they pack).
+__device__ __forceinline__ uint32_t pack_bf16x2(float& lo, float& hi) {
+  const bf2 v = {(__bf16)lo, (__bf16)hi};
+  lo = (float)v[0];
+  hi = (float)v[1];
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// MFMA on 16-bit operands given as raw bit patterns, f16 or bf16 by the element tag.
+__device__ __forceinline__ f4 mfma_16x16x32(u4 a, u4 b, f4 c, F16) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, a), __builtin_bit_cast(h8, b), c, 0, 0, 0);
+}
+__device__ __forceinline__ f4 mfma_16x16x32(u4 a, u4 b, f4 c, BF16) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf8, a), __builtin_bit_cast(bf8, b), c, 0, 0, 0);
+}
+__device__ __forceinline__ f16v mfma_32x32x16(u4 a, u4 b, f16v c, F16) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(h8, a), __builtin_bit_cast(h8, b), c, 0, 0, 0);
+}
+__device__ __forceinline__ f16v mfma_32x32x16(u4 a, u4 b, f16v c, BF16) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf8, a), __builtin_bit_cast(bf8, b), c, 0, 0, 0);
+}
+
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // Cross-lane helpers (wave64).

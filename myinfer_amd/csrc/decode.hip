@@ -1,5 +1,5 @@
-// Split-K flash-decoding over an MLX-layout affine-quantized KV cache (small L), with the
-// log-sum-exp merge of the key splits fused into the same launch.
+// Split-K flash-decoding over an MLX-layout affine-quantized KV cache (small L), or over an
+// unquantized fp16/bf16 cache, with a log-sum-exp merge of the key splits.
 //
 // Computes, per (sequence b, query head h, query row l):
 //   out = softmax(scale * q K^T + mask) V,   K = sK * codesK + bK,  V = sV * codesV + bV
@@ -27,8 +27,11 @@
 //    key row per lane) are free of LDS bank conflicts.
 //  * Online softmax in the log2 domain; rescaling of the output accumulators is lazy (only when a
 //    row maximum grows). The waves of a workgroup merge in LDS into one (m, l, o[D]) partial per
-//    query row. The last workgroup of each (sequence, KV head, row block) to finish -- found with
-//    a device-scope counter that it resets afterwards -- merges the splits and writes the output.
+//    query row. A second small launch (combine_kernel) merges the splits and writes the output;
+//    optionally (fused mode) the last workgroup of each (sequence, KV head, row block) to finish --
+//    found with a device-scope counter that it resets afterwards -- merges them instead.
+//  * The unquantized cache (BITS == 16) takes the same path with raw 16-bit rows as MFMA operands
+//    (bf16 MFMA for bf16 caches), no scales or biases, and the raw query as the Q operand.
 //  * Workgroups are numbered so that the splits of one KV head land on one XCD (hardware hands
 //    consecutive workgroups to the 8 XCDs in turn), keeping the merge inside one L2.
 
@@ -44,8 +47,12 @@ namespace kvq {
 constexpr int kTile = 32;
 constexpr int kXcds = 8;
 
+// BITS == 16 is the unquantized cache: raw T rows, no scales or biases. It keeps the column
+// layout of the quantized cache (R query rows, each in NG columns), with every column computing the
+// row's full dot product, so the wave epilogue below serves both.
 template <int D, int BITS>
 struct DecCfg {
+  static constexpr bool DENSE = BITS == 16;
   static constexpr int NG = D / 64;            // scale groups per row
   static constexpr int R = 16 / NG;            // query rows per wave
   static constexpr int KSTEPS = D / 32;        // QK MFMA k-steps (8 dims per lane each)
@@ -58,9 +65,9 @@ struct DecCfg {
   static constexpr int CI = kTile / RPI;       // DMA instructions per K (or V) tile
   static constexpr int TB = kTile * ROWB;      // bytes of a K (or V) tile
   // a ring slot: [K tile][V tile][sK, bK, sV, bV: 64 4-byte cells each, value in the low half;
-  // cell 32 g + k holds group g of key k]
-  static constexpr int SLOT = 2 * TB + 4 * 256;
-  static constexpr int IPT = 2 * CI + 4;       // DMA instructions per tile
+  // cell 32 g + k holds group g of key k] (no scale/bias cells for the unquantized cache)
+  static constexpr int SLOT = 2 * TB + (DENSE ? 0 : 4 * 256);
+  static constexpr int IPT = 2 * CI + (DENSE ? 0 : 4);  // DMA instructions per tile
 };
 
 struct DecParams {
@@ -222,6 +229,80 @@ __device__ __forceinline__ void read_tile(TileOps<32>& t, uint32_t ka0, uint32_t
       : "memory");
 }
 
+// The LDS operands of one 32-key tile of the unquantized cache (raw T rows):
+//   k[beta][c] : chunk c of the lane's D/4 dims of key 16 beta + n (chunk position swizzled by
+//                key, so each chunk has its own address: ka[c])
+//   v[i]       : the lane's D/16 dims of key v_token(lg, i)
+template <int D>
+struct DenseOps;
+template <>
+struct DenseOps<128> {
+  u4 k[2][4];
+  u4 v[8];
+};
+template <>
+struct DenseOps<64> {
+  u4 k[2][2];
+  u2 v[8];
+};
+
+__device__ __forceinline__ void read_tile_dense(DenseOps<128>& t, const uint32_t (&ka)[4], uint32_t va) {
+  asm volatile(
+      "ds_read_b128 %0, %16\n"
+      "ds_read_b128 %1, %17\n"
+      "ds_read_b128 %2, %18\n"
+      "ds_read_b128 %3, %19\n"
+      "ds_read_b128 %4, %16 offset:4096\n"
+      "ds_read_b128 %5, %17 offset:4096\n"
+      "ds_read_b128 %6, %18 offset:4096\n"
+      "ds_read_b128 %7, %19 offset:4096\n"
+      "ds_read_b128 %8, %20\n"
+      "ds_read_b128 %9, %20 offset:256\n"
+      "ds_read_b128 %10, %20 offset:512\n"
+      "ds_read_b128 %11, %20 offset:768\n"
+      "ds_read_b128 %12, %20 offset:4096\n"
+      "ds_read_b128 %13, %20 offset:4352\n"
+      "ds_read_b128 %14, %20 offset:4608\n"
+      "ds_read_b128 %15, %20 offset:4864\n"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(t.k[0][0]), "=&v"(t.k[0][1]), "=&v"(t.k[0][2]), "=&v"(t.k[0][3]), "=&v"(t.k[1][0]), "=&v"(t.k[1][1]),
+        "=&v"(t.k[1][2]), "=&v"(t.k[1][3]), "=&v"(t.v[0]), "=&v"(t.v[1]), "=&v"(t.v[2]), "=&v"(t.v[3]), "=&v"(t.v[4]),
+        "=&v"(t.v[5]), "=&v"(t.v[6]), "=&v"(t.v[7])
+      : "v"(ka[0]), "v"(ka[1]), "v"(ka[2]), "v"(ka[3]), "v"(va)
+      : "memory");
+}
+__device__ __forceinline__ void read_tile_dense(DenseOps<64>& t, const uint32_t (&ka)[2], uint32_t va) {
+  asm volatile(
+      "ds_read_b128 %0, %12\n"
+      "ds_read_b128 %1, %13\n"
+      "ds_read_b128 %2, %12 offset:2048\n"
+      "ds_read_b128 %3, %13 offset:2048\n"
+      "ds_read_b64 %4, %14\n"
+      "ds_read_b64 %5, %14 offset:128\n"
+      "ds_read_b64 %6, %14 offset:256\n"
+      "ds_read_b64 %7, %14 offset:384\n"
+      "ds_read_b64 %8, %14 offset:2048\n"
+      "ds_read_b64 %9, %14 offset:2176\n"
+      "ds_read_b64 %10, %14 offset:2304\n"
+      "ds_read_b64 %11, %14 offset:2432\n"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(t.k[0][0]), "=&v"(t.k[0][1]), "=&v"(t.k[1][0]), "=&v"(t.k[1][1]), "=&v"(t.v[0]), "=&v"(t.v[1]),
+        "=&v"(t.v[2]), "=&v"(t.v[3]), "=&v"(t.v[4]), "=&v"(t.v[5]), "=&v"(t.v[6]), "=&v"(t.v[7])
+      : "v"(ka[0]), "v"(ka[1]), "v"(va)
+      : "memory");
+}
+
+// V operand of the unquantized cache for column block jN: the 16-bit value at the lane's dim jN
+// of each of its 8 keys, packed in key order.
+template <typename VT>
+__device__ __forceinline__ u4 v_operand_dense(const VT (&vr)[8], int jN) {
+  const uint32_t sel = (jN & 1) ? 0x07060302u : 0x05040100u;
+  u4 r;
+#pragma unroll
+  for (int a = 0; a < 4; ++a) r[a] = perm(vr[2 * a + 1][jN >> 1], vr[2 * a][jN >> 1], sel);
+  return r;
+}
+
 // s_waitcnt vmcnt(N) (N < 64), other counters left alone.
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
@@ -348,8 +429,8 @@ __global__ __launch_bounds__(NW * 64, (dec_min_wgs<D, BITS, NW, NSLOT>())) void 
   const uint8_t* vbase = p.vc + (int64_t)b * p.vc_sb + (int64_t)kvh * p.vc_sh;
   const __amdgpu_buffer_rsrc_t krs = make_rsrc(kbase, (uint32_t)((int64_t)S_b * p.kc_ss));
   const __amdgpu_buffer_rsrc_t vrs = make_rsrc(vbase, (uint32_t)((int64_t)S_b * p.vc_ss));
-  __amdgpu_buffer_rsrc_t srs[4];
-  {
+  __amdgpu_buffer_rsrc_t srs[4] = {krs, krs, krs, krs};
+  if constexpr (!C::DENSE) {
     const int64_t ko = (int64_t)b * p.ksb_sb + (int64_t)kvh * p.ksb_sh;
     const int64_t vo = (int64_t)b * p.vsb_sb + (int64_t)kvh * p.vsb_sh;
     const uint32_t kn = (uint32_t)((int64_t)S_b * p.ksb_ss * 2), vn = (uint32_t)((int64_t)S_b * p.vsb_ss * 2);
@@ -366,12 +447,13 @@ __global__ __launch_bounds__(NW * 64, (dec_min_wgs<D, BITS, NW, NSLOT>())) void 
     const int rr = lane / C::CPR, cc = lane % C::CPR;
 #pragma unroll
     for (int c = 0; c < C::CI; ++c) {
-      dk[c] = (uint32_t)((int64_t)(c * C::RPI + rr) * p.kc_ss + 16 * (cc ^ (rr % C::CPR)));
+      const int kr = c * C::RPI + rr;
+      dk[c] = (uint32_t)((int64_t)kr * p.kc_ss + 16 * (cc ^ (kr % C::CPR)));
       dv[c] = (uint32_t)((int64_t)(c * C::RPI + rr) * p.vc_ss + 16 * cc);
     }
     const int sk = lane & 31, sg = C::NG == 2 ? lane >> 5 : 0;
-    dsb[0] = dsb[1] = (uint32_t)(sk * p.ksb_ss * 2 + 2 * sg);
-    dsb[2] = dsb[3] = (uint32_t)(sk * p.vsb_ss * 2 + 2 * sg);
+    dsb[0] = dsb[1] = C::DENSE ? 0u : (uint32_t)(sk * p.ksb_ss * 2 + 2 * sg);
+    dsb[2] = dsb[3] = C::DENSE ? 0u : (uint32_t)(sk * p.vsb_ss * 2 + 2 * sg);
   }
   uint8_t* const ring = smem + wave * (NSLOT * C::SLOT);
   auto tile_k0 = [&](int i) { return k_begin + kTile * (wave + NW * i); };
@@ -386,9 +468,11 @@ __global__ __launch_bounds__(NW * 64, (dec_min_wgs<D, BITS, NW, NSLOT>())) void 
     for (int c = 0; c < C::CI; ++c) dma16(krs, sl + 1024 * c, dk[c], ko);
 #pragma unroll
     for (int c = 0; c < C::CI; ++c) dma16(vrs, sl + C::TB + 1024 * c, dv[c], vo);
-    const uint32_t kso = (uint32_t)((int64_t)k0 * p.ksb_ss * 2), vso = (uint32_t)((int64_t)k0 * p.vsb_ss * 2);
+    if constexpr (!C::DENSE) {
+      const uint32_t kso = (uint32_t)((int64_t)k0 * p.ksb_ss * 2), vso = (uint32_t)((int64_t)k0 * p.vsb_ss * 2);
 #pragma unroll
-    for (int a = 0; a < 4; ++a) dma2(srs[a], sl + 2 * C::TB + 256 * a, dsb[a], a < 2 ? kso : vso);
+      for (int a = 0; a < 4; ++a) dma2(srs[a], sl + 2 * C::TB + 256 * a, dsb[a], a < 2 ? kso : vso);
+    }
   };
   // nothing that waits for the query loads may be scheduled into (or before) the first tile loads
   __builtin_amdgcn_sched_barrier(0);
@@ -402,45 +486,56 @@ __global__ __launch_bounds__(NW * 64, (dec_min_wgs<D, BITS, NW, NSLOT>())) void 
   const int lo_all = p.window > 0 ? max(0, S_b - p.window) : 0;
   const int hi_all = p.causal ? S_b - p.L + 1 : S_b;
 
-  // ---- Q operand: slot i of k-step j is q[row][lg*D/4 + 8j + dim(i)] if that dim is in group g
-  float qv[C::KSTEPS][8];
-  float qmax = 0.0f, qsum = 0.0f;
-  const bool q_on = row_ok && in_group;
-#pragma unroll
-  for (int j = 0; j < C::KSTEPS; ++j) {
-    if (!q_on) qraw[j] = u4{0, 0, 0, 0};
-    float e[8];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      e[2 * i] = to_float((uint16_t)(qraw[j][i] & 0xffffu), T{});
-      e[2 * i + 1] = to_float((uint16_t)(qraw[j][i] >> 16), T{});
-    }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      qv[j][i] = e[k_slot_dim<BITS>(i)];
-      qmax = fmaxf(qmax, fabsf(qv[j][i]));
-      qsum += qv[j][i];
-    }
-  }
-#pragma unroll
-  for (int m = R; m < 16; m <<= 1) qmax = fmaxf(qmax, shfl_xor(qmax, m));
-  qmax = max_xor32(max_xor16(qmax));
-  qsum = add_xor32(add_xor16(qsum));
-  int qexp = 0;
-  if (qmax > 0.0f) {
-    frexpf(qmax, &qexp);
-    qexp = 15 - qexp;  // |q| * 2^qexp < 2^15
-  }
-  const float qscale = ldexpf(1.0f, qexp);
+  // ---- Q operand. Unquantized cache: the raw query slice itself (exact), the scale applied to the
+  // fp32 scores. Quantized cache:
   h8 qop[C::KSTEPS];
+  u4 qd[C::KSTEPS];
+  float kf, qs2 = 0.0f;
+  if constexpr (C::DENSE) {
+    (void)in_group;
 #pragma unroll
-  for (int j = 0; j < C::KSTEPS; ++j) {
+    for (int j = 0; j < C::KSTEPS; ++j) qd[j] = row_ok ? qraw[j] : u4{0, 0, 0, 0};
+    kf = p.scale_log2;
+  } else {
+    // slot i of k-step j is q[row][lg*D/4 + 8j + dim(i)] if that dim is in group g
+    float qv[C::KSTEPS][8];
+    float qmax = 0.0f, qsum = 0.0f;
+    const bool q_on = row_ok && in_group;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) qop[j][i] = (_Float16)(qv[j][i] * qscale * k_slot_weight<BITS>(i));
+    for (int j = 0; j < C::KSTEPS; ++j) {
+      if (!q_on) qraw[j] = u4{0, 0, 0, 0};
+      float e[8];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        e[2 * i] = to_float((uint16_t)(qraw[j][i] & 0xffffu), T{});
+        e[2 * i + 1] = to_float((uint16_t)(qraw[j][i] >> 16), T{});
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        qv[j][i] = e[k_slot_dim<BITS>(i)];
+        qmax = fmaxf(qmax, fabsf(qv[j][i]));
+        qsum += qv[j][i];
+      }
+    }
+#pragma unroll
+    for (int m = R; m < 16; m <<= 1) qmax = fmaxf(qmax, shfl_xor(qmax, m));
+    qmax = max_xor32(max_xor16(qmax));
+    qsum = add_xor32(add_xor16(qsum));
+    int qexp = 0;
+    if (qmax > 0.0f) {
+      frexpf(qmax, &qexp);
+      qexp = 15 - qexp;  // |q| * 2^qexp < 2^15
+    }
+    const float qscale = ldexpf(1.0f, qexp);
+#pragma unroll
+    for (int j = 0; j < C::KSTEPS; ++j) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) qop[j][i] = (_Float16)(qv[j][i] * qscale * k_slot_weight<BITS>(i));
+    }
+    // score = sK * (acc * kf) + bK * qs2, then summed over the NG groups of the row
+    kf = ldexpf(1.0f, 24 - qexp) * p.scale_log2;
+    qs2 = qsum * p.scale_log2;
   }
-  // score = sK * (acc * kf) + bK * qs2, then summed over the NG groups of the row
-  const float kf = ldexpf(1.0f, 24 - qexp) * p.scale_log2;
-  const float qs2 = qsum * p.scale_log2;
 
   float m_run = -INFINITY, l_part = 0.0f, ob_part = 0.0f;
   f4 acc_o[C::NBLK];
@@ -460,43 +555,65 @@ __global__ __launch_bounds__(NW * 64, (dec_min_wgs<D, BITS, NW, NSLOT>())) void 
   }
   const uint32_t off_sb = 2 * C::TB + 4 * (32 * g + 4 * lg);
   const uint32_t off_v = C::TB + 4 * lg * C::ROWB + n * C::VLB;
+  // unquantized cache: chunk c of the lane's D/4 dims of key n sits at position (KCH lg + c) ^ sw
+  constexpr int KCH = C::DENSE ? C::KLB / 16 : 1;
+  uint32_t off_kd[KCH];
+#pragma unroll
+  for (int c = 0; c < KCH; ++c) off_kd[c] = n * C::ROWB + 16 * ((KCH * lg + c) ^ sw);
 
-  auto compute = [&](const TileOps<C::ROWB>& op, int k0) {
-    auto sbv = [&](int a, int beta, int i) -> float { return to_float((uint16_t)(op.sb[a][beta][i] & 0xffffu), T{}); };
-
-    // S^T = K Q^T: rows = 16 keys of block beta, columns = (query row, group)
-    f4 sacc[2];
-#pragma unroll
-    for (int beta = 0; beta < 2; ++beta) {
-      Bytes<C::KLB> kc;
-      if constexpr (C::KLB == 32) {
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          kc.w[w] = op.k[beta][0][w];
-          kc.w[4 + w] = op.k[beta][1][w];
-        }
-      } else if constexpr (C::KLB == 16) {
-#pragma unroll
-        for (int w = 0; w < 4; ++w) kc.w[w] = op.k[beta][w];
+  auto compute = [&](const auto& op, int k0) {
+    auto sbv = [&](int a, int beta, int i) -> float {
+      if constexpr (C::DENSE) {
+        return 0.0f;
       } else {
-        kc.w[0] = op.k[beta][0];
-        kc.w[1] = op.k[beta][1];
+        return to_float((uint16_t)(op.sb[a][beta][i] & 0xffffu), T{});
       }
-      sacc[beta] = f4{0, 0, 0, 0};
-#pragma unroll
-      for (int j = 0; j < C::KSTEPS; ++j)
-        sacc[beta] = __builtin_amdgcn_mfma_f32_16x16x32_f16(k_operand<D, BITS>(kc, j), qop[j], sacc[beta], 0, 0, 0);
-    }
+    };
     float sc[8];
+    if constexpr (C::DENSE) {
+      // S^T = K Q^T on the raw 16-bit rows: rows = 16 keys of block beta, columns = query rows
 #pragma unroll
-    for (int beta = 0; beta < 2; ++beta)
+      for (int beta = 0; beta < 2; ++beta) {
+        f4 sacc = f4{0, 0, 0, 0};
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        float x = sbv(0, beta, i) * (sacc[beta][i] * kf) + sbv(1, beta, i) * qs2;
-        if constexpr (C::NG >= 2) x += row_rotate<8>(x);
-        if constexpr (C::NG >= 4) x += row_rotate<4>(x);
-        sc[4 * beta + i] = x;
+        for (int j = 0; j < C::KSTEPS; ++j) sacc = mfma_16x16x32(op.k[beta][j], qd[j], sacc, T{});
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sc[4 * beta + i] = sacc[i] * kf;
       }
+    } else {
+      // S^T = K Q^T: rows = 16 keys of block beta, columns = (query row, group)
+      f4 sacc[2];
+#pragma unroll
+      for (int beta = 0; beta < 2; ++beta) {
+        Bytes<C::KLB> kc;
+        if constexpr (C::KLB == 32) {
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            kc.w[w] = op.k[beta][0][w];
+            kc.w[4 + w] = op.k[beta][1][w];
+          }
+        } else if constexpr (C::KLB == 16) {
+#pragma unroll
+          for (int w = 0; w < 4; ++w) kc.w[w] = op.k[beta][w];
+        } else {
+          kc.w[0] = op.k[beta][0];
+          kc.w[1] = op.k[beta][1];
+        }
+        sacc[beta] = f4{0, 0, 0, 0};
+#pragma unroll
+        for (int j = 0; j < C::KSTEPS; ++j)
+          sacc[beta] = __builtin_amdgcn_mfma_f32_16x16x32_f16(k_operand<D, BITS>(kc, j), qop[j], sacc[beta], 0, 0, 0);
+      }
+#pragma unroll
+      for (int beta = 0; beta < 2; ++beta)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float x = sbv(0, beta, i) * (sacc[beta][i] * kf) + sbv(1, beta, i) * qs2;
+          if constexpr (C::NG >= 2) x += row_rotate<8>(x);
+          if constexpr (C::NG >= 4) x += row_rotate<4>(x);
+          sc[4 * beta + i] = x;
+        }
+    }
     const bool need_mask = !(k0 >= lo_all && k0 + kTile <= hi_all);
     if (need_mask) {
 #pragma unroll
@@ -523,36 +640,56 @@ __global__ __launch_bounds__(NW * 64, (dec_min_wgs<D, BITS, NW, NSLOT>())) void 
       m_run = m_new;
     }
     const float msub = (m_run == -INFINITY) ? 0.0f : m_run;
-    float pa[8];
-    float psum = 0.0f, pb = 0.0f;
+    if constexpr (C::DENSE) {
+      // P' (A operand) in the cache's type; the row sum adds the rounded probabilities, so the
+      // output stays a convex combination of V rows whatever the rounding
+      float pr[8];
 #pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      const float pr = exp2_fast(sc[s] - msub);
-      psum += pr;
-      pb += pr * sbv(3, s >> 2, s & 3);
-      pa[s] = pr * sbv(2, s >> 2, s & 3);
-    }
-    l_part += psum;
-    ob_part += pb;
-    u4 aw;
+      for (int s2 = 0; s2 < 8; ++s2) pr[s2] = exp2_fast(sc[s2] - msub);
+      u4 aw;
 #pragma unroll
-    for (int a = 0; a < 4; ++a) aw[a] = pack_f16x2(pa[2 * a], pa[2 * a + 1]);
-    const h8 aop = __builtin_bit_cast(h8, aw);
-    // V codes of the lane's column slice at its 8 keys
-    constexpr int VB = C::VLB < 2 ? 2 : C::VLB;
-    Bytes<VB> vc[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      if constexpr (C::VLB == 8) {
-        vc[i].w[0] = op.v[i][0];
-        vc[i].w[1] = op.v[i][1];
-      } else {
-        vc[i].w[0] = op.v[i];
+      for (int a = 0; a < 4; ++a) {
+        if constexpr (T::id == KVQ_DTYPE_BF16) {
+          aw[a] = pack_bf16x2(pr[2 * a], pr[2 * a + 1]);
+        } else {
+          aw[a] = pack_f16x2(pr[2 * a], pr[2 * a + 1]);
+        }
+        l_part += pr[2 * a] + pr[2 * a + 1];
       }
-    }
 #pragma unroll
-    for (int jn = 0; jn < C::NBLK; ++jn)
-      acc_o[jn] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, v_operand<D, BITS, VB>(vc, jn), acc_o[jn], 0, 0, 0);
+      for (int jn = 0; jn < C::NBLK; ++jn) acc_o[jn] = mfma_16x16x32(aw, v_operand_dense(op.v, jn), acc_o[jn], T{});
+    } else {
+      float pa[8];
+      float psum = 0.0f, pb = 0.0f;
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        const float pr = exp2_fast(sc[s] - msub);
+        psum += pr;
+        pb += pr * sbv(3, s >> 2, s & 3);
+        pa[s] = pr * sbv(2, s >> 2, s & 3);
+      }
+      l_part += psum;
+      ob_part += pb;
+      u4 aw;
+#pragma unroll
+      for (int a = 0; a < 4; ++a) aw[a] = pack_f16x2(pa[2 * a], pa[2 * a + 1]);
+      const h8 aop = __builtin_bit_cast(h8, aw);
+      // V codes of the lane's column slice at its 8 keys
+      constexpr int VB = C::VLB < 2 ? 2 : C::VLB;
+      Bytes<VB> vc[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        if constexpr (C::VLB == 8) {
+          vc[i].w[0] = op.v[i][0];
+          vc[i].w[1] = op.v[i][1];
+        } else {
+          vc[i].w[0] = op.v[i];
+        }
+      }
+#pragma unroll
+      for (int jn = 0; jn < C::NBLK; ++jn)
+        acc_o[jn] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, v_operand<D, BITS, VB>(vc, jn), acc_o[jn], 0, 0, 0);
+    }
   };
 
   // ---- main loop: tile i is read out of its slot, the slot is refilled with tile i + NSLOT, and
@@ -562,10 +699,20 @@ __global__ __launch_bounds__(NW * 64, (dec_min_wgs<D, BITS, NW, NSLOT>())) void 
     const int slot = i % NSLOT;
     wait_vmcnt<(NSLOT - 1) * C::IPT>();  // tile i has landed
     const uint32_t sa = ring_lds + slot * C::SLOT;
-    TileOps<C::ROWB> op;
-    read_tile(op, sa + off_k0, sa + off_k1, sa + off_sb, sa + off_v);
-    issue(i + NSLOT, slot);
-    compute(op, tile_k0(i));
+    if constexpr (C::DENSE) {
+      DenseOps<D> op;
+      uint32_t ka[KCH];
+#pragma unroll
+      for (int c = 0; c < KCH; ++c) ka[c] = sa + off_kd[c];
+      read_tile_dense(op, ka, sa + off_v);
+      issue(i + NSLOT, slot);
+      compute(op, tile_k0(i));
+    } else {
+      TileOps<C::ROWB> op;
+      read_tile(op, sa + off_k0, sa + off_k1, sa + off_sb, sa + off_v);
+      issue(i + NSLOT, slot);
+      compute(op, tile_k0(i));
+    }
   }
   wait_vmcnt<0>();  // the look-ahead loads past the last tile land before the ring is reused
   __syncthreads();  // every wave is done with its ring: the space is reused below
@@ -590,7 +737,7 @@ __global__ __launch_bounds__(NW * 64, (dec_min_wgs<D, BITS, NW, NSLOT>())) void 
     if (m / R == n / R) {
 #pragma unroll
       for (int jn = 0; jn < C::NBLK; ++jn) {
-        float sc = 16777216.0f;
+        float sc = C::DENSE ? 1.0f : 16777216.0f;
         if constexpr (BITS == 4) sc = (jn & 1) ? 1048576.0f : 16777216.0f;
         w_o[(wave * R + m % R) * D + (D / 16) * n + jn] = acc_o[jn][i] * sc + obi[i];
       }
@@ -722,11 +869,12 @@ static DecTune decode_tune() {
   return t;
 }
 
-DecPlan decode_plan(int B, int Hq, int Hkv, int L, int D, int S, int window, int) {
+DecPlan decode_plan(int B, int Hq, int Hkv, int L, int D, int S, int window, int bits) {
   DecPlan pl;
   const DecTune tune = decode_tune();
-  pl.nw = D == 128 ? tune.nw : 4;
-  pl.nslot = D == 128 ? tune.nslot : 2;
+  const bool dense = bits == 16;
+  pl.nw = D == 128 && !dense ? tune.nw : 4;
+  pl.nslot = D == 128 && !dense ? tune.nslot : 2;
   pl.R = 16 / (D / 64);
   const int nrows = (Hq / Hkv) * L;
   pl.rowblocks = (nrows + pl.R - 1) / pl.R;
@@ -788,7 +936,9 @@ static hipError_t launch_decode_t(const DecParams& p, hipStream_t stream) {
 
 template <typename T, int D, int BITS>
 static hipError_t launch_decode_shape(const DecParams& p, const DecPlan& pl, hipStream_t stream) {
-  if constexpr (D == 128) {
+  if constexpr (BITS == 16) {
+    return launch_decode_t<T, D, BITS, 4, 2>(p, stream);  // a 3-slot ring of raw rows does not fit
+  } else if constexpr (D == 128) {
     if (pl.nw == 8) return launch_decode_t<T, D, BITS, 8, 2>(p, stream);
     if (pl.nslot == 2) return launch_decode_t<T, D, BITS, 4, 2>(p, stream);
     if (pl.nslot == 3) return launch_decode_t<T, D, BITS, 4, 3>(p, stream);
@@ -798,34 +948,16 @@ static hipError_t launch_decode_shape(const DecParams& p, const DecPlan& pl, hip
   }
 }
 
-hipError_t launch_decode(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v, const int32_t* seq_lens,
-                         const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int bits, int dtype,
-                         float scale, int causal, int window, void* workspace, hipStream_t stream) {
-  const DecPlan pl = decode_plan(B, Hq, Hkv, L, D, S, window, bits);
+// Everything but the K/V operands.
+static DecParams decode_params(const kvq_rows* q, const int32_t* seq_lens, const kvq_rows* out, int Hq, int Hkv,
+                               int L, int D, int S, float scale, int causal, int window, void* workspace,
+                               const DecPlan& pl) {
   const DecLayout lay = decode_layout(pl, D);
-  DecParams p;
+  DecParams p{};
   p.q = (const uint16_t*)q->data;
   p.q_sb = q->stride_b;
   p.q_sh = q->stride_h;
   p.q_sl = q->stride_l;
-  p.kc = (const uint8_t*)k->codes;
-  p.vc = (const uint8_t*)v->codes;
-  p.kc_sb = k->codes_stride_b * 4;
-  p.kc_sh = k->codes_stride_h * 4;
-  p.kc_ss = k->codes_stride_s * 4;
-  p.vc_sb = v->codes_stride_b * 4;
-  p.vc_sh = v->codes_stride_h * 4;
-  p.vc_ss = v->codes_stride_s * 4;
-  p.ks = (const uint16_t*)k->scales;
-  p.kb = (const uint16_t*)k->biases;
-  p.vs = (const uint16_t*)v->scales;
-  p.vb = (const uint16_t*)v->biases;
-  p.ksb_sb = k->sb_stride_b;
-  p.ksb_sh = k->sb_stride_h;
-  p.ksb_ss = k->sb_stride_s;
-  p.vsb_sb = v->sb_stride_b;
-  p.vsb_sh = v->sb_stride_h;
-  p.vsb_ss = v->sb_stride_s;
   p.seq_lens = seq_lens;
   p.out = (uint16_t*)out->data;
   p.o_sb = out->stride_b;
@@ -849,6 +981,32 @@ hipError_t launch_decode(const kvq_rows* q, const kvq_qtensor* k, const kvq_qten
   p.scale_log2 = scale * 1.4426950408889634f;
   p.causal = causal;
   p.window = window;
+  return p;
+}
+
+hipError_t launch_decode(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v, const int32_t* seq_lens,
+                         const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int bits, int dtype,
+                         float scale, int causal, int window, void* workspace, hipStream_t stream) {
+  const DecPlan pl = decode_plan(B, Hq, Hkv, L, D, S, window, bits);
+  DecParams p = decode_params(q, seq_lens, out, Hq, Hkv, L, D, S, scale, causal, window, workspace, pl);
+  p.kc = (const uint8_t*)k->codes;
+  p.vc = (const uint8_t*)v->codes;
+  p.kc_sb = k->codes_stride_b * 4;
+  p.kc_sh = k->codes_stride_h * 4;
+  p.kc_ss = k->codes_stride_s * 4;
+  p.vc_sb = v->codes_stride_b * 4;
+  p.vc_sh = v->codes_stride_h * 4;
+  p.vc_ss = v->codes_stride_s * 4;
+  p.ks = (const uint16_t*)k->scales;
+  p.kb = (const uint16_t*)k->biases;
+  p.vs = (const uint16_t*)v->scales;
+  p.vb = (const uint16_t*)v->biases;
+  p.ksb_sb = k->sb_stride_b;
+  p.ksb_sh = k->sb_stride_h;
+  p.ksb_ss = k->sb_stride_s;
+  p.vsb_sb = v->sb_stride_b;
+  p.vsb_sh = v->sb_stride_h;
+  p.vsb_ss = v->sb_stride_s;
   const bool bf = dtype == KVQ_DTYPE_BF16;
 #define KVQ_DEC(TT, DD, BB) return launch_decode_shape<TT, DD, BB>(p, pl, stream)
   if (D == 128) {
@@ -859,6 +1017,24 @@ hipError_t launch_decode(const kvq_rows* q, const kvq_qtensor* k, const kvq_qten
     else { if (bf) KVQ_DEC(BF16, 64, 4); else KVQ_DEC(F16, 64, 4); }
   }
 #undef KVQ_DEC
+}
+
+hipError_t launch_decode_dense(const kvq_rows* q, const kvq_rows* k, const kvq_rows* v, const int32_t* seq_lens,
+                               const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int dtype, float scale,
+                               int causal, int window, void* workspace, hipStream_t stream) {
+  const DecPlan pl = decode_plan(B, Hq, Hkv, L, D, S, window, 16);
+  DecParams p = decode_params(q, seq_lens, out, Hq, Hkv, L, D, S, scale, causal, window, workspace, pl);
+  p.kc = (const uint8_t*)k->data;
+  p.vc = (const uint8_t*)v->data;
+  p.kc_sb = k->stride_b * 2;
+  p.kc_sh = k->stride_h * 2;
+  p.kc_ss = k->stride_l * 2;
+  p.vc_sb = v->stride_b * 2;
+  p.vc_sh = v->stride_h * 2;
+  p.vc_ss = v->stride_l * 2;
+  const bool bf = dtype == KVQ_DTYPE_BF16;
+  if (D == 128) return bf ? launch_decode_shape<BF16, 128, 16>(p, pl, stream) : launch_decode_shape<F16, 128, 16>(p, pl, stream);
+  return bf ? launch_decode_shape<BF16, 64, 16>(p, pl, stream) : launch_decode_shape<F16, 64, 16>(p, pl, stream);
 }
 
 }  // namespace kvq

@@ -19,9 +19,16 @@ hipError_t launch_decode(const kvq_rows* q, const kvq_qtensor* k, const kvq_qten
                          const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int bits, int dtype,
                          float scale, int causal, int window, void* workspace, hipStream_t stream);
 
+hipError_t launch_decode_dense(const kvq_rows* q, const kvq_rows* k, const kvq_rows* v, const int32_t* seq_lens,
+                               const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int dtype, float scale,
+                               int causal, int window, void* workspace, hipStream_t stream);
+
 size_t prefill_workspace_bytes(int B, int Hq, int Hkv, int L, int D, int S, int window, int bits);
 hipError_t launch_prefill(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v, const int32_t* seq_lens,
                           const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int bits, int dtype,
                           float scale, int causal, int window, void* workspace, hipStream_t stream);
+hipError_t launch_prefill_dense(const kvq_rows* q, const kvq_rows* k, const kvq_rows* v, const int32_t* seq_lens,
+                                const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int dtype,
+                                float scale, int causal, int window, void* workspace, hipStream_t stream);
 
 }  // namespace kvq

@@ -30,6 +30,8 @@
 
 #include <math.h>
 
+#include <type_traits>
+
 #include "common.h"
 #include "launch.h"
 #include "merge.h"
@@ -49,16 +51,18 @@ constexpr int kRawSlots = 3;
 // code rows with their 16-byte chunks XOR-swizzled by row (chunk c of row r at position
 // c ^ (r % CPR)), each scale/bias array as 128 4-byte cells (cell 2 key + g holds group g of the
 // key in its low half).
+// BITS == 16 is the unquantized cache: raw T rows, no scales or biases.
 template <int BITS>
 struct RawCfg {
+  static constexpr bool DENSE = BITS == 16;
   static constexpr int ROWB = 128 * BITS / 8;       // code bytes per key row
   static constexpr int CPR = ROWB / 16;             // 16-byte chunks per row
   static constexpr int RPI = 64 / CPR;              // rows per 1 KiB DMA instruction
   static constexpr int CI = kPT / RPI;              // DMA instructions per K (or V) code tile
   static constexpr int KB = kPT * ROWB;             // bytes of a K (or V) code tile
-  static constexpr int SLOT = 2 * KB + 4 * 512;
+  static constexpr int SLOT = 2 * KB + (DENSE ? 0 : 4 * 512);
   static constexpr int CPW = 2 * CI / kPW;          // code DMA instructions per wave
-  static constexpr int IPT = CPW + 1;               // DMA instructions per wave per tile
+  static constexpr int IPT = CPW + (DENSE ? 0 : 1);  // DMA instructions per wave per tile
   static_assert(CPW * kPW == 2 * CI, "code DMAs divide evenly over the waves");
 };
 
@@ -99,19 +103,19 @@ __device__ __forceinline__ int v_slot_key(int slot) {
 // wait for them before the kernel's LDS accesses; the tile ring orders every slot with explicit
 // vmcnt waits and barriers. M0 (the LDS base of the wave's 64 lanes) is saved and restored around
 // the load. Lane i's 16 bytes (2 bytes, in the low half of a 4-byte cell) land at lds + 16 i
-// (lds + 4 i).
+// (lds + 4 i). `lds` and `so` are wave-uniform; readfirstlane states it to the compiler.
 __device__ __forceinline__ void dma_b128(__amdgpu_buffer_rsrc_t r, uint32_t lds, uint32_t vo, uint32_t so) {
   uint32_t m0;
   asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\tbuffer_load_dwordx4 %2, %3, %4 offen lds\n\ts_mov_b32 m0, %0"
                : "=&s"(m0)
-               : "s"(lds), "v"(vo), "s"(r), "s"(so)
+               : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(vo), "s"(r), "s"(__builtin_amdgcn_readfirstlane(so))
                : "memory");
 }
 __device__ __forceinline__ void dma_b16(__amdgpu_buffer_rsrc_t r, uint32_t lds, uint32_t vo, uint32_t so) {
   uint32_t m0;
   asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\tbuffer_load_ushort %2, %3, %4 offen lds\n\ts_mov_b32 m0, %0"
                : "=&s"(m0)
-               : "s"(lds), "v"(vo), "s"(r), "s"(so)
+               : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(vo), "s"(r), "s"(__builtin_amdgcn_readfirstlane(so))
                : "memory");
 }
 // s_waitcnt vmcnt(N), other counters left alone.
@@ -149,7 +153,7 @@ struct RawShare {
     }
     const int a = wave >> 1, cell = 64 * (wave & 1) + lane;
     sb_r = a == 0 ? sr[0] : a == 1 ? sr[1] : a == 2 ? sr[2] : sr[3];
-    sb_ss = 2 * (a < 2 ? p.ksb_ss : p.vsb_ss);
+    sb_ss = C::DENSE ? 0 : 2 * (a < 2 ? p.ksb_ss : p.vsb_ss);
     sb_vo = (uint32_t)((cell >> 1) * sb_ss + 2 * (cell & 1));
     sb_lds = 2 * C::KB + 512 * a + 256 * (wave & 1);
   }
@@ -157,7 +161,7 @@ struct RawShare {
   __device__ __forceinline__ void issue(uint32_t slot, int k0) const {
 #pragma unroll
     for (int j = 0; j < C::CPW; ++j) dma_b128(code_r[j], slot + code_lds[j], code_vo[j], (uint32_t)(k0 * code_ss[j]));
-    dma_b16(sb_r, slot + sb_lds, sb_vo, (uint32_t)(k0 * sb_ss));
+    if constexpr (!C::DENSE) dma_b16(sb_r, slot + sb_lds, sb_vo, (uint32_t)(k0 * sb_ss));
   }
 };
 
@@ -255,10 +259,34 @@ __device__ __forceinline__ void stage_from_raw(const uint8_t* raw, _Float16* kld
   }
 }
 
+// Unquantized cache: build half of V^T from the raw V rows of a tile (phase 0: slots 0-31, phase
+// 1: slots 32-63). Thread t (0..255) takes slot chunk c8 = 4 phase + t % 4 and dims 2 (t / 4),
+// 2 (t / 4) + 1: 8 keys x 2 dims read as 32-bit words, written as two 8-slot V^T rows.
+__device__ __forceinline__ void stage_v_raw(const uint8_t* raw, _Float16* vlds, int t, int phase) {
+  constexpr int ROWB = RawCfg<16>::ROWB, CPR = RawCfg<16>::CPR;
+  const int c8 = 4 * phase + (t & 3), d2 = t >> 2;
+  const uint8_t* vr = raw + RawCfg<16>::KB;
+  uint32_t w[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int key = v_slot_key(8 * c8 + i);
+    w[i] = *(const uint32_t*)(vr + key * ROWB + 16 * ((d2 >> 2) ^ (key % CPR)) + 4 * (d2 & 3));
+  }
+  u4 lo, hi;
+#pragma unroll
+  for (int a = 0; a < 4; ++a) {
+    lo[a] = perm(w[2 * a + 1], w[2 * a], 0x05040100u);
+    hi[a] = perm(w[2 * a + 1], w[2 * a], 0x07060302u);
+  }
+  *(u4*)&vlds[(2 * d2) * kVS + 8 * c8] = lo;
+  *(u4*)&vlds[(2 * d2 + 1) * kVS + 8 * c8] = hi;
+}
+
 template <typename T, int BITS>
 __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) {
   using RC = RawCfg<BITS>;
-  __shared__ __align__(16) _Float16 k_lds[2][kPT * kKS];
+  constexpr bool DENSE = RC::DENSE;  // unquantized cache: K operands are read from the raw ring
+  __shared__ __align__(16) _Float16 k_lds[DENSE ? 1 : 2][DENSE ? 8 : kPT * kKS];
   __shared__ __align__(16) _Float16 v_lds[2][128 * kVS];
   __shared__ __align__(16) uint8_t raw[kRawSlots][RC::SLOT];
   __shared__ unsigned s_arrived;
@@ -320,22 +348,36 @@ __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) 
     const int64_t ko = (int64_t)b * p.ksb_sb + (int64_t)kvh * p.ksb_sh;
     const int64_t vo = (int64_t)b * p.vsb_sb + (int64_t)kvh * p.vsb_sh;
     const uint32_t kn = (uint32_t)((int64_t)S_b * p.ksb_ss * 2), vn = (uint32_t)((int64_t)S_b * p.vsb_ss * 2);
-    const __amdgpu_buffer_rsrc_t sr[4] = {make_rsrc(p.ks + ko, kn), make_rsrc(p.kb + ko, kn), make_rsrc(p.vs + vo, vn),
-                                          make_rsrc(p.vb + vo, vn)};
+    __amdgpu_buffer_rsrc_t sr[4] = {kr, kr, kr, kr};
+    if constexpr (!DENSE) {
+      sr[0] = make_rsrc(p.ks + ko, kn);
+      sr[1] = make_rsrc(p.kb + ko, kn);
+      sr[2] = make_rsrc(p.vs + vo, vn);
+      sr[3] = make_rsrc(p.vb + vo, vn);
+    }
     share.init(p, kr, vr, sr, wave, lane);
   }
   const uint32_t raw_lds = lds_addr(&raw[0][0]);
   const int last = max(ntile - 1, 0);
   auto issue_raw = [&](int i) { share.issue(raw_lds + (i % kRawSlots) * RC::SLOT, k_begin + kPT * min(i, last)); };
+  // Quantized cache: the ring runs three tiles ahead (tile t + 3 is issued into the slot of tile t,
+  // which was dequantized in the previous step). Unquantized cache: K is read from the ring while
+  // tile t is computed, so tile t + 2 is issued into the slot of tile t - 1 and lands within the step.
   if (ntile > 0) {
 #pragma unroll
-    for (int j = 0; j < kRawSlots; ++j) issue_raw(j);
+    for (int j = 0; j < (DENSE ? 2 : kRawSlots); ++j) issue_raw(j);
   }
 
-  // ---- Q^T operand: k-step j holds dims 16j + 8hh .. +7, times scale*log2(e)*2^qe in fp16
-  h8 qop[8];
+  // ---- Q^T operand: k-step j holds dims 16j + 8hh .. +7. Quantized cache: times
+  // scale*log2(e)*2^qe in fp16, the scores corrected by inv2 = 2^-qe. Unquantized cache: the raw
+  // query (exact), the scores multiplied by scale*log2(e) in fp32.
+  u4 qop[8];
   float inv2;
-  {
+  if constexpr (DENSE) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) qop[j] = row_ok ? qraw[j] : u4{0, 0, 0, 0};
+    inv2 = 1.0f;
+  } else {
     float qv[8][8];
     float qmax = 0.0f;
 #pragma unroll
@@ -357,46 +399,82 @@ __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) 
 #pragma unroll
     for (int j = 0; j < 8; ++j)
 #pragma unroll
-      for (int i = 0; i < 8; ++i) qop[j][i] = (_Float16)(qv[j][i] * qmul);
+      for (int i = 0; i < 4; ++i) qop[j][i] = pack_f16x2(qv[j][2 * i] * qmul, qv[j][2 * i + 1] * qmul);
   }
+  // MFMA operand type: bf16 for an unquantized bf16 cache, else fp16
+  using OT = typename std::conditional<DENSE && T::id == KVQ_DTYPE_BF16, BF16, F16>::type;
 
   float m_run = -INFINITY, l_run = 0.0f;
   f16v oacc[4];
 #pragma unroll
   for (int db = 0; db < 4; ++db) oacc[db] = f16v{};
 
-  // ---- prologue: tile 0 dequantized, tile 1 landed
+  // ---- prologue: tile 0 staged, tile 1 landed
   if (ntile > 0) {
-    wait_vm<2 * RC::IPT>();
-    __syncthreads();
-    stage_from_raw<T, BITS>(raw[0], k_lds[0], v_lds[0], tid);
-    wait_vm<RC::IPT>();
-    __syncthreads();
+    if constexpr (DENSE) {
+      wait_vm<0>();
+      __syncthreads();
+      stage_v_raw(raw[0], v_lds[0], tid & 255, tid >> 8);
+      __syncthreads();
+    } else {
+      wait_vm<2 * RC::IPT>();
+      __syncthreads();
+      stage_from_raw<T, BITS>(raw[0], k_lds[0], v_lds[0], tid);
+      wait_vm<RC::IPT>();
+      __syncthreads();
+    }
   }
+
+  // this lane's K operand bytes within a raw slot (unquantized cache): key row 32 (i & 1) + qc,
+  // 16-byte chunk 2 (i >> 1) + hh at its swizzled position
+  const int kswz = qc % RawCfg<16>::CPR;
 
   for (int t = 0; t < ntile; ++t) {
     const int cur = t & 1;
     const int k0 = k_begin + kPT * t;
-    issue_raw(t + kRawSlots);  // into the slot of tile t, dequantized before the last barrier
-    // waves 4-7 (K) dequantize tile t + 1 before their MFMAs, waves 0-3 (V) after theirs: the two
-    // waves that share a SIMD (w and w + 4) are in opposite phases, one on the MFMA pipe while
-    // the other is on the VALU
-    if (t + 1 < ntile && wave >= kPW / 2)
-      stage_from_raw<T, BITS>(raw[(t + 1) % kRawSlots], k_lds[cur ^ 1], v_lds[cur ^ 1], tid);
+    if constexpr (DENSE) {
+      if (t + 2 < ntile) issue_raw(t + 2);
+    } else {
+      issue_raw(t + kRawSlots);  // into the slot of tile t, dequantized before the last barrier
+    }
+    // waves 4-7 stage tile t + 1 before their MFMAs, waves 0-3 after theirs: the two waves that
+    // share a SIMD (w and w + 4) are in opposite phases, one on the MFMA pipe while the other is on
+    // the VALU (quantized cache: 4-7 dequantize K, 0-3 V; unquantized: each half of V^T)
+    if (t + 1 < ntile && wave >= kPW / 2) {
+      if constexpr (DENSE) {
+        stage_v_raw(raw[(t + 1) % kRawSlots], v_lds[cur ^ 1], tid - 256, 0);
+      } else {
+        stage_from_raw<T, BITS>(raw[(t + 1) % kRawSlots], k_lds[cur ^ 1], v_lds[cur ^ 1], tid);
+      }
+    }
 
     // S^T = K Q^T for the two 32-key blocks of the tile (scores in log2 units times 2^qe)
     // the 16 K operands stream through a 4-deep register ring, so each MFMA's LDS read was issued
     // four MFMAs earlier; the two 32-key blocks alternate
     f16v sacc[2] = {f16v{}, f16v{}};
     {
-      const _Float16* kl = &k_lds[cur][qc * kKS + 8 * hh];
-      auto kop = [&](int i) { return *(const h8*)(kl + (i & 1) * 32 * kKS + 16 * (i >> 1)); };
-      h8 ring[4] = {kop(0), kop(1), kop(2), kop(3)};
+      const _Float16* kl = &k_lds[0][0];
+      const uint8_t* kraw = raw[t % kRawSlots] + qc * RawCfg<16>::ROWB;
+      if constexpr (!DENSE) kl = &k_lds[cur][qc * kKS + 8 * hh];
+      auto kop = [&](int i) -> u4 {
+        if constexpr (DENSE) {
+          return *(const u4*)(kraw + (i & 1) * 32 * RawCfg<16>::ROWB + 16 * ((2 * (i >> 1) + hh) ^ kswz));
+        } else {
+          return *(const u4*)(kl + (i & 1) * 32 * kKS + 16 * (i >> 1));
+        }
+      };
+      u4 ring[4] = {kop(0), kop(1), kop(2), kop(3)};
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        sacc[i & 1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ring[i & 3], qop[i >> 1], sacc[i & 1], 0, 0, 0);
+        sacc[i & 1] = mfma_32x32x16(ring[i & 3], qop[i >> 1], sacc[i & 1], OT{});
         if (i + 4 < 16) ring[i & 3] = kop(i + 4);
       }
+    }
+    if constexpr (DENSE) {
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) sacc[kb][i] *= p.scale_log2;
     }
     // this lane's query sees keys k0 + 32kb + 8(i/4) + 4hh + i%4
     const bool need_mask = !(k0 >= lo_all && k0 + kPT <= hi_all);
@@ -425,38 +503,50 @@ __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) 
         for (int i = 0; i < 16; ++i) oacc[db][i] *= corr;
       m_run = m_new;
     }
-    // p = 2^(acc * 2^-qe - m): rounded to fp16 it is the B operand of O^T = V^T P^T; the row sum
-    // is kept in fp32
+    // p = 2^(acc * inv2 - m): rounded to the operand type it is the B operand of O^T = V^T P^T;
+    // the row sum is kept in fp32 (of the rounded values for bf16 operands, so the output stays a
+    // convex combination of V rows)
     const float nm = m_run == -INFINITY ? 0.0f : -m_run;
-    h8 pop[4];
+    u4 pop[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      u4 w;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const float p0 = exp2_fast(fmaf(sacc[j >> 1][8 * (j & 1) + 2 * e], inv2, nm));
-        const float p1 = exp2_fast(fmaf(sacc[j >> 1][8 * (j & 1) + 2 * e + 1], inv2, nm));
-        w[e] = pack_f16x2(p0, p1);
+        float p0 = exp2_fast(fmaf(sacc[j >> 1][8 * (j & 1) + 2 * e], inv2, nm));
+        float p1 = exp2_fast(fmaf(sacc[j >> 1][8 * (j & 1) + 2 * e + 1], inv2, nm));
+        if constexpr (OT::id == KVQ_DTYPE_BF16) {
+          pop[j][e] = pack_bf16x2(p0, p1);
+        } else {
+          pop[j][e] = pack_f16x2(p0, p1);
+        }
         l_run += p0 + p1;
       }
-      pop[j] = __builtin_bit_cast(h8, w);
     }
     // O^T += V^T P^T
     {
       // the 16 V^T operands stream through a 4-deep register ring; the 4 dim blocks alternate
       const _Float16* vl = &v_lds[cur][qc * kVS + 8 * hh];
-      auto vop = [&](int i) { return *(const h8*)(vl + (i & 3) * 32 * kVS + 16 * (i >> 2)); };
-      h8 ring[4] = {vop(0), vop(1), vop(2), vop(3)};
+      auto vop = [&](int i) { return *(const u4*)(vl + (i & 3) * 32 * kVS + 16 * (i >> 2)); };
+      u4 ring[4] = {vop(0), vop(1), vop(2), vop(3)};
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        oacc[i & 3] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ring[i & 3], pop[i >> 2], oacc[i & 3], 0, 0, 0);
+        oacc[i & 3] = mfma_32x32x16(ring[i & 3], pop[i >> 2], oacc[i & 3], OT{});
         if (i + 4 < 16) ring[i & 3] = vop(i + 4);
       }
     }
 
-    if (t + 1 < ntile && wave < kPW / 2)
-      stage_from_raw<T, BITS>(raw[(t + 1) % kRawSlots], k_lds[cur ^ 1], v_lds[cur ^ 1], tid);
-    wait_vm<RC::IPT>();  // tile t + 2 has landed (tile t + 3 may be in flight)
+    if (t + 1 < ntile && wave < kPW / 2) {
+      if constexpr (DENSE) {
+        stage_v_raw(raw[(t + 1) % kRawSlots], v_lds[cur ^ 1], tid, 1);
+      } else {
+        stage_from_raw<T, BITS>(raw[(t + 1) % kRawSlots], k_lds[cur ^ 1], v_lds[cur ^ 1], tid);
+      }
+    }
+    if constexpr (DENSE) {
+      wait_vm<0>();  // tile t + 2 has landed
+    } else {
+      wait_vm<RC::IPT>();  // tile t + 2 has landed (tile t + 3 may be in flight)
+    }
     __syncthreads();
   }
   wait_vm<0>();  // no load into this workgroup's LDS outlives it
@@ -499,27 +589,38 @@ __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) 
       const float2 ml = load_agent_b64(rm, row_ml, s2 * (kPRows * 8));
       if (ml.y > 0.0f) M = fmaxf(M, ml.x);
     }
+    // the splits are summed in split order, each term one explicit fma, whichever of them merges:
+    // the result is bit-reproducible from call to call
     const float w_own = (M == -INFINITY || l_tot <= 0.0f) ? 0.0f : exp2_fast(m_run - M);
-    l_tot *= w_own;
+    f16v macc[4];
 #pragma unroll
-    for (int db = 0; db < 4; ++db)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) oacc[db][i] *= w_own;
+    for (int db = 0; db < 4; ++db) macc[db] = f16v{};
+    float l_acc = 0.0f;
     for (int s2 = 0; s2 < p.nsplit; ++s2) {
-      if (s2 == split) continue;
+      if (s2 == split) {
+        l_acc = fmaf(w_own, l_tot, l_acc);
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) macc[db][i] = fmaf(w_own, oacc[db][i], macc[db][i]);
+        continue;
+      }
       const float2 ml = load_agent_b64(rm, row_ml, s2 * (kPRows * 8));
       f4 po[16];
 #pragma unroll
       for (int u = 0; u < 16; ++u) po[u] = load_agent_b128(ro, lo + u * 1024, s2 * split_o);
       const float w = (M == -INFINITY || ml.y <= 0.0f) ? 0.0f : exp2_fast(ml.x - M);
-      l_tot += w * ml.y;
+      l_acc = fmaf(w, ml.y, l_acc);
 #pragma unroll
       for (int db = 0; db < 4; ++db)
 #pragma unroll
         for (int c = 0; c < 4; ++c)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) oacc[db][4 * c + e] += w * po[4 * db + c][e];
+          for (int e = 0; e < 4; ++e) macc[db][4 * c + e] = fmaf(w, po[4 * db + c][e], macc[db][4 * c + e]);
     }
+    l_tot = l_acc;
+#pragma unroll
+    for (int db = 0; db < 4; ++db) oacc[db] = macc[db];
   }
   if (!row_ok) return;
   const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
@@ -582,33 +683,14 @@ static hipError_t launch_prefill_t(const PreParams& p, hipStream_t stream) {
   return hipGetLastError();
 }
 
-hipError_t launch_prefill(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v, const int32_t* seq_lens,
-                          const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int bits, int dtype,
-                          float scale, int causal, int window, void* workspace, hipStream_t stream) {
-  const PrePlan pl = prefill_plan(B, Hq, Hkv, L, S, window);
-  PreParams p;
+// Everything but the K/V operands.
+static PreParams prefill_params(const kvq_rows* q, const int32_t* seq_lens, const kvq_rows* out, int Hq, int Hkv, int L,
+                                int S, float scale, int causal, int window, void* workspace, const PrePlan& pl) {
+  PreParams p{};
   p.q = (const uint16_t*)q->data;
   p.q_sb = q->stride_b;
   p.q_sh = q->stride_h;
   p.q_sl = q->stride_l;
-  p.kc = (const uint8_t*)k->codes;
-  p.vc = (const uint8_t*)v->codes;
-  p.kc_sb = k->codes_stride_b * 4;
-  p.kc_sh = k->codes_stride_h * 4;
-  p.kc_ss = k->codes_stride_s * 4;
-  p.vc_sb = v->codes_stride_b * 4;
-  p.vc_sh = v->codes_stride_h * 4;
-  p.vc_ss = v->codes_stride_s * 4;
-  p.ks = (const uint16_t*)k->scales;
-  p.kb = (const uint16_t*)k->biases;
-  p.vs = (const uint16_t*)v->scales;
-  p.vb = (const uint16_t*)v->biases;
-  p.ksb_sb = k->sb_stride_b;
-  p.ksb_sh = k->sb_stride_h;
-  p.ksb_ss = k->sb_stride_s;
-  p.vsb_sb = v->sb_stride_b;
-  p.vsb_sh = v->sb_stride_h;
-  p.vsb_ss = v->sb_stride_s;
   p.seq_lens = seq_lens;
   p.out = (uint16_t*)out->data;
   p.o_sb = out->stride_b;
@@ -630,6 +712,32 @@ hipError_t launch_prefill(const kvq_rows* q, const kvq_qtensor* k, const kvq_qte
   p.scale_log2 = scale * 1.4426950408889634f;
   p.causal = causal;
   p.window = window;
+  return p;
+}
+
+hipError_t launch_prefill(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v, const int32_t* seq_lens,
+                          const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int bits, int dtype,
+                          float scale, int causal, int window, void* workspace, hipStream_t stream) {
+  const PrePlan pl = prefill_plan(B, Hq, Hkv, L, S, window);
+  PreParams p = prefill_params(q, seq_lens, out, Hq, Hkv, L, S, scale, causal, window, workspace, pl);
+  p.kc = (const uint8_t*)k->codes;
+  p.vc = (const uint8_t*)v->codes;
+  p.kc_sb = k->codes_stride_b * 4;
+  p.kc_sh = k->codes_stride_h * 4;
+  p.kc_ss = k->codes_stride_s * 4;
+  p.vc_sb = v->codes_stride_b * 4;
+  p.vc_sh = v->codes_stride_h * 4;
+  p.vc_ss = v->codes_stride_s * 4;
+  p.ks = (const uint16_t*)k->scales;
+  p.kb = (const uint16_t*)k->biases;
+  p.vs = (const uint16_t*)v->scales;
+  p.vb = (const uint16_t*)v->biases;
+  p.ksb_sb = k->sb_stride_b;
+  p.ksb_sh = k->sb_stride_h;
+  p.ksb_ss = k->sb_stride_s;
+  p.vsb_sb = v->sb_stride_b;
+  p.vsb_sh = v->sb_stride_h;
+  p.vsb_ss = v->sb_stride_s;
   (void)D;
   if (dtype == KVQ_DTYPE_BF16) {
     if (bits == 8) return launch_prefill_t<BF16, 8>(p, stream);
@@ -637,6 +745,24 @@ hipError_t launch_prefill(const kvq_rows* q, const kvq_qtensor* k, const kvq_qte
   }
   if (bits == 8) return launch_prefill_t<F16, 8>(p, stream);
   return launch_prefill_t<F16, 4>(p, stream);
+}
+
+hipError_t launch_prefill_dense(const kvq_rows* q, const kvq_rows* k, const kvq_rows* v, const int32_t* seq_lens,
+                                const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int dtype,
+                                float scale, int causal, int window, void* workspace, hipStream_t stream) {
+  const PrePlan pl = prefill_plan(B, Hq, Hkv, L, S, window);
+  PreParams p = prefill_params(q, seq_lens, out, Hq, Hkv, L, S, scale, causal, window, workspace, pl);
+  p.kc = (const uint8_t*)k->data;
+  p.vc = (const uint8_t*)v->data;
+  p.kc_sb = k->stride_b * 2;
+  p.kc_sh = k->stride_h * 2;
+  p.kc_ss = k->stride_l * 2;
+  p.vc_sb = v->stride_b * 2;
+  p.vc_sh = v->stride_h * 2;
+  p.vc_ss = v->stride_l * 2;
+  (void)D;
+  if (dtype == KVQ_DTYPE_BF16) return launch_prefill_t<BF16, 16>(p, stream);
+  return launch_prefill_t<F16, 16>(p, stream);
 }
 
 }  // namespace kvq

@@ -158,45 +158,67 @@ class AttentionCall:
     views) is picked up by the next launch. Used by serving loops and HIP-graph capture.
     """
 
-    def __init__(self, fn, args, keep, kernel: str, out: torch.Tensor):
+    def __init__(self, fn, args, keep, kernel: str, out: torch.Tensor, symbol: str):
         self._fn = fn
         self._args = args
         self._keep = keep  # tensors and ctypes structs whose addresses are baked into _args
-        self.kernel = kernel
+        self.kernel = kernel  # "decode" or "prefill"
+        self.symbol = symbol  # the C entry point
         self.out = out
 
     def __call__(self) -> torch.Tensor:
         rc = self._fn(*self._args)
         if rc:
-            _lib.check(rc, f"kvq_{self.kernel}_attn")
+            _lib.check(rc, self.symbol)
         return self.out
 
 
-def prepare_attention(queries: torch.Tensor, keys: Triple, values: Triple, scale: float, *, causal: bool = False,
+def _rows_ok(t: torch.Tensor) -> bool:
+    """Rows the kernels can read directly: unit stride, 16-byte aligned, strides of 8 elements."""
+    return t.stride(-1) == 1 and not any(st % 8 for st in t.stride()[:3]) and t.data_ptr() % 16 == 0
+
+
+def prepare_attention(queries: torch.Tensor, keys, values, scale: float, *, causal: bool = False,
                       window: int = 0, seq_lens: Optional[torch.Tensor] = None, group_size: int = 64,
                       bits: int = 8, out: Optional[torch.Tensor] = None, kernel: str = "auto",
                       workspace: Optional[torch.Tensor] = None) -> AttentionCall:
     """Validate one attention launch and return it as an ``AttentionCall`` (see ``attention``)."""
-    _check_triple(keys, "keys")
-    _check_triple(values, "values")
-    dev = _require_cuda(queries, *keys, *values)
     if queries.dim() != 4:
         raise ValueError(f"queries must be [B, Hq, L, D], got {tuple(queries.shape)}")
     B, Hq, L, D = queries.shape
-    Hkv, S = keys[0].shape[1], keys[0].shape[2]
-    for name, tr in (("keys", keys), ("values", values)):
-        c, s, b = tr
-        if c.shape[0] != B or c.shape[1] != Hkv or c.shape[2] != S or s.shape[:3] != c.shape[:3]:
-            raise ValueError(f"{name} triple shapes {tuple(c.shape)}, {tuple(s.shape)} do not match B={B}, Hkv={Hkv}, S={S}")
-        if c.shape[3] * 32 // bits != D:
-            raise ValueError(f"{name} codes hold {c.shape[3] * 32 // bits} dims at {bits} bits, queries have {D}")
-        if s.shape[3] * group_size != D:
-            raise ValueError(f"{name} scales hold {s.shape[3]} groups, expected D/group_size = {D // group_size}")
-        if s.dtype != queries.dtype:
-            raise ValueError(f"{name} scales are {s.dtype}, queries are {queries.dtype}")
+    dense = torch.is_tensor(keys)
+    if dense:
+        if not torch.is_tensor(values):
+            raise ValueError("keys and values must both be tensors (unquantized) or both be triples")
+        dev = _require_cuda(queries, keys, values)
+        Hkv, S = keys.shape[1], keys.shape[2]
+        for name, t in (("keys", keys), ("values", values)):
+            if t.dim() != 4 or tuple(t.shape) != (B, Hkv, S, D):
+                raise ValueError(f"{name} must be [B, Hkv, S, D] = {(B, Hkv, S, D)}, got {tuple(t.shape)}")
+            if t.dtype != queries.dtype:
+                raise ValueError(f"{name} are {t.dtype}, queries are {queries.dtype}")
+        if not _rows_ok(keys):
+            keys = keys.contiguous()
+        if not _rows_ok(values):
+            values = values.contiguous()
+    else:
+        _check_triple(keys, "keys")
+        _check_triple(values, "values")
+        dev = _require_cuda(queries, *keys, *values)
+        Hkv, S = keys[0].shape[1], keys[0].shape[2]
+        for name, tr in (("keys", keys), ("values", values)):
+            c, s, b = tr
+            if c.shape[0] != B or c.shape[1] != Hkv or c.shape[2] != S or s.shape[:3] != c.shape[:3]:
+                raise ValueError(f"{name} triple shapes {tuple(c.shape)}, {tuple(s.shape)} do not match B={B}, Hkv={Hkv}, S={S}")
+            if c.shape[3] * 32 // bits != D:
+                raise ValueError(f"{name} codes hold {c.shape[3] * 32 // bits} dims at {bits} bits, queries have {D}")
+            if s.shape[3] * group_size != D:
+                raise ValueError(f"{name} scales hold {s.shape[3]} groups, expected D/group_size = {D // group_size}")
+            if s.dtype != queries.dtype:
+                raise ValueError(f"{name} scales are {s.dtype}, queries are {queries.dtype}")
     if Hq % Hkv:
         raise ValueError(f"Hq={Hq} is not a multiple of Hkv={Hkv}")
-    if queries.stride(-1) != 1 or any(st % 8 for st in queries.stride()[:3]) or queries.data_ptr() % 16:
+    if not _rows_ok(queries):
         queries = queries.contiguous()
     if out is None:
         out = torch.empty((B, Hq, L, D), dtype=queries.dtype, device=dev)
@@ -214,7 +236,8 @@ def prepare_attention(queries: torch.Tensor, keys: Triple, values: Triple, scale
         raise ValueError(f"kernel must be 'decode', 'prefill' or 'auto', got {kernel!r}")
     lib = _lib.lib()
     ws_fn = lib.kvq_decode_workspace_size if kernel == "decode" else lib.kvq_prefill_workspace_size
-    fn = lib.kvq_decode_attn if kernel == "decode" else lib.kvq_prefill_attn
+    symbol = f"kvq_{kernel}_attn" + ("_dense" if dense else "")
+    fn = getattr(lib, symbol)
     nbytes = ws_fn(B, Hq, Hkv, L, D, S, int(window))
     if nbytes == 0:
         raise NotImplementedError(f"{kernel} attention does not support B={B} Hq={Hq} Hkv={Hkv} L={L} D={D} S={S}")
@@ -226,20 +249,27 @@ def prepare_attention(queries: torch.Tensor, keys: Triple, values: Triple, scale
             raise ValueError(f"workspace must hold at least {nbytes} bytes on {dev}")
         ws = workspace
     qr, orr = _lib.rows(queries), _lib.rows(out)
-    kq, vq = _lib.qtensor(*keys), _lib.qtensor(*values)
-    args = (ctypes.byref(qr), ctypes.byref(kq), ctypes.byref(vq), sl_ptr, ctypes.byref(orr), B, Hq, Hkv, L, D, S,
-            int(bits), int(group_size), _lib.dtype_code(queries.dtype), float(scale), int(bool(causal)),
-            int(window), ws.data_ptr(), ws.numel() * ws.element_size(), stream)
+    tail = (_lib.dtype_code(queries.dtype), float(scale), int(bool(causal)), int(window), ws.data_ptr(),
+            ws.numel() * ws.element_size(), stream)
+    if dense:
+        kq, vq = _lib.rows(keys), _lib.rows(values)
+        args = (ctypes.byref(qr), ctypes.byref(kq), ctypes.byref(vq), sl_ptr, ctypes.byref(orr), B, Hq, Hkv, L, D, S,
+                *tail)
+    else:
+        kq, vq = _lib.qtensor(*keys), _lib.qtensor(*values)
+        args = (ctypes.byref(qr), ctypes.byref(kq), ctypes.byref(vq), sl_ptr, ctypes.byref(orr), B, Hq, Hkv, L, D, S,
+                int(bits), int(group_size), *tail)
     keep = (queries, keys, values, seq_lens, ws, qr, orr, kq, vq)
-    return AttentionCall(fn, args, keep, kernel, out)
+    return AttentionCall(fn, args, keep, kernel, out, symbol)
 
 
-def attention(queries: torch.Tensor, keys: Triple, values: Triple, scale: float, *, causal: bool = False,
+def attention(queries: torch.Tensor, keys, values, scale: float, *, causal: bool = False,
               window: int = 0, seq_lens: Optional[torch.Tensor] = None, group_size: int = 64, bits: int = 8,
               out: Optional[torch.Tensor] = None, kernel: str = "auto") -> torch.Tensor:
-    """softmax(scale * q K^T + mask) V over a quantized cache. queries [B, Hq, L, D]; keys/values
-    (codes [B, Hkv, S, D*bits/32], scales/biases [B, Hkv, S, D/G]); returns [B, Hq, L, D]
-    (or fills `out`). kernel: "decode", "prefill" or "auto" (decode while the GQA group's query
-    rows fit one MFMA column block, prefill otherwise)."""
+    """softmax(scale * q K^T + mask) V. queries [B, Hq, L, D]; keys/values either quantized triples
+    (codes [B, Hkv, S, D*bits/32], scales/biases [B, Hkv, S, D/G]) or unquantized tensors
+    [B, Hkv, S, D] in the queries' dtype; returns [B, Hq, L, D] (or fills `out`). kernel: "decode",
+    "prefill" or "auto" (decode while the GQA group's query rows fit one MFMA column block,
+    prefill otherwise)."""
     return prepare_attention(queries, keys, values, scale, causal=causal, window=window, seq_lens=seq_lens,
                              group_size=group_size, bits=bits, out=out, kernel=kernel)()

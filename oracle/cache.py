@@ -9,6 +9,12 @@ What the reference relies on (prefix_cache.py:17-38, 77-123; context.py:41-47, 5
   * nbytes is the byte size of the allocated buffers (capacity rows, not offset rows);
   * to_quantized(group_size, bits) quantizes the whole allocated buffer and keeps offset.
 This model tracks (offset, capacity) only; the GPU cache classes must match it step for step.
+
+RotatingCacheModel follows mlx-lm's RotatingKVCache (sliding-window layers; the caches
+m5engine/attention.py:106-112 leaves unquantized and context.py:65-66 sizes by max_size) on token
+positions instead of rows: which position each buffer row holds. Parity with mlx-lm itself is
+unpinned (the module is absent here); tests/test_cache_rotating.py pins the model by the
+properties a sliding-window cache must have.
 """
 
 from __future__ import annotations
@@ -45,3 +51,68 @@ def row_bytes(D: int, bits: int | None, elem_bytes: int = 2, group_size: int = 6
     if not bits:
         return D * elem_bytes
     return D * bits // 8 + 2 * (D // group_size) * elem_bytes
+
+
+class RotatingCacheModel:
+    """Buffer rows as token positions (None = an allocated row never written).
+
+    Single-token updates write in place into a ring of max_size rows whose first `keep` rows are
+    never overwritten, growing the buffer in steps of `step` until it reaches max_size. Multi-token
+    updates first put the buffer in temporal order, keep its first `keep` rows and the newest
+    max_size - 1 - keep others, and append the new tokens, so every new token sees at least
+    max_size - 1 earlier ones (the buffer then holds up to max_size - 1 + L rows).
+    """
+
+    def __init__(self, max_size: int, keep: int = 0, step: int = STEP) -> None:
+        self.max_size, self.keep, self.step = max_size, keep, step
+        self.rows: list | None = None
+        self.offset = 0
+        self.idx = 0
+
+    def _trim(self, n: int, rows: list, append: list | None = None) -> list:
+        out = rows[: self.keep] + rows[n + self.keep:] if n > 0 else list(rows)
+        return out + (append or [])
+
+    def _temporal(self, rows: list) -> list:
+        if self.idx == len(rows):
+            return list(rows)
+        if self.idx < self.offset:
+            return rows[: self.keep] + rows[self.idx:] + rows[self.keep: self.idx]
+        return rows[: self.idx]
+
+    def update(self, L: int) -> list:
+        """Append positions offset .. offset + L - 1; returns the fetched rows (as positions)."""
+        new = list(range(self.offset, self.offset + L))
+        if L > 1:
+            if self.rows is None:
+                self.rows = new
+            else:
+                self.rows = self._temporal(self.rows)
+                self.idx = len(self.rows)
+                self.rows = self._trim(self.idx - self.max_size + 1, self.rows, new)
+            self.offset += L
+            self.idx = len(self.rows)
+            return list(self.rows)
+        prev = self.offset
+        if self.rows is None or (prev >= len(self.rows) and len(self.rows) < self.max_size):
+            grow = min(self.step, self.max_size - prev)
+            self.rows = (self.rows or []) + [None] * grow
+            self.idx = prev
+        extra = len(self.rows) - self.max_size
+        if extra > 0:
+            self.rows = self._trim(extra, self.rows)
+            self.idx = self.max_size
+        if self.idx == self.max_size:
+            self.idx = self.keep
+        self.rows[self.idx] = new[0]
+        self.offset += 1
+        self.idx += 1
+        if self.offset < self.max_size:
+            return self.rows[: self.offset]
+        return list(self.rows)
+
+    def trim(self, n: int) -> int:
+        n = min(self.offset, n)
+        self.offset -= n
+        self.idx -= n
+        return n

@@ -91,3 +91,13 @@ def test_blocked_sdpa_string_mask_routes_to_prefill():
     torch.cuda.synchronize()
     ref = exact_reference(q, kt, vt, 1.0 / math.sqrt(D), bits=8, causal=True)
     assert_close(out, ref, "string-mask")
+
+
+def test_repeated_calls_are_bit_identical():
+    # the key splits are merged in split order whichever workgroup merges them
+    print("prefill repeat", flush=True)
+    kt, vt = make_cache(1, 4, 16384, 128, 8, torch.bfloat16, 81)
+    q = seeded_normal((1, 32, 512, 128), 82, torch.bfloat16, DEV)
+    outs = [kernels.attention(q, kt, vt, 0.088, causal=True, bits=8, kernel="prefill") for _ in range(3)]
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
