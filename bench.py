@@ -27,7 +27,12 @@ Timing:
 Algorithmic bytes of one decode call:
   sum_b S_b * Hkv * 2 * (D*bits/8 + 2*(D/G)*2)   (K and V codes, scales, biases)
   + 2 * B * Hq * D * 2                           (the query in, the output out)
-= 272 B per cached token and KV head at 8 bits, 144 B at 4 bits (D = 128, G = 64).
+= 272 B per cached token and KV head at 8 bits, 144 B at 4 bits (D = 128, G = 64); an
+unquantized cache (the "-dense" extras) reads D*2 bytes per row, 512 B per token and KV head.
+
+The "extra" object also times the other decode configurations and, over unquantized caches, the
+C5 window layer's decode step and prefill chunk and a C3 chunk (attention FLOPs: 4 * D * Hq per
+unmasked query-key pair).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra] [--no-parity]
                        [--no-prefill | --prefill-only] [--calibrate-copy]
@@ -61,7 +66,7 @@ def log(*a):
 def decode_bytes(seq_lens, Hq, Hkv, D, bits, G=64, elem=2, window=0):
     """Algorithmic HBM bytes of one decode call (see the module docstring). With a sliding
     window only the keys the query can see count: min(S_b, window) per sequence."""
-    row = D * bits // 8 + 2 * (D // G) * elem
+    row = D * elem if bits == 16 else D * bits // 8 + 2 * (D // G) * elem  # bits 16: unquantized rows
     keys = sum(min(s, window) if window > 0 else s for s in seq_lens)
     return keys * Hkv * 2 * row + 2 * len(seq_lens) * Hq * D * elem
 
@@ -80,6 +85,10 @@ DECODE = {
                       Hkv=16, D=128, S=8193, bits=8, dtype="bfloat16", seed=1005, causal=True),
     "C5-window": dict(desc="Gemma-3-27B decode step after 8192 prefill, window-1024 layer, batch 4", B=4, Hq=32,
                       Hkv=16, D=128, S=8193, bits=8, dtype="bfloat16", seed=1006, causal=True, window=1024),
+    # the window layer as the reference runs it: a RotatingKVCache of 1024 rows, left unquantized
+    # (m5engine/attention.py:106-112), attention over all of its rows
+    "C5-window-dense": dict(desc="Gemma-3-27B decode step, window-1024 layer on its unquantized rotating cache, "
+                                 "batch 4", B=4, Hq=32, Hkv=16, D=128, S=1024, bits=16, dtype="bfloat16", seed=1007),
 }
 
 
@@ -94,7 +103,8 @@ def seq_lens_of(cfg):
 
 
 def make_cache(cfg, seed, device):
-    """One seeded cache: K/V ~ N(0,1) in T, quantized by the append kernel into MLX-layout triples."""
+    """One seeded cache: K/V ~ N(0,1) in T, quantized by the append kernel into MLX-layout triples
+    (bits 16: left unquantized, two [B, Hkv, S, D] tensors)."""
     import torch
 
     from myinfer_amd import kernels
@@ -102,6 +112,9 @@ def make_cache(cfg, seed, device):
     B, Hkv, S, D, bits = cfg["B"], cfg["Hkv"], cfg["S"], cfg["D"], cfg["bits"]
     T = getattr(torch, cfg["dtype"])
     g = torch.Generator(device=device).manual_seed(seed)
+    if bits == 16:
+        return tuple(torch.randn((B, Hkv, S, D), generator=g, device=device, dtype=torch.float32).to(T)
+                     for _ in range(2))
     trip = []
     for which in ("k", "v"):
         x = torch.randn((B, Hkv, S, D), generator=g, device=device, dtype=torch.float32)
@@ -384,6 +397,64 @@ def time_prefill(cfg, steps, warmup, device, want_parity=False):
     return res
 
 
+def time_attention_shape(desc, q, k, v, scale, flops, steps, device, **mask):
+    """Attention-kernel TFLOP/s of one call shape over an unquantized cache: `steps` calls captured
+    in a HIP graph and replayed once, timed with events."""
+    import torch
+
+    from myinfer_amd import kernels
+
+    out = torch.empty_like(q)
+    log(f"[bench] {desc}: {flops / 1e12:.4f} TFLOP per call")
+    kernels.prepare_attention(q, k, v, scale, out=out, kernel="prefill", **mask)()
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        call = kernels.prepare_attention(q, k, v, scale, out=out, kernel="prefill", **mask)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        for _ in range(steps):
+            call()
+    graph.replay()
+    torch.cuda.synchronize()
+    s_, e_ = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s_.record()
+    graph.replay()
+    e_.record()
+    torch.cuda.synchronize()
+    ms = s_.elapsed_time(e_) / steps
+    del graph
+    return {"tflops": round(flops / (ms * 1e-3) / 1e12, 2), "frac": round(flops / (ms * 1e-3) / 1e12 / PEAK_MFMA_TFLOPS, 4),
+            "us_per_call": round(ms * 1e3, 2), "flops": flops}
+
+
+def dense_prefill_extras(steps, device):
+    """Prefill over unquantized caches: the C5 window layer's steady-state 2048-row chunk (its
+    rotating cache returns 1023 earlier rows + the chunk; every query sees 1024 keys), and the last
+    C3 chunk over an unquantized cache (the plain cache before quantized_kv_start)."""
+    import torch
+
+    g = torch.Generator(device=device).manual_seed(1008)
+    res = {}
+    B, Hq, Hkv, D, W, C = 4, 32, 16, 128, 1024, 2048
+    T = torch.bfloat16
+    q = torch.randn((B, Hq, C, D), generator=g, device=device).to(T)
+    k = torch.randn((B, Hkv, W - 1 + C, D), generator=g, device=device).to(T)
+    v = torch.randn((B, Hkv, W - 1 + C, D), generator=g, device=device).to(T)
+    res["C5-window-prefill-dense"] = time_attention_shape(
+        "C5 window-layer prefill chunk, unquantized bf16 (B=4, 2048 queries, window 1024)", q, k, v,
+        1.0 / math.sqrt(D), 4 * D * Hq * B * C * W, steps, device, causal=True, window=W)
+    B, Hq, Hkv, N, C = 1, 32, 4, 16384, 512
+    q = torch.randn((B, Hq, C, D), generator=g, device=device).to(T)
+    k = torch.randn((B, Hkv, N, D), generator=g, device=device).to(T)
+    v = torch.randn((B, Hkv, N, D), generator=g, device=device).to(T)
+    res["C3-last-chunk-dense"] = time_attention_shape(
+        "C3 last chunk over an unquantized bf16 cache (512 queries, 16384 keys, causal)", q, k, v,
+        1.0 / math.sqrt(D), prefill_flops(N, Hq, D, N - C, N), steps, device, causal=True)
+    return res
+
+
 def prefill_parity(cfg, q, out, kt, vt, scale, c):
     """Chunk c's output (as left by the timed steps) against the exact fp64 oracle."""
     import numpy as np
@@ -537,13 +608,17 @@ def main():
         f"per call {res['call_us_mean']:.2f} us mean -> {res['kernel_gbs']:.1f} GB/s")
     extra = {}
     if not args.no_extra:
-        for name in ("C1", "C2-b8", "C4", "C5-global", "C5-window"):
+        for name in ("C1", "C2-b8", "C4", "C5-global", "C5-window", "C5-window-dense"):
             r = time_decode(DECODE[name], args.steps, args.warmup, device)
             extra[name] = {"gbs": round(r["gbs"], 1), "frac": round(r["gbs"] / PEAK_HBM_GBS, 4),
                            "us_per_step": round(r["ms_per_step"] * 1e3, 3), "bytes": r["bytes"],
                            "kernel_us": round(r["call_us_mean"], 3)}
             log(f"[bench] {name}: {r['gbs']:.1f} GB/s ({r['ms_per_step'] * 1e3:.2f} us/step)")
             torch.cuda.empty_cache()
+        for name, r in dense_prefill_extras(min(args.steps, 20), device).items():
+            extra[name] = r
+            log(f"[bench] {name}: {r['tflops']:.1f} TFLOP/s ({r['us_per_call']:.1f} us/call)")
+        torch.cuda.empty_cache()
 
     cpu = None
     if not args.no_cpu:
