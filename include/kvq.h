@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define KVQ_ABI_VERSION 3
+#define KVQ_ABI_VERSION 4
 
 /* Element types of queries, K/V rows, outputs, scales and biases. */
 #define KVQ_DTYPE_F16 0
@@ -53,6 +53,7 @@ extern "C" {
 #define KVQ_ERR_UNSUPPORTED (-2) /* well-formed but not built: head_dim, group size, head ratio */
 #define KVQ_ERR_WORKSPACE (-3)   /* workspace missing or smaller than *_workspace_size()       */
 #define KVQ_ERR_HIP (-4)         /* the HIP runtime reported an error at launch                */
+#define KVQ_ERR_CAPACITY (-5)    /* the page pool cannot hold the request                      */
 
 /* A strided T[B][H][L][D] array (D contiguous). */
 typedef struct kvq_rows {
@@ -182,6 +183,80 @@ int kvq_prefill_attn_dense(const kvq_rows* q, const kvq_rows* k, const kvq_rows*
                            int B, int Hq, int Hkv, int L, int D, int S, int dtype,
                            float scale, int causal, int window,
                            void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * ---- Paged layout ----
+ * A paged pool holds one layer's K (or V) for many sequences in pages of KVQ_PAGE_ROWS rows:
+ * codes u32 [num_pages][H][KVQ_PAGE_ROWS][D*bits/32], scales/biases T [num_pages][H][KVQ_PAGE_ROWS][D/G]
+ * (head-major within a page), described by a kvq_qtensor whose batch strides are page strides.
+ * Row r of sequence b lives in page block_table[b * table_stride + r / KVQ_PAGE_ROWS], at row
+ * r % KVQ_PAGE_ROWS. Table entries are clamped to [0, num_pages) on the device.
+ * Replaces: the reference's paged KV layout (native/src/kv_cache.cpp:8-27, 16-token blocks read
+ * through a block table in native/src/kernels.metal:106-160, 384-450), here for the quantized MLX
+ * cache, as the alternative to whole-cache move-reuse (m5engine/prefix_cache.py:1-5). Pages are
+ * 64 rows so that a prefill tile (64 keys) reads one page and a decode tile (32 keys) half of one.
+ */
+#define KVQ_PAGE_ROWS 64
+
+/*
+ * kvq_quantize_append into a paged pool: row l of sequence b goes to row starts[b] + l (starts: a
+ * device int32 [B], or NULL for row_offset + l for every sequence). With `rope` the keys are
+ * rotated first, row l of sequence b at position rope->offset + (starts ? starts[b] : 0) + l.
+ * Rows whose page index is at or past table_stride are dropped.
+ */
+int kvq_paged_quantize_append(const kvq_rows* k_src, const kvq_qtensor* k_pool,
+                              const kvq_rows* v_src, const kvq_qtensor* v_pool, int num_pages,
+                              const int32_t* block_table, int64_t table_stride, const int32_t* starts,
+                              int64_t row_offset, const kvq_rope_params* rope,
+                              int B, int H, int L, int D, int bits, int group_size, int dtype, void* stream);
+
+/*
+ * kvq_decode_attn / kvq_prefill_attn over paged pools (same arguments, masks, workspace sizes and
+ * outputs; S is the longest sequence, table_stride >= ceil(S / KVQ_PAGE_ROWS)). The results are
+ * bit-identical to the contiguous entry points over the same rows.
+ */
+int kvq_paged_decode_attn(const kvq_rows* q, const kvq_qtensor* k_pool, const kvq_qtensor* v_pool,
+                          int num_pages, const int32_t* block_table, int64_t table_stride,
+                          const int32_t* seq_lens, const kvq_rows* out,
+                          int B, int Hq, int Hkv, int L, int D, int S, int bits, int group_size, int dtype,
+                          float scale, int causal, int window,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
+int kvq_paged_prefill_attn(const kvq_rows* q, const kvq_qtensor* k_pool, const kvq_qtensor* v_pool,
+                           int num_pages, const int32_t* block_table, int64_t table_stride,
+                           const int32_t* seq_lens, const kvq_rows* out,
+                           int B, int Hq, int Hkv, int L, int D, int S, int bits, int group_size, int dtype,
+                           float scale, int causal, int window,
+                           void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Radix prefix cache over a page pool (host memory and host code only; no HIP calls).
+ * Replaces: PagedRadixKVCache (native/include/kv_cache.hpp, native/src/kv_cache.cpp:73-157):
+ * match_and_allocate / commit_prefix_blocks / clear_cache, with page reference counts added:
+ * pages returned by match_and_allocate are held until kvq_radix_release, and held pages are
+ * never evicted. Not thread-safe: one radix per thread, or a lock around it.
+ */
+typedef struct kvq_radix kvq_radix;
+typedef struct kvq_radix_info {
+  int num_pages, page_tokens, cached_pages, free_pages, in_use_pages;
+  int64_t prefix_hit_tokens, prompt_tokens;
+} kvq_radix_info;
+
+kvq_radix* kvq_radix_create(int num_pages, int page_tokens);  /* NULL on bad sizes */
+void kvq_radix_destroy(kvq_radix* r);
+/* Match the longest cached prefix of whole pages (leaving the last prompt token unmatched) and
+ * allocate pages for the rest of n_tokens + max_new_tokens + 16 tokens (capped at the pool):
+ * table[0 .. *n_pages) holds them, the first *matched_tokens / page_tokens of them matched.
+ * KVQ_ERR_CAPACITY (nothing held) when free and evictable pages run out. */
+int kvq_radix_match_and_allocate(kvq_radix* r, const int32_t* tokens, int n_tokens, int max_new_tokens,
+                                 int32_t* table, int table_capacity, int* matched_tokens, int* n_pages);
+/* Key the full pages of tokens[0 .. valid_tokens) (held pages of `table`) for later matches. */
+int kvq_radix_commit(kvq_radix* r, const int32_t* tokens, int n_tokens, const int32_t* table, int n_pages,
+                     int valid_tokens);
+int kvq_radix_release(kvq_radix* r, const int32_t* table, int n_pages);
+void kvq_radix_clear(kvq_radix* r);
+int kvq_radix_stats(const kvq_radix* r, kvq_radix_info* out);
+const char* kvq_radix_last_error(void);
 
 #ifdef __cplusplus
 }

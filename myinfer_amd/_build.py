@@ -39,6 +39,9 @@ HIPCC_FLAGS = [
 ]
 
 
+HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall"]
+
+
 def _torch_lib_dir() -> Path:
     import importlib.util
 
@@ -68,18 +71,24 @@ def _run(cmd: list[str], verbose: bool) -> None:
 
 
 def build(verbose: bool = False, jobs: int | None = None) -> Path:
-    """Compile every ``csrc/*.hip`` for gfx950 and link ``libkvq.so``. Always recompiles."""
+    """Compile every ``csrc/*.hip`` for gfx950 (and the host-only ``csrc/*.cpp`` with g++) and link
+    ``libkvq.so``. Always recompiles."""
     hipcc = _hipcc()
     OBJ.mkdir(exist_ok=True)
     sources = sorted(CSRC.glob("*.hip"))
+    host_sources = sorted(CSRC.glob("*.cpp"))  # host-only code (no device code): g++
     if not sources:
         raise RuntimeError(f"no HIP sources in {CSRC}")
     objs = [OBJ / (s.stem + ".o") for s in sources]
-    jobs = jobs or min(len(sources), max(1, os.cpu_count() or 1), 8)
+    host_objs = [OBJ / (s.stem + ".host.o") for s in host_sources]
+    jobs = jobs or min(len(sources) + len(host_sources), max(1, os.cpu_count() or 1), 8)
     with cf.ThreadPoolExecutor(jobs) as ex:
         futs = [ex.submit(_run, [hipcc, *HIPCC_FLAGS, "-c", str(s), "-o", str(o)], verbose) for s, o in zip(sources, objs)]
+        futs += [ex.submit(_run, ["g++", *HOST_FLAGS, "-c", str(s), "-o", str(o)], verbose)
+                 for s, o in zip(host_sources, host_objs)]
         for f in futs:
             f.result()
+    objs += host_objs
     tlib = _torch_lib_dir()
     tmp = LIB.with_suffix(".so.tmp")
     link = [

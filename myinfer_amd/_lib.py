@@ -18,7 +18,7 @@ import os
 
 # The in-tree build; KVQ_LIB may name another build of the same library (A/B comparisons).
 LIB_PATH = Path(os.environ.get("KVQ_LIB") or (Path(__file__).resolve().parent / "libkvq.so"))
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 DTYPE_F16 = 0
 DTYPE_BF16 = 1
@@ -28,6 +28,8 @@ ERR_INVALID = -1
 ERR_UNSUPPORTED = -2
 ERR_WORKSPACE = -3
 ERR_HIP = -4
+ERR_CAPACITY = -5
+PAGE_ROWS = 64  # KVQ_PAGE_ROWS
 
 # Function name -> (restype, argtypes); the complete export list of include/kvq.h.
 
@@ -76,6 +78,20 @@ _DENSE_ARGS = [
     c_void_p, c_size_t, c_void_p,  # workspace bytes stream
 ]
 _WS_ARGS = [c_int, c_int, c_int, c_int, c_int, c_int, c_int]
+_PAGED_ATTN_ARGS = [
+    POINTER(Rows), POINTER(QTensor), POINTER(QTensor), c_int, c_void_p, c_int64, c_void_p, POINTER(Rows),
+    c_int, c_int, c_int, c_int, c_int, c_int,  # B Hq Hkv L D S
+    c_int, c_int, c_int,  # bits group dtype
+    c_float, c_int, c_int,  # scale causal window
+    c_void_p, c_size_t, c_void_p,  # workspace bytes stream
+]
+
+
+class RadixInfo(ctypes.Structure):
+    """kvq_radix_info: counters of a radix prefix cache."""
+
+    _fields_ = [("num_pages", c_int), ("page_tokens", c_int), ("cached_pages", c_int), ("free_pages", c_int),
+                ("in_use_pages", c_int), ("prefix_hit_tokens", c_int64), ("prompt_tokens", c_int64)]
 
 SIGNATURES = {
     "kvq_abi_version": (c_int, []),
@@ -92,6 +108,24 @@ SIGNATURES = {
          c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_void_p],
     ),
     "kvq_decode_attn": (c_int, _ATTN_ARGS),
+    "kvq_paged_quantize_append": (
+        c_int,
+        [POINTER(Rows), POINTER(QTensor), POINTER(Rows), POINTER(QTensor), c_int, c_void_p, c_int64, c_void_p, c_int64,
+         POINTER(RopeParams), c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_void_p],
+    ),
+    "kvq_paged_decode_attn": (c_int, _PAGED_ATTN_ARGS),
+    "kvq_paged_prefill_attn": (c_int, _PAGED_ATTN_ARGS),
+    "kvq_radix_create": (c_void_p, [c_int, c_int]),
+    "kvq_radix_destroy": (None, [c_void_p]),
+    "kvq_radix_match_and_allocate": (
+        c_int, [c_void_p, POINTER(ctypes.c_int32), c_int, c_int, POINTER(ctypes.c_int32), c_int, POINTER(c_int),
+                POINTER(c_int)],
+    ),
+    "kvq_radix_commit": (c_int, [c_void_p, POINTER(ctypes.c_int32), c_int, POINTER(ctypes.c_int32), c_int, c_int]),
+    "kvq_radix_release": (c_int, [c_void_p, POINTER(ctypes.c_int32), c_int]),
+    "kvq_radix_clear": (None, [c_void_p]),
+    "kvq_radix_stats": (c_int, [c_void_p, POINTER(RadixInfo)]),
+    "kvq_radix_last_error": (c_char_p, []),
     "kvq_decode_attn_dense": (c_int, _DENSE_ARGS),
     "kvq_prefill_attn_dense": (c_int, _DENSE_ARGS),
     "kvq_decode_workspace_size": (c_size_t, _WS_ARGS),

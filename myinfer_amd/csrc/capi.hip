@@ -147,6 +147,30 @@ int check_quantize(const kvq_rows* k_src, const kvq_qtensor* k_dst, const kvq_ro
   return KVQ_OK;
 }
 
+// A paged pool described by a kvq_qtensor whose batch strides are page strides: pages of
+// KVQ_PAGE_ROWS rows per head, head-major within a page.
+int check_pool(const kvq_qtensor* t, const char* name, int H, int D, int bits, int group_size, int num_pages) {
+  int rc;
+  if ((rc = check_qtensor(t, name))) return rc;
+  if (num_pages <= 0) return fail(KVQ_ERR_INVALID, "num_pages must be positive, got %d", num_pages);
+  const int64_t row_words = (int64_t)D * bits / 32, groups = D / group_size;
+  if (t->codes_stride_s < row_words || t->sb_stride_s < groups)
+    return fail(KVQ_ERR_INVALID, "%s row strides are smaller than one row", name);
+  if (t->codes_stride_h < KVQ_PAGE_ROWS * t->codes_stride_s || t->sb_stride_h < KVQ_PAGE_ROWS * t->sb_stride_s ||
+      t->codes_stride_b < H * t->codes_stride_h || t->sb_stride_b < H * t->sb_stride_h)
+    return fail(KVQ_ERR_INVALID, "%s is not [num_pages][H][%d][row]: its strides overlap", name, KVQ_PAGE_ROWS);
+  return KVQ_OK;
+}
+
+int check_table(const int32_t* table, int64_t table_stride, int64_t rows_needed) {
+  if (!table) return fail(KVQ_ERR_INVALID, "block_table is NULL");
+  if (table_stride <= 0) return fail(KVQ_ERR_INVALID, "table_stride must be positive");
+  if ((rows_needed + KVQ_PAGE_ROWS - 1) / KVQ_PAGE_ROWS > table_stride)
+    return fail(KVQ_ERR_INVALID, "table_stride %lld pages cannot hold %lld rows", (long long)table_stride,
+                (long long)rows_needed);
+  return KVQ_OK;
+}
+
 int check_rope(const kvq_rope_params* r, int D) {
   if (!r) return fail(KVQ_ERR_INVALID, "rope descriptor is NULL");
   if (r->dims <= 0 || r->dims > D || r->dims > 256 || r->dims % 16)
@@ -199,6 +223,24 @@ int kvq_rope_quantize_append(const kvq_rows* k_src, const kvq_qtensor* k_dst, co
                     "rope_quantize_append launch");
 }
 
+int kvq_paged_quantize_append(const kvq_rows* k_src, const kvq_qtensor* k_pool, const kvq_rows* v_src,
+                              const kvq_qtensor* v_pool, int num_pages, const int32_t* block_table,
+                              int64_t table_stride, const int32_t* starts, int64_t row_offset,
+                              const kvq_rope_params* rope, int B, int H, int L, int D, int bits, int group_size,
+                              int dtype, void* stream) {
+  int rc;
+  if ((rc = check_quantize(k_src, k_pool, v_src, v_pool, row_offset, B, H, L, D, bits, group_size, dtype))) return rc;
+  if ((rc = check_pool(k_pool, "k_pool", H, D, bits, group_size, num_pages))) return rc;
+  if (v_pool && (rc = check_pool(v_pool, "v_pool", H, D, bits, group_size, num_pages))) return rc;
+  if ((rc = check_table(block_table, table_stride, starts ? 1 : row_offset + L))) return rc;
+  if (rope && (rc = check_rope(rope, D))) return rc;
+  if (B == 0 || H == 0 || L == 0) return ok();
+  return hip_status(kvq::launch_paged_quantize_append(k_src, k_pool, v_src, v_pool, num_pages, block_table, table_stride,
+                                                      starts, row_offset, rope, B, H, L, D, bits, group_size, dtype,
+                                                      (hipStream_t)stream),
+                    "paged_quantize_append launch");
+}
+
 size_t kvq_decode_workspace_size(int B, int Hq, int Hkv, int L, int D, int S, int window) {
   if (B <= 0 || Hq <= 0 || Hkv <= 0 || L <= 0 || S <= 0 || (D != 64 && D != 128) || window < 0) return 0;
   // one size serves every cache format: the quantized (8-, 4-bit) and the unquantized (16) plans
@@ -240,6 +282,56 @@ int kvq_prefill_attn(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor*
   return hip_status(kvq::launch_prefill(q, k, v, seq_lens, out, B, Hq, Hkv, L, D, S, bits, dtype, scale, causal,
                                         window, workspace, (hipStream_t)stream),
                     "prefill_attn launch");
+}
+
+// Attention over paged pools: the quantized checks with the pool geometry and the block table.
+static int check_paged_attn(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v, int num_pages,
+                            const int32_t* table, int64_t table_stride, const kvq_rows* out, int B, int Hq, int Hkv,
+                            int L, int D, int S, int bits, int group_size, int dtype, float scale, int window,
+                            size_t ws_needed, void* workspace, size_t workspace_bytes) {
+  int rc;
+  if ((rc = check_attn_common(q, out, B, Hq, Hkv, L, D, S, dtype, scale, window))) return rc;
+  if (bits != 4 && bits != 8) return fail(KVQ_ERR_UNSUPPORTED, "attention supports 4- and 8-bit caches, got bits=%d", bits);
+  if (group_size != 64) return fail(KVQ_ERR_UNSUPPORTED, "attention supports group_size 64, got %d", group_size);
+  if ((rc = check_pool(k, "k_pool", Hkv, D, bits, group_size, num_pages))) return rc;
+  if ((rc = check_pool(v, "v_pool", Hkv, D, bits, group_size, num_pages))) return rc;
+  for (const kvq_qtensor* t : {k, v})
+    if (!aligned(t->codes, 16) || (t->codes_stride_s * 4) % 16 || (t->codes_stride_h * 4) % 16 || (t->codes_stride_b * 4) % 16)
+      return fail(KVQ_ERR_INVALID, "codes must be 16-byte aligned with 16-byte-multiple row, head and page strides");
+  if ((rc = check_table(table, table_stride, S))) return rc;
+  return check_workspace(ws_needed, workspace, workspace_bytes);
+}
+
+int kvq_paged_decode_attn(const kvq_rows* q, const kvq_qtensor* k_pool, const kvq_qtensor* v_pool, int num_pages,
+                          const int32_t* block_table, int64_t table_stride, const int32_t* seq_lens,
+                          const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int bits, int group_size,
+                          int dtype, float scale, int causal, int window, void* workspace, size_t workspace_bytes,
+                          void* stream) {
+  if (D != 64 && D != 128) return fail(KVQ_ERR_UNSUPPORTED, "decode supports head_dim 64 and 128, got %d", D);
+  int rc = check_paged_attn(q, k_pool, v_pool, num_pages, block_table, table_stride, out, B, Hq, Hkv, L, D, S, bits,
+                            group_size, dtype, scale, window, kvq_decode_workspace_size(B, Hq, Hkv, L, D, S, window),
+                            workspace, workspace_bytes);
+  if (rc) return rc;
+  return hip_status(kvq::launch_decode_paged(q, k_pool, v_pool, num_pages, block_table, table_stride, seq_lens, out, B,
+                                             Hq, Hkv, L, D, S, bits, dtype, scale, causal, window, workspace,
+                                             (hipStream_t)stream),
+                    "paged_decode_attn launch");
+}
+
+int kvq_paged_prefill_attn(const kvq_rows* q, const kvq_qtensor* k_pool, const kvq_qtensor* v_pool, int num_pages,
+                           const int32_t* block_table, int64_t table_stride, const int32_t* seq_lens,
+                           const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int bits, int group_size,
+                           int dtype, float scale, int causal, int window, void* workspace, size_t workspace_bytes,
+                           void* stream) {
+  if (D != 128) return fail(KVQ_ERR_UNSUPPORTED, "prefill supports head_dim 128, got %d", D);
+  int rc = check_paged_attn(q, k_pool, v_pool, num_pages, block_table, table_stride, out, B, Hq, Hkv, L, D, S, bits,
+                            group_size, dtype, scale, window, kvq_prefill_workspace_size(B, Hq, Hkv, L, D, S, window),
+                            workspace, workspace_bytes);
+  if (rc) return rc;
+  return hip_status(kvq::launch_prefill_paged(q, k_pool, v_pool, num_pages, block_table, table_stride, seq_lens, out, B,
+                                              Hq, Hkv, L, D, S, bits, dtype, scale, causal, window, workspace,
+                                              (hipStream_t)stream),
+                    "paged_prefill_attn launch");
 }
 
 int kvq_decode_attn_dense(const kvq_rows* q, const kvq_rows* k, const kvq_rows* v, const int32_t* seq_lens,

@@ -94,6 +94,11 @@ struct DecParams {
   int fused;      // 1: the last workgroup of a unit merges the splits; 0: combine_kernel does
   float scale_log2;
   int causal, window;
+  // paged cache (PAGED kernels): rows of sequence b live in 64-row pages, page table[b][r / 64];
+  // the codes/scales/biases batch strides above are then page strides
+  const int32_t* table;
+  int64_t table_stride;
+  int num_pages;
 };
 
 // Token (relative to the tile) of V slot i' (the MFMA k index 8*lg + i') for lane group lg.
@@ -374,7 +379,7 @@ constexpr int dec_min_wgs() {
   return (NW == 4 && 2 * NW * NSLOT * DecCfg<D, BITS>::SLOT <= 160 * 1024) ? 2 : 1;
 }
 
-template <typename T, int D, int BITS, int NW, int NSLOT>
+template <typename T, int D, int BITS, int NW, int NSLOT, bool PAGED = false>
 __global__ __launch_bounds__(NW * 64, (dec_min_wgs<D, BITS, NW, NSLOT>())) void decode_attn_kernel(DecParams p) {
   using C = DecCfg<D, BITS>;
   constexpr int R = C::R;
@@ -402,7 +407,9 @@ __global__ __launch_bounds__(NW * 64, (dec_min_wgs<D, BITS, NW, NSLOT>())) void 
   const int rb = unit % p.rowblocks;
 
   const int S_b = p.seq_lens ? min(max(p.seq_lens[b], 0), p.S) : p.S;  // clamped: never read past the view
-  const int key_base = p.window > 0 ? max(0, S_b - p.L - p.window + 1) : 0;
+  // the first key any row sees, rounded down to a tile boundary (tiles stay 32-aligned, so a tile of
+  // a paged cache lies in one page; the keys before the window are masked)
+  const int key_base = p.window > 0 ? max(0, S_b - p.L - p.window + 1) & ~(kTile - 1) : 0;
   const int k_begin = key_base + split * p.chunk;
   const int k_end = min(k_begin + p.chunk, S_b);
   const int ntile = k_end > k_begin ? (k_end - k_begin + kTile - 1) / kTile : 0;
@@ -460,18 +467,45 @@ __global__ __launch_bounds__(NW * 64, (dec_min_wgs<D, BITS, NW, NSLOT>())) void 
   // tile i of this wave -> slot `slot`; past the wave's last tile it re-reads that tile, so the
   // number of loads in flight behind any tile is always (NSLOT - 1) * IPT
   const int last = max(nmine - 1, 0);
+  // paged cache: a tile (32 rows, 32-aligned) lies in one 64-row page; its page number is read one
+  // tile ahead (a scalar load that the ring's waits cover), clamped to the pool, and the tile's
+  // buffer resources span only that page's valid rows, so rows past S_b still read as zero
+  auto page_of = [&](int k0) -> int {
+    const int pi = min(k0, max(S_b - 1, 0)) >> 6;
+    return __builtin_amdgcn_readfirstlane(min(max(p.table[(int64_t)b * p.table_stride + pi], 0), p.num_pages - 1));
+  };
+  int pg_next = PAGED ? page_of(tile_k0(0)) : 0;
   auto issue = [&](int i, int slot) {
     const int k0 = tile_k0(min(i, last));
     uint8_t* sl = ring + slot * C::SLOT;
-    const uint32_t ko = (uint32_t)((int64_t)k0 * p.kc_ss), vo = (uint32_t)((int64_t)k0 * p.vc_ss);
+    __amdgpu_buffer_rsrc_t kr = krs, vr = vrs, sr[4] = {srs[0], srs[1], srs[2], srs[3]};
+    int rk0 = k0;  // the tile's first row within the buffer resources
+    if constexpr (PAGED) {
+      const int pg = pg_next;
+      pg_next = page_of(tile_k0(min(i + 1, last)));
+      const int nv = __builtin_amdgcn_readfirstlane(max(min(64, S_b - (k0 & ~63)), 0));  // keeps the rsrc in SGPRs
+      kr = make_rsrc(p.kc + (int64_t)pg * p.kc_sb + (int64_t)kvh * p.kc_sh, (uint32_t)(nv * p.kc_ss));
+      vr = make_rsrc(p.vc + (int64_t)pg * p.vc_sb + (int64_t)kvh * p.vc_sh, (uint32_t)(nv * p.vc_ss));
+      if constexpr (!C::DENSE) {
+        const int64_t ko = (int64_t)pg * p.ksb_sb + (int64_t)kvh * p.ksb_sh;
+        const int64_t vo = (int64_t)pg * p.vsb_sb + (int64_t)kvh * p.vsb_sh;
+        const uint32_t kn = (uint32_t)(nv * p.ksb_ss * 2), vn = (uint32_t)(nv * p.vsb_ss * 2);
+        sr[0] = make_rsrc(p.ks + ko, kn);
+        sr[1] = make_rsrc(p.kb + ko, kn);
+        sr[2] = make_rsrc(p.vs + vo, vn);
+        sr[3] = make_rsrc(p.vb + vo, vn);
+      }
+      rk0 = k0 & 63;
+    }
+    const uint32_t ko = (uint32_t)((int64_t)rk0 * p.kc_ss), vo = (uint32_t)((int64_t)rk0 * p.vc_ss);
 #pragma unroll
-    for (int c = 0; c < C::CI; ++c) dma16(krs, sl + 1024 * c, dk[c], ko);
+    for (int c = 0; c < C::CI; ++c) dma16(kr, sl + 1024 * c, dk[c], ko);
 #pragma unroll
-    for (int c = 0; c < C::CI; ++c) dma16(vrs, sl + C::TB + 1024 * c, dv[c], vo);
+    for (int c = 0; c < C::CI; ++c) dma16(vr, sl + C::TB + 1024 * c, dv[c], vo);
     if constexpr (!C::DENSE) {
-      const uint32_t kso = (uint32_t)((int64_t)k0 * p.ksb_ss * 2), vso = (uint32_t)((int64_t)k0 * p.vsb_ss * 2);
+      const uint32_t kso = (uint32_t)((int64_t)rk0 * p.ksb_ss * 2), vso = (uint32_t)((int64_t)rk0 * p.vsb_ss * 2);
 #pragma unroll
-      for (int a = 0; a < 4; ++a) dma2(srs[a], sl + 2 * C::TB + 256 * a, dsb[a], a < 2 ? kso : vso);
+      for (int a = 0; a < 4; ++a) dma2(sr[a], sl + 2 * C::TB + 256 * a, dsb[a], a < 2 ? kso : vso);
     }
   };
   // nothing that waits for the query loads may be scheduled into (or before) the first tile loads
@@ -878,7 +912,7 @@ DecPlan decode_plan(int B, int Hq, int Hkv, int L, int D, int S, int window, int
   pl.R = 16 / (D / 64);
   const int nrows = (Hq / Hkv) * L;
   pl.rowblocks = (nrows + pl.R - 1) / pl.R;
-  pl.span = window > 0 ? std::min(S, window + L - 1) : S;
+  pl.span = window > 0 ? std::min(S, window + L - 1 + kTile - 1) : S;  // the window, from a tile boundary
   const int64_t tiles_seq = (pl.span + kTile - 1) / kTile;
   pl.nunits = B * Hkv * pl.rowblocks;
   int64_t tpw = (pl.nunits * tiles_seq + tune.target_wgs - 1) / tune.target_wgs;
@@ -911,10 +945,10 @@ size_t decode_workspace_bytes(int B, int Hq, int Hkv, int L, int D, int S, int w
   return decode_layout(pl, D).total;
 }
 
-template <typename T, int D, int BITS, int NW, int NSLOT>
+template <typename T, int D, int BITS, int NW, int NSLOT, bool PAGED = false>
 static hipError_t launch_decode_t(const DecParams& p, hipStream_t stream) {
-  hipLaunchKernelGGL((decode_attn_kernel<T, D, BITS, NW, NSLOT>), dim3(p.nunits * p.nsplit), dim3(NW * 64), 0, stream,
-                     p);
+  hipLaunchKernelGGL((decode_attn_kernel<T, D, BITS, NW, NSLOT, PAGED>), dim3(p.nunits * p.nsplit), dim3(NW * 64), 0,
+                     stream, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || p.nsplit == 1 || p.fused) return e;
   MergeParams m;
@@ -1017,6 +1051,45 @@ hipError_t launch_decode(const kvq_rows* q, const kvq_qtensor* k, const kvq_qten
     else { if (bf) KVQ_DEC(BF16, 64, 4); else KVQ_DEC(F16, 64, 4); }
   }
 #undef KVQ_DEC
+}
+
+hipError_t launch_decode_paged(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v, int num_pages,
+                               const int32_t* table, int64_t table_stride, const int32_t* seq_lens, const kvq_rows* out,
+                               int B, int Hq, int Hkv, int L, int D, int S, int bits, int dtype, float scale, int causal,
+                               int window, void* workspace, hipStream_t stream) {
+  const DecPlan pl = decode_plan(B, Hq, Hkv, L, D, S, window, bits);
+  DecParams p = decode_params(q, seq_lens, out, Hq, Hkv, L, D, S, scale, causal, window, workspace, pl);
+  p.kc = (const uint8_t*)k->codes;
+  p.vc = (const uint8_t*)v->codes;
+  p.kc_sb = k->codes_stride_b * 4;  // page strides
+  p.kc_sh = k->codes_stride_h * 4;
+  p.kc_ss = k->codes_stride_s * 4;
+  p.vc_sb = v->codes_stride_b * 4;
+  p.vc_sh = v->codes_stride_h * 4;
+  p.vc_ss = v->codes_stride_s * 4;
+  p.ks = (const uint16_t*)k->scales;
+  p.kb = (const uint16_t*)k->biases;
+  p.vs = (const uint16_t*)v->scales;
+  p.vb = (const uint16_t*)v->biases;
+  p.ksb_sb = k->sb_stride_b;
+  p.ksb_sh = k->sb_stride_h;
+  p.ksb_ss = k->sb_stride_s;
+  p.vsb_sb = v->sb_stride_b;
+  p.vsb_sh = v->sb_stride_h;
+  p.vsb_ss = v->sb_stride_s;
+  p.table = table;
+  p.table_stride = table_stride;
+  p.num_pages = num_pages;
+  const bool bf = dtype == KVQ_DTYPE_BF16;
+#define KVQ_DECP(TT, DD, BB) return launch_decode_t<TT, DD, BB, 4, 2, true>(p, stream)
+  if (D == 128) {
+    if (bits == 8) { if (bf) KVQ_DECP(BF16, 128, 8); else KVQ_DECP(F16, 128, 8); }
+    else { if (bf) KVQ_DECP(BF16, 128, 4); else KVQ_DECP(F16, 128, 4); }
+  } else {
+    if (bits == 8) { if (bf) KVQ_DECP(BF16, 64, 8); else KVQ_DECP(F16, 64, 8); }
+    else { if (bf) KVQ_DECP(BF16, 64, 4); else KVQ_DECP(F16, 64, 4); }
+  }
+#undef KVQ_DECP
 }
 
 hipError_t launch_decode_dense(const kvq_rows* q, const kvq_rows* k, const kvq_rows* v, const int32_t* seq_lens,

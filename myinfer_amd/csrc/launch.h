@@ -12,6 +12,11 @@ namespace kvq {
 hipError_t launch_quantize_append(const kvq_rows* k_src, const kvq_qtensor* k_dst, const kvq_rows* v_src,
                                   const kvq_qtensor* v_dst, const kvq_rope_params* rope, int64_t row_offset, int B, int H,
                                   int L, int D, int bits, int group_size, int dtype, hipStream_t stream);
+hipError_t launch_paged_quantize_append(const kvq_rows* k_src, const kvq_qtensor* k_pool, const kvq_rows* v_src,
+                                        const kvq_qtensor* v_pool, int num_pages, const int32_t* table,
+                                        int64_t table_stride, const int32_t* starts, int64_t row_offset,
+                                        const kvq_rope_params* rope, int B, int H, int L, int D, int bits,
+                                        int group_size, int dtype, hipStream_t stream);
 hipError_t launch_rope(const kvq_rows* x, const kvq_rope_params* rope, int B, int H, int L, int dtype, hipStream_t stream);
 
 size_t decode_workspace_bytes(int B, int Hq, int Hkv, int L, int D, int S, int window, int bits);
@@ -19,6 +24,10 @@ hipError_t launch_decode(const kvq_rows* q, const kvq_qtensor* k, const kvq_qten
                          const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int bits, int dtype,
                          float scale, int causal, int window, void* workspace, hipStream_t stream);
 
+hipError_t launch_decode_paged(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v, int num_pages,
+                               const int32_t* table, int64_t table_stride, const int32_t* seq_lens, const kvq_rows* out,
+                               int B, int Hq, int Hkv, int L, int D, int S, int bits, int dtype, float scale, int causal,
+                               int window, void* workspace, hipStream_t stream);
 hipError_t launch_decode_dense(const kvq_rows* q, const kvq_rows* k, const kvq_rows* v, const int32_t* seq_lens,
                                const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int dtype, float scale,
                                int causal, int window, void* workspace, hipStream_t stream);
@@ -27,6 +36,10 @@ size_t prefill_workspace_bytes(int B, int Hq, int Hkv, int L, int D, int S, int 
 hipError_t launch_prefill(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v, const int32_t* seq_lens,
                           const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int bits, int dtype,
                           float scale, int causal, int window, void* workspace, hipStream_t stream);
+hipError_t launch_prefill_paged(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v, int num_pages,
+                                const int32_t* table, int64_t table_stride, const int32_t* seq_lens, const kvq_rows* out,
+                                int B, int Hq, int Hkv, int L, int D, int S, int bits, int dtype, float scale, int causal,
+                                int window, void* workspace, hipStream_t stream);
 hipError_t launch_prefill_dense(const kvq_rows* q, const kvq_rows* k, const kvq_rows* v, const int32_t* seq_lens,
                                 const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int dtype,
                                 float scale, int causal, int window, void* workspace, hipStream_t stream);

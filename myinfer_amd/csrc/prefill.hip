@@ -90,6 +90,11 @@ struct PreParams {
   int Hq, Hkv, L, S, rep, nrows, rowblocks, nsplit, nunits;
   float scale_log2;
   int causal, window;
+  // paged cache (PAGED kernels): rows of sequence b live in 64-row pages, page table[b][r / 64];
+  // the codes/scales/biases batch strides above are then page strides
+  const int32_t* table;
+  int64_t table_stride;
+  int num_pages;
 };
 
 // V^T slot of key `kk` (0..63) inside a tile: the 16 keys of PV k-step j = kk / 16 are stored so
@@ -162,6 +167,32 @@ struct RawShare {
 #pragma unroll
     for (int j = 0; j < C::CPW; ++j) dma_b128(code_r[j], slot + code_lds[j], code_vo[j], (uint32_t)(k0 * code_ss[j]));
     if constexpr (!C::DENSE) dma_b16(sb_r, slot + sb_lds, sb_vo, (uint32_t)(k0 * sb_ss));
+  }
+
+  // Paged cache: the wave's arrays at page 0 of this KV head, and their page strides (bytes).
+  const uint8_t* code_base[C::CPW];
+  const uint8_t* sb_base;
+  int64_t code_ps[C::CPW], sb_ps;
+  __device__ __forceinline__ void init_paged(const PreParams& p, int kvh, int wave) {
+#pragma unroll
+    for (int j = 0; j < C::CPW; ++j) {
+      const bool is_k = wave * C::CPW + j < C::CI;
+      code_base[j] = is_k ? p.kc + (int64_t)kvh * p.kc_sh : p.vc + (int64_t)kvh * p.vc_sh;
+      code_ps[j] = is_k ? p.kc_sb : p.vc_sb;
+    }
+    const int a = wave >> 1;
+    const uint16_t* arr = a == 0 ? p.ks : a == 1 ? p.kb : a == 2 ? p.vs : p.vb;
+    sb_base = (const uint8_t*)(arr + (int64_t)kvh * (a < 2 ? p.ksb_sh : p.vsb_sh));
+    sb_ps = 2 * (a < 2 ? p.ksb_sb : p.vsb_sb);
+  }
+  // raw tile of page `pg` (its first nv rows valid) into the slot at LDS address `slot`
+  __device__ __forceinline__ void issue_paged(uint32_t slot, int pg, int nv) const {
+#pragma unroll
+    for (int j = 0; j < C::CPW; ++j)
+      dma_b128(make_rsrc(code_base[j] + (int64_t)pg * code_ps[j], (uint32_t)(nv * code_ss[j])), slot + code_lds[j],
+               code_vo[j], 0u);
+    if constexpr (!C::DENSE)
+      dma_b16(make_rsrc(sb_base + (int64_t)pg * sb_ps, (uint32_t)(nv * sb_ss)), slot + sb_lds, sb_vo, 0u);
   }
 };
 
@@ -282,7 +313,7 @@ __device__ __forceinline__ void stage_v_raw(const uint8_t* raw, _Float16* vlds, 
   *(u4*)&vlds[(2 * d2 + 1) * kVS + 8 * c8] = hi;
 }
 
-template <typename T, int BITS>
+template <typename T, int BITS, bool PAGED = false>
 __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) {
   using RC = RawCfg<BITS>;
   constexpr bool DENSE = RC::DENSE;  // unquantized cache: K operands are read from the raw ring
@@ -356,10 +387,29 @@ __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) 
       sr[3] = make_rsrc(p.vb + vo, vn);
     }
     share.init(p, kr, vr, sr, wave, lane);
+    if constexpr (PAGED) share.init_paged(p, kvh, wave);
   }
   const uint32_t raw_lds = lds_addr(&raw[0][0]);
   const int last = max(ntile - 1, 0);
-  auto issue_raw = [&](int i) { share.issue(raw_lds + (i % kRawSlots) * RC::SLOT, k_begin + kPT * min(i, last)); };
+  // paged cache: a tile (64 rows, 64-aligned) is one page; its page number is read one tile ahead
+  // (a scalar load), clamped to the pool, and the tile's buffer resources span only that page's
+  // valid rows, so rows past S_b still read as zero
+  auto page_of = [&](int k0) -> int {
+    const int pi = min(k0, max(S_b - 1, 0)) >> 6;
+    return __builtin_amdgcn_readfirstlane(min(max(p.table[(int64_t)b * p.table_stride + pi], 0), p.num_pages - 1));
+  };
+  int pg_next = PAGED ? page_of(k_begin) : 0;
+  auto issue_raw = [&](int i) {
+    const int k0 = k_begin + kPT * min(i, last);
+    const uint32_t slot = raw_lds + (i % kRawSlots) * RC::SLOT;
+    if constexpr (PAGED) {
+      const int pg = pg_next;
+      pg_next = page_of(k_begin + kPT * min(i + 1, last));
+      share.issue_paged(slot, pg, __builtin_amdgcn_readfirstlane(max(min(kPT, S_b - k0), 0)));
+    } else {
+      share.issue(slot, k0);
+    }
+  };
   // Quantized cache: the ring runs three tiles ahead (tile t + 3 is issued into the slot of tile t,
   // which was dequantized in the previous step). Unquantized cache: K is read from the ring while
   // tile t is computed, so tile t + 2 is issued into the slot of tile t - 1 and lands within the step.
@@ -677,9 +727,9 @@ size_t prefill_workspace_bytes(int B, int Hq, int Hkv, int L, int D, int S, int 
   return prefill_layout(pl).total;
 }
 
-template <typename T, int BITS>
+template <typename T, int BITS, bool PAGED = false>
 static hipError_t launch_prefill_t(const PreParams& p, hipStream_t stream) {
-  hipLaunchKernelGGL((prefill_attn_kernel<T, BITS>), dim3(p.nunits * p.nsplit), dim3(kPW * 64), 0, stream, p);
+  hipLaunchKernelGGL((prefill_attn_kernel<T, BITS, PAGED>), dim3(p.nunits * p.nsplit), dim3(kPW * 64), 0, stream, p);
   return hipGetLastError();
 }
 
@@ -745,6 +795,42 @@ hipError_t launch_prefill(const kvq_rows* q, const kvq_qtensor* k, const kvq_qte
   }
   if (bits == 8) return launch_prefill_t<F16, 8>(p, stream);
   return launch_prefill_t<F16, 4>(p, stream);
+}
+
+hipError_t launch_prefill_paged(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v, int num_pages,
+                                const int32_t* table, int64_t table_stride, const int32_t* seq_lens, const kvq_rows* out,
+                                int B, int Hq, int Hkv, int L, int D, int S, int bits, int dtype, float scale, int causal,
+                                int window, void* workspace, hipStream_t stream) {
+  const PrePlan pl = prefill_plan(B, Hq, Hkv, L, S, window);
+  PreParams p = prefill_params(q, seq_lens, out, Hq, Hkv, L, S, scale, causal, window, workspace, pl);
+  p.kc = (const uint8_t*)k->codes;
+  p.vc = (const uint8_t*)v->codes;
+  p.kc_sb = k->codes_stride_b * 4;  // page strides
+  p.kc_sh = k->codes_stride_h * 4;
+  p.kc_ss = k->codes_stride_s * 4;
+  p.vc_sb = v->codes_stride_b * 4;
+  p.vc_sh = v->codes_stride_h * 4;
+  p.vc_ss = v->codes_stride_s * 4;
+  p.ks = (const uint16_t*)k->scales;
+  p.kb = (const uint16_t*)k->biases;
+  p.vs = (const uint16_t*)v->scales;
+  p.vb = (const uint16_t*)v->biases;
+  p.ksb_sb = k->sb_stride_b;
+  p.ksb_sh = k->sb_stride_h;
+  p.ksb_ss = k->sb_stride_s;
+  p.vsb_sb = v->sb_stride_b;
+  p.vsb_sh = v->sb_stride_h;
+  p.vsb_ss = v->sb_stride_s;
+  p.table = table;
+  p.table_stride = table_stride;
+  p.num_pages = num_pages;
+  (void)D;
+  if (dtype == KVQ_DTYPE_BF16) {
+    if (bits == 8) return launch_prefill_t<BF16, 8, true>(p, stream);
+    return launch_prefill_t<BF16, 4, true>(p, stream);
+  }
+  if (bits == 8) return launch_prefill_t<F16, 8, true>(p, stream);
+  return launch_prefill_t<F16, 4, true>(p, stream);
 }
 
 hipError_t launch_prefill_dense(const kvq_rows* q, const kvq_rows* k, const kvq_rows* v, const int32_t* seq_lens,

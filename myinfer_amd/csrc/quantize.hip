@@ -103,9 +103,20 @@ struct QuantJob {
   int64_t g_b, g_h, g_s;
 };
 
+// Paged destination: row r of sequence b goes to row r % 64 of page table[b][r / 64] (the job's
+// batch strides are then page strides); r = starts[b] + l when `starts` is given, else
+// row_offset + l. table == nullptr: the contiguous cache.
+struct PageMap {
+  const int32_t* table;
+  int64_t table_stride;
+  const int32_t* starts;
+  int num_pages;
+};
+
 template <typename T, int BITS, int G, bool ROPE>
 __global__ __launch_bounds__(256) void quantize_append_kernel(QuantJob job0, QuantJob job1, int H, int L,
-                                                              int D, int64_t total, int64_t row_offset, RopeArgs rope) {
+                                                              int D, int64_t total, int64_t row_offset, RopeArgs rope,
+                                                              PageMap pm) {
 #pragma clang fp contract(off)
   const QuantJob job = blockIdx.y == 0 ? job0 : job1;
   const int64_t tid = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -126,7 +137,7 @@ __global__ __launch_bounds__(256) void quantize_append_kernel(QuantJob job0, Qua
       const int d0 = chunk * 8, half = rope.dims / 2;
       float xp[8];
       if (!rope.traditional && d0 < rope.dims) load8<T>(srow + (d0 < half ? d0 + half : d0 - half), xp);
-      rope8(rope, rope.offset + l, d0, x, xp);
+      rope8(rope, rope.offset + (pm.starts ? pm.starts[b] : 0) + l, d0, x, xp);
 #pragma unroll
       for (int i = 0; i < 8; ++i) x[i] = to_float(from_float(x[i], T{}), T{});
     }
@@ -166,8 +177,14 @@ __global__ __launch_bounds__(256) void quantize_append_kernel(QuantJob job0, Qua
     packed[bit / 32] |= code << (bit % 32);
   }
 
-  const int64_t drow = row_offset + l;
-  uint32_t* cdst = job.codes + b * job.c_b + h * job.c_h + drow * job.c_s;
+  int64_t drow = row_offset + l, bb = b;
+  if (pm.table) {
+    const int64_t r = (pm.starts ? (int64_t)pm.starts[b] : row_offset) + l;
+    if (r < 0 || (r >> 6) >= pm.table_stride) return;  // a row outside the sequence's table is dropped
+    bb = min(max(pm.table[b * pm.table_stride + (r >> 6)], 0), pm.num_pages - 1);
+    drow = r & 63;
+  }
+  uint32_t* cdst = job.codes + bb * job.c_b + h * job.c_h + drow * job.c_s;
   if constexpr (BITS == 8) {
     *(u2*)(cdst + chunk * 2) = u2{packed[0], packed[1]};
   } else if constexpr (BITS == 4) {
@@ -177,7 +194,7 @@ __global__ __launch_bounds__(256) void quantize_append_kernel(QuantJob job0, Qua
     if ((chunk & 1) == 0) cdst[chunk / 2] = packed[0] | (other << 16);
   }
   if (chunk % (G / 8) == 0) {
-    const int64_t gi = b * job.g_b + h * job.g_h + drow * job.g_s + chunk / (G / 8);
+    const int64_t gi = bb * job.g_b + h * job.g_h + drow * job.g_s + chunk / (G / 8);
     job.scales[gi] = from_float(s, T{});
     job.biases[gi] = from_float(bias, T{});
   }
@@ -185,35 +202,35 @@ __global__ __launch_bounds__(256) void quantize_append_kernel(QuantJob job0, Qua
 
 template <typename T, int BITS, int G>
 static hipError_t launch_quant(const QuantJob& k, const QuantJob& v, int njobs, int B, int H, int L, int D,
-                               int64_t row_offset, const RopeArgs* rope, hipStream_t stream) {
+                               int64_t row_offset, const RopeArgs* rope, const PageMap& pm, hipStream_t stream) {
   const int64_t total = (int64_t)B * H * L * (D / 8);
   const int64_t blocks = (total + 255) / 256;
   if (rope)
     hipLaunchKernelGGL((quantize_append_kernel<T, BITS, G, true>), dim3((unsigned)blocks, njobs), dim3(256), 0, stream,
-                       k, v, H, L, D, total, row_offset, *rope);
+                       k, v, H, L, D, total, row_offset, *rope, pm);
   else
     hipLaunchKernelGGL((quantize_append_kernel<T, BITS, G, false>), dim3((unsigned)blocks, njobs), dim3(256), 0,
-                       stream, k, v, H, L, D, total, row_offset, RopeArgs{});
+                       stream, k, v, H, L, D, total, row_offset, RopeArgs{}, pm);
   return hipGetLastError();
 }
 
 template <typename T, int BITS>
 static hipError_t dispatch_group(int G, const QuantJob& k, const QuantJob& v, int njobs, int B, int H, int L, int D,
-                                 int64_t row_offset, const RopeArgs* rope, hipStream_t stream) {
+                                 int64_t row_offset, const RopeArgs* rope, const PageMap& pm, hipStream_t stream) {
   switch (G) {
-    case 32: return launch_quant<T, BITS, 32>(k, v, njobs, B, H, L, D, row_offset, rope, stream);
-    case 64: return launch_quant<T, BITS, 64>(k, v, njobs, B, H, L, D, row_offset, rope, stream);
-    default: return launch_quant<T, BITS, 128>(k, v, njobs, B, H, L, D, row_offset, rope, stream);
+    case 32: return launch_quant<T, BITS, 32>(k, v, njobs, B, H, L, D, row_offset, rope, pm, stream);
+    case 64: return launch_quant<T, BITS, 64>(k, v, njobs, B, H, L, D, row_offset, rope, pm, stream);
+    default: return launch_quant<T, BITS, 128>(k, v, njobs, B, H, L, D, row_offset, rope, pm, stream);
   }
 }
 
 template <typename T>
 static hipError_t dispatch_bits(int bits, int G, const QuantJob& k, const QuantJob& v, int njobs, int B, int H, int L,
-                                int D, int64_t row_offset, const RopeArgs* rope, hipStream_t stream) {
+                                int D, int64_t row_offset, const RopeArgs* rope, const PageMap& pm, hipStream_t stream) {
   switch (bits) {
-    case 2: return dispatch_group<T, 2>(G, k, v, njobs, B, H, L, D, row_offset, rope, stream);
-    case 4: return dispatch_group<T, 4>(G, k, v, njobs, B, H, L, D, row_offset, rope, stream);
-    default: return dispatch_group<T, 8>(G, k, v, njobs, B, H, L, D, row_offset, rope, stream);
+    case 2: return dispatch_group<T, 2>(G, k, v, njobs, B, H, L, D, row_offset, rope, pm, stream);
+    case 4: return dispatch_group<T, 4>(G, k, v, njobs, B, H, L, D, row_offset, rope, pm, stream);
+    default: return dispatch_group<T, 8>(G, k, v, njobs, B, H, L, D, row_offset, rope, pm, stream);
   }
 }
 
@@ -244,8 +261,27 @@ hipError_t launch_quantize_append(const kvq_rows* k_src, const kvq_qtensor* k_ds
   RopeArgs ra{};
   if (rope) ra = make_rope_args(rope);
   const RopeArgs* rp = rope ? &ra : nullptr;
-  if (dtype == KVQ_DTYPE_BF16) return dispatch_bits<BF16>(bits, group_size, k, v, njobs, B, H, L, D, row_offset, rp, stream);
-  return dispatch_bits<F16>(bits, group_size, k, v, njobs, B, H, L, D, row_offset, rp, stream);
+  const PageMap pm{nullptr, 0, nullptr, 0};
+  if (dtype == KVQ_DTYPE_BF16)
+    return dispatch_bits<BF16>(bits, group_size, k, v, njobs, B, H, L, D, row_offset, rp, pm, stream);
+  return dispatch_bits<F16>(bits, group_size, k, v, njobs, B, H, L, D, row_offset, rp, pm, stream);
+}
+
+hipError_t launch_paged_quantize_append(const kvq_rows* k_src, const kvq_qtensor* k_pool, const kvq_rows* v_src,
+                                        const kvq_qtensor* v_pool, int num_pages, const int32_t* table,
+                                        int64_t table_stride, const int32_t* starts, int64_t row_offset,
+                                        const kvq_rope_params* rope, int B, int H, int L, int D, int bits,
+                                        int group_size, int dtype, hipStream_t stream) {
+  QuantJob k = make_job(k_src, k_pool);
+  QuantJob v = v_src ? make_job(v_src, v_pool) : k;
+  const int njobs = v_src ? 2 : 1;
+  RopeArgs ra{};
+  if (rope) ra = make_rope_args(rope);
+  const RopeArgs* rp = rope ? &ra : nullptr;
+  const PageMap pm{table, table_stride, starts, num_pages};
+  if (dtype == KVQ_DTYPE_BF16)
+    return dispatch_bits<BF16>(bits, group_size, k, v, njobs, B, H, L, D, row_offset, rp, pm, stream);
+  return dispatch_bits<F16>(bits, group_size, k, v, njobs, B, H, L, D, row_offset, rp, pm, stream);
 }
 
 // In-place RoPE: one thread per rotated pair of 8-value chunks (NeoX: dims [8j, +8) and

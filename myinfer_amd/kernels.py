@@ -273,3 +273,97 @@ def attention(queries: torch.Tensor, keys, values, scale: float, *, causal: bool
     prefill otherwise)."""
     return prepare_attention(queries, keys, values, scale, causal=causal, window=window, seq_lens=seq_lens,
                              group_size=group_size, bits=bits, out=out, kernel=kernel)()
+
+
+# ---- paged pools (64-row pages; include/kvq.h "Paged layout")
+
+PAGE_ROWS = _lib.PAGE_ROWS
+
+
+def _check_table(block_tables: torch.Tensor, B: int, dev) -> None:
+    if block_tables.dtype != torch.int32 or block_tables.dim() != 2 or block_tables.shape[0] != B:
+        raise ValueError(f"block_tables must be int32 [B={B}, max_pages], got {block_tables.dtype} "
+                         f"{tuple(block_tables.shape)}")
+    if block_tables.device != dev or block_tables.stride(1) != 1:
+        raise ValueError("block_tables must be on the queries' device with contiguous rows")
+
+
+def paged_quantize_append(k: torch.Tensor, k_pool: Triple, v: Optional[torch.Tensor], v_pool: Optional[Triple],
+                          block_tables: torch.Tensor, *, starts: Optional[torch.Tensor] = None, row_offset: int = 0,
+                          group_size: int = 64, bits: int = 8, rope: Optional[Rope] = None) -> None:
+    """Quantize k (and v) [B, H, L, D] into paged pools ([num_pages, H, 64, *] triples): row l of
+    sequence b goes to row starts[b] + l (or row_offset + l) of that sequence's pages. With `rope`
+    the keys are rotated at those positions first."""
+    _check_triple(k_pool, "k_pool")
+    tens = [k, *k_pool]
+    if v is not None:
+        _check_triple(v_pool, "v_pool")
+        tens += [v, *v_pool]
+    dev = _require_cuda(*tens)
+    B, H, L, D = k.shape
+    _check_table(block_tables, B, dev)
+    st_ptr = None
+    if starts is not None:
+        if starts.dtype != torch.int32 or starts.numel() != B or starts.device != dev:
+            raise ValueError("starts must be an int32 tensor of B entries on the same device")
+        st_ptr = starts.data_ptr()
+    kr, kq = _lib.rows(k), _lib.qtensor(*k_pool)
+    vr_p = vq_p = None
+    if v is not None:
+        vr, vq = _lib.rows(v), _lib.qtensor(*v_pool)
+        vr_p, vq_p = ctypes.byref(vr), ctypes.byref(vq)
+    rp = None
+    if rope is not None:
+        rparams = rope.params(0 if starts is not None else row_offset)
+        rp = ctypes.byref(rparams)
+    rc = _lib.lib().kvq_paged_quantize_append(
+        ctypes.byref(kr), ctypes.byref(kq), vr_p, vq_p, k_pool[0].shape[0], block_tables.data_ptr(),
+        block_tables.stride(0), st_ptr, int(row_offset), rp, B, H, L, D, int(bits), int(group_size),
+        _lib.dtype_code(k.dtype), _lib.stream_ptr(dev))
+    _lib.check(rc, "kvq_paged_quantize_append")
+
+
+def paged_attention(queries: torch.Tensor, k_pool: Triple, v_pool: Triple, block_tables: torch.Tensor,
+                    seq_lens: torch.Tensor, scale: float, *, causal: bool = False, window: int = 0,
+                    group_size: int = 64, bits: int = 8, max_len: Optional[int] = None,
+                    out: Optional[torch.Tensor] = None, kernel: str = "auto") -> torch.Tensor:
+    """softmax(scale * q K^T + mask) V over paged pools: sequence b holds seq_lens[b] rows in the
+    pages block_tables[b]; queries [B, Hq, L, D] sit at its last L positions. max_len bounds
+    seq_lens (default: the table's capacity) and sizes the split plan."""
+    _check_triple(k_pool, "k_pool")
+    _check_triple(v_pool, "v_pool")
+    dev = _require_cuda(queries, *k_pool, *v_pool)
+    if queries.dim() != 4:
+        raise ValueError(f"queries must be [B, Hq, L, D], got {tuple(queries.shape)}")
+    B, Hq, L, D = queries.shape
+    _check_table(block_tables, B, dev)
+    if seq_lens.dtype != torch.int32 or seq_lens.numel() != B or seq_lens.device != dev:
+        raise ValueError("seq_lens must be an int32 tensor of B entries on the queries' device")
+    Hkv = k_pool[0].shape[1]
+    if k_pool[0].shape[2] != PAGE_ROWS or k_pool[1].dtype != queries.dtype:
+        raise ValueError(f"pools must be [num_pages, Hkv, {PAGE_ROWS}, *] with scales in the queries' dtype")
+    if Hq % Hkv:
+        raise ValueError(f"Hq={Hq} is not a multiple of Hkv={Hkv}")
+    S = int(max_len) if max_len is not None else block_tables.shape[1] * PAGE_ROWS
+    if not _rows_ok(queries):
+        queries = queries.contiguous()
+    if out is None:
+        out = torch.empty((B, Hq, L, D), dtype=queries.dtype, device=dev)
+    if kernel == "auto":
+        kernel = "decode" if ((Hq // Hkv) * L <= decode_rows_per_pass(D) or D != 128) else "prefill"
+    lib = _lib.lib()
+    ws_fn = lib.kvq_decode_workspace_size if kernel == "decode" else lib.kvq_prefill_workspace_size
+    nbytes = ws_fn(B, Hq, Hkv, L, D, S, int(window))
+    if nbytes == 0:
+        raise NotImplementedError(f"{kernel} attention does not support B={B} Hq={Hq} Hkv={Hkv} L={L} D={D} S={S}")
+    stream = _lib.stream_ptr(dev)
+    ws = _workspace(dev, stream, nbytes)
+    qr, orr = _lib.rows(queries), _lib.rows(out)
+    kq, vq = _lib.qtensor(*k_pool), _lib.qtensor(*v_pool)
+    fn = lib.kvq_paged_decode_attn if kernel == "decode" else lib.kvq_paged_prefill_attn
+    rc = fn(ctypes.byref(qr), ctypes.byref(kq), ctypes.byref(vq), k_pool[0].shape[0], block_tables.data_ptr(),
+            block_tables.stride(0), seq_lens.data_ptr(), ctypes.byref(orr), B, Hq, Hkv, L, D, S, int(bits),
+            int(group_size), _lib.dtype_code(queries.dtype), float(scale), int(bool(causal)), int(window),
+            ws.data_ptr(), ws.numel() * ws.element_size(), stream)
+    _lib.check(rc, f"kvq_paged_{kernel}_attn")
+    return out
