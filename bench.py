@@ -30,7 +30,8 @@ Algorithmic bytes of one decode call:
 = 272 B per cached token and KV head at 8 bits, 144 B at 4 bits (D = 128, G = 64); an
 unquantized cache (the "-dense" extras) reads D*2 bytes per row, 512 B per token and KV head.
 
-The "extra" object also times the other decode configurations and, over unquantized caches, the
+The "extra" object also times the other decode configurations, C2 at batch 8 over a paged pool
+(64-row pages in shuffled order, read through block tables), and, over unquantized caches, the
 C5 window layer's decode step and prefill chunk and a C3 chunk (attention FLOPs: 4 * D * Hq per
 unmasked query-key pair).
 
@@ -218,6 +219,79 @@ def time_decode(cfg, steps, warmup, device, want_parity=False):
         res["cpu_inputs"] = (q, caches[0], scale)
     del graph, calls, gcalls
     return res
+
+
+def time_paged_decode(cfg, steps, warmup, device):
+    """The decode workload over a paged pool: each sequence's rows in shuffled 64-row pages read
+    through its block table. Enough disjoint page sets that every call streams from HBM."""
+    import torch
+
+    from myinfer_amd import kernels
+
+    PAGE = kernels.PAGE_ROWS
+    lens = seq_lens_of(cfg)
+    B, Hq, Hkv, D, bits = cfg["B"], cfg["Hq"], cfg["Hkv"], cfg["D"], cfg["bits"]
+    T = getattr(torch, cfg["dtype"])
+    nbytes = decode_bytes(lens, Hq, Hkv, D, bits)
+    ncache = max(3, math.ceil(2.5 * MALL_BYTES / nbytes))
+    per_set = sum(math.ceil(n / PAGE) for n in lens)
+    npages = ncache * per_set
+    log(f"[bench] {cfg['desc']} (paged): {nbytes / 1e6:.2f} MB per call, {ncache} page sets of {per_set} pages")
+    W, G = D * bits // 32, D // 64
+    pools = []
+    for _ in range(2):
+        codes = torch.empty((npages, Hkv, PAGE, W), dtype=torch.int32, device=device).view(torch.uint32)
+        sc = torch.empty((npages, Hkv, PAGE, G), dtype=T, device=device)
+        pools.append((codes, sc, torch.empty_like(sc)))
+    g = torch.Generator().manual_seed(cfg["seed"] + 11)
+    perm = torch.randperm(npages, generator=g).tolist()
+    width = max(math.ceil(n / PAGE) for n in lens)
+    gd = torch.Generator(device=device).manual_seed(cfg["seed"] + 12)
+    tables, k = [], 0
+    for _ in range(ncache):
+        rows = []
+        for n in lens:
+            need = math.ceil(n / PAGE)
+            rows.append(perm[k:k + need] + [perm[k + need - 1]] * (width - need))
+            k += need
+        t = torch.tensor(rows, dtype=torch.int32, device=device)
+        for b, n in enumerate(lens):
+            x = torch.randn((1, Hkv, n, D), generator=gd, device=device).to(T)
+            y = torch.randn((1, Hkv, n, D), generator=gd, device=device).to(T)
+            kernels.paged_quantize_append(x, pools[0], y, pools[1], t[b:b + 1], bits=bits)
+        tables.append(t)
+    q = torch.randn((B, Hq, 1, D), generator=gd, device=device).to(T)
+    out = torch.empty_like(q)
+    sl = torch.tensor(lens, dtype=torch.int32, device=device)
+    scale = 1.0 / math.sqrt(D)
+    S = max(lens)
+
+    def call(i):
+        kernels.paged_attention(q, pools[0], pools[1], tables[i % ncache], sl, scale, bits=bits, max_len=S, out=out,
+                                kernel="decode")
+
+    for i in range(warmup):
+        call(i)
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        call(0)  # the side stream's workspace exists before capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        for i in range(steps):
+            call(i)
+    graph.replay()
+    torch.cuda.synchronize()
+    s_, e_ = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s_.record()
+    graph.replay()
+    e_.record()
+    torch.cuda.synchronize()
+    ms = s_.elapsed_time(e_) / steps
+    del graph
+    return dict(bytes=nbytes, ms_per_step=ms, gbs=nbytes / (ms * 1e-3) / 1e9)
 
 
 def parity_check(cfg, q, cache, sl, scale):
@@ -615,6 +689,11 @@ def main():
                            "kernel_us": round(r["call_us_mean"], 3)}
             log(f"[bench] {name}: {r['gbs']:.1f} GB/s ({r['ms_per_step'] * 1e3:.2f} us/step)")
             torch.cuda.empty_cache()
+        r = time_paged_decode(DECODE["C2-b8"], args.steps, args.warmup, device)
+        extra["C2-b8-paged"] = {"gbs": round(r["gbs"], 1), "frac": round(r["gbs"] / PEAK_HBM_GBS, 4),
+                                "us_per_step": round(r["ms_per_step"] * 1e3, 3), "bytes": r["bytes"]}
+        log(f"[bench] C2-b8-paged: {r['gbs']:.1f} GB/s ({r['ms_per_step'] * 1e3:.2f} us/step)")
+        torch.cuda.empty_cache()
         for name, r in dense_prefill_extras(min(args.steps, 20), device).items():
             extra[name] = r
             log(f"[bench] {name}: {r['tflops']:.1f} TFLOP/s ({r['us_per_call']:.1f} us/call)")
