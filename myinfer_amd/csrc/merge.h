@@ -47,63 +47,82 @@ struct MergeParams {
   int Hq, Hkv, L, rep, R, rowblocks, nsplit;
 };
 
-// One wave per (output row, 64 columns) item, grid-stride over the items beyond two waves of
-// resident workgroups. Every lane issues all its partial
-// loads (32 at a time) before the weights are formed, so an item costs one round trip.
+// One thread per (output row, 4 columns): the D/4 threads of a row load its float4 of every split
+// at once, share the split weights through LDS (computed by the row's threads from the (m, l)
+// pairs, a few splits each) and sum the splits in split order. One wave per workgroup: 64 / (D/4)
+// rows, so a call spreads its partial reads over many CUs.
 template <typename T, int D>
-__global__ __launch_bounds__(64) void combine_kernel(MergeParams p, int nitems) {
-  constexpr int CH = 32;
-  __shared__ float s_w[kMaxSplit];
-  const int lane = threadIdx.x;
-  for (int item = blockIdx.x; item < nitems; item += gridDim.x) {
-    const int grow = item / (D / 64), d = (item % (D / 64)) * 64 + lane;
-    const int l = grow % p.L, h = (grow / p.L) % p.Hq, b = grow / (p.L * p.Hq);
-    const int kvh = h / p.rep;
-    const int rw = (h - kvh * p.rep) * p.L + l;
-    const int unit = (b * p.Hkv + kvh) * p.rowblocks + rw / p.R;
-    const int64_t base = (int64_t)unit * p.nsplit * p.R + rw % p.R;  // split s at base + s * R
-    const float* po = p.part_o + base * D + d;
-    float o[CH];
+__global__ __launch_bounds__(64) void combine_kernel(MergeParams p, int nrows) {
+  constexpr int TPR = D / 4;      // threads per row
+  constexpr int RPW = 64 / TPR;   // rows per workgroup
+  constexpr int SPT = kMaxSplit / TPR;  // splits whose (m, l) one thread reads
+  constexpr int CH = 32;          // partial loads in flight per thread
+  __shared__ float s_w[RPW][kMaxSplit];
+  const int tr = threadIdx.x / TPR, j = threadIdx.x % TPR;
+  const int grow = blockIdx.x * RPW + tr;
+  const bool ok = grow < nrows;
+  const int g = ok ? grow : 0;
+  const int l = g % p.L, h = (g / p.L) % p.Hq, b = g / (p.L * p.Hq);
+  const int kvh = h / p.rep;
+  const int rw = (h - kvh * p.rep) * p.L + l;
+  const int unit = (b * p.Hkv + kvh) * p.rowblocks + rw / p.R;
+  const int64_t base = (int64_t)unit * p.nsplit * p.R + rw % p.R;  // split s at base + s * R
+  const f4* po = (const f4*)(p.part_o + base * D) + j;
+  const int64_t sstride = (int64_t)p.R * D / 4;  // float4s between splits
+  f4 o[CH];
 #pragma unroll
-    for (int u = 0; u < CH; ++u) o[u] = u < p.nsplit ? po[(int64_t)u * p.R * D] : 0.0f;
-    {
-      const float2* ml = (const float2*)p.part_ml + base;
-      const float2 v0 = lane < p.nsplit ? ml[(int64_t)lane * p.R] : make_float2(-INFINITY, 0.0f);
-      const float2 v1 = lane + 64 < p.nsplit ? ml[(int64_t)(lane + 64) * p.R] : make_float2(-INFINITY, 0.0f);
-      const float m0 = v0.y > 0.0f ? v0.x : -INFINITY, m1 = v1.y > 0.0f ? v1.x : -INFINITY;
-      const float M = wave_max(fmaxf(m0, m1));
-      const float w0 = (M == -INFINITY || m0 == -INFINITY) ? 0.0f : exp2_fast(m0 - M);
-      const float w1 = (M == -INFINITY || m1 == -INFINITY) ? 0.0f : exp2_fast(m1 - M);
-      const float Lsum = wave_sum(w0 * v0.y + w1 * v1.y);
-      const float inv = Lsum > 0.0f ? 1.0f / Lsum : 0.0f;
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");  // the previous item's reads of s_w are done
-      __builtin_amdgcn_wave_barrier();
-      if (lane < p.nsplit) s_w[lane] = w0 * inv;
-      if (lane + 64 < p.nsplit) s_w[lane + 64] = w1 * inv;
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-    float acc = 0.0f;
+  for (int u = 0; u < CH; ++u) o[u] = u < p.nsplit ? po[u * sstride] : f4{0, 0, 0, 0};
+  // the row's weights 2^(m_s - M) / sum_s 2^(m_s - M) l_s, this thread's splits j, j + TPR, ...
+  const float2* ml = (const float2*)p.part_ml + base;
+  float mk[SPT], lk[SPT];
+  float M = -INFINITY;
+#pragma unroll
+  for (int k = 0; k < SPT; ++k) {
+    const int sp = j + TPR * k;
+    const float2 v = sp < p.nsplit ? ml[(int64_t)sp * p.R] : make_float2(-INFINITY, 0.0f);
+    mk[k] = v.y > 0.0f ? v.x : -INFINITY;
+    lk[k] = v.y;
+    M = fmaxf(M, mk[k]);
+  }
+#pragma unroll
+  for (int m = 1; m < TPR; m <<= 1) M = fmaxf(M, shfl_xor(M, m));
+  float Ls = 0.0f;
+#pragma unroll
+  for (int k = 0; k < SPT; ++k) {
+    mk[k] = (M == -INFINITY || mk[k] == -INFINITY) ? 0.0f : exp2_fast(mk[k] - M);
+    Ls += mk[k] * lk[k];
+  }
+#pragma unroll
+  for (int m = 1; m < TPR; m <<= 1) Ls += shfl_xor(Ls, m);
+  const float inv = Ls > 0.0f ? 1.0f / Ls : 0.0f;
+#pragma unroll
+  for (int k = 0; k < SPT; ++k)
+    if (j + TPR * k < p.nsplit) s_w[tr][j + TPR * k] = mk[k] * inv;
+  __syncthreads();
+  f4 acc = {0, 0, 0, 0};
+#pragma unroll
+  for (int u = 0; u < CH; ++u)
+    if (u < p.nsplit) acc += s_w[tr][u] * o[u];
+  for (int s0 = CH; s0 < p.nsplit; s0 += CH) {
+#pragma unroll
+    for (int u = 0; u < CH; ++u) o[u] = s0 + u < p.nsplit ? po[(s0 + u) * sstride] : f4{0, 0, 0, 0};
 #pragma unroll
     for (int u = 0; u < CH; ++u)
-      if (u < p.nsplit) acc += s_w[u] * o[u];
-    for (int s0 = CH; s0 < p.nsplit; s0 += CH) {
-#pragma unroll
-      for (int u = 0; u < CH; ++u) o[u] = s0 + u < p.nsplit ? po[(int64_t)(s0 + u) * p.R * D] : 0.0f;
-#pragma unroll
-      for (int u = 0; u < CH; ++u)
-        if (s0 + u < p.nsplit) acc += s_w[s0 + u] * o[u];
-    }
-    p.out[(int64_t)b * p.o_sb + (int64_t)h * p.o_sh + (int64_t)l * p.o_sl + d] = from_float(acc, T{});
+      if (s0 + u < p.nsplit) acc += s_w[tr][s0 + u] * o[u];
   }
+  if (!ok) return;
+  uint16_t* dst = p.out + (int64_t)b * p.o_sb + (int64_t)h * p.o_sh + (int64_t)l * p.o_sl + 4 * j;
+  u2 w;
+  w[0] = (uint32_t)from_float(acc[0], T{}) | ((uint32_t)from_float(acc[1], T{}) << 16);
+  w[1] = (uint32_t)from_float(acc[2], T{}) | ((uint32_t)from_float(acc[3], T{}) << 16);
+  *(u2*)dst = w;
 }
 
 template <typename T, int D>
 inline hipError_t launch_combine(const MergeParams& m, int B, hipStream_t stream) {
-  const int nitems = B * m.Hq * m.L * (D / 64);
-  const int grid = nitems < 16384 ? nitems : 16384;
-  hipLaunchKernelGGL((combine_kernel<T, D>), dim3(grid), dim3(64), 0, stream, m, nitems);
+  const int nrows = B * m.Hq * m.L;
+  const int grid = (nrows + (256 / D) - 1) / (256 / D);  // 64 / (D / 4) rows per workgroup
+  hipLaunchKernelGGL((combine_kernel<T, D>), dim3(grid), dim3(64), 0, stream, m, nrows);
   return hipGetLastError();
 }
 

@@ -526,16 +526,27 @@ __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) 
 #pragma unroll
         for (int i = 0; i < 16; ++i) sacc[kb][i] *= p.scale_log2;
     }
-    // this lane's query sees keys k0 + 32kb + 8(i/4) + 4hh + i%4
+    // this lane's query sees keys k0 + 32kb + 8(i/4) + 4hh + i%4. Only tiles on a causal diagonal
+    // or window edge need a mask (a branch the whole workgroup takes or skips); there, each element's
+    // offset c = 32kb + 8(i/4) + i%4 is a constant compared with the lane's bounds
     const bool need_mask = !(k0 >= lo_all && k0 + kPT <= hi_all);
-    if (need_mask) {
+    if (__builtin_expect(need_mask, 0)) {
+      const int lo = lo_r - k0 - 4 * hh, hi = hi_r - k0 - 4 * hh;
+      if (lo <= 0) {  // no key of the tile is below the lane's window
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+        for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int key = k0 + 32 * kb + 8 * (i >> 2) + 4 * hh + (i & 3);
-          if (key < lo_r || key >= hi_r) sacc[kb][i] = -INFINITY;
-        }
+          for (int i = 0; i < 16; ++i)
+            if (32 * kb + 8 * (i >> 2) + (i & 3) >= hi) sacc[kb][i] = -INFINITY;
+      } else {
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int c = 32 * kb + 8 * (i >> 2) + (i & 3);
+            if (c < lo || c >= hi) sacc[kb][i] = -INFINITY;
+          }
+      }
     }
     float tm = -INFINITY;
 #pragma unroll
