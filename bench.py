@@ -31,7 +31,9 @@ Algorithmic bytes of one decode call:
 unquantized cache (the "-dense" extras) reads D*2 bytes per row, 512 B per token and KV head.
 
 The "extra" object also times the other decode configurations, C2 at batch 8 over a paged pool
-(64-row pages in shuffled order, read through block tables), and, over unquantized caches, the
+(64-row pages in shuffled order, read through block tables), the C3 chunk's cache update with and
+without fused RoPE (device time from a graph replay, and the host time of an eager call), and,
+over unquantized caches, the
 C5 window layer's decode step and prefill chunk and a C3 chunk (attention FLOPs: 4 * D * Hq per
 unmasked query-key pair).
 
@@ -529,6 +531,65 @@ def dense_prefill_extras(steps, device):
     return res
 
 
+def append_extras(device, calls=200):
+    """The C3 chunk's cache update: quantize-append of 512 rows x 4 KV heads (bf16, 8-bit), plain and
+    with the keys rotated in the same launch (kvq_rope_quantize_append); device microseconds per call
+    (graph replay) and the HBM bytes it moves (reads 2 B and writes 1.0625 B per element, K and V),
+    and the host microseconds of one eager call from Python, plain and through prepare_append."""
+    import torch
+
+    from myinfer_amd import kernels
+
+    g = torch.Generator(device=device).manual_seed(1009)
+    k = torch.randn((1, 4, 512, 128), generator=g, device=device).to(torch.bfloat16)
+    v = torch.randn((1, 4, 512, 128), generator=g, device=device).to(torch.bfloat16)
+
+    def triple():
+        c = torch.zeros((1, 4, 16384, 32), dtype=torch.int32, device=device).view(torch.uint32)
+        sc = torch.zeros((1, 4, 16384, 2), dtype=torch.bfloat16, device=device)
+        return c, sc, torch.zeros_like(sc)
+
+    kd, vd = triple(), triple()
+    rope = kernels.Rope(128, False, 1000000.0)
+    res = {}
+    for name, kw in (("append", {}), ("rope_append", {"rope": rope})):
+        kernels.quantize_append(k, kd, v, vd, row_offset=15872, bits=8, **kw)
+        torch.cuda.synchronize()
+        # device time: the calls captured in a HIP graph and replayed
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=side):
+            for _ in range(calls):
+                kernels.quantize_append(k, kd, v, vd, row_offset=15872, bits=8, **kw)
+        graph.replay()
+        torch.cuda.synchronize()
+        s_, e_ = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s_.record()
+        graph.replay()
+        e_.record()
+        torch.cuda.synchronize()
+        us = 1e3 * s_.elapsed_time(e_) / calls
+        # host cost of one eager call from Python (descriptor packing and the foreign call)
+        t0 = time.perf_counter()
+        for _ in range(calls):
+            kernels.quantize_append(k, kd, v, vd, row_offset=15872, bits=8, **kw)
+        host_us = 1e6 * (time.perf_counter() - t0) / calls
+        torch.cuda.synchronize()
+        # the same through a prepared call (descriptors built once, as the cache objects do)
+        call = kernels.prepare_append(kd, vd, bits=8, **kw)
+        t0 = time.perf_counter()
+        for _ in range(calls):
+            call(k, v, 15872)
+        prep_us = 1e6 * (time.perf_counter() - t0) / calls
+        torch.cuda.synchronize()
+        nbytes = 2 * 4 * 512 * (128 * 2 + 128 + 8)
+        res[name] = {"us_per_call": round(us, 2), "gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
+                     "host_us_per_eager_call": round(host_us, 2), "host_us_per_prepared_call": round(prep_us, 2)}
+        del graph
+    return res
+
+
 def prefill_parity(cfg, q, out, kt, vt, scale, c):
     """Chunk c's output (as left by the timed steps) against the exact fp64 oracle."""
     import numpy as np
@@ -694,6 +755,10 @@ def main():
                                 "us_per_step": round(r["ms_per_step"] * 1e3, 3), "bytes": r["bytes"]}
         log(f"[bench] C2-b8-paged: {r['gbs']:.1f} GB/s ({r['ms_per_step'] * 1e3:.2f} us/step)")
         torch.cuda.empty_cache()
+        for name, r in append_extras(device).items():
+            extra["C3-chunk-" + name] = r
+            log(f"[bench] C3-chunk-{name}: {r['us_per_call']:.2f} us/call on the device ({r['gbs']:.0f} GB/s); "
+                f"{r['host_us_per_eager_call']:.1f} us of host time per eager call")
         for name, r in dense_prefill_extras(min(args.steps, 20), device).items():
             extra[name] = r
             log(f"[bench] {name}: {r['tflops']:.1f} TFLOP/s ({r['us_per_call']:.1f} us/call)")

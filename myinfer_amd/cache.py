@@ -300,8 +300,13 @@ class QuantizedKVCache:
         L = keys.shape[2]
         if self.keys is None or prev + L > self.keys[0].shape[2]:
             self._resize(keys, values, L)
-        kernels.quantize_append(keys, self.keys, values, self.values, row_offset=prev,
-                                group_size=self.group_size, bits=self.bits, rope=rope)
+        # the append's descriptors are built once per buffer set, RoPE and stream
+        key = (id(self.keys[0]), id(self.values[0]), rope, torch.cuda.current_stream(keys.device).cuda_stream)
+        if getattr(self, "_append_key", None) != key:
+            self._append = kernels.prepare_append(self.keys, self.values, group_size=self.group_size,
+                                                  bits=self.bits, rope=rope)
+            self._append_key = key
+        self._append(keys, values, prev)
         self.offset += L
         return self.fetch()
 

@@ -126,6 +126,84 @@ def quantize_append(k: torch.Tensor, k_dst: Triple, v: Optional[torch.Tensor] = 
         _lib.check(rc, "kvq_rope_quantize_append")
 
 
+class AppendCall:
+    """A quantize-append into fixed destination buffers with its C-ABI descriptors built once.
+
+    ``prepare_append`` validates the destinations; calling the object with new source rows fills
+    two preallocated row descriptors and makes one foreign call, so a decode loop pays a few
+    microseconds of host time per layer instead of rebuilding every descriptor. Launches go to
+    the stream that was current at preparation time.
+    """
+
+    def __init__(self, k_dst: Triple, v_dst: Optional[Triple], group_size: int, bits: int,
+                 rope: Optional[Rope]):
+        _check_triple(k_dst, "k_dst")
+        tens = list(k_dst)
+        if v_dst is not None:
+            _check_triple(v_dst, "v_dst")
+            tens += list(v_dst)
+        self._dev = _require_cuda(*tens)
+        self._k_dst, self._v_dst = k_dst, v_dst  # the descriptors point into these
+        codes, scales, _ = k_dst
+        self._lead = tuple(codes.shape[:2])
+        self._rows = min(codes.shape[2], scales.shape[2])
+        self._widths = (codes.shape[3], scales.shape[3])
+        if v_dst is not None:
+            if tuple(v_dst[0].shape) != tuple(codes.shape) or tuple(v_dst[1].shape) != tuple(scales.shape):
+                raise ValueError("k_dst and v_dst must have the same shapes")
+            if v_dst[1].dtype != scales.dtype:
+                raise ValueError("k_dst and v_dst must share a dtype")
+        self._kq = _lib.qtensor(*k_dst)
+        self._vq = _lib.qtensor(*v_dst) if v_dst is not None else None
+        self._kr, self._vr = _lib.Rows(), _lib.Rows()
+        self._dtype = k_dst[1].dtype
+        self._code = _lib.dtype_code(self._dtype)
+        self._bits, self._group = int(bits), int(group_size)
+        self._rope = rope
+        self._rp = rope.params(0) if rope is not None else None
+        lib = _lib.lib()
+        self._fn = lib.kvq_rope_quantize_append if rope is not None else lib.kvq_quantize_append
+        self._stream = _lib.stream_ptr(self._dev)
+
+    def __call__(self, k: torch.Tensor, v: Optional[torch.Tensor], row_offset: int,
+                 rope_offset: Optional[int] = None) -> None:
+        if k.dtype != self._dtype or k.device != self._dev or k.dim() != 4 or k.stride(-1) != 1:
+            raise ValueError("rows must match the prepared dtype and device, as [B, H, L, D] with D contiguous")
+        B, H, L, D = k.shape
+        if (B, H) != self._lead:
+            raise ValueError(f"destination leads {self._lead} do not match source {(B, H)}")
+        if row_offset < 0 or row_offset + L > self._rows:
+            raise ValueError(f"rows [{row_offset}, {row_offset + L}) exceed the destination's {self._rows} rows")
+        if self._widths != (D * self._bits // 32, D // self._group):
+            raise ValueError("destination row widths do not match D, bits and group_size")
+        kr = self._kr
+        kr.data = k.data_ptr()
+        kr.stride_b, kr.stride_h, kr.stride_l = k.stride()[:3]
+        vr_p = vq_p = None
+        if v is not None:
+            if self._vq is None or v.shape != k.shape or v.dtype != k.dtype or v.stride(-1) != 1:
+                raise ValueError("values must match the keys and a prepared value destination")
+            vr = self._vr
+            vr.data = v.data_ptr()
+            vr.stride_b, vr.stride_h, vr.stride_l = v.stride()[:3]
+            vr_p, vq_p = ctypes.byref(vr), ctypes.byref(self._vq)
+        if self._rp is None:
+            rc = self._fn(ctypes.byref(kr), ctypes.byref(self._kq), vr_p, vq_p, int(row_offset), B, H, L, D,
+                          self._bits, self._group, self._code, self._stream)
+        else:
+            self._rp.offset = int(row_offset if rope_offset is None else rope_offset)
+            rc = self._fn(ctypes.byref(kr), ctypes.byref(self._kq), vr_p, vq_p, ctypes.byref(self._rp),
+                          int(row_offset), B, H, L, D, self._bits, self._group, self._code, self._stream)
+        if rc:
+            _lib.check(rc, "kvq_rope_quantize_append" if self._rp is not None else "kvq_quantize_append")
+
+
+def prepare_append(k_dst: Triple, v_dst: Optional[Triple] = None, *, group_size: int = 64, bits: int = 8,
+                   rope: Optional[Rope] = None) -> AppendCall:
+    """Build an ``AppendCall`` for repeated appends into the same (codes, scales, biases) buffers."""
+    return AppendCall(k_dst, v_dst, group_size, bits, rope)
+
+
 def quantize(x: torch.Tensor, group_size: int = 64, bits: int = 8) -> Triple:
     """Counterpart of mx.quantize(x, group_size, bits) for x [..., D] on the GPU:
     returns (codes uint32 [..., D*bits/32], scales [..., D/G], biases [..., D/G])."""

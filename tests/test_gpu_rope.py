@@ -171,3 +171,33 @@ def test_rope_then_attention_depends_on_relative_position():
     # fp16 rounding of the rotated rows and the fp32 angle (error ~ position * 2^-24 rad) bound the
     # spread; a rotation that is not a function of m - n moves the dot by O(|q| |k|)
     assert max(dots) - min(dots) <= 1e-2 * float(q.float().norm() * k.float().norm()), dots
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("use_rope", [False, True])
+@pytest.mark.parametrize("with_v", [False, True])
+def test_prepared_append_equals_append(dtype, use_rope, with_v):
+    # prepare_append builds the descriptors once; each call must store exactly what quantize_append
+    # stores, for strided sources and successive offsets
+    print(f"prepared append dtype={dtype} rope={use_rope} v={with_v}", flush=True)
+    r = kernels.Rope(128, False, 10000.0, 1.0) if use_rope else None
+    B, H, D, cap = 2, 4, 128, 320
+    src_k = seeded_normal((B, 300, H, D), 71, dtype).to(DEV).transpose(1, 2)  # [B, H, L, D], strided
+    src_v = seeded_normal((B, H, 300, D), 72, dtype).to(DEV)
+    a_k, a_v = _alloc(B, H, cap, D, 4, 64, dtype), _alloc(B, H, cap, D, 4, 64, dtype)
+    b_k, b_v = _alloc(B, H, cap, D, 4, 64, dtype), _alloc(B, H, cap, D, 4, 64, dtype)
+    call = kernels.prepare_append(b_k, b_v if with_v else None, group_size=64, bits=4, rope=r)
+    for lo, hi in ((0, 1), (1, 130), (130, 131), (131, 300)):
+        k, v = src_k[:, :, lo:hi], src_v[:, :, lo:hi] if with_v else None
+        kernels.quantize_append(k, a_k, v, a_v if with_v else None, row_offset=lo + 7, group_size=64, bits=4,
+                                rope=r, rope_offset=lo + 100)
+        call(k, v, lo + 7, rope_offset=lo + 100)
+    torch.cuda.synchronize()
+    for x, y in zip((*a_k, *a_v), (*b_k, *b_v)):
+        assert torch.equal(x, y)
+    with pytest.raises(ValueError):
+        call(src_k[:, :, :20], None, cap - 19)  # past the last row
+    with pytest.raises(ValueError):
+        call(src_k[:1, :, :4], None, 0)  # batch does not match the destination
+    with pytest.raises(ValueError):
+        call(src_k[:, :, :4].float(), None, 0)  # dtype differs
