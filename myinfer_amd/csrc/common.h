@@ -58,6 +58,19 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float& lo, float& hi) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
+// Two values packed as the operand type (f16 or bf16 by the element tag), rounded to nearest even.
+__device__ __forceinline__ uint32_t pack2(float lo, float hi, F16) { return pack_f16x2(lo, hi); }
+__device__ __forceinline__ uint32_t pack2(float lo, float hi, BF16) { return pack_bf16x2(lo, hi); }
+
+// acc + lo + hi of two packed 16-bit values (one dot-product instruction against (1, 1)): sums the
+// rounded probabilities exactly as the MFMA consumes them.
+__device__ __forceinline__ float add_pair(uint32_t packed, float acc, F16) {
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, packed), h2{(_Float16)1.0f, (_Float16)1.0f}, acc, false);
+}
+__device__ __forceinline__ float add_pair(uint32_t packed, float acc, BF16) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2, packed), bf2{(__bf16)1.0f, (__bf16)1.0f}, acc, false);
+}
+
 // MFMA on 16-bit operands given as raw bit patterns, f16 or bf16 by the element tag.
 __device__ __forceinline__ f4 mfma_16x16x32(u4 a, u4 b, f4 c, F16) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, a), __builtin_bit_cast(h8, b), c, 0, 0, 0);

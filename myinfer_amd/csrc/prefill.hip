@@ -568,21 +568,20 @@ __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) 
     // the row sum is kept in fp32 (of the rounded values for bf16 operands, so the output stays a
     // convex combination of V rows)
     const float nm = m_run == -INFINITY ? 0.0f : -m_run;
+    // the row sum of the rounded probabilities, in two chains
+    float lsum[2] = {0.0f, 0.0f};
     u4 pop[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        float p0 = exp2_fast(fmaf(sacc[j >> 1][8 * (j & 1) + 2 * e], inv2, nm));
-        float p1 = exp2_fast(fmaf(sacc[j >> 1][8 * (j & 1) + 2 * e + 1], inv2, nm));
-        if constexpr (OT::id == KVQ_DTYPE_BF16) {
-          pop[j][e] = pack_bf16x2(p0, p1);
-        } else {
-          pop[j][e] = pack_f16x2(p0, p1);
-        }
-        l_run += p0 + p1;
+        const float p0 = exp2_fast(fmaf(sacc[j >> 1][8 * (j & 1) + 2 * e], inv2, nm));
+        const float p1 = exp2_fast(fmaf(sacc[j >> 1][8 * (j & 1) + 2 * e + 1], inv2, nm));
+        pop[j][e] = pack2(p0, p1, OT{});
+        lsum[e & 1] = add_pair(pop[j][e], lsum[e & 1], OT{});
       }
     }
+    l_run += lsum[0] + lsum[1];
     // O^T += V^T P^T
     {
       // the 16 V^T operands stream through a 4-deep register ring; the 4 dim blocks alternate
