@@ -217,7 +217,7 @@ def time_decode(cfg, steps, warmup, device, want_parity=False):
                call_us_mean=call_us_mean, call_us_median=call_us_median,
                kernel_gbs=nbytes / (call_us_mean * 1e-6) / 1e9, seq_lens=lens)
     if want_parity:
-        res["parity"] = parity_check(cfg, q, caches[0], sl, scale)
+        res["parity"], res["parity_arrays"] = parity_check(cfg, q, caches[0], sl, scale)
         res["cpu_inputs"] = (q, caches[0], scale)
     del graph, calls, gcalls
     return res
@@ -319,8 +319,9 @@ def parity_check(cfg, q, cache, sl, scale):
     vdq = OQ.dequantize(*trip(cache[1]), dt, 64, cfg["bits"])
     ref = OA.exact_attention(q.cpu().double().numpy(), kdq, vdq, scale, causal=cfg.get("causal", False),
                              window=cfg.get("window", 0), seq_lens=None if sl is None else sl.cpu().tolist())
-    st = OA.error_stats(out.cpu().double().numpy(), ref)
-    return {"vs": "exact fp64 oracle", "max_abs": st["max_abs"], "rel_l2": st["rel_l2"]}
+    got = out.cpu().double().numpy()
+    st = OA.error_stats(got, ref)
+    return {"vs": "exact fp64 oracle", "max_abs": st["max_abs"], "rel_l2": st["rel_l2"]}, (got, ref)
 
 
 def cpu_baseline(cfg, q, cache, scale, budget_s=15.0, max_calls=8):
@@ -344,7 +345,7 @@ def cpu_baseline(cfg, q, cache, scale, budget_s=15.0, max_calls=8):
     t_all = time.perf_counter()
     while len(times) < max_calls and (time.perf_counter() - t_all) < budget_s:
         t0 = time.perf_counter()
-        OA.reference_sdpa(qc, kt, vt, scale, None, 64, cfg["bits"])
+        ref_out = OA.reference_sdpa(qc, kt, vt, scale, None, 64, cfg["bits"])
         times.append(time.perf_counter() - t0)
     times.sort()
     med = times[len(times) // 2]
@@ -365,7 +366,7 @@ def cpu_baseline(cfg, q, cache, scale, budget_s=15.0, max_calls=8):
         "kind": "port",
         "sample": (f"{len(times)} calls of the headline workload (one 32K-token cache, B=1) through "
                    f"oracle.attention.reference_sdpa on the host CPU ({cpu_model}); median {med * 1e3:.1f} ms/call"),
-    }
+    }, ref_out.float().double().numpy()
 
 
 # Prefill workload C3 (seed 1003): Qwen3-30B-A3B shapes, a 16384-token prompt in 512-token chunks;
@@ -466,7 +467,8 @@ def time_prefill(cfg, steps, warmup, device, want_parity=False):
                attn_tflops=flops / (sum(attn_ms) * 1e-3) / 1e12,
                chunk_attn_us={c: round(1e3 * attn_ms[c], 2) for c in (0, nchunk // 2, nchunk - 1)})
     if want_parity:
-        res["parity"] = prefill_parity(cfg, q, out, (kc, ks, kb), (vc, vs, vb), scale, nchunk - 1)
+        res["parity"], res["parity_arrays"] = prefill_parity(cfg, q, out, (kc, ks, kb), (vc, vs, vb), scale,
+                                                             nchunk - 1)
         last = nchunk - 1
         res["cpu_inputs"] = (q[:, :, last * C:], (kc, ks, kb), (vc, vs, vb), scale)
     del graph
@@ -610,8 +612,9 @@ def prefill_parity(cfg, q, out, kt, vt, scale, c):
     vdq = OQ.dequantize(*trip(vt), cfg["dtype"], 64, cfg["bits"])
     qc = q[:, :, c * C:hi].float().cpu().double().numpy()
     ref = OA.exact_attention(qc, kdq, vdq, scale, causal=True)
-    st = OA.error_stats(out[:, :, c * C:hi].float().cpu().double().numpy(), ref)
-    return {"vs": "exact fp64 oracle", "chunk": c, "max_abs": st["max_abs"], "rel_l2": st["rel_l2"]}
+    got = out[:, :, c * C:hi].float().cpu().double().numpy()
+    st = OA.error_stats(got, ref)
+    return {"vs": "exact fp64 oracle", "chunk": c, "max_abs": st["max_abs"], "rel_l2": st["rel_l2"]}, (got, ref)
 
 
 def prefill_cpu_baseline(cfg, q_last, kt, vt, scale, budget_s=20.0):
@@ -635,13 +638,27 @@ def prefill_cpu_baseline(cfg, q_last, kt, vt, scale, budget_s=20.0):
     t_all = time.perf_counter()
     while not times or (time.perf_counter() - t_all < budget_s and len(times) < 3):
         t0 = time.perf_counter()
-        OA.reference_sdpa(qc, ktc, vtc, scale, "causal", 64, cfg["bits"])
+        ref_out = OA.reference_sdpa(qc, ktc, vtc, scale, "causal", 64, cfg["bits"])
         times.append(time.perf_counter() - t0)
     med = sorted(times)[len(times) // 2]
     fl = prefill_flops(N, cfg["Hq"], cfg["D"], N - C, N)
     return {"value": round(fl / med / 1e12, 5), "unit": "TFLOP/s", "cores": torch.get_num_threads(), "kind": "port",
             "sample": f"{len(times)} run(s) of the last 512-token chunk (16384 keys) through oracle.attention."
-                      f"reference_sdpa on the host CPU; median {med:.2f} s"}
+                      f"reference_sdpa on the host CPU; median {med:.2f} s"}, ref_out.float().double().numpy()
+
+
+def add_faithful(parity, arrays, faithful):
+    """Extend a parity record with the error against the reference-faithful CPU port (the output
+    the CPU baseline computed on the same inputs) and that port's own error against exact fp64."""
+    if parity is None or arrays is None or faithful is None:
+        return parity
+    from oracle import attention as OA
+
+    got, exact = arrays
+    a, b = OA.error_stats(got, faithful), OA.error_stats(faithful, exact)
+    parity["vs_faithful_oracle"] = {"max_abs": a["max_abs"], "rel_l2": a["rel_l2"]}
+    parity["faithful_oracle_vs_exact"] = {"max_abs": b["max_abs"], "rel_l2": b["rel_l2"]}
+    return parity
 
 
 TRAFFIC_FILE = Path(__file__).resolve().parent / "profiles" / "hbm_traffic_decode_c2_b1_prefill_c3.md"
@@ -709,7 +726,8 @@ def main():
             f"attention kernels {pr['attn_ms']:.3f} ms -> {pr['attn_tflops']:.1f} TFLOP/s; appends {pr['append_ms']:.3f} ms")
         pcpu = None
         if not args.no_cpu and "cpu_inputs" in pr:
-            pcpu = prefill_cpu_baseline(PREFILL, *pr["cpu_inputs"])
+            pcpu, faithful = prefill_cpu_baseline(PREFILL, *pr["cpu_inputs"])
+            add_faithful(pr.get("parity"), pr.get("parity_arrays"), faithful)
             log(f"[bench] C3 CPU baseline: {pcpu['value']} TFLOP/s on {pcpu['cores']} cores")
         prefill = {
             "metric": "prefill TFLOP/s (% MFMA)",
@@ -770,7 +788,8 @@ def main():
         if q is None:
             r2 = time_decode(head, 1, 0, device, want_parity=True)
             q, cache, scale = r2["cpu_inputs"]
-        cpu = cpu_baseline(head, q, cache, scale)
+        cpu, faithful = cpu_baseline(head, q, cache, scale)
+        add_faithful(res.get("parity"), res.get("parity_arrays"), faithful)
         log(f"[bench] CPU baseline: {cpu['value']} GB/s on {cpu['cores']} cores")
 
     achieved = res["kernel_gbs"]
