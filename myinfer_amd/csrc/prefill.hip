@@ -99,10 +99,22 @@ struct PreParams {
 
 // V^T slot of key `kk` (0..63) inside a tile: the 16 keys of PV k-step j = kk / 16 are stored so
 // that slots 16j + 8h + i hold the keys the score layout gives lane half h at i.
-__device__ __forceinline__ int v_slot_key(int slot) {
-  const int j = slot >> 4, h = (slot >> 3) & 1, i = slot & 7;
-  return 16 * j + (i < 4 ? 4 * h + i : 8 + 4 * h + (i - 4));
+__host__ __device__ constexpr int v_slot_key(int slot) {
+  return 16 * (slot >> 4) + ((slot & 7) < 4 ? 4 * ((slot >> 3) & 1) + (slot & 7) : 8 + 4 * ((slot >> 3) & 1) + (slot & 7) - 4);
 }
+// The 8 keys of V^T slot chunk c8 are v_base_key(c8) + v_key_offset(i): a per-lane base plus
+// compile-time offsets, so the staging addresses them with immediate offsets.
+__host__ __device__ constexpr int v_base_key(int c8) { return 16 * (c8 >> 1) + 4 * (c8 & 1); }
+__host__ __device__ constexpr int v_key_offset(int i) { return i < 4 ? i : i + 4; }
+constexpr bool v_keys_split() {
+  for (int c8 = 0; c8 < 8; ++c8)
+    for (int i = 0; i < 8; ++i)
+      if (v_slot_key(8 * c8 + i) != v_base_key(c8) + v_key_offset(i) || (v_base_key(c8) & 3) != 0 ||
+          (v_key_offset(i) & 7) != (i & 3))
+        return false;
+  return true;
+}
+static_assert(v_keys_split(), "slot keys are a per-lane base (low two bits clear) plus i-dependent offsets");
 
 // Buffer->LDS DMA issued from inline asm: the compiler does not model these loads, so it adds no
 // wait for them before the kernel's LDS accesses; the tile ring orders every slot with explicit
@@ -230,7 +242,8 @@ __device__ __forceinline__ void dequant8(const uint32_t* w, h2 s2, h2 b2, uint32
 // the 8 keys of slot chunk t % 8 at dims [4 (t / 8), +4) and writes 4 V^T rows of 8 slots. Threads
 // 256-511 build K: thread t takes dims [32 q, +32) of key t % 64, q = (t - 256) / 64.
 template <typename T, int BITS>
-__device__ __forceinline__ void stage_from_raw(const uint8_t* raw, _Float16* klds, _Float16* vlds, int tid) {
+__device__ __forceinline__ void stage_from_raw(const uint8_t* raw, _Float16* klds, _Float16* vlds, uint32_t* sbt,
+                                               int tid) {
   using C = RawCfg<BITS>;
   const uint8_t* sbase = raw + 2 * C::KB;
   auto sb_at = [&](int a, int key, int g) -> _Float16 {
@@ -238,19 +251,35 @@ __device__ __forceinline__ void stage_from_raw(const uint8_t* raw, _Float16* kld
   };
   if (tid < 256) {
     const int c8 = tid & 7, d4 = tid >> 3, g = d4 >> 4;
-    const uint8_t* vr = raw + C::KB;
+    // key i of the chunk is kb + v_key_offset(i), and its swizzle key % CPR is (kb % CPR) | (i & 3)
+    // (kb has its low two bits clear, the offsets are i & 3 modulo 8): four code addresses per
+    // lane, one per i & 3, and one scale/bias address; everything else is an immediate offset
+    const int kb = v_base_key(c8);
+    const uint8_t* vr = raw + C::KB + kb * C::ROWB;
+    // the wave's lanes convert the scale and bias of its group g for the 64 keys once (lane = key)
+    // into a per-wave table of (scale, bias) fp16 pairs; each lane then reads the pairs of its 8
+    // keys. Only this wave touches its table and LDS operations of a wave execute in order, so no
+    // barrier is needed.
+    {
+      const int key = tid & 63;
+      const h2 sbp = {sb_at(2, key, g), sb_at(3, key, g)};
+      sbt[key] = __builtin_bit_cast(uint32_t, sbp);
+    }
+    __builtin_amdgcn_wave_barrier();
     uint32_t x[8][2];  // key i, dim pair m
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const int key = v_slot_key(8 * c8 + i);
+      const int ko = v_key_offset(i);
+      const int sw = (kb % C::CPR) | (i & 3);
       uint32_t bytes;  // codes of dims 4 d4 .. 4 d4 + 3 as 4 bytes
       if constexpr (BITS == 8) {
-        bytes = *(const uint32_t*)(vr + key * C::ROWB + 16 * ((d4 >> 2) ^ (key % C::CPR)) + 4 * (d4 & 3));
+        bytes = *(const uint32_t*)(vr + ko * C::ROWB + 16 * ((d4 >> 2) ^ sw) + 4 * (d4 & 3));
       } else {
-        const uint32_t h = *(const uint16_t*)(vr + key * C::ROWB + 16 * ((d4 >> 3) ^ (key % C::CPR)) + 2 * (d4 & 7));
+        const uint32_t h = *(const uint16_t*)(vr + ko * C::ROWB + 16 * ((d4 >> 3) ^ sw) + 2 * (d4 & 7));
         bytes = perm((h >> 4) & 0x0F0Fu, h & 0x0F0Fu, 0x05010400u);
       }
-      const _Float16 sh = sb_at(2, key, g), bh = sb_at(3, key, g);
+      const h2 sbp = __builtin_bit_cast(h2, sbt[kb + ko]);
+      const _Float16 sh = sbp[0], bh = sbp[1];
       x[i][0] = dequant_pair(bytes, 0x04010400u, h2{sh, sh}, h2{bh, bh});
       x[i][1] = dequant_pair(bytes, 0x04030402u, h2{sh, sh}, h2{bh, bh});
     }
@@ -320,6 +349,7 @@ __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) 
   __shared__ __align__(16) _Float16 k_lds[DENSE ? 1 : 2][DENSE ? 8 : kPT * kKS];
   __shared__ __align__(16) _Float16 v_lds[2][128 * kVS];
   __shared__ __align__(16) uint8_t raw[kRawSlots][RC::SLOT];
+  __shared__ uint32_t sb_tab[DENSE ? 1 : kPW / 2][64];  // per V^T-building wave: (scale, bias) pairs
   __shared__ unsigned s_arrived;
 
   const int tid = threadIdx.x;
@@ -469,7 +499,7 @@ __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) 
     } else {
       wait_vm<2 * RC::IPT>();
       __syncthreads();
-      stage_from_raw<T, BITS>(raw[0], k_lds[0], v_lds[0], tid);
+      stage_from_raw<T, BITS>(raw[0], k_lds[0], v_lds[0], sb_tab[wave & 3], tid);
       wait_vm<RC::IPT>();
       __syncthreads();
     }
@@ -494,7 +524,7 @@ __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) 
       if constexpr (DENSE) {
         stage_v_raw(raw[(t + 1) % kRawSlots], v_lds[cur ^ 1], tid - 256, 0);
       } else {
-        stage_from_raw<T, BITS>(raw[(t + 1) % kRawSlots], k_lds[cur ^ 1], v_lds[cur ^ 1], tid);
+        stage_from_raw<T, BITS>(raw[(t + 1) % kRawSlots], k_lds[cur ^ 1], v_lds[cur ^ 1], sb_tab[wave & 3], tid);
       }
     }
 
@@ -599,7 +629,7 @@ __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) 
       if constexpr (DENSE) {
         stage_v_raw(raw[(t + 1) % kRawSlots], v_lds[cur ^ 1], tid, 1);
       } else {
-        stage_from_raw<T, BITS>(raw[(t + 1) % kRawSlots], k_lds[cur ^ 1], v_lds[cur ^ 1], tid);
+        stage_from_raw<T, BITS>(raw[(t + 1) % kRawSlots], k_lds[cur ^ 1], v_lds[cur ^ 1], sb_tab[wave & 3], tid);
       }
     }
     if constexpr (DENSE) {
