@@ -101,3 +101,37 @@ def test_repeated_calls_are_bit_identical():
     outs = [kernels.attention(q, kt, vt, 0.088, causal=True, bits=8, kernel="prefill") for _ in range(3)]
     torch.cuda.synchronize()
     assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("causal,bits", [(False, 8), (True, 8), (False, 4)])
+def test_running_max_moves_mid_split(dtype, causal, bits):
+    # every query shares a +-1 component u, the keys are small noise except three "spike" keys
+    # beta * u that score about 16 beta (log2 units) above the rest. The spikes sit in the third
+    # and fourth tiles of one 256-key split and in the second tile of the last split, so each row's
+    # running maximum is stale by far more than the rescale bound mid-split, with live
+    # accumulators: the probabilities against it would overflow fp16 unless the kernel moves the
+    # maximum, rescales and recomputes. Scores stay moderate, so fp16 operand rounding keeps the
+    # result within the usual bar.
+    print(f"prefill mid-split maxima dtype={dtype} causal={causal} bits={bits}", flush=True)
+    B, Hq, Hkv, L, S, D = 1, 16, 4, 96, 2048, 128
+    g = torch.Generator().manual_seed(95)
+    u = torch.randint(0, 2, (D,), generator=g).float() * 2 - 1
+    k = 0.3 * seeded_normal((B, Hkv, S, D), 96, torch.float32)
+    for pos, beta in ((400, 1.0), (480, 2.0), (1850, 1.5)):
+        k[:, :, pos] = beta * u
+    k = k.to(dtype).to(DEV)
+    v = seeded_normal((B, Hkv, S, D), 97, dtype, DEV)
+    trip = []
+    for x in (k, v):
+        codes = torch.zeros((B, Hkv, S, D * bits // 32), dtype=torch.int32, device=DEV).view(torch.uint32)
+        sc = torch.zeros((B, Hkv, S, D // 64), dtype=dtype, device=DEV)
+        bi = torch.zeros_like(sc)
+        kernels.quantize_append(x, (codes, sc, bi), row_offset=0, group_size=64, bits=bits)
+        trip.append((codes, sc, bi))
+    q = (u + 0.3 * seeded_normal((B, Hq, L, D), 98, torch.float32)).to(dtype).to(DEV)
+    scale = 1.0 / math.sqrt(D)
+    out = kernels.attention(q, trip[0], trip[1], scale, causal=causal, bits=bits, kernel="prefill")
+    torch.cuda.synchronize()
+    ref = exact_reference(q, trip[0], trip[1], scale, bits=bits, causal=causal)
+    assert_close(out, ref, "mid-split maxima")
