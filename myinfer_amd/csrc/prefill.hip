@@ -46,6 +46,7 @@ constexpr int kVS = 72;       // fp16 per V^T row in LDS: 64 + 8
 constexpr float kPSlack = 6.0f;
 constexpr int kPTargetWgs = 256;  // one workgroup per CU
 constexpr int kRawSlots = 3;
+constexpr int kXcds = 8;  // MI355X: 8 XCDs, each with its own L2
 
 // The raw tile ring. A slot holds one 64-key tile as loaded: [K codes][V codes][sK, bK, sV, bV],
 // code rows with their 16-byte chunks XOR-swizzled by row (chunk c of row r at position
@@ -87,6 +88,7 @@ struct PreParams {
   float* part_o;
   float* part_ml;
   unsigned* counters;  // arrivals per unit, zero between launches
+  int xcd_remap;       // 1: the grid is a multiple of the XCD count (see the numbering in the kernel)
   int Hq, Hkv, L, S, rep, nrows, rowblocks, nsplit, nunits;
   float scale_log2;
   int causal, window;
@@ -357,10 +359,19 @@ __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) 
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int qc = lane & 31, hh = lane >> 5;
 
-  const int unit = blockIdx.x / p.nsplit, split = blockIdx.x % p.nsplit;
-  const int b = unit / (p.Hkv * p.rowblocks);
-  const int kvh = (unit / p.rowblocks) % p.Hkv;
-  const int rb = unit % p.rowblocks;
+  // Workgroup numbering: the row blocks of one (sequence, KV head, split) share every K/V tile, so
+  // they are consecutive, and consecutive workgroups are placed on one XCD (the hardware hands
+  // workgroups to the 8 XCDs in turn): each tile is fetched into one L2 rather than eight.
+  int wg = blockIdx.x;
+  if (p.xcd_remap) {
+    const int per_xcd = (int)(gridDim.x / kXcds);
+    wg = (wg % kXcds) * per_xcd + wg / kXcds;
+  }
+  const int rb = wg % p.rowblocks;
+  const int split = (wg / p.rowblocks) % p.nsplit;
+  const int bk = wg / (p.rowblocks * p.nsplit);  // b * Hkv + kvh
+  const int b = bk / p.Hkv, kvh = bk % p.Hkv;
+  const int unit = bk * p.rowblocks + rb;
   const int S_b = p.seq_lens ? min(max(p.seq_lens[b], 0), p.S) : p.S;
 
   // ---- the workgroup's rows, their positions, and the key range they see
@@ -799,6 +810,7 @@ static PreParams prefill_params(const kvq_rows* q, const int32_t* seq_lens, cons
   p.rowblocks = pl.rowblocks;
   p.nsplit = pl.nsplit;
   p.nunits = pl.nunits;
+  p.xcd_remap = ((int64_t)pl.nunits * pl.nsplit) % kXcds == 0;
   p.scale_log2 = scale * 1.4426950408889634f;
   p.causal = causal;
   p.window = window;
