@@ -656,24 +656,50 @@ __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) 
   float l_tot = add_xor32(l_run);
   if (p.nsplit > 1) {
     // Key split: publish this split's partials, count the arrival, and let the unit's last split to
-    // arrive merge them into its own registers. Partials keep the register image, so every access
-    // is a coalesced 1 KiB per wave: o word (4 db + c) of lane `lane` of wave `wave` of split s at
-    // byte ((s * kPW + wave) * 16 + 4 db + c) * 1024 + 16 lane of the unit's o block; (m, l) of
-    // row r at byte 8 (s * kPRows + r) of the unit's (m, l) block.
-    const __amdgpu_buffer_rsrc_t ro = make_rsrc(p.part_o + (int64_t)unit * p.nsplit * (kPRows * 128),
-                                                (uint32_t)p.nsplit * (kPRows * 128 * 4));
-    const __amdgpu_buffer_rsrc_t rm = make_rsrc(p.part_ml + (int64_t)unit * p.nsplit * (kPRows * 2),
-                                                (uint32_t)p.nsplit * (kPRows * 8));
-    const uint32_t lo = (uint32_t)wave * (16 * 1024) + 16 * lane;
-    const uint32_t split_o = kPW * 16 * 1024;
-    const uint32_t row_ml = 8 * (wave * 32 + qc);
+    // arrive merge them into its own registers.
+    //  * A partial row is o / l in fp16, times 2^-e with e chosen per row so every stored value is
+    //    below 2^14, and the row's record (m, l, 2^e). The merge scales row s by w_s l_s 2^e_s.
+    //  * The merging split rounds its own partial through the same fp16 packing, so every split's
+    //    term is formed from the same values whichever split merges: the result is
+    //    bit-reproducible from call to call.
+    //  * The packed row keeps the register image: lane `lane` of wave `wave` of split s holds words
+    //    u (0..7) of 16 bytes at byte ((s * kPW + wave) * 8 + u) * 1024 + 16 lane of the unit's o
+    //    block; word u packs value groups 2u and 2u + 1 (group 4 db + c = oacc[db][4c .. 4c+3]).
+    //    Record of row r at byte 16 (s * kPRows + r) of the unit's record block.
+    const __amdgpu_buffer_rsrc_t ro = make_rsrc((const uint8_t*)p.part_o + (int64_t)unit * p.nsplit * (kPRows * 256),
+                                                (uint32_t)p.nsplit * (kPRows * 256));
+    const __amdgpu_buffer_rsrc_t rm = make_rsrc(p.part_ml + (int64_t)unit * p.nsplit * (kPRows * 4),
+                                                (uint32_t)p.nsplit * (kPRows * 16));
+    const uint32_t lo = (uint32_t)wave * (8 * 1024) + 16 * lane;
+    const uint32_t split_o = kPW * 8 * 1024;
+    const uint32_t row_ml = 16 * (wave * 32 + qc);
+    u4 own[8];
+    float own_sc;
+    {
+      const float inv_l = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+      float mx = 0.0f;
 #pragma unroll
-    for (int db = 0; db < 4; ++db)
+      for (int db = 0; db < 4; ++db)
 #pragma unroll
-      for (int c = 0; c < 4; ++c)
-        store_agent_b128(ro, lo + (4 * db + c) * 1024 + split * split_o,
-                         f4{oacc[db][4 * c], oacc[db][4 * c + 1], oacc[db][4 * c + 2], oacc[db][4 * c + 3]});
-    if (hh == 0) store_agent_b64(rm, row_ml + split * (kPRows * 8), make_float2(m_run, l_tot));
+        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, fabsf(oacc[db][i]));
+      mx = max_xor32(mx) * inv_l;
+      int ex = 0;
+      if (mx >= 16384.0f) frexpf(mx, &ex);
+      const int e = ex > 14 ? ex - 14 : 0;  // mx * 2^-e < 2^14
+      own_sc = ldexpf(1.0f, e);
+      const float f = ldexpf(inv_l, -e);
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int g = 2 * u + h, db = g >> 2, c = g & 3;
+          own[u][2 * h] = pack_f16x2(oacc[db][4 * c] * f, oacc[db][4 * c + 1] * f);
+          own[u][2 * h + 1] = pack_f16x2(oacc[db][4 * c + 2] * f, oacc[db][4 * c + 3] * f);
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) store_agent_b128(ro, lo + u * 1024 + split * split_o, __builtin_bit_cast(f4, own[u]));
+    if (hh == 0) store_agent_b128(rm, row_ml + split * (kPRows * 16), f4{m_run, l_tot, own_sc, 0.0f});
     // The stores are acknowledged (written through to the device's coherence point) before the
     // arrival is counted, so the last arrival sees every split's partials.
     __builtin_amdgcn_s_waitcnt(0);
@@ -687,37 +713,44 @@ __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) 
     float M = l_tot > 0.0f ? m_run : -INFINITY;
     for (int s2 = 0; s2 < p.nsplit; ++s2) {
       if (s2 == split) continue;
-      const float2 ml = load_agent_b64(rm, row_ml, s2 * (kPRows * 8));
-      if (ml.y > 0.0f) M = fmaxf(M, ml.x);
+      const f4 rec = load_agent_b128(rm, row_ml, s2 * (kPRows * 16));
+      if (rec[1] > 0.0f) M = fmaxf(M, rec[0]);
     }
-    // the splits are summed in split order, each term one explicit fma, whichever of them merges:
-    // the result is bit-reproducible from call to call
-    const float w_own = (M == -INFINITY || l_tot <= 0.0f) ? 0.0f : exp2_fast(m_run - M);
+    // the splits are summed in split order, each term one explicit fma
     f16v macc[4];
 #pragma unroll
     for (int db = 0; db < 4; ++db) macc[db] = f16v{};
     float l_acc = 0.0f;
     for (int s2 = 0; s2 < p.nsplit; ++s2) {
+      f4 rec;
+      u4 po[8];
       if (s2 == split) {
-        l_acc = fmaf(w_own, l_tot, l_acc);
+        rec = f4{m_run, l_tot, own_sc, 0.0f};
 #pragma unroll
-        for (int db = 0; db < 4; ++db)
+        for (int u = 0; u < 8; ++u) po[u] = own[u];
+      } else {
+        rec = load_agent_b128(rm, row_ml, s2 * (kPRows * 16));
 #pragma unroll
-          for (int i = 0; i < 16; ++i) macc[db][i] = fmaf(w_own, oacc[db][i], macc[db][i]);
-        continue;
+        for (int u = 0; u < 8; ++u) po[u] = __builtin_bit_cast(u4, load_agent_b128(ro, lo + u * 1024, s2 * split_o));
       }
-      const float2 ml = load_agent_b64(rm, row_ml, s2 * (kPRows * 8));
-      f4 po[16];
+      const float w = (M == -INFINITY || rec[1] <= 0.0f) ? 0.0f : exp2_fast(rec[0] - M);
+      l_acc = fmaf(w, rec[1], l_acc);
+      const float F = (w * rec[1]) * rec[2];
 #pragma unroll
-      for (int u = 0; u < 16; ++u) po[u] = load_agent_b128(ro, lo + u * 1024, s2 * split_o);
-      const float w = (M == -INFINITY || ml.y <= 0.0f) ? 0.0f : exp2_fast(ml.x - M);
-      l_acc = fmaf(w, ml.y, l_acc);
+      for (int u = 0; u < 8; ++u)
 #pragma unroll
-      for (int db = 0; db < 4; ++db)
+        for (int h = 0; h < 2; ++h) {
+          const int g = 2 * u + h, db = g >> 2, c = g & 3;
+          // halves are extracted with integer shifts: converting the elements of an h2 bit-cast
+          // from a u4 element let the compiler (ROCm 7.2) fold all four words of a u4 into the
+          // first one's register in v_fma_mix_f32
 #pragma unroll
-        for (int c = 0; c < 4; ++c)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) macc[db][4 * c + e] = fmaf(w, po[4 * db + c][e], macc[db][4 * c + e]);
+          for (int k = 0; k < 4; ++k) {
+            const uint32_t w = po[u][2 * h + (k >> 1)];
+            const float x = (float)__builtin_bit_cast(_Float16, (uint16_t)((k & 1) ? w >> 16 : w & 0xffffu));
+            macc[db][4 * c + k] = fmaf(F, x, macc[db][4 * c + k]);
+          }
+        }
     }
     l_tot = l_acc;
 #pragma unroll
@@ -767,8 +800,8 @@ static PreLayout prefill_layout(const PrePlan& pl) {
   PreLayout l;
   const size_t slots = (size_t)pl.nunits * pl.nsplit * kPRows;
   l.o = kCounterBytes;
-  l.ml = l.o + slots * 128 * sizeof(float);
-  l.total = l.ml + (slots * 2 * sizeof(float) + 255) / 256 * 256;
+  l.ml = l.o + slots * 128 * sizeof(uint16_t);  // fp16 rows
+  l.total = l.ml + (slots * 4 * sizeof(float) + 255) / 256 * 256;  // (m, l, 2^e, -) records
   return l;
 }
 
