@@ -4,17 +4,22 @@ Each case draws batch, GQA ratio, head dim, query and key lengths, cache capacit
 causal and window masks and per-sequence lengths from a fixed seed, so a failure names a case
 that reruns identically. The hand-written tests pin the edges one at a time; these cover their
 combinations (partial tiles and row blocks with windows, variable lengths and capacity views
-together, grids that are and are not a multiple of the XCD count).
+together, grids that are and are not a multiple of the XCD count), and the paged pools against
+the contiguous caches.
 """
 
+import math
 import random
 
 import pytest
 import torch
 
+from myinfer_amd import kernels
 from tests import test_gpu_decode as TD
 from tests import test_gpu_dense as TN
+from tests import test_gpu_paged as TG
 from tests import test_gpu_prefill as TP
+from tests.helpers import assert_close, exact_reference, seeded_normal
 
 pytestmark = pytest.mark.gpu
 DTYPES = (torch.float16, torch.bfloat16)
@@ -70,3 +75,31 @@ def test_unquantized_fuzz(case):
     causal, window, seq_lens = _masks(rng, B, L, S)
     TN.run_case(kernel, B, Hkv * rep, Hkv, L, S, D, dtype, causal=causal, window=window, seq_lens=seq_lens,
                 seed=7300 + case, cap=cap, what=f"fuzz {case}")
+
+
+@pytest.mark.parametrize("case", range(16))
+def test_paged_fuzz(case):
+    # pools in shuffled 64-row pages, unused rows poisoned with NaN scales; the paged kernels must
+    # equal the contiguous ones bit for bit, and both the oracle
+    rng = random.Random(7400 + case)
+    kernel = rng.choice(["decode", "prefill"])
+    D = 128 if kernel == "prefill" else rng.choice([64, 128])
+    bits, dtype = rng.choice([4, 8]), rng.choice(DTYPES)
+    Hkv, rep, B = rng.choice([1, 2, 4]), rng.choice([1, 2, 4, 8]), rng.choice([1, 2, 3])
+    L = rng.choice([1, 2, 4]) if kernel == "decode" else rng.randrange(1, 300)
+    lens = [rng.randrange(L, 2500) for _ in range(B)]
+    causal, window = rng.random() < 0.5, rng.choice([0, 0, rng.randrange(1, max(lens) + 1)])
+    print(f"paged fuzz {case}: {kernel} B={B} Hq={Hkv * rep} Hkv={Hkv} L={L} lens={lens} D={D} bits={bits} "
+          f"{dtype} causal={causal} window={window}", flush=True)
+    rows, tables, kp, vp, kc, vc = TG.build(B, Hkv, lens, D, bits, dtype, 7400 + case)
+    q = seeded_normal((B, Hkv * rep, L, D), 7500 + case, dtype, "cuda")
+    sl = torch.tensor(lens, dtype=torch.int32, device="cuda")
+    scale = 1.0 / math.sqrt(D)
+    out_p = kernels.paged_attention(q, kp, vp, tables, sl, scale, causal=causal, window=window, bits=bits,
+                                    max_len=max(lens), kernel=kernel)
+    out_c = kernels.attention(q, kc, vc, scale, causal=causal, window=window, seq_lens=sl, bits=bits, kernel=kernel)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out_p.float()).all(), "a row past a sequence's end was read"
+    assert torch.equal(out_p, out_c)
+    assert_close(out_p, exact_reference(q, kc, vc, scale, bits=bits, causal=causal, window=window, seq_lens=sl),
+                 f"paged fuzz {case}")
