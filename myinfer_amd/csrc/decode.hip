@@ -395,11 +395,16 @@ __global__ __launch_bounds__(NW * 64, (dec_min_wgs<D, BITS, NW, NSLOT>())) void 
   const int n = lane & 15, lg = lane >> 4;
 
   // ---- workgroup -> (unit, split); a unit is (sequence, KV head, row block)
-  int wg = blockIdx.x;
-  if (p.xcd_remap) {
-    const int per_xcd = (p.nunits * p.nsplit) / kXcds;
-    wg = (wg % kXcds) * per_xcd + wg / kXcds;
-  }
+  // Kernel arguments arrive in dependent rounds of scalar loads wherever a branch separates their
+  // uses. The pointers and strides the query and first tile loads need are requested up front
+  // (an empty asm takes them as operands) and the workgroup numbering is a select, so they arrive
+  // in one round.
+  asm volatile("" ::"s"(p.q), "s"(p.kc), "s"(p.vc), "s"(p.ks), "s"(p.kb), "s"(p.vs), "s"(p.vb));
+  asm volatile("" ::"s"(p.q_sb), "s"(p.q_sh), "s"(p.q_sl), "s"(p.kc_sb), "s"(p.kc_sh), "s"(p.kc_ss), "s"(p.vc_sb),
+               "s"(p.vc_sh), "s"(p.vc_ss));
+  asm volatile("" ::"s"(p.ksb_sb), "s"(p.ksb_sh), "s"(p.ksb_ss), "s"(p.vsb_sb), "s"(p.vsb_sh), "s"(p.vsb_ss));
+  const int wg0 = blockIdx.x;
+  const int wg = p.xcd_remap ? (wg0 % kXcds) * ((p.nunits * p.nsplit) / kXcds) + wg0 / kXcds : wg0;
   const int unit = wg / p.nsplit;
   const int split = wg % p.nsplit;
   const int b = unit / (p.Hkv * p.rowblocks);
