@@ -893,15 +893,23 @@ struct DecTune {
   int nw, nslot, target_wgs, fused;
 };
 
-// Launch-shape defaults; KVQ_DECODE_TUNE="waves,slots,workgroups,fused" overrides them (read once
-// per process). 8-wave workgroups take 2 ring slots (the ring of 3 would not fit in LDS).
+// The in-kernel split merge (the last split of a unit merges) costs an arrival counter and a
+// round trip per split partial in one workgroup; the combine launch costs a kernel boundary. With
+// few splits the in-kernel merge is faster (3-4 splits: C5 window layer 12.5 against 13.3 us, C2 at
+// batch 8 and C5's global layer about 1% faster), with many it is slower (17 splits: C1 12.6 against
+// 11.4 us; 32: C2 at batch 1 24.2 against 21.7 us).
+constexpr int kFusedMaxSplit = 4;
+
+// Launch-shape defaults; KVQ_DECODE_TUNE="waves,slots,workgroups[,fused]" overrides them (read
+// once per process; fused 0 or 1 forces the split merge's form, omitted leaves it to the plan).
+// 8-wave workgroups take 2 ring slots (the ring of 3 would not fit in LDS).
 static DecTune decode_tune() {
   static DecTune t = [] {
-    DecTune d{4, 2, 256, 0};
+    DecTune d{4, 2, 256, -1};
     if (const char* e = getenv("KVQ_DECODE_TUNE")) {
-      int a = 0, b = 0, c = 0, f = 1;
+      int a = 0, b = 0, c = 0, f = -1;
       if (sscanf(e, "%d,%d,%d,%d", &a, &b, &c, &f) >= 3 && (a == 4 || (a == 8 && b == 2)) && b >= 2 && b <= 4 && c >= 1)
-        d = {a, b, c, f != 0};
+        d = {a, b, c, f < 0 ? -1 : f != 0};
     }
     return d;
   }();
@@ -925,7 +933,8 @@ DecPlan decode_plan(int B, int Hq, int Hkv, int L, int D, int S, int window, int
   tpw = std::max<int64_t>(pl.nw, (tpw + pl.nw - 1) / pl.nw * pl.nw);
   pl.chunk = (int)(tpw * kTile);
   pl.nsplit = (pl.span + pl.chunk - 1) / pl.chunk;
-  pl.fused = tune.fused && pl.nunits <= kMaxCountedUnits;
+  const bool fused = tune.fused < 0 ? pl.nsplit <= kFusedMaxSplit : tune.fused != 0;
+  pl.fused = fused && pl.nunits <= kMaxCountedUnits;
   return pl;
 }
 
