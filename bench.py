@@ -742,8 +742,8 @@ def main():
                          "unit": "TFLOP/s", "frac": round(pr["attn_tflops"] / PEAK_MFMA_TFLOPS, 4),
                          "traffic": measured_traffic("prefill_c3_chunk"),
                          "kernel_ms": round(pr["attn_ms"], 4),
-                         "kernel": "prefill_attn_kernel (+ combine_kernel where a chunk's keys are split), summed "
-                                   "over the 32 chunks"},
+                         "kernel": "prefill_attn_kernel (one launch per chunk; split keys are merged inside it), "
+                                   "summed over the 32 chunks"},
             "append_ms": round(pr["append_ms"], 4),
             "chunk_attn_us": pr["chunk_attn_us"],
             "cpu_baseline": pcpu,
