@@ -48,16 +48,16 @@ struct MergeParams {
 };
 
 // One thread per (output row, 4 columns): the D/4 threads of a row load its float4 of every split
-// at once, share the split weights through LDS (computed by the row's threads from the (m, l)
-// pairs, a few splits each) and sum the splits in split order. One wave per workgroup: 64 / (D/4)
-// rows, so a call spreads its partial reads over many CUs.
+// at once, and each of them also reads all of the row's (m, l) pairs (the same addresses for the
+// whole row) and forms the split weights itself, so no exchange between threads is needed. The
+// splits are summed in split order; the weighted sum is divided by the weighted sum of the l's.
+// One wave per workgroup: 64 / (D/4) rows, so a call spreads its partial reads over many CUs.
 template <typename T, int D>
 __global__ __launch_bounds__(64) void combine_kernel(MergeParams p, int nrows) {
   constexpr int TPR = D / 4;      // threads per row
   constexpr int RPW = 64 / TPR;   // rows per workgroup
-  constexpr int SPT = kMaxSplit / TPR;  // splits whose (m, l) one thread reads
   constexpr int CH = 32;          // partial loads in flight per thread
-  __shared__ float s_w[RPW][kMaxSplit];
+  constexpr int R = 1024 / D;     // rows per decode unit (16 / groups per row); the host checks p.R
   const int tr = threadIdx.x / TPR, j = threadIdx.x % TPR;
   const int grow = blockIdx.x * RPW + tr;
   const bool ok = grow < nrows;
@@ -65,51 +65,54 @@ __global__ __launch_bounds__(64) void combine_kernel(MergeParams p, int nrows) {
   const int l = g % p.L, h = (g / p.L) % p.Hq, b = g / (p.L * p.Hq);
   const int kvh = h / p.rep;
   const int rw = (h - kvh * p.rep) * p.L + l;
-  const int unit = (b * p.Hkv + kvh) * p.rowblocks + rw / p.R;
-  const int64_t base = (int64_t)unit * p.nsplit * p.R + rw % p.R;  // split s at base + s * R
+  const int unit = (b * p.Hkv + kvh) * p.rowblocks + rw / R;
+  const int64_t base = (int64_t)unit * p.nsplit * R + rw % R;  // split s at base + s * R
   const f4* po = (const f4*)(p.part_o + base * D) + j;
-  const int64_t sstride = (int64_t)p.R * D / 4;  // float4s between splits
-  f4 o[CH];
-#pragma unroll
-  for (int u = 0; u < CH; ++u) o[u] = u < p.nsplit ? po[u * sstride] : f4{0, 0, 0, 0};
-  // the row's weights 2^(m_s - M) / sum_s 2^(m_s - M) l_s, this thread's splits j, j + TPR, ...
   const float2* ml = (const float2*)p.part_ml + base;
-  float mk[SPT], lk[SPT];
+  constexpr int ss = R * D / 4;  // float4s between splits
+  // loads past the last split re-read it (in bounds, no per-split branches) and count with l = 0
+  // (held in a VGPR, so that the 64 clamped offsets are vector values, not scalar registers)
+  int last;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(last) : "s"(p.nsplit - 1));
+  f4 o[CH];
+  float2 mv[CH];
+#pragma unroll
+  for (int u = 0; u < CH; ++u) o[u] = po[min(u, last) * ss];
+#pragma unroll
+  for (int u = 0; u < CH; ++u) {
+    mv[u] = ml[min(u, last) * R];
+    if (u > last) mv[u].y = 0.0f;
+  }
+  // the row's maximum over the splits that saw a key (l > 0)
   float M = -INFINITY;
 #pragma unroll
-  for (int k = 0; k < SPT; ++k) {
-    const int sp = j + TPR * k;
-    const float2 v = sp < p.nsplit ? ml[(int64_t)sp * p.R] : make_float2(-INFINITY, 0.0f);
-    mk[k] = v.y > 0.0f ? v.x : -INFINITY;
-    lk[k] = v.y;
-    M = fmaxf(M, mk[k]);
-  }
-#pragma unroll
-  for (int m = 1; m < TPR; m <<= 1) M = fmaxf(M, shfl_xor(M, m));
-  float Ls = 0.0f;
-#pragma unroll
-  for (int k = 0; k < SPT; ++k) {
-    mk[k] = (M == -INFINITY || mk[k] == -INFINITY) ? 0.0f : exp2_fast(mk[k] - M);
-    Ls += mk[k] * lk[k];
-  }
-#pragma unroll
-  for (int m = 1; m < TPR; m <<= 1) Ls += shfl_xor(Ls, m);
-  const float inv = Ls > 0.0f ? 1.0f / Ls : 0.0f;
-#pragma unroll
-  for (int k = 0; k < SPT; ++k)
-    if (j + TPR * k < p.nsplit) s_w[tr][j + TPR * k] = mk[k] * inv;
-  __syncthreads();
-  f4 acc = {0, 0, 0, 0};
-#pragma unroll
   for (int u = 0; u < CH; ++u)
-    if (u < p.nsplit) acc += s_w[tr][u] * o[u];
-  for (int s0 = CH; s0 < p.nsplit; s0 += CH) {
-#pragma unroll
-    for (int u = 0; u < CH; ++u) o[u] = s0 + u < p.nsplit ? po[(s0 + u) * sstride] : f4{0, 0, 0, 0};
-#pragma unroll
-    for (int u = 0; u < CH; ++u)
-      if (s0 + u < p.nsplit) acc += s_w[tr][s0 + u] * o[u];
+    if (mv[u].y > 0.0f) M = fmaxf(M, mv[u].x);
+  for (int s = CH; s < p.nsplit; ++s) {
+    const float2 v = ml[s * R];
+    if (v.y > 0.0f) M = fmaxf(M, v.x);
   }
+  f4 acc = {0, 0, 0, 0};
+  float Ls = 0.0f;
+  auto add = [&](const float2 v, const f4 ov) __attribute__((always_inline)) {
+    const float w = (v.y > 0.0f) ? exp2_fast(v.x - M) : 0.0f;  // M is finite when any l > 0
+    acc += w * ov;
+    Ls += w * v.y;
+  };
+#pragma unroll
+  for (int u = 0; u < CH; ++u) add(mv[u], o[u]);
+  for (int s0 = CH; s0 <= last; s0 += CH) {
+#pragma unroll
+    for (int u = 0; u < CH; ++u) o[u] = po[min(s0 + u, last) * ss];
+#pragma unroll
+    for (int u = 0; u < CH; ++u) {
+      mv[u] = ml[min(s0 + u, last) * R];
+      if (s0 + u > last) mv[u].y = 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < CH; ++u) add(mv[u], o[u]);
+  }
+  acc *= Ls > 0.0f ? 1.0f / Ls : 0.0f;
   if (!ok) return;
   uint16_t* dst = p.out + (int64_t)b * p.o_sb + (int64_t)h * p.o_sh + (int64_t)l * p.o_sl + 4 * j;
   u2 w;
@@ -120,6 +123,7 @@ __global__ __launch_bounds__(64) void combine_kernel(MergeParams p, int nrows) {
 
 template <typename T, int D>
 inline hipError_t launch_combine(const MergeParams& m, int B, hipStream_t stream) {
+  if (m.R != 1024 / D) return hipErrorInvalidValue;  // the kernel's split strides assume this
   const int nrows = B * m.Hq * m.L;
   const int grid = (nrows + (256 / D) - 1) / (256 / D);  // 64 / (D / 4) rows per workgroup
   hipLaunchKernelGGL((combine_kernel<T, D>), dim3(grid), dim3(64), 0, stream, m, nrows);
