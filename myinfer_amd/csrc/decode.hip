@@ -372,6 +372,9 @@ __device__ __forceinline__ h8 v_operand(const Bytes<VB> (&vc)[8], int jN) {
 // below 2^kSlack; with fp16 scales (|s| <= 514) the fp16 PV operand p*s stays finite.
 constexpr float kSlack = 6.0f;
 
+// Split counts up to which the in-kernel merge loads every split's partial in one round.
+constexpr int kFewSplits = 4;
+
 // Workgroups per CU the launch bounds ask for: two 4-wave workgroups when their rings fit in LDS
 // together, else one.
 template <int D, int BITS, int NW, int NSLOT>
@@ -844,6 +847,36 @@ __global__ __launch_bounds__(NW * 64, (dec_min_wgs<D, BITS, NW, NSLOT>())) void 
   if (s_prev != (unsigned)(p.nsplit - 1)) return;
   if (threadIdx.x == 0) __hip_atomic_store(&p.counters[unit], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
+  if (p.nsplit <= kFewSplits) {
+    // few splits (the plan's choice for this form): each thread loads its float4 and its row's
+    // (m, l) of every split in one round (loads past the last split re-read it and count with
+    // l = 0) and forms the weights itself: no wave reductions, no exchange through LDS
+    if (!mine) return;
+    const int last = p.nsplit - 1;
+    f4 po[kFewSplits];
+    float2 mv[kFewSplits];
+#pragma unroll
+    for (int u = 0; u < kFewSplits; ++u) {
+      const int su = min(u, last);
+      po[u] = load_agent_b128(ro, 16 * i4, su * (R * D * 4));
+      mv[u] = load_agent_b64(rm, 8 * rr, su * (R * 8));
+    }
+    float Mx = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < kFewSplits; ++u)
+      if (u <= last && mv[u].y > 0.0f) Mx = fmaxf(Mx, mv[u].x);
+    f4 acc = {0, 0, 0, 0};
+    float Ls = 0.0f;
+#pragma unroll
+    for (int u = 0; u < kFewSplits; ++u) {
+      const float w = (u <= last && mv[u].y > 0.0f) ? exp2_fast(mv[u].x - Mx) : 0.0f;
+      acc += w * po[u];
+      Ls += w * mv[u].y;
+    }
+    write_out(acc, Ls > 0.0f ? 1.0f / Ls : 0.0f);
+    return;
+  }
+
   // this thread's float4 of the first 32 splits, in flight while the weights are formed
   constexpr int CH = 32;
   f4 po[CH];
@@ -898,7 +931,7 @@ struct DecTune {
 // few splits the in-kernel merge is faster (3-4 splits: C5 window layer 12.5 against 13.3 us, C2 at
 // batch 8 and C5's global layer about 1% faster), with many it is slower (17 splits: C1 12.6 against
 // 11.4 us; 32: C2 at batch 1 24.2 against 21.7 us).
-constexpr int kFusedMaxSplit = 4;
+constexpr int kFusedMaxSplit = kFewSplits;
 
 // Launch-shape defaults; KVQ_DECODE_TUNE="waves,slots,workgroups[,fused]" overrides them (read
 // once per process; fused 0 or 1 forces the split merge's form, omitted leaves it to the plan).
