@@ -133,8 +133,9 @@ int kvq_rope_quantize_append(const kvq_rows* k_src, const kvq_qtensor* k_dst,
  *   window:   0 = none; otherwise keys k > position - window only (sliding window).
  *   workspace: device buffer of at least kvq_decode_workspace_size(...) bytes, 256-byte aligned,
  *              zero-filled at allocation (see the conventions above).
- * The key range is split over workgroups; their log-sum-exp partials are merged by a second,
- * small launch on the same stream (both are enqueued by this call).
+ * The key range is split over workgroups; their log-sum-exp partials are merged by the last
+ * workgroup of each unit to finish when there are at most 4 splits, otherwise by a second, small
+ * launch on the same stream (both are enqueued by this call).
  */
 int kvq_decode_attn(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v,
                     const int32_t* seq_lens, const kvq_rows* out,
