@@ -191,7 +191,9 @@ int kvq_prefill_attn_dense(const kvq_rows* q, const kvq_rows* k, const kvq_rows*
  * codes u32 [num_pages][H][KVQ_PAGE_ROWS][D*bits/32], scales/biases T [num_pages][H][KVQ_PAGE_ROWS][D/G]
  * (head-major within a page), described by a kvq_qtensor whose batch strides are page strides.
  * Row r of sequence b lives in page block_table[b * table_stride + r / KVQ_PAGE_ROWS], at row
- * r % KVQ_PAGE_ROWS. Table entries are clamped to [0, num_pages) on the device.
+ * r % KVQ_PAGE_ROWS. The attention kernels clamp table entries to [0, num_pages) (a read of a
+ * wrong page is harmless); the paged append drops a row whose entry lies outside [0, num_pages),
+ * such as a -1 "unallocated" sentinel, so it never writes into a page it was not given.
  * Replaces: the reference's paged KV layout (native/src/kv_cache.cpp:8-27, 16-token blocks read
  * through a block table in native/src/kernels.metal:106-160, 384-450), here for the quantized MLX
  * cache, as the alternative to whole-cache move-reuse (m5engine/prefix_cache.py:1-5). Pages are
@@ -203,7 +205,8 @@ int kvq_prefill_attn_dense(const kvq_rows* q, const kvq_rows* k, const kvq_rows*
  * kvq_quantize_append into a paged pool: row l of sequence b goes to row starts[b] + l (starts: a
  * device int32 [B], or NULL for row_offset + l for every sequence). With `rope` the keys are
  * rotated first, row l of sequence b at position rope->offset + (starts ? starts[b] : 0) + l.
- * Rows whose page index is at or past table_stride are dropped.
+ * Rows whose page index is at or past table_stride, or whose table entry lies outside
+ * [0, num_pages), are dropped.
  */
 int kvq_paged_quantize_append(const kvq_rows* k_src, const kvq_qtensor* k_pool,
                               const kvq_rows* v_src, const kvq_qtensor* v_pool, int num_pages,

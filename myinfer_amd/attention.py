@@ -186,18 +186,44 @@ def safe_maybe_quantize_kv_cache(prompt_cache, quantized_kv_start, kv_group_size
             prompt_cache[i] = c.to_quantized(group_size=kv_group_size, bits=kv_bits)
 
 
+# The host framework's modules that install() patches when it is called without arguments, as the
+# reference's engine calls it (m5engine/engine.py:138): the same two mlx-lm modules the reference
+# patches (m5engine/attention.py:122-125). A host framework with other module names sets these.
+HOST_BASE_MODULE = "mlx_lm.models.base"
+HOST_GENERATE_MODULE = "mlx_lm.generate"
+
 _installed = False
+_patched: set = set()  # (id(module), attribute) pairs already routed here
+
+
+def _patch(module, attr: str, fn) -> None:
+    setattr(module, attr, fn)
+    _patched.add((id(module), attr))
 
 
 def install(base_module=None, generate_module=None) -> None:
     """Route a host framework's quantized attention and cache quantization to this module
-    (m5engine/attention.py:118-126): sets `quantized_scaled_dot_product_attention` on
-    `base_module` and `maybe_quantize_kv_cache` on `generate_module` when given. Idempotent."""
+    (m5engine/attention.py:118-126): sets `quantized_scaled_dot_product_attention` on the base
+    module and `maybe_quantize_kv_cache` on the generate module.
+
+    Called with no arguments (the reference engine's call, m5engine/engine.py:138) it imports the
+    modules named by HOST_BASE_MODULE / HOST_GENERATE_MODULE and patches them; if they cannot be
+    imported it raises ImportError and patches nothing, so a later call can still install. Modules
+    passed in are patched whatever an earlier call did. Idempotent per module."""
     global _installed
-    if _installed:
-        return
-    if base_module is not None:
-        base_module.quantized_scaled_dot_product_attention = blocked_quantized_sdpa
-    if generate_module is not None:
-        generate_module.maybe_quantize_kv_cache = safe_maybe_quantize_kv_cache
-    _installed = True
+    if base_module is None and generate_module is None:
+        import importlib
+
+        try:
+            base_module = importlib.import_module(HOST_BASE_MODULE)
+            generate_module = importlib.import_module(HOST_GENERATE_MODULE)
+        except ImportError as e:
+            raise ImportError(
+                f"install() found no host framework to patch ({HOST_BASE_MODULE}, {HOST_GENERATE_MODULE}: {e}); "
+                "pass the modules, as install(base_module, generate_module), or set HOST_BASE_MODULE / "
+                "HOST_GENERATE_MODULE") from e
+    if base_module is not None and (id(base_module), "quantized_scaled_dot_product_attention") not in _patched:
+        _patch(base_module, "quantized_scaled_dot_product_attention", blocked_quantized_sdpa)
+    if generate_module is not None and (id(generate_module), "maybe_quantize_kv_cache") not in _patched:
+        _patch(generate_module, "maybe_quantize_kv_cache", safe_maybe_quantize_kv_cache)
+    _installed = bool(_patched)

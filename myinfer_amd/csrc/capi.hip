@@ -70,6 +70,9 @@ int check_attn_common(const kvq_rows* q, const kvq_rows* out, int B, int Hq, int
   if (!isfinite(scale)) return fail(KVQ_ERR_INVALID, "scale is not finite");
   if ((rc = check_rows(q, "queries", D, true))) return rc;
   if ((rc = check_rows(out, "out", D, false))) return rc;
+  // every attention kernel writes 4 output elements (8 bytes) at a time
+  if (!aligned(out->data, 8) || out->stride_b % 4 || out->stride_h % 4 || out->stride_l % 4)
+    return fail(KVQ_ERR_INVALID, "out must be 8-byte aligned with strides that are multiples of 4 elements");
   return KVQ_OK;
 }
 

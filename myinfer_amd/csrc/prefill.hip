@@ -21,8 +21,10 @@
 //    A = K rows from LDS, B = Q^T held in registers). In the MFMA result layout every lane holds
 //    16 keys of one query column, so the row max / sum are lane-local plus one permlane swap, and
 //    the probabilities converted to fp16 are already the B operand of O^T = V^T P^T: no shuffle.
-//  * Q carries the softmax scale in log2 units and a per-row power of two that keeps it inside
-//    the fp16 range; scores are fp32 and are corrected by that power before the softmax.
+//  * Q enters the MFMA exactly (times a per-row power of two that keeps it inside the fp16
+//    range); the softmax scale in log2 units and that power are applied to the fp32 scores.
+//  * A bf16 cache group beyond the fp16 range (its bias overflows on conversion) cannot be held by
+//    the fp16 operands: the row blocks that read one return NaN rather than wrong finite values.
 //  * Online softmax with threshold rescaling (a row's running maximum moves only when a tile's
 //    maximum exceeds it by more than 2^6), fp32 accumulators.
 //  * Long key ranges are split over several workgroups; the last split of a row block to finish
@@ -245,7 +247,7 @@ __device__ __forceinline__ void dequant8(const uint32_t* w, h2 s2, h2 b2, uint32
 // 256-511 build K: thread t takes dims [32 q, +32) of key t % 64, q = (t - 256) / 64.
 template <typename T, int BITS>
 __device__ __forceinline__ void stage_from_raw(const uint8_t* raw, _Float16* klds, _Float16* vlds, uint32_t* sbt,
-                                               int tid) {
+                                               int tid, bool& range_bad) {
   using C = RawCfg<BITS>;
   const uint8_t* sbase = raw + 2 * C::KB;
   auto sb_at = [&](int a, int key, int g) -> _Float16 {
@@ -266,6 +268,9 @@ __device__ __forceinline__ void stage_from_raw(const uint8_t* raw, _Float16* kld
       const int key = tid & 63;
       const h2 sbp = {sb_at(2, key, g), sb_at(3, key, g)};
       sbt[key] = __builtin_bit_cast(uint32_t, sbp);
+      // a bf16 group beyond the fp16 range has a bias (its largest-magnitude element) that
+      // converts to inf; the operands cannot hold it
+      if constexpr (T::id == KVQ_DTYPE_BF16) range_bad |= __builtin_isinf((float)sbp[1]);
     }
     __builtin_amdgcn_wave_barrier();
     uint32_t x[8][2];  // key i, dim pair m
@@ -312,6 +317,7 @@ __device__ __forceinline__ void stage_from_raw(const uint8_t* raw, _Float16* kld
       for (int i = 0; i < 4; ++i) w[i] = a0[i];
     }
     const _Float16 sh = sb_at(0, key, q >> 1), bh = sb_at(1, key, q >> 1);
+    if constexpr (T::id == KVQ_DTYPE_BF16) range_bad |= __builtin_isinf((float)bh);
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       uint32_t x[4];
@@ -353,6 +359,9 @@ __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) 
   __shared__ __align__(16) uint8_t raw[kRawSlots][RC::SLOT];
   __shared__ uint32_t sb_tab[DENSE ? 1 : kPW / 2][64];  // per V^T-building wave: (scale, bias) pairs
   __shared__ unsigned s_arrived;
+  __shared__ unsigned s_range_bad;  // some staged tile held a group beyond the fp16 range
+  bool range_bad = false;
+  if (threadIdx.x == 0) s_range_bad = 0;  // ordered before any staging by the prologue's barrier
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -459,9 +468,12 @@ __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) 
     for (int j = 0; j < (DENSE ? 2 : kRawSlots); ++j) issue_raw(j);
   }
 
-  // ---- Q^T operand: k-step j holds dims 16j + 8hh .. +7. Quantized cache: times
-  // scale*log2(e)*2^qe in fp16, the scores corrected by inv2 = 2^-qe. Unquantized cache: the raw
-  // query (exact), the scores multiplied by scale*log2(e) in fp32.
+  // ---- Q^T operand: k-step j holds dims 16j + 8hh .. +7. Quantized cache: the query times 2^qe in
+  // fp16 (exact: a power of two, with qe chosen so the row's largest element lands in [2^13, 2^14);
+  // a bf16 query has 8 significant bits, so only elements below 2^-14 of the operand's scale lose
+  // bits), and the scores are multiplied by inv2 = scale * log2(e) * 2^-qe in fp32. Folding the
+  // softmax scale into the fp16 operand instead would round every query element. Unquantized
+  // cache: the raw query (exact), the scores multiplied by scale*log2(e) in fp32.
   u4 qop[8];
   float inv2;
   if constexpr (DENSE) {
@@ -481,12 +493,12 @@ __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) 
         qmax = fmaxf(qmax, fmaxf(fabsf(qv[j][2 * i]), fabsf(qv[j][2 * i + 1])));
       }
     }
-    qmax = max_xor32(qmax) * p.scale_log2;
+    qmax = max_xor32(qmax);
     int e = 0;
     if (qmax > 0.0f) frexpf(qmax, &e);
-    const int qe = 14 - e;  // |q * scale * log2(e)| * 2^qe < 2^14
-    const float qmul = ldexpf(p.scale_log2, qe);
-    inv2 = ldexpf(1.0f, -qe);
+    const int qe = 14 - e;  // |q| * 2^qe < 2^14
+    const float qmul = ldexpf(1.0f, qe);
+    inv2 = ldexpf(p.scale_log2, -qe);
 #pragma unroll
     for (int j = 0; j < 8; ++j)
 #pragma unroll
@@ -510,7 +522,7 @@ __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) 
     } else {
       wait_vm<2 * RC::IPT>();
       __syncthreads();
-      stage_from_raw<T, BITS>(raw[0], k_lds[0], v_lds[0], sb_tab[wave & 3], tid);
+      stage_from_raw<T, BITS>(raw[0], k_lds[0], v_lds[0], sb_tab[wave & 3], tid, range_bad);
       wait_vm<RC::IPT>();
       __syncthreads();
     }
@@ -535,7 +547,8 @@ __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) 
       if constexpr (DENSE) {
         stage_v_raw(raw[(t + 1) % kRawSlots], v_lds[cur ^ 1], tid - 256, 0);
       } else {
-        stage_from_raw<T, BITS>(raw[(t + 1) % kRawSlots], k_lds[cur ^ 1], v_lds[cur ^ 1], sb_tab[wave & 3], tid);
+        stage_from_raw<T, BITS>(raw[(t + 1) % kRawSlots], k_lds[cur ^ 1], v_lds[cur ^ 1], sb_tab[wave & 3], tid,
+                                 range_bad);
       }
     }
 
@@ -640,7 +653,8 @@ __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) 
       if constexpr (DENSE) {
         stage_v_raw(raw[(t + 1) % kRawSlots], v_lds[cur ^ 1], tid, 1);
       } else {
-        stage_from_raw<T, BITS>(raw[(t + 1) % kRawSlots], k_lds[cur ^ 1], v_lds[cur ^ 1], sb_tab[wave & 3], tid);
+        stage_from_raw<T, BITS>(raw[(t + 1) % kRawSlots], k_lds[cur ^ 1], v_lds[cur ^ 1], sb_tab[wave & 3], tid,
+                                 range_bad);
       }
     }
     if constexpr (DENSE) {
@@ -651,6 +665,18 @@ __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) 
     __syncthreads();
   }
   wait_vm<0>();  // no load into this workgroup's LDS outlives it
+  if constexpr (!DENSE && T::id == KVQ_DTYPE_BF16) {
+    // a group beyond the fp16 range poisons the workgroup's rows: NaN propagates through the split
+    // merge (0 * NaN is NaN) to every output row of the row block
+    if (range_bad) s_range_bad = 1;
+    __syncthreads();
+    if (s_range_bad) {
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) oacc[db][i] = __builtin_nanf("");
+    }
+  }
 
   // ---- epilogue: this lane holds O^T[d][row] for d = 32db + 8(i/4) + 4hh + i%4
   float l_tot = add_xor32(l_run);
@@ -683,9 +709,11 @@ __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) 
 #pragma unroll
         for (int i = 0; i < 16; ++i) mx = fmaxf(mx, fabsf(oacc[db][i]));
       mx = max_xor32(mx) * inv_l;
+      // mx * 2^-e lies in [2^13, 2^14): every row uses the full fp16 mantissa whatever its
+      // magnitude (small rows would otherwise be stored as subnormals)
       int ex = 0;
-      if (mx >= 16384.0f) frexpf(mx, &ex);
-      const int e = ex > 14 ? ex - 14 : 0;  // mx * 2^-e < 2^14
+      if (mx > 0.0f) frexpf(mx, &ex);
+      const int e = mx > 0.0f ? min(max(ex - 14, -100), 100) : 0;
       own_sc = ldexpf(1.0f, e);
       const float f = ldexpf(inv_l, -e);
 #pragma unroll

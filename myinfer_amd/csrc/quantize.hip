@@ -181,7 +181,11 @@ __global__ __launch_bounds__(256) void quantize_append_kernel(QuantJob job0, Qua
   if (pm.table) {
     const int64_t r = (pm.starts ? (int64_t)pm.starts[b] : row_offset) + l;
     if (r < 0 || (r >> 6) >= pm.table_stride) return;  // a row outside the sequence's table is dropped
-    bb = min(max(pm.table[b * pm.table_stride + (r >> 6)], 0), pm.num_pages - 1);
+    // A table entry outside the pool (such as a -1 "unallocated" sentinel) drops the row too:
+    // clamping it would write into a page that may belong to another sequence.
+    const int pg = pm.table[b * pm.table_stride + (r >> 6)];
+    if (pg < 0 || pg >= pm.num_pages) return;
+    bb = pg;
     drow = r & 63;
   }
   uint32_t* cdst = job.codes + bb * job.c_b + h * job.c_h + drow * job.c_s;

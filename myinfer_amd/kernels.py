@@ -256,6 +256,20 @@ def _rows_ok(t: torch.Tensor) -> bool:
     return t.stride(-1) == 1 and not any(st % 8 for st in t.stride()[:3]) and t.data_ptr() % 16 == 0
 
 
+def _check_out(out: Optional[torch.Tensor], queries: torch.Tensor, dev) -> torch.Tensor:
+    """A fresh output, or the caller's after the checks the kernels' stores rely on: the queries'
+    shape, dtype and device, unit stride along D, 8-byte alignment and strides of 4 elements (the
+    kernels write 4 elements at a time; prefill also needs 16-byte rows, checked by the library)."""
+    B, Hq, L, D = queries.shape
+    if out is None:
+        return torch.empty((B, Hq, L, D), dtype=queries.dtype, device=dev)
+    if tuple(out.shape) != (B, Hq, L, D) or out.dtype != queries.dtype or out.device != dev:
+        raise ValueError(f"out must be a {queries.dtype} tensor of shape {(B, Hq, L, D)} on {dev}")
+    if out.stride(-1) != 1 or any(st % 4 for st in out.stride()[:3]) or out.data_ptr() % 8:
+        raise ValueError("out must have unit stride along D, 8-byte alignment and strides that are multiples of 4")
+    return out
+
+
 def prepare_attention(queries: torch.Tensor, keys, values, scale: float, *, causal: bool = False,
                       window: int = 0, seq_lens: Optional[torch.Tensor] = None, group_size: int = 64,
                       bits: int = 8, out: Optional[torch.Tensor] = None, kernel: str = "auto",
@@ -298,10 +312,7 @@ def prepare_attention(queries: torch.Tensor, keys, values, scale: float, *, caus
         raise ValueError(f"Hq={Hq} is not a multiple of Hkv={Hkv}")
     if not _rows_ok(queries):
         queries = queries.contiguous()
-    if out is None:
-        out = torch.empty((B, Hq, L, D), dtype=queries.dtype, device=dev)
-    elif out.shape != (B, Hq, L, D) or out.dtype != queries.dtype or out.device != dev:
-        raise ValueError(f"out must be a {queries.dtype} tensor of shape {(B, Hq, L, D)} on {dev}")
+    out = _check_out(out, queries, dev)
     sl_ptr = None
     if seq_lens is not None:
         if seq_lens.dtype != torch.int32 or seq_lens.device != dev or seq_lens.numel() != B:
@@ -420,13 +431,19 @@ def paged_attention(queries: torch.Tensor, k_pool: Triple, v_pool: Triple, block
     Hkv = k_pool[0].shape[1]
     if k_pool[0].shape[2] != PAGE_ROWS or k_pool[1].dtype != queries.dtype:
         raise ValueError(f"pools must be [num_pages, Hkv, {PAGE_ROWS}, *] with scales in the queries' dtype")
+    for a, b_ in zip(k_pool, v_pool):
+        if tuple(a.shape) != tuple(b_.shape) or a.dtype != b_.dtype:
+            raise ValueError("v_pool must match k_pool in every shape and dtype (the kernels read both through "
+                             "one block table over k_pool's page count)")
+    if k_pool[0].shape[3] * 32 // bits != D or k_pool[1].shape[3] * group_size != D or k_pool[1].shape[:3] != \
+            k_pool[0].shape[:3]:
+        raise ValueError(f"pools' row widths do not match D={D}, bits={bits} and group_size={group_size}")
     if Hq % Hkv:
         raise ValueError(f"Hq={Hq} is not a multiple of Hkv={Hkv}")
     S = int(max_len) if max_len is not None else block_tables.shape[1] * PAGE_ROWS
     if not _rows_ok(queries):
         queries = queries.contiguous()
-    if out is None:
-        out = torch.empty((B, Hq, L, D), dtype=queries.dtype, device=dev)
+    out = _check_out(out, queries, dev)
     if kernel == "auto":
         kernel = "decode" if ((Hq // Hkv) * L <= decode_rows_per_pass(D) or D != 128) else "prefill"
     lib = _lib.lib()

@@ -45,6 +45,23 @@ def exact_reference(q: torch.Tensor, k_tr, v_tr, scale, *, bits, group_size=64, 
     return OA.exact_attention(qn, kdq, vdq, scale, causal=causal, window=window, seq_lens=sl)
 
 
+def fp16_key_floor(q: torch.Tensor, k_tr, v_tr, scale, ref: np.ndarray, *, bits, group_size=64, causal=False,
+                   window=0, seq_lens=None) -> dict:
+    """Error (vs the exact fp64 answer `ref`) of exact fp64 attention whose dequantized keys were
+    rounded to fp16 first: the error floor of any kernel that feeds the dequantized keys to fp16
+    operands (as mlx-lm's fp16 quantized_matmul does when it dequantizes in T). It grows with the
+    score magnitude: a key element k carries a rounding of up to 2^-11 |k|, so a score of size s
+    moves by about 2^-11 s / sqrt(3) times a mixing factor; at N(0,1) inputs it is far below the
+    north-star bar, with keys of norm 65x it is not."""
+    dt = NP_DTYPE[q.dtype]
+    qn = q.detach().cpu().float().numpy().astype(np.float64)
+    kdq = OQ.dequantize(*triple_to_np(k_tr), dt, group_size, bits).astype(np.float16).astype(np.float64)
+    vdq = OQ.dequantize(*triple_to_np(v_tr), dt, group_size, bits)
+    sl = None if seq_lens is None else [int(x) for x in seq_lens.cpu().tolist()]
+    floor = OA.exact_attention(qn, kdq, vdq, scale, causal=causal, window=window, seq_lens=sl)
+    return OA.error_stats(floor, ref)
+
+
 def assert_close(out: torch.Tensor, ref: np.ndarray, what: str = ""):
     o = out.detach().cpu().float().numpy().astype(np.float64)
     assert np.isfinite(o).all(), f"{what}: non-finite output"

@@ -71,10 +71,49 @@ def test_additive_and_unsupported_masks():
 
 def test_install_is_idempotent(monkeypatch):
     monkeypatch.setattr(A, "_installed", False)
+    monkeypatch.setattr(A, "_patched", set())
+    base, gen = types.SimpleNamespace(), types.SimpleNamespace()
+    A.install(base, gen)
+    assert A._installed
+    assert base.quantized_scaled_dot_product_attention is A.blocked_quantized_sdpa
+    assert gen.maybe_quantize_kv_cache is A.safe_maybe_quantize_kv_cache
+    # a second call on the same modules leaves an attribute a user changed since alone
+    base.quantized_scaled_dot_product_attention = "user"
+    A.install(base, gen)
+    assert base.quantized_scaled_dot_product_attention == "user"
+    # other modules are still patched
+    other = types.SimpleNamespace()
+    A.install(other, None)
+    assert other.quantized_scaled_dot_product_attention is A.blocked_quantized_sdpa
+
+
+def test_install_engine_sequence_without_host_framework(monkeypatch):
+    # the reference engine calls install() with no arguments (m5engine/engine.py:138); without the
+    # host framework that raises and patches nothing, so a later call with modules still installs
+    monkeypatch.setattr(A, "_installed", False)
+    monkeypatch.setattr(A, "_patched", set())
+    monkeypatch.setattr(A, "HOST_BASE_MODULE", "no_such_host_framework.models.base")
+    with pytest.raises(ImportError, match="no host framework"):
+        A.install()
+    assert not A._installed and not A._patched
     base, gen = types.SimpleNamespace(), types.SimpleNamespace()
     A.install(base, gen)
     assert base.quantized_scaled_dot_product_attention is A.blocked_quantized_sdpa
     assert gen.maybe_quantize_kv_cache is A.safe_maybe_quantize_kv_cache
-    other = types.SimpleNamespace()
-    A.install(other, None)  # second call is a no-op
-    assert not hasattr(other, "quantized_scaled_dot_product_attention")
+
+
+def test_install_without_arguments_patches_named_modules(monkeypatch):
+    import sys
+
+    monkeypatch.setattr(A, "_installed", False)
+    monkeypatch.setattr(A, "_patched", set())
+    base, gen = types.ModuleType("fakehost_base"), types.ModuleType("fakehost_generate")
+    monkeypatch.setitem(sys.modules, "fakehost_base", base)
+    monkeypatch.setitem(sys.modules, "fakehost_generate", gen)
+    monkeypatch.setattr(A, "HOST_BASE_MODULE", "fakehost_base")
+    monkeypatch.setattr(A, "HOST_GENERATE_MODULE", "fakehost_generate")
+    A.install()
+    A.install()  # idempotent
+    assert A._installed
+    assert base.quantized_scaled_dot_product_attention is A.blocked_quantized_sdpa
+    assert gen.maybe_quantize_kv_cache is A.safe_maybe_quantize_kv_cache

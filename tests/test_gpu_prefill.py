@@ -135,3 +135,54 @@ def test_running_max_moves_mid_split(dtype, causal, bits):
     torch.cuda.synchronize()
     ref = exact_reference(q, trip[0], trip[1], scale, bits=bits, causal=causal)
     assert_close(out, ref, "mid-split maxima")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("causal,bits", [(False, 8), (True, 8), (False, 4)])
+def test_rising_key_norms(dtype, causal, bits):
+    # Key norms grow x1 -> x65 along the sequence, so each row's maximum keeps rising tile after
+    # tile (the running maximum moves, rescales and recomputes again and again) and the scores
+    # reach about 300 in natural-log units. At that magnitude fp16 key operands alone move a
+    # score by about 300 * 2^-11 / sqrt(3) ~ 0.08, so no kernel that dequantizes keys to fp16 --
+    # the reference's fp16 quantized_matmul included -- meets the north-star bar of N(0,1)
+    # inputs here. The bar is therefore derived on the same inputs:
+    #   floor = error of exact fp64 attention over the dequantized keys rounded to fp16
+    #   the kernel: error <= floor + the north-star (fp16) or bf16 bar
+    # and the kernel must also be closer to the exact answer than the reference-faithful port
+    # (the reference's blocked loop with its roundings to T, m5engine/attention.py:49, 66-69,
+    # 87-90), which the reference itself would produce.
+    import numpy as np
+
+    from oracle import attention as OA
+    from tests.helpers import TOL, fp16_key_floor
+
+    print(f"prefill rising key norms dtype={dtype} causal={causal} bits={bits}", flush=True)
+    B, Hq, Hkv, L, S, D = 1, 16, 4, 96, 2048, 128
+    growth = 1.0 + torch.arange(S, dtype=torch.float32) / 32.0
+    k = (seeded_normal((B, Hkv, S, D), 91, torch.float32) * growth[None, None, :, None]).to(dtype).to(DEV)
+    v = seeded_normal((B, Hkv, S, D), 92, dtype, DEV)
+    trip = []
+    for x in (k, v):
+        codes = torch.zeros((B, Hkv, S, D * bits // 32), dtype=torch.int32, device=DEV).view(torch.uint32)
+        sc = torch.zeros((B, Hkv, S, D // 64), dtype=dtype, device=DEV)
+        bi = torch.zeros_like(sc)
+        kernels.quantize_append(x, (codes, sc, bi), row_offset=0, group_size=64, bits=bits)
+        trip.append((codes, sc, bi))
+    q = seeded_normal((B, Hq, L, D), 93, dtype, DEV)
+    scale = 1.0 / math.sqrt(D)
+    out = kernels.attention(q, trip[0], trip[1], scale, causal=causal, bits=bits, kernel="prefill")
+    torch.cuda.synchronize()
+    ref = exact_reference(q, trip[0], trip[1], scale, bits=bits, causal=causal)
+    o = out.cpu().float().numpy().astype(np.float64)
+    assert np.isfinite(o).all()
+    st = OA.error_stats(o, ref)
+    floor = fp16_key_floor(q, trip[0], trip[1], scale, ref, bits=bits, causal=causal)
+    ns_abs, ns_rel = TOL[dtype](ref)
+    if dtype == torch.float16:  # (bf16 4-bit codes times bf16 scales mostly fit fp16 exactly)
+        assert floor["max_abs"] > ns_abs, "the case must exercise scores beyond the north-star regime"
+    assert st["max_abs"] <= floor["max_abs"] + ns_abs and st["rel_l2"] <= floor["rel_l2"] + ns_rel, (st, floor)
+    cpu = [tuple(t.cpu() for t in tr) for tr in trip]
+    port = OA.reference_sdpa(q.cpu(), cpu[0], cpu[1], scale, "causal" if causal else None, 64, bits)
+    pst = OA.error_stats(port.float().numpy().astype(np.float64), ref)
+    print(f"  gpu {st}  fp16-key floor {floor}  reference port {pst}", flush=True)
+    assert st["max_abs"] <= pst["max_abs"] and st["rel_l2"] <= pst["rel_l2"], (st, pst)
