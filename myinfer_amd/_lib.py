@@ -14,10 +14,8 @@ from pathlib import Path
 
 import torch  # noqa: F401  (binds the HIP runtime before libkvq.so is loaded)
 
-import os
-
-# The in-tree build; KVQ_LIB may name another build of the same library (A/B comparisons).
-LIB_PATH = Path(os.environ.get("KVQ_LIB") or (Path(__file__).resolve().parent / "libkvq.so"))
+# The in-tree build, the only library this package loads.
+LIB_PATH = Path(__file__).resolve().parent / "libkvq.so"
 ABI_VERSION = 4
 
 DTYPE_F16 = 0
