@@ -147,6 +147,27 @@ int kvq_decode_attn(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* 
 size_t kvq_decode_workspace_size(int B, int Hq, int Hkv, int L, int D, int S, int window);
 
 /*
+ * kvq_decode_attn without a workspace argument, for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). No
+ * counterpart in the reference: its MLX path allocates freely.
+ * The split partials and arrival counters live in a static device array of
+ * KVQ_STATIC_SCRATCH_BYTES that the library holds on every GPU it runs on until the process
+ * ends; the call allocates nothing. A call whose plan needs more scratch than that
+ * (kvq_decode_workspace_size(...) > KVQ_STATIC_SCRATCH_BYTES, e.g. B * Hq * L above about
+ * 15 000 rows at D = 128) returns KVQ_ERR_WORKSPACE and launches nothing.
+ * Every call on one GPU shares that GPU's scratch: calls that overlap on one GPU (different
+ * streams or threads without ordering between them) race and give undefined results. The first
+ * call on a GPU also zeroes the scratch's counters on `stream` (a kernel, not a memset).
+ * Arguments, requirements and results are those of kvq_decode_attn; the kernels are the same.
+ */
+#define KVQ_STATIC_SCRATCH_BYTES (8u << 20)
+int kvq_decode_attn_static(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v,
+                           const int32_t* seq_lens, const kvq_rows* out,
+                           int B, int Hq, int Hkv, int L, int D, int S,
+                           int bits, int group_size, int dtype,
+                           float scale, int causal, int window, void* stream);
+
+/*
  * Attention for prefill chunks (any L): same contract as kvq_decode_attn, MFMA tiles with
  * K/V tiles dequantized into LDS. Replaces m5engine/attention.py:29-103 for L > 1.
  * Requirements: D == 128; group_size 64; bits in {4, 8}; Hq a multiple of Hkv.

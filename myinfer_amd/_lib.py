@@ -106,6 +106,7 @@ SIGNATURES = {
          c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_void_p],
     ),
     "kvq_decode_attn": (c_int, _ATTN_ARGS),
+    "kvq_decode_attn_static": (c_int, _ATTN_ARGS[:-3] + [c_void_p]),  # no workspace: the library's scratch
     "kvq_paged_quantize_append": (
         c_int,
         [POINTER(Rows), POINTER(QTensor), POINTER(Rows), POINTER(QTensor), c_int, c_void_p, c_int64, c_void_p, c_int64,

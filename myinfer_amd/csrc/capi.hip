@@ -5,7 +5,22 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <mutex>
+
 #include "launch.h"
+#include "merge.h"
+
+// Scratch of kvq_decode_attn_static: device memory the library owns, one copy per GPU, held until
+// the process ends. In host code `scratch` is a host-side stand-in for the symbol, not a device
+// address: the kernels get the per-device address hipGetSymbolAddress returns (static_scratch
+// below), never the name.
+static __device__ __align__(256) uint8_t scratch[KVQ_STATIC_SCRATCH_BYTES];
+
+// Zero `n` words (the scratch's arrival counters, once per device). A kernel rather than
+// hipMemsetAsync, so that a caller may capture the first call into a HIP graph.
+__global__ void zero_words_kernel(uint32_t* p, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) p[i] = 0u;
+}
 
 namespace {
 
@@ -83,9 +98,9 @@ int check_workspace(size_t ws_needed, void* workspace, size_t workspace_bytes) {
   return KVQ_OK;
 }
 
-int check_attn(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v, const kvq_rows* out, int B, int Hq,
-               int Hkv, int L, int D, int S, int bits, int group_size, int dtype, float scale, int window,
-               size_t ws_needed, void* workspace, size_t workspace_bytes) {
+// Everything check_attn checks but the workspace.
+int check_attn_args(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v, const kvq_rows* out, int B, int Hq,
+                    int Hkv, int L, int D, int S, int bits, int group_size, int dtype, float scale, int window) {
   int rc;
   if ((rc = check_attn_common(q, out, B, Hq, Hkv, L, D, S, dtype, scale, window))) return rc;
   if (bits != 4 && bits != 8) return fail(KVQ_ERR_UNSUPPORTED, "attention supports 4- and 8-bit caches, got bits=%d", bits);
@@ -102,6 +117,14 @@ int check_attn(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v, co
     if ((int64_t)S * t->codes_stride_s * 4 > (int64_t)UINT32_MAX || (int64_t)S * t->sb_stride_s * 2 > (int64_t)UINT32_MAX)
       return fail(KVQ_ERR_UNSUPPORTED, "attention needs S times each row stride within 4 GiB (S=%d)", S);
   }
+  return KVQ_OK;
+}
+
+int check_attn(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v, const kvq_rows* out, int B, int Hq,
+               int Hkv, int L, int D, int S, int bits, int group_size, int dtype, float scale, int window,
+               size_t ws_needed, void* workspace, size_t workspace_bytes) {
+  int rc;
+  if ((rc = check_attn_args(q, k, v, out, B, Hq, Hkv, L, D, S, bits, group_size, dtype, scale, window))) return rc;
   return check_workspace(ws_needed, workspace, workspace_bytes);
 }
 
@@ -171,6 +194,37 @@ int check_table(const int32_t* table, int64_t table_stride, int64_t rows_needed)
   if ((rows_needed + KVQ_PAGE_ROWS - 1) / KVQ_PAGE_ROWS > table_stride)
     return fail(KVQ_ERR_INVALID, "table_stride %lld pages cannot hold %lld rows", (long long)table_stride,
                 (long long)rows_needed);
+  return KVQ_OK;
+}
+
+// The address of this device's copy of `scratch`, looked up once per device (with the device
+// current) by hipGetSymbolAddress; the first call on a device also zeroes its arrival counters on
+// `stream` (every later call leaves them at zero).
+constexpr int kMaxDevices = 64;
+struct ScratchSlot {
+  std::once_flag once;
+  void* ptr = nullptr;
+  hipError_t err = hipSuccess;
+};
+ScratchSlot g_scratch[kMaxDevices];
+
+int static_scratch(hipStream_t stream, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_status(e, "hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices) return fail(KVQ_ERR_UNSUPPORTED, "device %d is beyond the %d the library tracks", dev, kMaxDevices);
+  ScratchSlot& s = g_scratch[dev];
+  std::call_once(s.once, [&] {
+    void* p = nullptr;
+    s.err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (s.err != hipSuccess) return;
+    const size_t words = kvq::kCounterBytes / 4;
+    hipLaunchKernelGGL(zero_words_kernel, dim3((unsigned)((words + 255) / 256)), dim3(256), 0, stream, (uint32_t*)p, words);
+    s.err = hipGetLastError();
+    if (s.err == hipSuccess) s.ptr = p;
+  });
+  if (!s.ptr) return hip_status(s.err != hipSuccess ? s.err : hipErrorInvalidSymbol, "static scratch set-up");
+  *out = s.ptr;
   return KVQ_OK;
 }
 
@@ -266,6 +320,23 @@ int kvq_decode_attn(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* 
   return hip_status(kvq::launch_decode(q, k, v, seq_lens, out, B, Hq, Hkv, L, D, S, bits, dtype, scale, causal,
                                        window, workspace, (hipStream_t)stream),
                     "decode_attn launch");
+}
+
+int kvq_decode_attn_static(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v, const int32_t* seq_lens,
+                           const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int bits, int group_size,
+                           int dtype, float scale, int causal, int window, void* stream) {
+  if (D != 64 && D != 128) return fail(KVQ_ERR_UNSUPPORTED, "decode supports head_dim 64 and 128, got %d", D);
+  int rc = check_attn_args(q, k, v, out, B, Hq, Hkv, L, D, S, bits, group_size, dtype, scale, window);
+  if (rc) return rc;
+  const size_t need = kvq_decode_workspace_size(B, Hq, Hkv, L, D, S, window);
+  if (need > (size_t)KVQ_STATIC_SCRATCH_BYTES)
+    return fail(KVQ_ERR_WORKSPACE, "this call needs %zu bytes of scratch; the static scratch holds %zu (use kvq_decode_attn "
+                "with a workspace)", need, (size_t)KVQ_STATIC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  if ((rc = static_scratch((hipStream_t)stream, &ws))) return rc;
+  return hip_status(kvq::launch_decode(q, k, v, seq_lens, out, B, Hq, Hkv, L, D, S, bits, dtype, scale, causal,
+                                       window, ws, (hipStream_t)stream),
+                    "decode_attn_static launch");
 }
 
 size_t kvq_prefill_workspace_size(int B, int Hq, int Hkv, int L, int D, int S, int window) {
