@@ -47,19 +47,34 @@ struct MergeParams {
   int Hq, Hkv, L, rep, R, rowblocks, nsplit;
 };
 
-// One thread per (output row, 4 columns): the D/4 threads of a row load its float4 of every split
-// at once, and each of them also reads all of the row's (m, l) pairs (the same addresses for the
-// whole row) and forms the split weights itself, so no exchange between threads is needed. The
-// splits are summed in split order; the weighted sum is divided by the weighted sum of the l's.
-// One wave per workgroup: 64 / (D/4) rows, so a call spreads its partial reads over many CUs.
+// Quad lane exchanges (lane i with lane i ^ 1, i ^ 2) through DPP quad permutes.
+template <int CTRL>
+__device__ __forceinline__ float quad_perm(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float quad_max(float v) {
+  v = fmaxf(v, quad_perm<0xB1>(v));     // [1, 0, 3, 2]
+  return fmaxf(v, quad_perm<0x4E>(v));  // [2, 3, 0, 1]
+}
+__device__ __forceinline__ float quad_sum(float v) {
+  v += quad_perm<0xB1>(v);
+  return v + quad_perm<0x4E>(v);
+}
+
+// Four threads per (output row, 4 columns): thread q of a quad takes splits q, q + 4, q + 8, ...,
+// loads its float4 and (m, l) of each in one round (a quarter of the loads a thread would issue
+// alone: the merge is bound by the latency of these loads), forms the split weights against the
+// quad's maximum, and the quad sums its terms with two DPP exchanges. Fixed order, so repeated
+// calls are bit-identical. 256 / D rows per workgroup of 256 threads.
 template <typename T, int D>
-__global__ __launch_bounds__(64) void combine_kernel(MergeParams p, int nrows) {
-  constexpr int TPR = D / 4;      // threads per row
-  constexpr int RPW = 64 / TPR;   // rows per workgroup
-  constexpr int CH = 32;          // partial loads in flight per thread
-  constexpr int R = 1024 / D;     // rows per decode unit (16 / groups per row); the host checks p.R
-  const int tr = threadIdx.x / TPR, j = threadIdx.x % TPR;
-  const int grow = blockIdx.x * RPW + tr;
+__global__ __launch_bounds__(256) void combine_kernel(MergeParams p, int nrows) {
+  constexpr int F4 = D / 4;              // float4s per row
+  constexpr int RPB = 256 / (4 * F4);    // rows per workgroup
+  constexpr int CH = 8;                  // splits per thread loaded in the first round
+  constexpr int R = 1024 / D;            // rows per decode unit (16 / groups per row); the host checks p.R
+  const int t = threadIdx.x;
+  const int q = t & 3, j = (t >> 2) % F4;
+  const int grow = blockIdx.x * RPB + t / (4 * F4);
   const bool ok = grow < nrows;
   const int g = ok ? grow : 0;
   const int l = g % p.L, h = (g / p.L) % p.Hq, b = g / (p.L * p.Hq);
@@ -71,27 +86,28 @@ __global__ __launch_bounds__(64) void combine_kernel(MergeParams p, int nrows) {
   const float2* ml = (const float2*)p.part_ml + base;
   constexpr int ss = R * D / 4;  // float4s between splits
   // loads past the last split re-read it (in bounds, no per-split branches) and count with l = 0
-  // (held in a VGPR, so that the 64 clamped offsets are vector values, not scalar registers)
+  // (held in a VGPR, so that the clamped offsets are vector values, not scalar registers)
   int last;
   asm volatile("v_mov_b32 %0, %1" : "=v"(last) : "s"(p.nsplit - 1));
   f4 o[CH];
   float2 mv[CH];
 #pragma unroll
-  for (int u = 0; u < CH; ++u) o[u] = po[min(u, last) * ss];
-#pragma unroll
   for (int u = 0; u < CH; ++u) {
-    mv[u] = ml[min(u, last) * R];
-    if (u > last) mv[u].y = 0.0f;
+    const int s = q + 4 * u;
+    o[u] = po[min(s, last) * ss];
+    mv[u] = ml[min(s, last) * R];
+    if (s > last) mv[u].y = 0.0f;
   }
   // the row's maximum over the splits that saw a key (l > 0)
   float M = -INFINITY;
 #pragma unroll
   for (int u = 0; u < CH; ++u)
     if (mv[u].y > 0.0f) M = fmaxf(M, mv[u].x);
-  for (int s = CH; s < p.nsplit; ++s) {
+  for (int s = 4 * CH + q; s < p.nsplit; s += 4) {
     const float2 v = ml[s * R];
     if (v.y > 0.0f) M = fmaxf(M, v.x);
   }
+  M = quad_max(M);
   f4 acc = {0, 0, 0, 0};
   float Ls = 0.0f;
   auto add = [&](const float2 v, const f4 ov) __attribute__((always_inline)) {
@@ -101,19 +117,12 @@ __global__ __launch_bounds__(64) void combine_kernel(MergeParams p, int nrows) {
   };
 #pragma unroll
   for (int u = 0; u < CH; ++u) add(mv[u], o[u]);
-  for (int s0 = CH; s0 <= last; s0 += CH) {
+  for (int s = 4 * CH + q; s < p.nsplit; s += 4) add(ml[s * R], po[s * ss]);
 #pragma unroll
-    for (int u = 0; u < CH; ++u) o[u] = po[min(s0 + u, last) * ss];
-#pragma unroll
-    for (int u = 0; u < CH; ++u) {
-      mv[u] = ml[min(s0 + u, last) * R];
-      if (s0 + u > last) mv[u].y = 0.0f;
-    }
-#pragma unroll
-    for (int u = 0; u < CH; ++u) add(mv[u], o[u]);
-  }
+  for (int e = 0; e < 4; ++e) acc[e] = quad_sum(acc[e]);
+  Ls = quad_sum(Ls);
   acc *= Ls > 0.0f ? 1.0f / Ls : 0.0f;
-  if (!ok) return;
+  if (!ok || q != 0) return;
   uint16_t* dst = p.out + (int64_t)b * p.o_sb + (int64_t)h * p.o_sh + (int64_t)l * p.o_sl + 4 * j;
   u2 w;
   w[0] = (uint32_t)from_float(acc[0], T{}) | ((uint32_t)from_float(acc[1], T{}) << 16);
@@ -125,8 +134,8 @@ template <typename T, int D>
 inline hipError_t launch_combine(const MergeParams& m, int B, hipStream_t stream) {
   if (m.R != 1024 / D) return hipErrorInvalidValue;  // the kernel's split strides assume this
   const int nrows = B * m.Hq * m.L;
-  const int grid = (nrows + (256 / D) - 1) / (256 / D);  // 64 / (D / 4) rows per workgroup
-  hipLaunchKernelGGL((combine_kernel<T, D>), dim3(grid), dim3(64), 0, stream, m, nrows);
+  constexpr int rpb = 256 / D;  // rows per 256-thread workgroup
+  hipLaunchKernelGGL((combine_kernel<T, D>), dim3((nrows + rpb - 1) / rpb), dim3(256), 0, stream, m, nrows);
   return hipGetLastError();
 }
 
