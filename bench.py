@@ -320,52 +320,88 @@ def parity_check(cfg, q, cache, sl, scale):
     ref = OA.exact_attention(q.cpu().double().numpy(), kdq, vdq, scale, causal=cfg.get("causal", False),
                              window=cfg.get("window", 0), seq_lens=None if sl is None else sl.cpu().tolist())
     got = out.cpu().double().numpy()
+    return parity_record(got, ref, dt), (got, ref)
+
+
+def parity_record(got, ref, dtype: str, **extra):
+    """Error against the exact fp64 oracle and the bar it is judged by: the north-star bar for fp16
+    outputs (max-abs 2e-3, relative L2 1e-3); for bf16 outputs half an ulp of the output rounding on
+    top (max-abs 2^-8 max|ref| + 1e-3, relative L2 3e-3), as in tests/helpers.py."""
+    import numpy as np
+
+    from oracle import attention as OA
+
     st = OA.error_stats(got, ref)
-    return {"vs": "exact fp64 oracle", "max_abs": st["max_abs"], "rel_l2": st["rel_l2"]}, (got, ref)
+    bar = (2e-3, 1e-3) if dtype == "float16" else (2.0**-8 * float(np.abs(ref).max()) + 1e-3, 3e-3)
+    return {"vs": "exact fp64 oracle", **extra, "max_abs": st["max_abs"], "rel_l2": st["rel_l2"],
+            "bar": {"max_abs": bar[0], "rel_l2": bar[1]},
+            "within_bar": bool(st["max_abs"] <= bar[0] and st["rel_l2"] <= bar[1])}
 
 
-def cpu_baseline(cfg, q, cache, scale, budget_s=15.0, max_calls=8):
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown CPU"
+
+
+def reference_mask(cfg, lens, L, S):
+    """The mask the reference's caller would pass for this workload (m5engine/attention.py:55-58,
+    70-81): None (every key visible), "causal", or a bool [B, 1, L, S] array for per-sequence
+    lengths and sliding windows."""
+    import numpy as np
+    import torch
+
+    from oracle import attention as OA
+
+    window, causal = cfg.get("window", 0), cfg.get("causal", False)
+    if window == 0 and all(n == S for n in lens):
+        return "causal" if causal and L > 1 else None
+    m = np.stack([OA.key_mask(L, S, n, causal, window) for n in lens])[:, None]
+    return torch.from_numpy(m)
+
+
+def cpu_trip(tr):
+    import torch
+
+    c, s, b = tr
+    return (c.cpu().view(torch.int32).to(torch.int64) & 0xFFFFFFFF, s.cpu(), b.cpu())
+
+
+def cpu_baseline(cfg, q, cache, scale, lens, budget_s=15.0, max_calls=8):
     """The reference algorithm restated for the CPU (oracle.attention.reference_sdpa: mlx-lm's
-    quantized SDPA for L == 1 with the reference's dtype casts), timed on the host's cores."""
+    quantized SDPA for L == 1 with the reference's dtype casts and masks), timed on the host's
+    cores over the same workload (one cache, every sequence of the batch) for a bounded number of
+    calls."""
     import torch
 
     from oracle import attention as OA
 
     ncores = len(os.sched_getaffinity(0))
     torch.set_num_threads(ncores)
-
-    def cpu_trip(tr):
-        c, s, b = tr
-        return (c.cpu().view(torch.int32).to(torch.int64) & 0xFFFFFFFF, s.cpu(), b.cpu())
-
     qc = q.cpu()
     kt, vt = cpu_trip(cache[0]), cpu_trip(cache[1])
-    OA.reference_sdpa(qc, kt, vt, scale, None, 64, cfg["bits"])  # warm-up (allocator, threads)
+    mask = reference_mask(cfg, lens, 1, cfg["S"])
+    OA.reference_sdpa(qc, kt, vt, scale, mask, 64, cfg["bits"])  # warm-up (allocator, threads)
     times = []
     t_all = time.perf_counter()
     while len(times) < max_calls and (time.perf_counter() - t_all) < budget_s:
         t0 = time.perf_counter()
-        ref_out = OA.reference_sdpa(qc, kt, vt, scale, None, 64, cfg["bits"])
+        ref_out = OA.reference_sdpa(qc, kt, vt, scale, mask, 64, cfg["bits"])
         times.append(time.perf_counter() - t0)
     times.sort()
     med = times[len(times) // 2]
-    lens = [cfg["S"]] * cfg["B"]
-    nbytes = decode_bytes(lens, cfg["Hq"], cfg["Hkv"], cfg["D"], cfg["bits"])
-    cpu_model = ""
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                cpu_model = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
+    nbytes = decode_bytes(lens, cfg["Hq"], cfg["Hkv"], cfg["D"], cfg["bits"], window=cfg.get("window", 0))
     return {
         "value": round(nbytes / med / 1e9, 3),
         "unit": "GB/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": (f"{len(times)} calls of the headline workload (one 32K-token cache, B=1) through "
-                   f"oracle.attention.reference_sdpa on the host CPU ({cpu_model}); median {med * 1e3:.1f} ms/call"),
+        "sample": (f"{len(times)} calls of this workload (one cache, B={cfg['B']}) through "
+                   f"oracle.attention.reference_sdpa on the host CPU ({cpu_model()}); median {med * 1e3:.1f} ms/call"),
     }, ref_out.float().double().numpy()
 
 
@@ -375,12 +411,29 @@ PREFILL = dict(desc="Qwen3-30B-A3B chunked prefill, 16384 tokens in 512-token ch
                Hq=32, Hkv=4, D=128, N=16384, chunk=512, bits=8, dtype="bfloat16", seed=1003)
 
 
-def prefill_flops(N, Hq, D, L0=0, L1=None):
-    """Algorithmic FLOPs of causal attention for query positions [L0, L1) of an N-token prompt:
-    4 * D * Hq per unmasked (query, key) pair; position p sees p + 1 keys."""
+# C5 (Gemma-3-27B shapes) prefill legs over the quantized cache: B=4 sequences of 8192 tokens in
+# 2048-token chunks, 32 query heads / 16 KV heads, bf16; the global causal layer and a window-1024
+# layer (5 of every 6 layers; quantized here as SURVEY's C5 configuration asks, although the
+# reference leaves sliding-window caches unquantized: m5engine/attention.py:106-112).
+PREFILL_C5 = {
+    "C5-global-prefill": dict(desc="Gemma-3-27B global-layer chunked prefill, B=4 x 8192 tokens in 2048-token "
+                                   "chunks, 8-bit KV, bf16", B=4, Hq=32, Hkv=16, D=128, N=8192, chunk=2048, bits=8,
+                              dtype="bfloat16", seed=1015),
+    "C5-window-prefill": dict(desc="Gemma-3-27B window-1024-layer chunked prefill, B=4 x 8192 tokens in 2048-token "
+                                   "chunks, 8-bit KV, bf16", B=4, Hq=32, Hkv=16, D=128, N=8192, chunk=2048, bits=8,
+                              dtype="bfloat16", seed=1016, window=1024),
+}
+
+
+def prefill_flops(N, Hq, D, L0=0, L1=None, window=0, B=1):
+    """Algorithmic FLOPs of causal attention for query positions [L0, L1) of B N-token prompts:
+    4 * D * Hq per unmasked (query, key) pair; position p sees p + 1 keys, or min(p + 1, window)."""
     L1 = N if L1 is None else L1
-    pairs = (L1 * (L1 + 1) - L0 * (L0 + 1)) // 2
-    return 4 * D * Hq * pairs
+    if window > 0:
+        pairs = sum(min(p + 1, window) for p in range(L0, L1))
+    else:
+        pairs = (L1 * (L1 + 1) - L0 * (L0 + 1)) // 2
+    return 4 * D * Hq * pairs * B
 
 
 def time_prefill(cfg, steps, warmup, device, want_parity=False):
@@ -391,6 +444,7 @@ def time_prefill(cfg, steps, warmup, device, want_parity=False):
     from myinfer_amd import kernels
 
     B, Hq, Hkv, D, N, C, bits = cfg["B"], cfg["Hq"], cfg["Hkv"], cfg["D"], cfg["N"], cfg["chunk"], cfg["bits"]
+    W = cfg.get("window", 0)
     T = getattr(torch, cfg["dtype"])
     g = torch.Generator(device=device).manual_seed(cfg["seed"])
     k = torch.randn((B, Hkv, N, D), generator=g, device=device).to(T)
@@ -402,7 +456,7 @@ def time_prefill(cfg, steps, warmup, device, want_parity=False):
     ks, kb, vs, vb = (torch.zeros((B, Hkv, N, D // 64), dtype=T, device=device) for _ in range(4))
     scale = 1.0 / math.sqrt(D)
     nchunk = N // C
-    flops = prefill_flops(N, Hq, D)
+    flops = prefill_flops(N, Hq, D, window=W, B=B)
     log(f"[bench] {cfg['desc']}: {flops / 1e12:.3f} TFLOP of attention per step")
 
     def make_calls():
@@ -412,7 +466,7 @@ def time_prefill(cfg, steps, warmup, device, want_parity=False):
             appends.append((k[:, :, lo:hi], v[:, :, lo:hi], lo))
             attns.append(kernels.prepare_attention(q[:, :, lo:hi], (kc[:, :, :hi], ks[:, :, :hi], kb[:, :, :hi]),
                                                    (vc[:, :, :hi], vs[:, :, :hi], vb[:, :, :hi]), scale, causal=True,
-                                                   bits=bits, out=out[:, :, lo:hi], kernel="prefill"))
+                                                   window=W, bits=bits, out=out[:, :, lo:hi], kernel="prefill"))
         return appends, attns
 
     def append(a):
@@ -611,40 +665,38 @@ def prefill_parity(cfg, q, out, kt, vt, scale, c):
     kdq = OQ.dequantize(*trip(kt), cfg["dtype"], 64, cfg["bits"])
     vdq = OQ.dequantize(*trip(vt), cfg["dtype"], 64, cfg["bits"])
     qc = q[:, :, c * C:hi].float().cpu().double().numpy()
-    ref = OA.exact_attention(qc, kdq, vdq, scale, causal=True)
+    ref = OA.exact_attention(qc, kdq, vdq, scale, causal=True, window=cfg.get("window", 0))
     got = out[:, :, c * C:hi].float().cpu().double().numpy()
-    st = OA.error_stats(got, ref)
-    return {"vs": "exact fp64 oracle", "chunk": c, "max_abs": st["max_abs"], "rel_l2": st["rel_l2"]}, (got, ref)
+    return parity_record(got, ref, cfg["dtype"], chunk=c), (got, ref)
 
 
 def prefill_cpu_baseline(cfg, q_last, kt, vt, scale, budget_s=20.0):
     """The reference algorithm (oracle.attention.reference_sdpa: m5engine/attention.py's blocked
-    loop with its dtype casts) on the last chunk of the prompt, timed on the host's cores."""
+    loop with its dtype casts and masks) on the last chunk of the prompt of the first sequence,
+    timed on the host's cores. Returns the baseline and the port's output for that sequence."""
     import torch
 
     from oracle import attention as OA
 
     ncores = len(os.sched_getaffinity(0))
     torch.set_num_threads(ncores)
-    N, C = cfg["N"], cfg["chunk"]
-
-    def cpu_trip(tr):
-        c, s, b = tr
-        return (c.cpu().view(torch.int32).to(torch.int64) & 0xFFFFFFFF, s.cpu(), b.cpu())
-
-    qc = q_last.cpu()
-    ktc, vtc = cpu_trip(kt), cpu_trip(vt)
+    N, C, W = cfg["N"], cfg["chunk"], cfg.get("window", 0)
+    qc = q_last[:1].cpu()
+    ktc, vtc = (tuple(x[:1] for x in cpu_trip(t)) for t in (kt, vt))
+    mask = reference_mask(dict(cfg, causal=True), [N], C, N)
+    mask = "causal" if mask is None and W == 0 else mask
     times = []
     t_all = time.perf_counter()
     while not times or (time.perf_counter() - t_all < budget_s and len(times) < 3):
         t0 = time.perf_counter()
-        ref_out = OA.reference_sdpa(qc, ktc, vtc, scale, "causal", 64, cfg["bits"])
+        ref_out = OA.reference_sdpa(qc, ktc, vtc, scale, mask, 64, cfg["bits"])
         times.append(time.perf_counter() - t0)
     med = sorted(times)[len(times) // 2]
-    fl = prefill_flops(N, cfg["Hq"], cfg["D"], N - C, N)
+    fl = prefill_flops(N, cfg["Hq"], cfg["D"], N - C, N, window=W)
     return {"value": round(fl / med / 1e12, 5), "unit": "TFLOP/s", "cores": torch.get_num_threads(), "kind": "port",
-            "sample": f"{len(times)} run(s) of the last 512-token chunk (16384 keys) through oracle.attention."
-                      f"reference_sdpa on the host CPU; median {med:.2f} s"}, ref_out.float().double().numpy()
+            "sample": f"{len(times)} run(s) of the last {C}-token chunk ({N} keys{f', window {W}' if W else ''}) of "
+                      f"one sequence through oracle.attention.reference_sdpa on the host CPU ({cpu_model()}); "
+                      f"median {med:.2f} s"}, ref_out.float().double().numpy()
 
 
 def add_faithful(parity, arrays, faithful):
@@ -655,9 +707,22 @@ def add_faithful(parity, arrays, faithful):
     from oracle import attention as OA
 
     got, exact = arrays
-    a, b = OA.error_stats(got, faithful), OA.error_stats(faithful, exact)
+    n = faithful.shape[0]  # the port may have run on the first sequences only
+    got, exact = got[:n], exact[:n]
+    a, b, g = OA.error_stats(got, faithful), OA.error_stats(faithful, exact), OA.error_stats(got, exact)
     parity["vs_faithful_oracle"] = {"max_abs": a["max_abs"], "rel_l2": a["rel_l2"]}
     parity["faithful_oracle_vs_exact"] = {"max_abs": b["max_abs"], "rel_l2": b["rel_l2"]}
+    if n < arrays[0].shape[0]:
+        parity["faithful_sequences"] = n
+    # the bound the GPU-to-port distance must meet: within (GPU error + port error), the triangle
+    # inequality through the exact answer (both errors measured against it); and whether the GPU is
+    # at least as close to the exact answer as the reference's own algorithm (same sequences)
+    parity["checks"] = {
+        "port_distance_within_gpu_plus_port_error": bool(
+            a["max_abs"] <= (g["max_abs"] + b["max_abs"]) * (1 + 1e-9) and
+            a["rel_l2"] <= (g["rel_l2"] + b["rel_l2"]) * (1 + 1e-9)),
+        "gpu_no_less_accurate_than_port": bool(g["max_abs"] <= b["max_abs"] and g["rel_l2"] <= b["rel_l2"]),
+    }
     return parity
 
 
@@ -762,11 +827,35 @@ def main():
     extra = {}
     if not args.no_extra:
         for name in ("C1", "C2-b8", "C4", "C5-global", "C5-window", "C5-window-dense"):
-            r = time_decode(DECODE[name], args.steps, args.warmup, device)
+            cfg = DECODE[name]
+            quantized = cfg["bits"] != 16
+            r = time_decode(cfg, args.steps, args.warmup, device, want_parity=quantized)
             extra[name] = {"gbs": round(r["gbs"], 1), "frac": round(r["gbs"] / PEAK_HBM_GBS, 4),
                            "us_per_step": round(r["ms_per_step"] * 1e3, 3), "bytes": r["bytes"],
-                           "kernel_us": round(r["call_us_mean"], 3)}
+                           "kernel_us": round(r["call_us_mean"], 3), "parity": r.get("parity")}
             log(f"[bench] {name}: {r['gbs']:.1f} GB/s ({r['ms_per_step'] * 1e3:.2f} us/step)")
+            if quantized and not args.no_cpu:
+                q, cache, scale = r["cpu_inputs"]
+                c, faithful = cpu_baseline(cfg, q, cache, scale, r["seq_lens"], budget_s=6.0, max_calls=3)
+                add_faithful(extra[name]["parity"], r.get("parity_arrays"), faithful)
+                extra[name]["cpu_baseline"] = c
+                log(f"[bench] {name} CPU baseline: {c['value']} GB/s on {c['cores']} cores")
+            del r
+            torch.cuda.empty_cache()
+        for name, cfg in PREFILL_C5.items():
+            pr = time_prefill(cfg, 1, max(1, args.warmup // 10), device, want_parity=not args.no_parity)
+            e = {"tflops": round(pr["tflops"], 2), "attn_tflops": round(pr["attn_tflops"], 2),
+                 "frac": round(pr["attn_tflops"] / PEAK_MFMA_TFLOPS, 4), "ms_per_step": round(pr["ms_per_step"], 4),
+                 "attn_ms": round(pr["attn_ms"], 4), "append_ms": round(pr["append_ms"], 4),
+                 "flops": pr["flops"], "chunk_attn_us": pr["chunk_attn_us"], "parity": pr.get("parity")}
+            if not args.no_cpu and "cpu_inputs" in pr:
+                c, faithful = prefill_cpu_baseline(cfg, *pr["cpu_inputs"], budget_s=10.0)
+                add_faithful(e["parity"], pr.get("parity_arrays"), faithful)
+                e["cpu_baseline"] = c
+            extra[name] = e
+            log(f"[bench] {name}: {pr['attn_tflops']:.1f} TFLOP/s attention ({pr['attn_ms']:.3f} ms), "
+                f"{pr['tflops']:.1f} TFLOP/s whole step")
+            del pr
             torch.cuda.empty_cache()
         r = time_paged_decode(DECODE["C2-b8"], args.steps, args.warmup, device)
         extra["C2-b8-paged"] = {"gbs": round(r["gbs"], 1), "frac": round(r["gbs"] / PEAK_HBM_GBS, 4),
@@ -788,7 +877,7 @@ def main():
         if q is None:
             r2 = time_decode(head, 1, 0, device, want_parity=True)
             q, cache, scale = r2["cpu_inputs"]
-        cpu, faithful = cpu_baseline(head, q, cache, scale)
+        cpu, faithful = cpu_baseline(head, q, cache, scale, seq_lens_of(head))
         add_faithful(res.get("parity"), res.get("parity_arrays"), faithful)
         log(f"[bench] CPU baseline: {cpu['value']} GB/s on {cpu['cores']} cores")
 
