@@ -752,6 +752,8 @@ def main():
     ap.add_argument("--prefill-only", action="store_true", help="time only the C3 chunked-prefill leg")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run 10 device copies of 256 MiB (reference for rocprofv3 FETCH_SIZE/WRITE_SIZE)")
+    ap.add_argument("--config", choices=sorted(DECODE) + sorted(PREFILL_C5) + ["C3"],
+                    help="time only this workload (no CPU leg, no parity) and print its numbers: for profiling")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -782,6 +784,22 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         log(f"[bench] calibrate-copy: 10 copies of {n} bytes")
+        return
+
+    if args.config:
+        # one workload alone, as a profiler run needs it
+        if args.config in DECODE:
+            r = time_decode(DECODE[args.config], args.steps, args.warmup, device)
+            out = {"config": args.config, "gbs": round(r["gbs"], 1), "frac": round(r["gbs"] / PEAK_HBM_GBS, 4),
+                   "us_per_step": round(r["ms_per_step"] * 1e3, 3), "kernel_us": round(r["call_us_mean"], 3),
+                   "bytes": r["bytes"]}
+        else:
+            cfg = PREFILL if args.config == "C3" else PREFILL_C5[args.config]
+            r = time_prefill(cfg, max(1, min(args.steps, 3)), args.warmup, device)
+            out = {"config": args.config, "attn_tflops": round(r["attn_tflops"], 2),
+                   "frac": round(r["attn_tflops"] / PEAK_MFMA_TFLOPS, 4), "attn_ms": round(r["attn_ms"], 4),
+                   "flops": r["flops"]}
+        print(json.dumps(out), flush=True)
         return
 
     prefill = None
