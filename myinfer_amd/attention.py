@@ -38,6 +38,7 @@ give the same structure without building a mask.
 
 from __future__ import annotations
 
+import weakref
 from typing import Optional
 
 import torch
@@ -71,14 +72,40 @@ def _expected_mask(L: int, S: int, S_b: torch.Tensor, causal: bool, window: int,
     return m.expand(S_b.shape[0], L, S)
 
 
-def mask_structure(mask, B: int, n_q_heads: int, L: int, S: int):
-    """Translate a reference-style mask into (causal, window, seq_lens) for the kernels."""
+# Analysed boolean / float masks: id(mask) -> (weak reference, version, shape key, result). A model
+# builds one mask per forward pass and hands it to every layer; the analysis (a host pass over the
+# mask) then runs once for all of them, and a mask on the host never costs a device synchronization.
+_mask_cache: dict = {}
+
+
+def mask_structure(mask, B: int, n_q_heads: int, L: int, S: int, device=None):
+    """Translate a reference-style mask into (causal, window, seq_lens) for the kernels.
+
+    String and None masks cost nothing. An array mask is analysed on the host (a device mask is
+    copied there once) and the result is cached for that mask object until it is modified, so the
+    layers of one forward pass share one analysis. seq_lens comes back as an int32 tensor on
+    `device` (default: the mask's device)."""
     if mask is None:
         return False, 0, None
     if isinstance(mask, str):
         return True, 0, None
     if not torch.is_tensor(mask):
         raise NotImplementedError(f"unsupported mask type {type(mask)}")
+    device = torch.device(device) if device is not None else mask.device
+    key = (B, n_q_heads, L, S, str(device))
+    hit = _mask_cache.get(id(mask))
+    if hit is not None and hit[0]() is mask and hit[1] == mask._version and hit[2] == key:
+        return hit[3]
+    causal, window, seq = _analyse_mask(mask.detach().cpu(), B, n_q_heads, L, S)
+    res = (causal, window, None if seq is None else seq.to(device))
+    if len(_mask_cache) > 64:
+        _mask_cache.clear()
+    _mask_cache[id(mask)] = (weakref.ref(mask), mask._version, key, res)
+    return res
+
+
+def _analyse_mask(mask: torch.Tensor, B: int, n_q_heads: int, L: int, S: int):
+    """mask_structure for a host tensor (seq_lens on the host)."""
     if mask.dtype != torch.bool:
         if bool((mask == 0).all()):
             return False, 0, None
@@ -124,14 +151,14 @@ def blocked_quantized_sdpa(queries: torch.Tensor, q_keys, q_values, scale: float
     """
     B, n_q_heads, L, D = queries.shape
     S = q_keys[0].shape[-2]
-    causal, window, seq_lens = _resolve_mask(mask, B, n_q_heads, L, S, window, seq_lens)
+    causal, window, seq_lens = _resolve_mask(mask, B, n_q_heads, L, S, window, seq_lens, queries.device)
     return kernels.attention(queries, tuple(q_keys), tuple(q_values), scale, causal=causal, window=window,
                              seq_lens=seq_lens, group_size=group_size, bits=bits)
 
 
-def _resolve_mask(mask, B: int, n_q_heads: int, L: int, S: int, window: int, seq_lens):
+def _resolve_mask(mask, B: int, n_q_heads: int, L: int, S: int, window: int, seq_lens, device=None):
     """(causal, window, seq_lens) from a reference-style mask plus the keyword extensions."""
-    causal, mwin, mseq = mask_structure(mask, B, n_q_heads, L, S)
+    causal, mwin, mseq = mask_structure(mask, B, n_q_heads, L, S, device=device)
     if window and mwin and window != mwin:
         raise ValueError(f"window={window} disagrees with the mask's window {mwin}")
     window = window or mwin
@@ -155,7 +182,7 @@ def fast_scaled_dot_product_attention(queries: torch.Tensor, keys: torch.Tensor,
     """
     B, n_q_heads, L, D = queries.shape
     S = keys.shape[-2]
-    causal, window, seq_lens = _resolve_mask(mask, B, n_q_heads, L, S, window, seq_lens)
+    causal, window, seq_lens = _resolve_mask(mask, B, n_q_heads, L, S, window, seq_lens, queries.device)
     return kernels.attention(queries, keys, values, scale, causal=causal, window=window, seq_lens=seq_lens)
 
 

@@ -117,3 +117,26 @@ def test_install_without_arguments_patches_named_modules(monkeypatch):
     assert A._installed
     assert base.quantized_scaled_dot_product_attention is A.blocked_quantized_sdpa
     assert gen.maybe_quantize_kv_cache is A.safe_maybe_quantize_kv_cache
+
+
+def test_mask_analysis_runs_once_per_mask(monkeypatch):
+    # the layers of one forward pass share one mask object: it is analysed once, on the host, and
+    # analysed again only after it is modified in place
+    calls = []
+    real = A._analyse_mask
+
+    def counting(*a):
+        calls.append(1)
+        return real(*a)
+
+    monkeypatch.setattr(A, "_analyse_mask", counting)
+    monkeypatch.setattr(A, "_mask_cache", {})
+    L, S = 4, 50
+    m = torch.ones(1, 1, L, S, dtype=torch.bool).tril(S - L)
+    first = A.mask_structure(m, 1, 8, L, S)
+    for _ in range(5):
+        assert A.mask_structure(m, 1, 8, L, S) == first
+    assert len(calls) == 1 and first == (True, 0, None)
+    m.fill_(True)  # modified in place: a new analysis, a new answer (every key visible)
+    assert A.mask_structure(m, 1, 8, L, S) == (False, 0, None)
+    assert len(calls) == 2
