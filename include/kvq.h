@@ -127,7 +127,9 @@ int kvq_rope_quantize_append(const kvq_rows* k_src, const kvq_qtensor* k_dst,
  * out = softmax(scale * q K^T + mask) V over the dequantized K/V.
  * Replaces: m5engine/attention.py:42-45 (the L == 1 hand-off to mlx-lm's
  * quantized_scaled_dot_product_attention) and, for L > 1, the blocked loop at :64-103.
- * Requirements: (Hq / Hkv) * L <= 16 * 64 / D; D in {64, 128}; group_size 64; bits in {4, 8}.
+ * Requirements: D in {64, 128}; group_size in {32, 64, 128} and <= D; bits in {4, 8}. One pass of
+ *   the kernel serves 16 * group_size / D query rows ((Hq / Hkv) * L) of a KV head; more rows take
+ *   more passes over the keys.
  *   seq_lens: NULL (every sequence has S keys) or device int32[B] with 1 <= seq_lens[b] <= S.
  *   causal:   query l of sequence b sits at position seq_len_b - L + l and sees keys <= it.
  *   window:   0 = none; otherwise keys k > position - window only (sliding window).
@@ -170,7 +172,7 @@ int kvq_decode_attn_static(const kvq_rows* q, const kvq_qtensor* k, const kvq_qt
 /*
  * Attention for prefill chunks (any L): same contract as kvq_decode_attn, MFMA tiles with
  * K/V tiles dequantized into LDS. Replaces m5engine/attention.py:29-103 for L > 1.
- * Requirements: D == 128; group_size 64; bits in {4, 8}; Hq a multiple of Hkv.
+ * Requirements: D == 128; group_size in {32, 64, 128}; bits in {4, 8}; Hq a multiple of Hkv.
  */
 int kvq_prefill_attn(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v,
                      const int32_t* seq_lens, const kvq_rows* out,

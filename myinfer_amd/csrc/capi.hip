@@ -98,13 +98,21 @@ int check_workspace(size_t ws_needed, void* workspace, size_t workspace_bytes) {
   return KVQ_OK;
 }
 
+// Scale-group sizes the attention kernels are built for: 32, 64 and 128, at most D.
+int check_attn_group(int group_size, int D) {
+  if ((group_size != 32 && group_size != 64 && group_size != 128) || group_size > D)
+    return fail(KVQ_ERR_UNSUPPORTED, "attention supports group_size 32, 64 and 128 (at most head_dim %d), got %d", D,
+                group_size);
+  return KVQ_OK;
+}
+
 // Everything check_attn checks but the workspace.
 int check_attn_args(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v, const kvq_rows* out, int B, int Hq,
                     int Hkv, int L, int D, int S, int bits, int group_size, int dtype, float scale, int window) {
   int rc;
   if ((rc = check_attn_common(q, out, B, Hq, Hkv, L, D, S, dtype, scale, window))) return rc;
   if (bits != 4 && bits != 8) return fail(KVQ_ERR_UNSUPPORTED, "attention supports 4- and 8-bit caches, got bits=%d", bits);
-  if (group_size != 64) return fail(KVQ_ERR_UNSUPPORTED, "attention supports group_size 64, got %d", group_size);
+  if ((rc = check_attn_group(group_size, D))) return rc;
   if ((rc = check_qtensor(k, "keys"))) return rc;
   if ((rc = check_qtensor(v, "values"))) return rc;
   const int64_t row_words = (int64_t)D * bits / 32;
@@ -112,7 +120,8 @@ int check_attn_args(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* 
     if (!aligned(t->codes, 16) || (t->codes_stride_s * 4) % 16 || (t->codes_stride_h * 4) % 16 || (t->codes_stride_b * 4) % 16)
       return fail(KVQ_ERR_INVALID, "codes must be 16-byte aligned with 16-byte-multiple row, head and batch strides");
     if (t->codes_stride_s < row_words) return fail(KVQ_ERR_INVALID, "codes row stride %lld is smaller than D*bits/32=%lld", (long long)t->codes_stride_s, (long long)row_words);
-    if (t->sb_stride_s < D / 64) return fail(KVQ_ERR_INVALID, "scales row stride %lld is smaller than D/group=%d", (long long)t->sb_stride_s, D / 64);
+    if (t->sb_stride_s < D / group_size)
+      return fail(KVQ_ERR_INVALID, "scales row stride %lld is smaller than D/group=%d", (long long)t->sb_stride_s, D / group_size);
     // the kernels address each (sequence, KV head)'s rows with 32-bit byte offsets
     if ((int64_t)S * t->codes_stride_s * 4 > (int64_t)UINT32_MAX || (int64_t)S * t->sb_stride_s * 2 > (int64_t)UINT32_MAX)
       return fail(KVQ_ERR_UNSUPPORTED, "attention needs S times each row stride within 4 GiB (S=%d)", S);
@@ -301,11 +310,14 @@ int kvq_paged_quantize_append(const kvq_rows* k_src, const kvq_qtensor* k_pool, 
 size_t kvq_decode_workspace_size(int B, int Hq, int Hkv, int L, int D, int S, int window) {
   if (B <= 0 || Hq <= 0 || Hkv <= 0 || L <= 0 || S <= 0 || (D != 64 && D != 128) || window < 0) return 0;
   // one size serves every cache format: the quantized (8-, 4-bit) and the unquantized (16) plans
+  // and every scale-group size (the group sets the query rows per workgroup)
   size_t n = 0;
-  for (int bits : {8, 4, 16}) {
-    const size_t x = kvq::decode_workspace_bytes(B, Hq, Hkv, L, D, S, window, bits);
-    n = x > n ? x : n;
-  }
+  for (int bits : {8, 4, 16})
+    for (int G : {32, 64, 128}) {
+      if (G > D) continue;
+      const size_t x = kvq::decode_workspace_bytes(B, Hq, Hkv, L, D, S, window, bits, G);
+      n = x > n ? x : n;
+    }
   return n;
 }
 
@@ -317,8 +329,8 @@ int kvq_decode_attn(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* 
   int rc = check_attn(q, k, v, out, B, Hq, Hkv, L, D, S, bits, group_size, dtype, scale, window,
                       kvq_decode_workspace_size(B, Hq, Hkv, L, D, S, window), workspace, workspace_bytes);
   if (rc) return rc;
-  return hip_status(kvq::launch_decode(q, k, v, seq_lens, out, B, Hq, Hkv, L, D, S, bits, dtype, scale, causal,
-                                       window, workspace, (hipStream_t)stream),
+  return hip_status(kvq::launch_decode(q, k, v, seq_lens, out, B, Hq, Hkv, L, D, S, bits, group_size, dtype, scale,
+                                       causal, window, workspace, (hipStream_t)stream),
                     "decode_attn launch");
 }
 
@@ -334,8 +346,8 @@ int kvq_decode_attn_static(const kvq_rows* q, const kvq_qtensor* k, const kvq_qt
                 "with a workspace)", need, (size_t)KVQ_STATIC_SCRATCH_BYTES);
   void* ws = nullptr;
   if ((rc = static_scratch((hipStream_t)stream, &ws))) return rc;
-  return hip_status(kvq::launch_decode(q, k, v, seq_lens, out, B, Hq, Hkv, L, D, S, bits, dtype, scale, causal,
-                                       window, ws, (hipStream_t)stream),
+  return hip_status(kvq::launch_decode(q, k, v, seq_lens, out, B, Hq, Hkv, L, D, S, bits, group_size, dtype, scale,
+                                       causal, window, ws, (hipStream_t)stream),
                     "decode_attn_static launch");
 }
 
@@ -353,8 +365,8 @@ int kvq_prefill_attn(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor*
                       kvq_prefill_workspace_size(B, Hq, Hkv, L, D, S, window), workspace, workspace_bytes);
   if (rc) return rc;
   if ((rc = check_rows(out, "out", D, true))) return rc;  // rows are written 8 bytes at a time
-  return hip_status(kvq::launch_prefill(q, k, v, seq_lens, out, B, Hq, Hkv, L, D, S, bits, dtype, scale, causal,
-                                        window, workspace, (hipStream_t)stream),
+  return hip_status(kvq::launch_prefill(q, k, v, seq_lens, out, B, Hq, Hkv, L, D, S, bits, group_size, dtype, scale,
+                                        causal, window, workspace, (hipStream_t)stream),
                     "prefill_attn launch");
 }
 
@@ -366,7 +378,7 @@ static int check_paged_attn(const kvq_rows* q, const kvq_qtensor* k, const kvq_q
   int rc;
   if ((rc = check_attn_common(q, out, B, Hq, Hkv, L, D, S, dtype, scale, window))) return rc;
   if (bits != 4 && bits != 8) return fail(KVQ_ERR_UNSUPPORTED, "attention supports 4- and 8-bit caches, got bits=%d", bits);
-  if (group_size != 64) return fail(KVQ_ERR_UNSUPPORTED, "attention supports group_size 64, got %d", group_size);
+  if ((rc = check_attn_group(group_size, D))) return rc;
   if ((rc = check_pool(k, "k_pool", Hkv, D, bits, group_size, num_pages))) return rc;
   if ((rc = check_pool(v, "v_pool", Hkv, D, bits, group_size, num_pages))) return rc;
   for (const kvq_qtensor* t : {k, v})
@@ -387,8 +399,8 @@ int kvq_paged_decode_attn(const kvq_rows* q, const kvq_qtensor* k_pool, const kv
                             workspace, workspace_bytes);
   if (rc) return rc;
   return hip_status(kvq::launch_decode_paged(q, k_pool, v_pool, num_pages, block_table, table_stride, seq_lens, out, B,
-                                             Hq, Hkv, L, D, S, bits, dtype, scale, causal, window, workspace,
-                                             (hipStream_t)stream),
+                                             Hq, Hkv, L, D, S, bits, group_size, dtype, scale, causal, window,
+                                             workspace, (hipStream_t)stream),
                     "paged_decode_attn launch");
 }
 
@@ -403,8 +415,8 @@ int kvq_paged_prefill_attn(const kvq_rows* q, const kvq_qtensor* k_pool, const k
                             workspace, workspace_bytes);
   if (rc) return rc;
   return hip_status(kvq::launch_prefill_paged(q, k_pool, v_pool, num_pages, block_table, table_stride, seq_lens, out, B,
-                                              Hq, Hkv, L, D, S, bits, dtype, scale, causal, window, workspace,
-                                              (hipStream_t)stream),
+                                              Hq, Hkv, L, D, S, bits, group_size, dtype, scale, causal, window,
+                                              workspace, (hipStream_t)stream),
                     "paged_prefill_attn launch");
 }
 

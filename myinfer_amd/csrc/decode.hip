@@ -38,6 +38,8 @@
 #include <math.h>
 #include <stdlib.h>
 
+#include <type_traits>
+
 #include "common.h"
 #include "launch.h"
 #include "merge.h"
@@ -50,10 +52,12 @@ constexpr int kXcds = 8;
 // BITS == 16 is the unquantized cache: raw T rows, no scales or biases. It keeps the column
 // layout of the quantized cache (R query rows, each in NG columns), with every column computing the
 // row's full dot product, so the wave epilogue below serves both.
-template <int D, int BITS>
+template <int D, int BITS, int G = 64>
 struct DecCfg {
   static constexpr bool DENSE = BITS == 16;
-  static constexpr int NG = D / 64;            // scale groups per row
+  static_assert(G == 32 || G == 64 || G == 128, "group sizes 32, 64, 128");
+  static_assert(D % G == 0 && D / 4 <= G, "a lane group's quarter of a row lies in one scale group");
+  static constexpr int NG = D / G;             // scale groups per row
   static constexpr int R = 16 / NG;            // query rows per wave
   static constexpr int KSTEPS = D / 32;        // QK MFMA k-steps (8 dims per lane each)
   static constexpr int NBLK = D / 16;          // PV MFMA column blocks
@@ -64,10 +68,14 @@ struct DecCfg {
   static constexpr int RPI = 64 / CPR;         // code rows per 1 KiB DMA instruction
   static constexpr int CI = kTile / RPI;       // DMA instructions per K (or V) tile
   static constexpr int TB = kTile * ROWB;      // bytes of a K (or V) tile
-  // a ring slot: [K tile][V tile][sK, bK, sV, bV: 64 4-byte cells each, value in the low half;
-  // cell 32 g + k holds group g of key k] (no scale/bias cells for the unquantized cache)
-  static constexpr int SLOT = 2 * TB + (DENSE ? 0 : 4 * 256);
-  static constexpr int IPT = 2 * CI + (DENSE ? 0 : 4);  // DMA instructions per tile
+  // a ring slot: [K tile][V tile][sK, bK, sV, bV: SBC 4-byte cells each, value in the low half;
+  // cell 32 g + k holds group g of key k] (no scale/bias cells for the unquantized cache). One
+  // 2-byte DMA fills 64 cells (two groups of 32 keys), so NSB of them fill an array.
+  static constexpr int NSB = NG > 2 ? NG / 2 : 1;
+  static constexpr int SBC = 64 * NSB;
+  static constexpr int AS = 4 * SBC;  // bytes between the arrays
+  static constexpr int SLOT = 2 * TB + (DENSE ? 0 : 4 * AS);
+  static constexpr int IPT = 2 * CI + (DENSE ? 0 : 4 * NSB);  // DMA instructions per tile
 };
 
 struct DecParams {
@@ -148,7 +156,8 @@ struct TileOps<32> {
 };
 
 // ka0/ka1: the two K chunk addresses of key n (ka1 unused below 128-byte rows); sa: the sb base;
-// va: the V slice address of key 4 lg.
+// va: the V slice address of key 4 lg. AS: bytes between the scale/bias arrays of a slot.
+template <int AS>
 __device__ __forceinline__ void read_tile(TileOps<128>& t, uint32_t ka0, uint32_t ka1, uint32_t sa, uint32_t va) {
   asm volatile(
       "ds_read_b128 %0, %20\n"
@@ -157,12 +166,12 @@ __device__ __forceinline__ void read_tile(TileOps<128>& t, uint32_t ka0, uint32_
       "ds_read_b128 %3, %21 offset:2048\n"
       "ds_read_b128 %4, %22\n"
       "ds_read_b128 %5, %22 offset:64\n"
-      "ds_read_b128 %6, %22 offset:256\n"
-      "ds_read_b128 %7, %22 offset:320\n"
-      "ds_read_b128 %8, %22 offset:512\n"
-      "ds_read_b128 %9, %22 offset:576\n"
-      "ds_read_b128 %10, %22 offset:768\n"
-      "ds_read_b128 %11, %22 offset:832\n"
+      "ds_read_b128 %6, %22 offset:%24\n"
+      "ds_read_b128 %7, %22 offset:%25\n"
+      "ds_read_b128 %8, %22 offset:%26\n"
+      "ds_read_b128 %9, %22 offset:%27\n"
+      "ds_read_b128 %10, %22 offset:%28\n"
+      "ds_read_b128 %11, %22 offset:%29\n"
       "ds_read_b64 %12, %23\n"
       "ds_read_b64 %13, %23 offset:128\n"
       "ds_read_b64 %14, %23 offset:256\n"
@@ -176,21 +185,23 @@ __device__ __forceinline__ void read_tile(TileOps<128>& t, uint32_t ka0, uint32_
         "=&v"(t.sb[1][0]), "=&v"(t.sb[1][1]), "=&v"(t.sb[2][0]), "=&v"(t.sb[2][1]), "=&v"(t.sb[3][0]),
         "=&v"(t.sb[3][1]), "=&v"(t.v[0]), "=&v"(t.v[1]), "=&v"(t.v[2]), "=&v"(t.v[3]), "=&v"(t.v[4]), "=&v"(t.v[5]),
         "=&v"(t.v[6]), "=&v"(t.v[7])
-      : "v"(ka0), "v"(ka1), "v"(sa), "v"(va)
+      : "v"(ka0), "v"(ka1), "v"(sa), "v"(va), "i"(AS), "i"(AS + 64), "i"(2 * AS), "i"(2 * AS + 64), "i"(3 * AS),
+        "i"(3 * AS + 64)
       : "memory");
 }
+template <int AS>
 __device__ __forceinline__ void read_tile(TileOps<64>& t, uint32_t ka0, uint32_t, uint32_t sa, uint32_t va) {
   asm volatile(
       "ds_read_b128 %0, %18\n"
       "ds_read_b128 %1, %18 offset:1024\n"
       "ds_read_b128 %2, %19\n"
       "ds_read_b128 %3, %19 offset:64\n"
-      "ds_read_b128 %4, %19 offset:256\n"
-      "ds_read_b128 %5, %19 offset:320\n"
-      "ds_read_b128 %6, %19 offset:512\n"
-      "ds_read_b128 %7, %19 offset:576\n"
-      "ds_read_b128 %8, %19 offset:768\n"
-      "ds_read_b128 %9, %19 offset:832\n"
+      "ds_read_b128 %4, %19 offset:%21\n"
+      "ds_read_b128 %5, %19 offset:%22\n"
+      "ds_read_b128 %6, %19 offset:%23\n"
+      "ds_read_b128 %7, %19 offset:%24\n"
+      "ds_read_b128 %8, %19 offset:%25\n"
+      "ds_read_b128 %9, %19 offset:%26\n"
       "ds_read_b32 %10, %20\n"
       "ds_read_b32 %11, %20 offset:64\n"
       "ds_read_b32 %12, %20 offset:128\n"
@@ -203,21 +214,22 @@ __device__ __forceinline__ void read_tile(TileOps<64>& t, uint32_t ka0, uint32_t
       : "=&v"(t.k[0]), "=&v"(t.k[1]), "=&v"(t.sb[0][0]), "=&v"(t.sb[0][1]), "=&v"(t.sb[1][0]), "=&v"(t.sb[1][1]),
         "=&v"(t.sb[2][0]), "=&v"(t.sb[2][1]), "=&v"(t.sb[3][0]), "=&v"(t.sb[3][1]), "=&v"(t.v[0]), "=&v"(t.v[1]),
         "=&v"(t.v[2]), "=&v"(t.v[3]), "=&v"(t.v[4]), "=&v"(t.v[5]), "=&v"(t.v[6]), "=&v"(t.v[7])
-      : "v"(ka0), "v"(sa), "v"(va)
+      : "v"(ka0), "v"(sa), "v"(va), "i"(AS), "i"(AS + 64), "i"(2 * AS), "i"(2 * AS + 64), "i"(3 * AS), "i"(3 * AS + 64)
       : "memory");
 }
+template <int AS>
 __device__ __forceinline__ void read_tile(TileOps<32>& t, uint32_t ka0, uint32_t, uint32_t sa, uint32_t va) {
   asm volatile(
       "ds_read_b64 %0, %18\n"
       "ds_read_b64 %1, %18 offset:512\n"
       "ds_read_b128 %2, %19\n"
       "ds_read_b128 %3, %19 offset:64\n"
-      "ds_read_b128 %4, %19 offset:256\n"
-      "ds_read_b128 %5, %19 offset:320\n"
-      "ds_read_b128 %6, %19 offset:512\n"
-      "ds_read_b128 %7, %19 offset:576\n"
-      "ds_read_b128 %8, %19 offset:768\n"
-      "ds_read_b128 %9, %19 offset:832\n"
+      "ds_read_b128 %4, %19 offset:%21\n"
+      "ds_read_b128 %5, %19 offset:%22\n"
+      "ds_read_b128 %6, %19 offset:%23\n"
+      "ds_read_b128 %7, %19 offset:%24\n"
+      "ds_read_b128 %8, %19 offset:%25\n"
+      "ds_read_b128 %9, %19 offset:%26\n"
       "ds_read_u16 %10, %20\n"
       "ds_read_u16 %11, %20 offset:32\n"
       "ds_read_u16 %12, %20 offset:64\n"
@@ -230,7 +242,7 @@ __device__ __forceinline__ void read_tile(TileOps<32>& t, uint32_t ka0, uint32_t
       : "=&v"(t.k[0]), "=&v"(t.k[1]), "=&v"(t.sb[0][0]), "=&v"(t.sb[0][1]), "=&v"(t.sb[1][0]), "=&v"(t.sb[1][1]),
         "=&v"(t.sb[2][0]), "=&v"(t.sb[2][1]), "=&v"(t.sb[3][0]), "=&v"(t.sb[3][1]), "=&v"(t.v[0]), "=&v"(t.v[1]),
         "=&v"(t.v[2]), "=&v"(t.v[3]), "=&v"(t.v[4]), "=&v"(t.v[5]), "=&v"(t.v[6]), "=&v"(t.v[7])
-      : "v"(ka0), "v"(sa), "v"(va)
+      : "v"(ka0), "v"(sa), "v"(va), "i"(AS), "i"(AS + 64), "i"(2 * AS), "i"(2 * AS + 64), "i"(3 * AS), "i"(3 * AS + 64)
       : "memory");
 }
 
@@ -318,7 +330,7 @@ __device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xC
 
 // K operand (A of S^T = K Q^T) for k-step j: 8 codes of the lane's key as f16 subnormals.
 template <int D, int BITS>
-__device__ __forceinline__ h8 k_operand(const Bytes<DecCfg<D, BITS>::KLB>& kc, int j) {
+__device__ __forceinline__ h8 k_operand(const Bytes<D * BITS / 32>& kc, int j) {
   u4 r;
   if constexpr (BITS == 8) {
     const uint32_t w0 = kc.w[2 * j], w1 = kc.w[2 * j + 1];
@@ -377,14 +389,14 @@ constexpr int kFewSplits = 4;
 
 // Workgroups per CU the launch bounds ask for: two 4-wave workgroups when their rings fit in LDS
 // together, else one.
-template <int D, int BITS, int NW, int NSLOT>
+template <int D, int BITS, int NW, int NSLOT, int G>
 constexpr int dec_min_wgs() {
-  return (NW == 4 && 2 * NW * NSLOT * DecCfg<D, BITS>::SLOT <= 160 * 1024) ? 2 : 1;
+  return (NW == 4 && 2 * NW * NSLOT * DecCfg<D, BITS, G>::SLOT <= 160 * 1024) ? 2 : 1;
 }
 
-template <typename T, int D, int BITS, int NW, int NSLOT, bool PAGED = false>
-__global__ __launch_bounds__(NW * 64, (dec_min_wgs<D, BITS, NW, NSLOT>())) void decode_attn_kernel(DecParams p) {
-  using C = DecCfg<D, BITS>;
+template <typename T, int D, int BITS, int NW, int NSLOT, bool PAGED = false, int G = 64>
+__global__ __launch_bounds__(NW * 64, (dec_min_wgs<D, BITS, NW, NSLOT, G>())) void decode_attn_kernel(DecParams p) {
+  using C = DecCfg<D, BITS, G>;
   constexpr int R = C::R;
   constexpr int NT = NW * 64;
   // the tile ring while streaming; the waves' (m, l, o) and the split weights afterwards
@@ -430,7 +442,7 @@ __global__ __launch_bounds__(NW * 64, (dec_min_wgs<D, BITS, NW, NSLOT>())) void 
   const bool row_ok = row < p.nrows;
   const int hq = kvh * p.rep + (row_ok ? row / p.L : 0);
   const int lq = row_ok ? row % p.L : 0;
-  const bool in_group = (lg * (D / 4)) / 64 == g;
+  const bool in_group = (lg * (D / 4)) / G == g;
   u4 qraw[C::KSTEPS];
   {
     const uint16_t* qrow = p.q + (int64_t)b * p.q_sb + (int64_t)hq * p.q_sh + (int64_t)lq * p.q_sl + lg * (D / 4);
@@ -457,7 +469,7 @@ __global__ __launch_bounds__(NW * 64, (dec_min_wgs<D, BITS, NW, NSLOT>())) void 
   // lane offsets: code lane l fills 16-byte cell l of each KiB, i.e. row l / CPR and -- for K,
   // swizzled -- chunk (l % CPR) ^ (row % CPR); scale/bias lane l reads group l / 32 of key l % 32
   // (for NG == 1 the upper half re-reads the lower half's keys)
-  uint32_t dk[C::CI], dv[C::CI], dsb[4];
+  uint32_t dk[C::CI], dv[C::CI], dsb[4][C::NSB];
   {
     const int rr = lane / C::CPR, cc = lane % C::CPR;
 #pragma unroll
@@ -466,9 +478,13 @@ __global__ __launch_bounds__(NW * 64, (dec_min_wgs<D, BITS, NW, NSLOT>())) void 
       dk[c] = (uint32_t)((int64_t)kr * p.kc_ss + 16 * (cc ^ (kr % C::CPR)));
       dv[c] = (uint32_t)((int64_t)(c * C::RPI + rr) * p.vc_ss + 16 * cc);
     }
-    const int sk = lane & 31, sg = C::NG == 2 ? lane >> 5 : 0;
-    dsb[0] = dsb[1] = C::DENSE ? 0u : (uint32_t)(sk * p.ksb_ss * 2 + 2 * sg);
-    dsb[2] = dsb[3] = C::DENSE ? 0u : (uint32_t)(sk * p.vsb_ss * 2 + 2 * sg);
+#pragma unroll
+    for (int h = 0; h < C::NSB; ++h) {
+      // DMA h of an array fills cells 64 h + lane: group 2 h + lane / 32 of key lane % 32
+      const int sk = lane & 31, sg = C::NG >= 2 ? 2 * h + (lane >> 5) : 0;
+      dsb[0][h] = dsb[1][h] = C::DENSE ? 0u : (uint32_t)(sk * p.ksb_ss * 2 + 2 * sg);
+      dsb[2][h] = dsb[3][h] = C::DENSE ? 0u : (uint32_t)(sk * p.vsb_ss * 2 + 2 * sg);
+    }
   }
   uint8_t* const ring = smem + wave * (NSLOT * C::SLOT);
   auto tile_k0 = [&](int i) { return k_begin + kTile * (wave + NW * i); };
@@ -513,7 +529,9 @@ __global__ __launch_bounds__(NW * 64, (dec_min_wgs<D, BITS, NW, NSLOT>())) void 
     if constexpr (!C::DENSE) {
       const uint32_t kso = (uint32_t)((int64_t)rk0 * p.ksb_ss * 2), vso = (uint32_t)((int64_t)rk0 * p.vsb_ss * 2);
 #pragma unroll
-      for (int a = 0; a < 4; ++a) dma2(sr[a], sl + 2 * C::TB + 256 * a, dsb[a], a < 2 ? kso : vso);
+      for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int h = 0; h < C::NSB; ++h) dma2(sr[a], sl + 2 * C::TB + C::AS * a + 256 * h, dsb[a][h], a < 2 ? kso : vso);
     }
   };
   // nothing that waits for the query loads may be scheduled into (or before) the first tile loads
@@ -751,7 +769,7 @@ __global__ __launch_bounds__(NW * 64, (dec_min_wgs<D, BITS, NW, NSLOT>())) void 
       compute(op, tile_k0(i));
     } else {
       TileOps<C::ROWB> op;
-      read_tile(op, sa + off_k0, sa + off_k1, sa + off_sb, sa + off_v);
+      read_tile<C::AS>(op, sa + off_k0, sa + off_k1, sa + off_sb, sa + off_v);
       issue(i + NSLOT, slot);
       compute(op, tile_k0(i));
     }
@@ -787,50 +805,64 @@ __global__ __launch_bounds__(NW * 64, (dec_min_wgs<D, BITS, NW, NSLOT>())) void 
   }
   __syncthreads();
 
-  // ---- merge the waves: this workgroup's (m, l, o) per row, one float4 of o per thread; a single
+  // ---- merge the waves: this workgroup's (m, l, o) per row, NPT float4s of o per thread; a single
   // split writes the output, otherwise the partial goes to the workspace split-major:
   // o at ((unit * nsplit + split) * R + row) * D, (m, l) at the same index in pairs
   constexpr int NV = R * D / 4;
-  static_assert(NV <= NT, "one float4 of a partial per thread");
+  constexpr int NPT = (NV + NT - 1) / NT;
+  static_assert(NV % NT == 0 || NV < NT, "whole float4s of a partial per thread");
   const bool single = p.nsplit == 1;
-  const int i4 = threadIdx.x;
-  const int rr = (4 * i4) / D, d0 = (4 * i4) % D;
-  const int rw = rb * R + rr;
-  const bool mine = i4 < NV && rw < p.nrows;
-  const int hh = kvh * p.rep + rw / p.L, ll = rw % p.L;
-  uint16_t* const orow = p.out + (int64_t)b * p.o_sb + (int64_t)hh * p.o_sh + (int64_t)ll * p.o_sl + d0;
-  auto write_out = [&](f4 o, float inv) {
+  struct Slot {
+    int i4, rr, d0;
+    bool mine;
+    uint16_t* orow;
+  };
+  auto slot_of = [&](int it) {
+    Slot s;
+    s.i4 = threadIdx.x + it * NT;
+    s.rr = (4 * s.i4) / D;
+    s.d0 = (4 * s.i4) % D;
+    const int rw = rb * R + s.rr;
+    s.mine = s.i4 < NV && rw < p.nrows;
+    const int hh = kvh * p.rep + rw / p.L, ll = rw % p.L;
+    s.orow = p.out + (int64_t)b * p.o_sb + (int64_t)hh * p.o_sh + (int64_t)ll * p.o_sl + s.d0;
+    return s;
+  };
+  auto write_out = [&](const Slot& s, f4 o, float inv) {
 #pragma unroll
-    for (int e = 0; e < 4; ++e) orow[e] = from_float(o[e] * inv, T{});
+    for (int e = 0; e < 4; ++e) s.orow[e] = from_float(o[e] * inv, T{});
   };
   const __amdgpu_buffer_rsrc_t ro = make_rsrc(p.part_o + (int64_t)unit * p.nsplit * (R * D), (uint32_t)(p.nsplit * R * D * 4));
   const __amdgpu_buffer_rsrc_t rm = make_rsrc(p.part_ml + (int64_t)unit * p.nsplit * (2 * R), (uint32_t)(p.nsplit * R * 8));
-  if (i4 < NV) {
+#pragma unroll
+  for (int it = 0; it < NPT; ++it) {
+    const Slot sl = slot_of(it);
+    if (sl.i4 >= NV) continue;
     float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < NW; ++w) M = fmaxf(M, w_m[w * R + rr]);
+    for (int w = 0; w < NW; ++w) M = fmaxf(M, w_m[w * R + sl.rr]);
     f4 o = {0, 0, 0, 0};
     float lsum = 0.0f;
     if (M != -INFINITY) {
 #pragma unroll
       for (int w = 0; w < NW; ++w) {
-        const float mw = w_m[w * R + rr];
+        const float mw = w_m[w * R + sl.rr];
         if (mw != -INFINITY) {
           const float f = exp2_fast(mw - M);
-          o += f * *(const f4*)&w_o[(w * R + rr) * D + d0];
-          lsum += f * w_l[w * R + rr];
+          o += f * *(const f4*)&w_o[(w * R + sl.rr) * D + sl.d0];
+          lsum += f * w_l[w * R + sl.rr];
         }
       }
     }
     if (single) {
-      if (mine) write_out(o, lsum > 0.0f ? 1.0f / lsum : 0.0f);
+      if (sl.mine) write_out(sl, o, lsum > 0.0f ? 1.0f / lsum : 0.0f);
     } else if (p.fused) {
-      store_agent_b128(ro, 16 * i4 + split * (R * D * 4), o);
-      if (d0 == 0) store_agent_b64(rm, 8 * rr + split * (R * 8), make_float2(M, lsum));
+      store_agent_b128(ro, 16 * sl.i4 + split * (R * D * 4), o);
+      if (sl.d0 == 0) store_agent_b64(rm, 8 * sl.rr + split * (R * 8), make_float2(M, lsum));
     } else {
-      const int64_t pi = ((int64_t)unit * p.nsplit + split) * R + rr;
-      *(f4*)(p.part_o + pi * D + d0) = o;
-      if (d0 == 0) ((float2*)p.part_ml)[pi] = make_float2(M, lsum);
+      const int64_t pi = ((int64_t)unit * p.nsplit + split) * R + sl.rr;
+      *(f4*)(p.part_o + pi * D + sl.d0) = o;
+      if (sl.d0 == 0) ((float2*)p.part_ml)[pi] = make_float2(M, lsum);
     }
   }
   if (single || !p.fused) return;
@@ -847,72 +879,80 @@ __global__ __launch_bounds__(NW * 64, (dec_min_wgs<D, BITS, NW, NSLOT>())) void 
   if (s_prev != (unsigned)(p.nsplit - 1)) return;
   if (threadIdx.x == 0) __hip_atomic_store(&p.counters[unit], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
-  if (p.nsplit <= kFewSplits) {
-    // few splits (the plan's choice for this form): each thread loads its float4 and its row's
-    // (m, l) of every split in one round (loads past the last split re-read it and count with
-    // l = 0) and forms the weights itself: no wave reductions, no exchange through LDS
-    if (!mine) return;
+  if (NPT > 1 || p.nsplit <= kFewSplits) {
+    // few splits (the plan's choice for this form, and the only one with several float4s per
+    // thread): each thread loads its float4 and its row's (m, l) of every split in one round (loads
+    // past the last split re-read it and count with l = 0) and forms the weights itself: no wave
+    // reductions, no exchange through LDS
     const int last = p.nsplit - 1;
-    f4 po[kFewSplits];
-    float2 mv[kFewSplits];
 #pragma unroll
-    for (int u = 0; u < kFewSplits; ++u) {
-      const int su = min(u, last);
-      po[u] = load_agent_b128(ro, 16 * i4, su * (R * D * 4));
-      mv[u] = load_agent_b64(rm, 8 * rr, su * (R * 8));
+    for (int it = 0; it < NPT; ++it) {
+      const Slot sl = slot_of(it);
+      if (!sl.mine) continue;
+      f4 po[kFewSplits];
+      float2 mv[kFewSplits];
+#pragma unroll
+      for (int u = 0; u < kFewSplits; ++u) {
+        const int su = min(u, last);
+        po[u] = load_agent_b128(ro, 16 * sl.i4, su * (R * D * 4));
+        mv[u] = load_agent_b64(rm, 8 * sl.rr, su * (R * 8));
+      }
+      float Mx = -INFINITY;
+#pragma unroll
+      for (int u = 0; u < kFewSplits; ++u)
+        if (u <= last && mv[u].y > 0.0f) Mx = fmaxf(Mx, mv[u].x);
+      f4 acc = {0, 0, 0, 0};
+      float Ls = 0.0f;
+#pragma unroll
+      for (int u = 0; u < kFewSplits; ++u) {
+        const float w = (u <= last && mv[u].y > 0.0f) ? exp2_fast(mv[u].x - Mx) : 0.0f;
+        acc += w * po[u];
+        Ls += w * mv[u].y;
+      }
+      write_out(sl, acc, Ls > 0.0f ? 1.0f / Ls : 0.0f);
     }
-    float Mx = -INFINITY;
-#pragma unroll
-    for (int u = 0; u < kFewSplits; ++u)
-      if (u <= last && mv[u].y > 0.0f) Mx = fmaxf(Mx, mv[u].x);
-    f4 acc = {0, 0, 0, 0};
-    float Ls = 0.0f;
-#pragma unroll
-    for (int u = 0; u < kFewSplits; ++u) {
-      const float w = (u <= last && mv[u].y > 0.0f) ? exp2_fast(mv[u].x - Mx) : 0.0f;
-      acc += w * po[u];
-      Ls += w * mv[u].y;
-    }
-    write_out(acc, Ls > 0.0f ? 1.0f / Ls : 0.0f);
     return;
   }
-
-  // this thread's float4 of the first 32 splits, in flight while the weights are formed
-  constexpr int CH = 32;
-  f4 po[CH];
-#pragma unroll
-  for (int u = 0; u < CH; ++u)
-    po[u] = (i4 < NV && u < p.nsplit) ? load_agent_b128(ro, 16 * i4, u * (R * D * 4)) : f4{0, 0, 0, 0};
-  // weights w_s / sum_s w_s l_s per row: one wave per row, lane = split
-  for (int r2 = wave; r2 < R; r2 += NW) {
-    float2 v0 = make_float2(-INFINITY, 0.0f), v1 = v0;
-    if (lane < p.nsplit) v0 = load_agent_b64(rm, 8 * r2, lane * (R * 8));
-    if (lane + 64 < p.nsplit) v1 = load_agent_b64(rm, 8 * r2, (lane + 64) * (R * 8));
-    const float m0 = v0.y > 0.0f ? v0.x : -INFINITY, m1 = v1.y > 0.0f ? v1.x : -INFINITY;
-    const float Mx = wave_max(fmaxf(m0, m1));
-    const float w0 = (Mx == -INFINITY || m0 == -INFINITY) ? 0.0f : exp2_fast(m0 - Mx);
-    const float w1 = (Mx == -INFINITY || m1 == -INFINITY) ? 0.0f : exp2_fast(m1 - Mx);
-    const float Lsum = wave_sum(w0 * v0.y + w1 * v1.y);
-    const float inv = Lsum > 0.0f ? 1.0f / Lsum : 0.0f;
-    if (lane < p.nsplit) s_w[r2 * kMaxSplit + lane] = w0 * inv;
-    if (lane + 64 < p.nsplit) s_w[r2 * kMaxSplit + lane + 64] = w1 * inv;
-  }
-  __syncthreads();
-  if (!mine) return;
-  const float* wrow = s_w + rr * kMaxSplit;
-  f4 acc = {0, 0, 0, 0};
-#pragma unroll
-  for (int u = 0; u < CH; ++u)
-    if (u < p.nsplit) acc += wrow[u] * po[u];
-  for (int s0 = CH; s0 < p.nsplit; s0 += CH) {
+  if constexpr (NPT == 1) {
+    const Slot sl = slot_of(0);
+    const int i4 = sl.i4;
+    // this thread's float4 of the first 32 splits, in flight while the weights are formed
+    constexpr int CH = 32;
+    f4 po[CH];
 #pragma unroll
     for (int u = 0; u < CH; ++u)
-      po[u] = s0 + u < p.nsplit ? load_agent_b128(ro, 16 * i4, (s0 + u) * (R * D * 4)) : f4{0, 0, 0, 0};
+      po[u] = (i4 < NV && u < p.nsplit) ? load_agent_b128(ro, 16 * i4, u * (R * D * 4)) : f4{0, 0, 0, 0};
+    // weights w_s / sum_s w_s l_s per row: one wave per row, lane = split
+    for (int r2 = wave; r2 < R; r2 += NW) {
+      float2 v0 = make_float2(-INFINITY, 0.0f), v1 = v0;
+      if (lane < p.nsplit) v0 = load_agent_b64(rm, 8 * r2, lane * (R * 8));
+      if (lane + 64 < p.nsplit) v1 = load_agent_b64(rm, 8 * r2, (lane + 64) * (R * 8));
+      const float m0 = v0.y > 0.0f ? v0.x : -INFINITY, m1 = v1.y > 0.0f ? v1.x : -INFINITY;
+      const float Mx = wave_max(fmaxf(m0, m1));
+      const float w0 = (Mx == -INFINITY || m0 == -INFINITY) ? 0.0f : exp2_fast(m0 - Mx);
+      const float w1 = (Mx == -INFINITY || m1 == -INFINITY) ? 0.0f : exp2_fast(m1 - Mx);
+      const float Lsum = wave_sum(w0 * v0.y + w1 * v1.y);
+      const float inv = Lsum > 0.0f ? 1.0f / Lsum : 0.0f;
+      if (lane < p.nsplit) s_w[r2 * kMaxSplit + lane] = w0 * inv;
+      if (lane + 64 < p.nsplit) s_w[r2 * kMaxSplit + lane + 64] = w1 * inv;
+    }
+    __syncthreads();
+    if (!sl.mine) return;
+    const float* wrow = s_w + sl.rr * kMaxSplit;
+    f4 acc = {0, 0, 0, 0};
 #pragma unroll
     for (int u = 0; u < CH; ++u)
-      if (s0 + u < p.nsplit) acc += wrow[s0 + u] * po[u];
+      if (u < p.nsplit) acc += wrow[u] * po[u];
+    for (int s0 = CH; s0 < p.nsplit; s0 += CH) {
+#pragma unroll
+      for (int u = 0; u < CH; ++u)
+        po[u] = s0 + u < p.nsplit ? load_agent_b128(ro, 16 * i4, (s0 + u) * (R * D * 4)) : f4{0, 0, 0, 0};
+#pragma unroll
+      for (int u = 0; u < CH; ++u)
+        if (s0 + u < p.nsplit) acc += wrow[s0 + u] * po[u];
+    }
+    write_out(sl, acc, 1.0f);
   }
-  write_out(acc, 1.0f);
 }
 
 // ------------------------------------------------------------------------------------------
@@ -949,13 +989,15 @@ static DecTune decode_tune() {
   return t;
 }
 
-DecPlan decode_plan(int B, int Hq, int Hkv, int L, int D, int S, int window, int bits) {
+DecPlan decode_plan(int B, int Hq, int Hkv, int L, int D, int S, int window, int bits, int G) {
   DecPlan pl;
   const DecTune tune = decode_tune();
   const bool dense = bits == 16;
-  pl.nw = D == 128 && !dense ? tune.nw : 4;
-  pl.nslot = D == 128 && !dense ? tune.nslot : 2;
-  pl.R = 16 / (D / 64);
+  if (dense) G = 64;  // the unquantized kernels keep the column layout of group 64
+  const bool tuned = D == 128 && !dense && G == 64;  // the launch shapes built for other than 4 waves x 2 slots
+  pl.nw = tuned ? tune.nw : 4;
+  pl.nslot = tuned ? tune.nslot : 2;
+  pl.R = 16 / (D / G);
   const int nrows = (Hq / Hkv) * L;
   pl.rowblocks = (nrows + pl.R - 1) / pl.R;
   pl.span = window > 0 ? std::min(S, window + L - 1 + kTile - 1) : S;  // the window, from a tile boundary
@@ -967,7 +1009,10 @@ DecPlan decode_plan(int B, int Hq, int Hkv, int L, int D, int S, int window, int
   pl.chunk = (int)(tpw * kTile);
   pl.nsplit = (pl.span + pl.chunk - 1) / pl.chunk;
   const bool fused = tune.fused < 0 ? pl.nsplit <= kFusedMaxSplit : tune.fused != 0;
-  pl.fused = fused && pl.nunits <= kMaxCountedUnits;
+  // (with 16 query rows of 128 dims a thread owns two float4s of a partial; the in-kernel merge
+  // then handles at most kFewSplits splits)
+  const bool few_only = pl.R * D / 4 > 4 * 64;
+  pl.fused = fused && pl.nunits <= kMaxCountedUnits && (!few_only || pl.nsplit <= kFewSplits);
   return pl;
 }
 
@@ -987,14 +1032,14 @@ static DecLayout decode_layout(const DecPlan& pl, int D) {
   return l;
 }
 
-size_t decode_workspace_bytes(int B, int Hq, int Hkv, int L, int D, int S, int window, int bits) {
-  const DecPlan pl = decode_plan(B, Hq, Hkv, L, D, S, window, bits);
+size_t decode_workspace_bytes(int B, int Hq, int Hkv, int L, int D, int S, int window, int bits, int G) {
+  const DecPlan pl = decode_plan(B, Hq, Hkv, L, D, S, window, bits, G);
   return decode_layout(pl, D).total;
 }
 
-template <typename T, int D, int BITS, int NW, int NSLOT, bool PAGED = false>
+template <typename T, int D, int BITS, int NW, int NSLOT, bool PAGED = false, int G = 64>
 static hipError_t launch_decode_t(const DecParams& p, hipStream_t stream) {
-  hipLaunchKernelGGL((decode_attn_kernel<T, D, BITS, NW, NSLOT, PAGED>), dim3(p.nunits * p.nsplit), dim3(NW * 64), 0,
+  hipLaunchKernelGGL((decode_attn_kernel<T, D, BITS, NW, NSLOT, PAGED, G>), dim3(p.nunits * p.nsplit), dim3(NW * 64), 0,
                      stream, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || p.nsplit == 1 || p.fused) return e;
@@ -1009,16 +1054,18 @@ static hipError_t launch_decode_t(const DecParams& p, hipStream_t stream) {
   m.Hkv = p.Hkv;
   m.L = p.L;
   m.rep = p.rep;
-  m.R = DecCfg<D, BITS>::R;
+  m.R = DecCfg<D, BITS, G>::R;
   m.rowblocks = p.rowblocks;
   m.nsplit = p.nsplit;
   return launch_combine<T, D>(m, p.nunits / (p.Hkv * p.rowblocks), stream);
 }
 
-template <typename T, int D, int BITS>
+template <typename T, int D, int BITS, int G = 64>
 static hipError_t launch_decode_shape(const DecParams& p, const DecPlan& pl, hipStream_t stream) {
   if constexpr (BITS == 16) {
     return launch_decode_t<T, D, BITS, 4, 2>(p, stream);  // a 3-slot ring of raw rows does not fit
+  } else if constexpr (G != 64) {
+    return launch_decode_t<T, D, BITS, 4, 2, false, G>(p, stream);
   } else if constexpr (D == 128) {
     if (pl.nw == 8) return launch_decode_t<T, D, BITS, 8, 2>(p, stream);
     if (pl.nslot == 2) return launch_decode_t<T, D, BITS, 4, 2>(p, stream);
@@ -1065,10 +1112,29 @@ static DecParams decode_params(const kvq_rows* q, const int32_t* seq_lens, const
   return p;
 }
 
+// Calls f(T{}, D, BITS, G) (the last three as std::integral_constant) for the quantized
+// instantiation that matches the runtime arguments: D in {64, 128}, bits in {4, 8}, G in {32, 64,
+// 128} with G <= D.
+template <int N>
+using IC = std::integral_constant<int, N>;
+template <typename F>
+static hipError_t dispatch_quant(int dtype, int D, int bits, int G, F&& f) {
+  auto by_g = [&](auto t, auto d, auto b) -> hipError_t {
+    if (G == 32) return f(t, d, b, IC<32>{});
+    if constexpr (decltype(d)::value >= 128) {
+      if (G == 128) return f(t, d, b, IC<128>{});
+    }
+    return f(t, d, b, IC<64>{});
+  };
+  auto by_b = [&](auto t, auto d) -> hipError_t { return bits == 8 ? by_g(t, d, IC<8>{}) : by_g(t, d, IC<4>{}); };
+  auto by_d = [&](auto t) -> hipError_t { return D == 128 ? by_b(t, IC<128>{}) : by_b(t, IC<64>{}); };
+  return dtype == KVQ_DTYPE_BF16 ? by_d(BF16{}) : by_d(F16{});
+}
+
 hipError_t launch_decode(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v, const int32_t* seq_lens,
-                         const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int bits, int dtype,
+                         const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int bits, int G, int dtype,
                          float scale, int causal, int window, void* workspace, hipStream_t stream) {
-  const DecPlan pl = decode_plan(B, Hq, Hkv, L, D, S, window, bits);
+  const DecPlan pl = decode_plan(B, Hq, Hkv, L, D, S, window, bits, G);
   DecParams p = decode_params(q, seq_lens, out, Hq, Hkv, L, D, S, scale, causal, window, workspace, pl);
   p.kc = (const uint8_t*)k->codes;
   p.vc = (const uint8_t*)v->codes;
@@ -1088,23 +1154,16 @@ hipError_t launch_decode(const kvq_rows* q, const kvq_qtensor* k, const kvq_qten
   p.vsb_sb = v->sb_stride_b;
   p.vsb_sh = v->sb_stride_h;
   p.vsb_ss = v->sb_stride_s;
-  const bool bf = dtype == KVQ_DTYPE_BF16;
-#define KVQ_DEC(TT, DD, BB) return launch_decode_shape<TT, DD, BB>(p, pl, stream)
-  if (D == 128) {
-    if (bits == 8) { if (bf) KVQ_DEC(BF16, 128, 8); else KVQ_DEC(F16, 128, 8); }
-    else { if (bf) KVQ_DEC(BF16, 128, 4); else KVQ_DEC(F16, 128, 4); }
-  } else {
-    if (bits == 8) { if (bf) KVQ_DEC(BF16, 64, 8); else KVQ_DEC(F16, 64, 8); }
-    else { if (bf) KVQ_DEC(BF16, 64, 4); else KVQ_DEC(F16, 64, 4); }
-  }
-#undef KVQ_DEC
+  return dispatch_quant(dtype, D, bits, G, [&](auto t, auto d, auto b, auto g) {
+    return launch_decode_shape<decltype(t), decltype(d)::value, decltype(b)::value, decltype(g)::value>(p, pl, stream);
+  });
 }
 
 hipError_t launch_decode_paged(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v, int num_pages,
                                const int32_t* table, int64_t table_stride, const int32_t* seq_lens, const kvq_rows* out,
-                               int B, int Hq, int Hkv, int L, int D, int S, int bits, int dtype, float scale, int causal,
-                               int window, void* workspace, hipStream_t stream) {
-  const DecPlan pl = decode_plan(B, Hq, Hkv, L, D, S, window, bits);
+                               int B, int Hq, int Hkv, int L, int D, int S, int bits, int G, int dtype, float scale,
+                               int causal, int window, void* workspace, hipStream_t stream) {
+  const DecPlan pl = decode_plan(B, Hq, Hkv, L, D, S, window, bits, G);
   DecParams p = decode_params(q, seq_lens, out, Hq, Hkv, L, D, S, scale, causal, window, workspace, pl);
   p.kc = (const uint8_t*)k->codes;
   p.vc = (const uint8_t*)v->codes;
@@ -1127,22 +1186,15 @@ hipError_t launch_decode_paged(const kvq_rows* q, const kvq_qtensor* k, const kv
   p.table = table;
   p.table_stride = table_stride;
   p.num_pages = num_pages;
-  const bool bf = dtype == KVQ_DTYPE_BF16;
-#define KVQ_DECP(TT, DD, BB) return launch_decode_t<TT, DD, BB, 4, 2, true>(p, stream)
-  if (D == 128) {
-    if (bits == 8) { if (bf) KVQ_DECP(BF16, 128, 8); else KVQ_DECP(F16, 128, 8); }
-    else { if (bf) KVQ_DECP(BF16, 128, 4); else KVQ_DECP(F16, 128, 4); }
-  } else {
-    if (bits == 8) { if (bf) KVQ_DECP(BF16, 64, 8); else KVQ_DECP(F16, 64, 8); }
-    else { if (bf) KVQ_DECP(BF16, 64, 4); else KVQ_DECP(F16, 64, 4); }
-  }
-#undef KVQ_DECP
+  return dispatch_quant(dtype, D, bits, G, [&](auto t, auto d, auto b, auto g) {
+    return launch_decode_t<decltype(t), decltype(d)::value, decltype(b)::value, 4, 2, true, decltype(g)::value>(p, stream);
+  });
 }
 
 hipError_t launch_decode_dense(const kvq_rows* q, const kvq_rows* k, const kvq_rows* v, const int32_t* seq_lens,
                                const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int dtype, float scale,
                                int causal, int window, void* workspace, hipStream_t stream) {
-  const DecPlan pl = decode_plan(B, Hq, Hkv, L, D, S, window, 16);
+  const DecPlan pl = decode_plan(B, Hq, Hkv, L, D, S, window, 16, 64);
   DecParams p = decode_params(q, seq_lens, out, Hq, Hkv, L, D, S, scale, causal, window, workspace, pl);
   p.kc = (const uint8_t*)k->data;
   p.vc = (const uint8_t*)v->data;

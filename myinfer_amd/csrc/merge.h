@@ -66,12 +66,11 @@ __device__ __forceinline__ float quad_sum(float v) {
 // alone: the merge is bound by the latency of these loads), forms the split weights against the
 // quad's maximum, and the quad sums its terms with two DPP exchanges. Fixed order, so repeated
 // calls are bit-identical. 256 / D rows per workgroup of 256 threads.
-template <typename T, int D>
+template <typename T, int D, int R>
 __global__ __launch_bounds__(256) void combine_kernel(MergeParams p, int nrows) {
   constexpr int F4 = D / 4;              // float4s per row
   constexpr int RPB = 256 / (4 * F4);    // rows per workgroup
   constexpr int CH = 8;                  // splits per thread loaded in the first round
-  constexpr int R = 1024 / D;            // rows per decode unit (16 / groups per row); the host checks p.R
   const int t = threadIdx.x;
   const int q = t & 3, j = (t >> 2) % F4;
   const int grow = blockIdx.x * RPB + t / (4 * F4);
@@ -132,10 +131,16 @@ __global__ __launch_bounds__(256) void combine_kernel(MergeParams p, int nrows) 
 
 template <typename T, int D>
 inline hipError_t launch_combine(const MergeParams& m, int B, hipStream_t stream) {
-  if (m.R != 1024 / D) return hipErrorInvalidValue;  // the kernel's split strides assume this
   const int nrows = B * m.Hq * m.L;
   constexpr int rpb = 256 / D;  // rows per 256-thread workgroup
-  hipLaunchKernelGGL((combine_kernel<T, D>), dim3((nrows + rpb - 1) / rpb), dim3(256), 0, stream, m, nrows);
+  const dim3 grid((nrows + rpb - 1) / rpb);
+  // R (rows per decode unit, 16 / scale groups per row) fixes the kernel's split strides
+  switch (m.R) {
+    case 4: hipLaunchKernelGGL((combine_kernel<T, D, 4>), grid, dim3(256), 0, stream, m, nrows); break;
+    case 8: hipLaunchKernelGGL((combine_kernel<T, D, 8>), grid, dim3(256), 0, stream, m, nrows); break;
+    case 16: hipLaunchKernelGGL((combine_kernel<T, D, 16>), grid, dim3(256), 0, stream, m, nrows); break;
+    default: return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 

@@ -52,20 +52,26 @@ constexpr int kXcds = 8;  // MI355X: 8 XCDs, each with its own L2
 
 // The raw tile ring. A slot holds one 64-key tile as loaded: [K codes][V codes][sK, bK, sV, bV],
 // code rows with their 16-byte chunks XOR-swizzled by row (chunk c of row r at position
-// c ^ (r % CPR)), each scale/bias array as 128 4-byte cells (cell 2 key + g holds group g of the
-// key in its low half).
+// c ^ (r % CPR)), each scale/bias array as 64 NG 4-byte cells (cell NG key + g holds group g of
+// the key in its low half; NG = 128 / G scale groups per row).
 // BITS == 16 is the unquantized cache: raw T rows, no scales or biases.
-template <int BITS>
+template <int BITS, int G = 64>
 struct RawCfg {
   static constexpr bool DENSE = BITS == 16;
+  static_assert(G == 32 || G == 64 || G == 128, "group sizes 32, 64, 128");
+  static constexpr int NG = 128 / G;                // scale groups per key row
   static constexpr int ROWB = 128 * BITS / 8;       // code bytes per key row
   static constexpr int CPR = ROWB / 16;             // 16-byte chunks per row
   static constexpr int RPI = 64 / CPR;              // rows per 1 KiB DMA instruction
   static constexpr int CI = kPT / RPI;              // DMA instructions per K (or V) code tile
   static constexpr int KB = kPT * ROWB;             // bytes of a K (or V) code tile
-  static constexpr int SLOT = 2 * KB + (DENSE ? 0 : 4 * 512);
+  static constexpr int SBB = DENSE ? 0 : 256 * NG;  // bytes of one scale/bias array
+  static constexpr int SLOT = 2 * KB + 4 * SBB;
   static constexpr int CPW = 2 * CI / kPW;          // code DMA instructions per wave
-  static constexpr int IPT = CPW + (DENSE ? 0 : 1);  // DMA instructions per wave per tile
+  // 64-cell scale/bias DMA instructions per wave: 4 NG of them fill the four arrays (with NG = 1
+  // two waves fill the same cells), spread evenly over the 8 waves
+  static constexpr int SBW = DENSE ? 0 : (NG > 2 ? NG / 2 : 1);
+  static constexpr int IPT = CPW + SBW;             // DMA instructions per wave per tile
   static_assert(CPW * kPW == 2 * CI, "code DMAs divide evenly over the waves");
 };
 
@@ -149,14 +155,16 @@ __device__ __forceinline__ uint32_t lds_addr(const void* ptr) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)ptr;
 }
 
-// This wave's share of a raw tile: CPW 1 KiB code loads (K instructions first, then V) and one
-// 64-cell scale/bias load (array wave / 2, cells 64 (wave % 2) ..).
-template <int BITS>
+// This wave's share of a raw tile: CPW 1 KiB code loads (K instructions first, then V) and SBW
+// 64-cell scale/bias loads (load li = SBW wave + j of the 8 SBW: array li / (2 SBW), cells
+// 64 part .. with part = (li % (2 SBW)) % NG).
+template <int BITS, int G = 64>
 struct RawShare {
-  using C = RawCfg<BITS>;
-  __amdgpu_buffer_rsrc_t code_r[C::CPW], sb_r;
-  uint32_t code_vo[C::CPW], code_lds[C::CPW], sb_vo, sb_lds;
-  int64_t code_ss[C::CPW], sb_ss;  // bytes per key row
+  using C = RawCfg<BITS, G>;
+  static constexpr int SBN = C::SBW > 0 ? C::SBW : 1;
+  __amdgpu_buffer_rsrc_t code_r[C::CPW], sb_r[SBN];
+  uint32_t code_vo[C::CPW], code_lds[C::CPW], sb_vo[SBN], sb_lds[SBN];
+  int64_t code_ss[C::CPW], sb_ss[SBN];  // bytes per key row
 
   __device__ __forceinline__ void init(const PreParams& p, __amdgpu_buffer_rsrc_t kr, __amdgpu_buffer_rsrc_t vr,
                                        const __amdgpu_buffer_rsrc_t (&sr)[4], int wave, int lane) {
@@ -172,23 +180,28 @@ struct RawShare {
       code_vo[j] = (uint32_t)(r * code_ss[j] + 16 * c);
       code_lds[j] = (is_k ? 0 : C::KB) + 1024 * i;
     }
-    const int a = wave >> 1, cell = 64 * (wave & 1) + lane;
-    sb_r = a == 0 ? sr[0] : a == 1 ? sr[1] : a == 2 ? sr[2] : sr[3];
-    sb_ss = C::DENSE ? 0 : 2 * (a < 2 ? p.ksb_ss : p.vsb_ss);
-    sb_vo = (uint32_t)((cell >> 1) * sb_ss + 2 * (cell & 1));
-    sb_lds = 2 * C::KB + 512 * a + 256 * (wave & 1);
+#pragma unroll
+    for (int j = 0; j < SBN; ++j) {
+      const int li = wave * C::SBW + j, a = li / (2 * SBN), part = (li % (2 * SBN)) % C::NG;
+      const int cell = 64 * part + lane;  // group cell % NG of key cell / NG
+      sb_r[j] = a == 0 ? sr[0] : a == 1 ? sr[1] : a == 2 ? sr[2] : sr[3];
+      sb_ss[j] = C::DENSE ? 0 : 2 * (a < 2 ? p.ksb_ss : p.vsb_ss);
+      sb_vo[j] = (uint32_t)((cell / C::NG) * sb_ss[j] + 2 * (cell % C::NG));
+      sb_lds[j] = 2 * C::KB + C::SBB * a + 256 * part;
+    }
   }
   // raw tile of keys [k0, k0 + 64) into the slot at LDS address `slot`
   __device__ __forceinline__ void issue(uint32_t slot, int k0) const {
 #pragma unroll
     for (int j = 0; j < C::CPW; ++j) dma_b128(code_r[j], slot + code_lds[j], code_vo[j], (uint32_t)(k0 * code_ss[j]));
-    if constexpr (!C::DENSE) dma_b16(sb_r, slot + sb_lds, sb_vo, (uint32_t)(k0 * sb_ss));
+#pragma unroll
+    for (int j = 0; j < C::SBW; ++j) dma_b16(sb_r[j], slot + sb_lds[j], sb_vo[j], (uint32_t)(k0 * sb_ss[j]));
   }
 
   // Paged cache: the wave's arrays at page 0 of this KV head, and their page strides (bytes).
   const uint8_t* code_base[C::CPW];
-  const uint8_t* sb_base;
-  int64_t code_ps[C::CPW], sb_ps;
+  const uint8_t* sb_base[SBN];
+  int64_t code_ps[C::CPW], sb_ps[SBN];
   __device__ __forceinline__ void init_paged(const PreParams& p, int kvh, int wave) {
 #pragma unroll
     for (int j = 0; j < C::CPW; ++j) {
@@ -196,10 +209,13 @@ struct RawShare {
       code_base[j] = is_k ? p.kc + (int64_t)kvh * p.kc_sh : p.vc + (int64_t)kvh * p.vc_sh;
       code_ps[j] = is_k ? p.kc_sb : p.vc_sb;
     }
-    const int a = wave >> 1;
-    const uint16_t* arr = a == 0 ? p.ks : a == 1 ? p.kb : a == 2 ? p.vs : p.vb;
-    sb_base = (const uint8_t*)(arr + (int64_t)kvh * (a < 2 ? p.ksb_sh : p.vsb_sh));
-    sb_ps = 2 * (a < 2 ? p.ksb_sb : p.vsb_sb);
+#pragma unroll
+    for (int j = 0; j < SBN; ++j) {
+      const int a = (wave * C::SBW + j) / (2 * SBN);
+      const uint16_t* arr = a == 0 ? p.ks : a == 1 ? p.kb : a == 2 ? p.vs : p.vb;
+      sb_base[j] = (const uint8_t*)(arr + (int64_t)kvh * (a < 2 ? p.ksb_sh : p.vsb_sh));
+      sb_ps[j] = 2 * (a < 2 ? p.ksb_sb : p.vsb_sb);
+    }
   }
   // raw tile of page `pg` (its first nv rows valid) into the slot at LDS address `slot`
   __device__ __forceinline__ void issue_paged(uint32_t slot, int pg, int nv) const {
@@ -207,8 +223,10 @@ struct RawShare {
     for (int j = 0; j < C::CPW; ++j)
       dma_b128(make_rsrc(code_base[j] + (int64_t)pg * code_ps[j], (uint32_t)(nv * code_ss[j])), slot + code_lds[j],
                code_vo[j], 0u);
-    if constexpr (!C::DENSE)
-      dma_b16(make_rsrc(sb_base + (int64_t)pg * sb_ps, (uint32_t)(nv * sb_ss)), slot + sb_lds, sb_vo, 0u);
+#pragma unroll
+    for (int j = 0; j < C::SBW; ++j)
+      dma_b16(make_rsrc(sb_base[j] + (int64_t)pg * sb_ps[j], (uint32_t)(nv * sb_ss[j])), slot + sb_lds[j], sb_vo[j],
+              0u);
   }
 };
 
@@ -245,16 +263,16 @@ __device__ __forceinline__ void dequant8(const uint32_t* w, h2 s2, h2 b2, uint32
 // Dequantize the raw tile at `raw` into the fp16 operands. Threads 0-255 build V^T: thread t takes
 // the 8 keys of slot chunk t % 8 at dims [4 (t / 8), +4) and writes 4 V^T rows of 8 slots. Threads
 // 256-511 build K: thread t takes dims [32 q, +32) of key t % 64, q = (t - 256) / 64.
-template <typename T, int BITS>
+template <typename T, int BITS, int G>
 __device__ __forceinline__ void stage_from_raw(const uint8_t* raw, _Float16* klds, _Float16* vlds, uint32_t* sbt,
                                                int tid, bool& range_bad) {
-  using C = RawCfg<BITS>;
+  using C = RawCfg<BITS, G>;
   const uint8_t* sbase = raw + 2 * C::KB;
   auto sb_at = [&](int a, int key, int g) -> _Float16 {
-    return to_half(*(const uint16_t*)(sbase + 512 * a + 4 * (2 * key + g)), T{});
+    return to_half(*(const uint16_t*)(sbase + C::SBB * a + 4 * (C::NG * key + g)), T{});
   };
   if (tid < 256) {
-    const int c8 = tid & 7, d4 = tid >> 3, g = d4 >> 4;
+    const int c8 = tid & 7, d4 = tid >> 3, g = (4 * d4) / G;
     // key i of the chunk is kb + v_key_offset(i), and its swizzle key % CPR is (kb % CPR) | (i & 3)
     // (kb has its low two bits clear, the offsets are i & 3 modulo 8): four code addresses per
     // lane, one per i & 3, and one scale/bias address; everything else is an immediate offset
@@ -316,7 +334,7 @@ __device__ __forceinline__ void stage_from_raw(const uint8_t* raw, _Float16* kld
 #pragma unroll
       for (int i = 0; i < 4; ++i) w[i] = a0[i];
     }
-    const _Float16 sh = sb_at(0, key, q >> 1), bh = sb_at(1, key, q >> 1);
+    const _Float16 sh = sb_at(0, key, (32 * q) / G), bh = sb_at(1, key, (32 * q) / G);
     if constexpr (T::id == KVQ_DTYPE_BF16) range_bad |= __builtin_isinf((float)bh);
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
@@ -350,9 +368,9 @@ __device__ __forceinline__ void stage_v_raw(const uint8_t* raw, _Float16* vlds, 
   *(u4*)&vlds[(2 * d2 + 1) * kVS + 8 * c8] = hi;
 }
 
-template <typename T, int BITS, bool PAGED = false>
+template <typename T, int BITS, bool PAGED = false, int G = 64>
 __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) {
-  using RC = RawCfg<BITS>;
+  using RC = RawCfg<BITS, G>;
   constexpr bool DENSE = RC::DENSE;  // unquantized cache: K operands are read from the raw ring
   __shared__ __align__(16) _Float16 k_lds[DENSE ? 1 : 2][DENSE ? 8 : kPT * kKS];
   __shared__ __align__(16) _Float16 v_lds[2][128 * kVS];
@@ -420,7 +438,7 @@ __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) 
 
   // ---- raw tile stream: buffer resources over the S_b valid rows of this (sequence, KV head)
   // (the host checks S * row stride fits 32 bits); tiles past the last re-read the last one
-  RawShare<BITS> share;
+  RawShare<BITS, G> share;
   {
     const __amdgpu_buffer_rsrc_t kr =
         make_rsrc(p.kc + (int64_t)b * p.kc_sb + (int64_t)kvh * p.kc_sh, (uint32_t)((int64_t)S_b * p.kc_ss));
@@ -522,7 +540,7 @@ __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) 
     } else {
       wait_vm<2 * RC::IPT>();
       __syncthreads();
-      stage_from_raw<T, BITS>(raw[0], k_lds[0], v_lds[0], sb_tab[wave & 3], tid, range_bad);
+      stage_from_raw<T, BITS, G>(raw[0], k_lds[0], v_lds[0], sb_tab[wave & 3], tid, range_bad);
       wait_vm<RC::IPT>();
       __syncthreads();
     }
@@ -547,7 +565,7 @@ __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) 
       if constexpr (DENSE) {
         stage_v_raw(raw[(t + 1) % kRawSlots], v_lds[cur ^ 1], tid - 256, 0);
       } else {
-        stage_from_raw<T, BITS>(raw[(t + 1) % kRawSlots], k_lds[cur ^ 1], v_lds[cur ^ 1], sb_tab[wave & 3], tid,
+        stage_from_raw<T, BITS, G>(raw[(t + 1) % kRawSlots], k_lds[cur ^ 1], v_lds[cur ^ 1], sb_tab[wave & 3], tid,
                                  range_bad);
       }
     }
@@ -653,7 +671,7 @@ __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) 
       if constexpr (DENSE) {
         stage_v_raw(raw[(t + 1) % kRawSlots], v_lds[cur ^ 1], tid, 1);
       } else {
-        stage_from_raw<T, BITS>(raw[(t + 1) % kRawSlots], k_lds[cur ^ 1], v_lds[cur ^ 1], sb_tab[wave & 3], tid,
+        stage_from_raw<T, BITS, G>(raw[(t + 1) % kRawSlots], k_lds[cur ^ 1], v_lds[cur ^ 1], sb_tab[wave & 3], tid,
                                  range_bad);
       }
     }
@@ -839,10 +857,26 @@ size_t prefill_workspace_bytes(int B, int Hq, int Hkv, int L, int D, int S, int 
   return prefill_layout(pl).total;
 }
 
-template <typename T, int BITS, bool PAGED = false>
+template <typename T, int BITS, bool PAGED = false, int G = 64>
 static hipError_t launch_prefill_t(const PreParams& p, hipStream_t stream) {
-  hipLaunchKernelGGL((prefill_attn_kernel<T, BITS, PAGED>), dim3(p.nunits * p.nsplit), dim3(kPW * 64), 0, stream, p);
+  hipLaunchKernelGGL((prefill_attn_kernel<T, BITS, PAGED, G>), dim3(p.nunits * p.nsplit), dim3(kPW * 64), 0, stream, p);
   return hipGetLastError();
+}
+
+// The quantized instantiation for (dtype, bits in {4, 8}, G in {32, 64, 128}).
+template <bool PAGED>
+static hipError_t launch_prefill_quant(const PreParams& p, int dtype, int bits, int G, hipStream_t stream) {
+  auto by_g = [&](auto t, auto b) -> hipError_t {
+    using TT = decltype(t);
+    constexpr int BB = decltype(b)::value;
+    if (G == 32) return launch_prefill_t<TT, BB, PAGED, 32>(p, stream);
+    if (G == 128) return launch_prefill_t<TT, BB, PAGED, 128>(p, stream);
+    return launch_prefill_t<TT, BB, PAGED, 64>(p, stream);
+  };
+  auto by_b = [&](auto t) -> hipError_t {
+    return bits == 8 ? by_g(t, std::integral_constant<int, 8>{}) : by_g(t, std::integral_constant<int, 4>{});
+  };
+  return dtype == KVQ_DTYPE_BF16 ? by_b(BF16{}) : by_b(F16{});
 }
 
 // Everything but the K/V operands.
@@ -879,10 +913,11 @@ static PreParams prefill_params(const kvq_rows* q, const int32_t* seq_lens, cons
 }
 
 hipError_t launch_prefill(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v, const int32_t* seq_lens,
-                          const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int bits, int dtype,
+                          const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int bits, int G, int dtype,
                           float scale, int causal, int window, void* workspace, hipStream_t stream) {
   const PrePlan pl = prefill_plan(B, Hq, Hkv, L, S, window);
   PreParams p = prefill_params(q, seq_lens, out, Hq, Hkv, L, S, scale, causal, window, workspace, pl);
+  (void)D;
   p.kc = (const uint8_t*)k->codes;
   p.vc = (const uint8_t*)v->codes;
   p.kc_sb = k->codes_stride_b * 4;
@@ -901,19 +936,13 @@ hipError_t launch_prefill(const kvq_rows* q, const kvq_qtensor* k, const kvq_qte
   p.vsb_sb = v->sb_stride_b;
   p.vsb_sh = v->sb_stride_h;
   p.vsb_ss = v->sb_stride_s;
-  (void)D;
-  if (dtype == KVQ_DTYPE_BF16) {
-    if (bits == 8) return launch_prefill_t<BF16, 8>(p, stream);
-    return launch_prefill_t<BF16, 4>(p, stream);
-  }
-  if (bits == 8) return launch_prefill_t<F16, 8>(p, stream);
-  return launch_prefill_t<F16, 4>(p, stream);
+  return launch_prefill_quant<false>(p, dtype, bits, G, stream);
 }
 
 hipError_t launch_prefill_paged(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v, int num_pages,
                                 const int32_t* table, int64_t table_stride, const int32_t* seq_lens, const kvq_rows* out,
-                                int B, int Hq, int Hkv, int L, int D, int S, int bits, int dtype, float scale, int causal,
-                                int window, void* workspace, hipStream_t stream) {
+                                int B, int Hq, int Hkv, int L, int D, int S, int bits, int G, int dtype, float scale,
+                                int causal, int window, void* workspace, hipStream_t stream) {
   const PrePlan pl = prefill_plan(B, Hq, Hkv, L, S, window);
   PreParams p = prefill_params(q, seq_lens, out, Hq, Hkv, L, S, scale, causal, window, workspace, pl);
   p.kc = (const uint8_t*)k->codes;
@@ -938,12 +967,7 @@ hipError_t launch_prefill_paged(const kvq_rows* q, const kvq_qtensor* k, const k
   p.table_stride = table_stride;
   p.num_pages = num_pages;
   (void)D;
-  if (dtype == KVQ_DTYPE_BF16) {
-    if (bits == 8) return launch_prefill_t<BF16, 8, true>(p, stream);
-    return launch_prefill_t<BF16, 4, true>(p, stream);
-  }
-  if (bits == 8) return launch_prefill_t<F16, 8, true>(p, stream);
-  return launch_prefill_t<F16, 4, true>(p, stream);
+  return launch_prefill_quant<true>(p, dtype, bits, G, stream);
 }
 
 hipError_t launch_prefill_dense(const kvq_rows* q, const kvq_rows* k, const kvq_rows* v, const int32_t* seq_lens,

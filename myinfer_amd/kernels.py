@@ -221,9 +221,16 @@ def quantize(x: torch.Tensor, group_size: int = 64, bits: int = 8) -> Triple:
     return (codes.reshape(*lead, -1), scales.reshape(*lead, -1), biases.reshape(*lead, -1))
 
 
-def decode_rows_per_pass(D: int) -> int:
-    """Query rows (heads of a GQA group x query positions) one decode pass serves."""
-    return 16 * 64 // D
+def decode_rows_per_pass(D: int, group_size: int = 64) -> int:
+    """Query rows (heads of a GQA group x query positions) one decode pass serves: the 16 MFMA
+    columns hold each row once per scale group (an unquantized cache counts as group 64)."""
+    return 16 * group_size // D
+
+
+def _auto_kernel(rep_rows: int, D: int, group_size: int) -> str:
+    """Decode while a KV head's query rows fit at most two decode passes over its keys (one pass for
+    group 64, where 8 rows fit one pass), the prefill kernel otherwise; decode for D != 128."""
+    return "decode" if (rep_rows <= max(decode_rows_per_pass(D, group_size), 8) or D != 128) else "prefill"
 
 
 class AttentionCall:
@@ -320,7 +327,7 @@ def prepare_attention(queries: torch.Tensor, keys, values, scale: float, *, caus
         sl_ptr = seq_lens.data_ptr()
     rep = Hq // Hkv
     if kernel == "auto":
-        kernel = "decode" if (rep * L <= decode_rows_per_pass(D) or D != 128) else "prefill"
+        kernel = _auto_kernel(rep * L, D, 64 if dense else group_size)
     if kernel not in ("decode", "prefill"):
         raise ValueError(f"kernel must be 'decode', 'prefill' or 'auto', got {kernel!r}")
     lib = _lib.lib()
@@ -358,8 +365,8 @@ def attention(queries: torch.Tensor, keys, values, scale: float, *, causal: bool
     """softmax(scale * q K^T + mask) V. queries [B, Hq, L, D]; keys/values either quantized triples
     (codes [B, Hkv, S, D*bits/32], scales/biases [B, Hkv, S, D/G]) or unquantized tensors
     [B, Hkv, S, D] in the queries' dtype; returns [B, Hq, L, D] (or fills `out`). kernel: "decode",
-    "prefill" or "auto" (decode while the GQA group's query rows fit one MFMA column block,
-    prefill otherwise)."""
+    "prefill" or "auto" (decode while a KV head's query rows fit max(16*G/D, 8) columns, that is
+    at most two decode passes over its keys, prefill otherwise)."""
     return prepare_attention(queries, keys, values, scale, causal=causal, window=window, seq_lens=seq_lens,
                              group_size=group_size, bits=bits, out=out, kernel=kernel)()
 
@@ -445,7 +452,7 @@ def paged_attention(queries: torch.Tensor, k_pool: Triple, v_pool: Triple, block
         queries = queries.contiguous()
     out = _check_out(out, queries, dev)
     if kernel == "auto":
-        kernel = "decode" if ((Hq // Hkv) * L <= decode_rows_per_pass(D) or D != 128) else "prefill"
+        kernel = _auto_kernel((Hq // Hkv) * L, D, group_size)
     lib = _lib.lib()
     ws_fn = lib.kvq_decode_workspace_size if kernel == "decode" else lib.kvq_prefill_workspace_size
     nbytes = ws_fn(B, Hq, Hkv, L, D, S, int(window))

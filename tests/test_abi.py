@@ -56,7 +56,8 @@ def _attn(fn, **kw):
 
 @pytest.mark.parametrize("kw,code,needle", [
     (dict(bits=3), _lib.ERR_UNSUPPORTED, "bits"),
-    (dict(group=32), _lib.ERR_UNSUPPORTED, "group_size"),
+    (dict(group=48), _lib.ERR_UNSUPPORTED, "group_size"),
+    (dict(group=128, D=64, S=256), _lib.ERR_UNSUPPORTED, "group_size"),
     (dict(D=96), _lib.ERR_UNSUPPORTED, "head_dim"),
     (dict(Hq=7, Hkv=2), _lib.ERR_INVALID, "multiple"),
     (dict(dtype=5), _lib.ERR_INVALID, "dtype"),

@@ -59,7 +59,7 @@ def test_prefill_workspace_size():
 @pytest.mark.parametrize("kw,code,needle", [
     (dict(D=64), _lib.ERR_UNSUPPORTED, "head_dim 128"),
     (dict(bits=3), _lib.ERR_UNSUPPORTED, "bits"),
-    (dict(group=128), _lib.ERR_UNSUPPORTED, "group_size"),
+    (dict(group=16), _lib.ERR_UNSUPPORTED, "group_size"),
     (dict(Hq=6, Hkv=4), _lib.ERR_INVALID, "multiple"),
     (dict(L=0), _lib.ERR_INVALID, "positive"),
     (dict(dtype=2), _lib.ERR_INVALID, "dtype"),

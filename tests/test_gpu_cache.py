@@ -120,3 +120,22 @@ def test_decode_through_cache_views():
         torch.cuda.synchronize()
         ref = exact_reference(q, fk, fv, 1.0 / math.sqrt(128), bits=8)
         assert_close(out, ref, f"step {step}")
+
+
+@pytest.mark.parametrize("group,bits", [(32, 4), (128, 8)])
+def test_group_sizes_through_cache_views(group, bits):
+    # mlx-lm's other kv_group_size values: quantize a plain cache, then prefill and decode over it
+    plain = KVCache()
+    plain.update_and_fetch(rows(600, 60, H=4), rows(600, 61, H=4))
+    caches = [plain]
+    A.safe_maybe_quantize_kv_cache(caches, quantized_kv_start=0, kv_group_size=group, kv_bits=bits)
+    c = caches[0]
+    assert c.group_size == group and c.keys[1].shape[-1] == 128 // group
+    scale = 1.0 / math.sqrt(128)
+    for step, n in enumerate((90, 1, 1)):
+        fk, fv = c.update_and_fetch(rows(n, 70 + step, H=4), rows(n, 80 + step, H=4))
+        q = seeded_normal((1, 16, n, 128), 90 + step, torch.float16, DEV)
+        out = A.blocked_quantized_sdpa(q, fk, fv, scale, "causal" if n > 1 else None, group_size=group, bits=bits)
+        torch.cuda.synchronize()
+        ref = exact_reference(q, fk, fv, scale, bits=bits, group_size=group, causal=n > 1)
+        assert_close(out, ref, f"group={group} step {step}")

@@ -19,7 +19,7 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda"
 
 
-def make_cache(B, Hkv, S, D, bits, dtype, seed, cap=None, outliers=False):
+def make_cache(B, Hkv, S, D, bits, dtype, seed, cap=None, outliers=False, group=64):
     cap = cap or S
     k = seeded_normal((B, Hkv, S, D), seed, torch.float32)
     if outliers:
@@ -34,24 +34,25 @@ def make_cache(B, Hkv, S, D, bits, dtype, seed, cap=None, outliers=False):
     trip = []
     for x in (k, v):
         codes = torch.zeros((B, Hkv, cap, D * bits // 32), dtype=torch.int32, device=DEV).view(torch.uint32)
-        sc = torch.zeros((B, Hkv, cap, D // 64), dtype=dtype, device=DEV)
+        sc = torch.zeros((B, Hkv, cap, D // group), dtype=dtype, device=DEV)
         bi = torch.zeros_like(sc)
-        kernels.quantize_append(x, (codes, sc, bi), row_offset=0, group_size=64, bits=bits)
+        kernels.quantize_append(x, (codes, sc, bi), row_offset=0, group_size=group, bits=bits)
         trip.append((codes[:, :, :S], sc[:, :, :S], bi[:, :, :S]))
     return trip[0], trip[1]
 
 
 def run_case(B, Hq, Hkv, L, S, D, bits, dtype, *, causal=False, window=0, seq_lens=None, seed=0, cap=None,
-             outliers=False, what=""):
-    print(f"decode case {what} B={B} Hq={Hq} Hkv={Hkv} L={L} S={S} D={D} bits={bits} {dtype} "
+             outliers=False, group=64, what=""):
+    print(f"decode case {what} B={B} Hq={Hq} Hkv={Hkv} L={L} S={S} D={D} bits={bits} group={group} {dtype} "
           f"causal={causal} window={window} var={seq_lens is not None}", flush=True)
-    kt, vt = make_cache(B, Hkv, S, D, bits, dtype, seed, cap=cap, outliers=outliers)
+    kt, vt = make_cache(B, Hkv, S, D, bits, dtype, seed, cap=cap, outliers=outliers, group=group)
     q = seeded_normal((B, Hq, L, D), seed + 2, dtype, DEV)
     sl = None if seq_lens is None else torch.tensor(seq_lens, dtype=torch.int32, device=DEV)
     scale = 1.0 / math.sqrt(D)
-    out = kernels.attention(q, kt, vt, scale, causal=causal, window=window, seq_lens=sl, bits=bits, kernel="decode")
+    out = kernels.attention(q, kt, vt, scale, causal=causal, window=window, seq_lens=sl, bits=bits,
+                            group_size=group, kernel="decode")
     torch.cuda.synchronize()
-    ref = exact_reference(q, kt, vt, scale, bits=bits, causal=causal, window=window, seq_lens=sl)
+    ref = exact_reference(q, kt, vt, scale, bits=bits, group_size=group, causal=causal, window=window, seq_lens=sl)
     return assert_close(out, ref, what)
 
 
@@ -72,6 +73,22 @@ def test_ragged_lengths(S):
 def test_head_dim_64(bits, Hq, Hkv, L):
     # the shapes of the reference's own test (tests/test_core.py:27: D=64, S=700, L=6)
     run_case(1, Hq, Hkv, L, 700, 64, bits, torch.float16, causal=L > 1, seed=L + Hq, what="d64")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("bits", [8, 4])
+@pytest.mark.parametrize("group,D", [(32, 128), (128, 128), (32, 64)])
+@pytest.mark.parametrize("Hq,Hkv,L,S", [(8, 1, 1, 1000), (16, 2, 1, 4097), (4, 4, 1, 33), (8, 2, 3, 700)])
+def test_group_sizes(dtype, bits, group, D, Hq, Hkv, L, S):
+    # 32 and 128 are mlx's other group sizes; a pass then serves 16*group/D query rows
+    run_case(2, Hq, Hkv, L, S, D, bits, dtype, causal=L > 1, seed=400 + group + S, group=group, what="group")
+
+
+def test_group_sizes_window_and_lengths():
+    run_case(3, 16, 2, 1, 3000, 128, 4, torch.float16, window=700, seq_lens=[3000, 1, 1777], seed=77, group=32,
+             what="group32-window")
+    run_case(3, 32, 4, 1, 3000, 128, 8, torch.bfloat16, window=513, seq_lens=[2, 3000, 999], seed=78, group=128,
+             what="group128-window")
 
 
 @pytest.mark.parametrize("L,Hq,Hkv", [(2, 8, 2), (4, 8, 4), (3, 4, 2), (2, 16, 2)])

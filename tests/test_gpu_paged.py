@@ -21,9 +21,9 @@ DEV = "cuda"
 NAN_BITS = {torch.float16: 0x7E00, torch.bfloat16: 0x7FC0}
 
 
-def poisoned_pool(npages, H, D, bits, dtype):
+def poisoned_pool(npages, H, D, bits, dtype, group=64):
     codes = torch.randint(0, 2**31 - 1, (npages, H, PAGE_ROWS, D * bits // 32), dtype=torch.int32, device=DEV)
-    sc = torch.full((npages, H, PAGE_ROWS, D // 64), NAN_BITS[dtype], dtype=torch.int16, device=DEV).view(dtype)
+    sc = torch.full((npages, H, PAGE_ROWS, D // group), NAN_BITS[dtype], dtype=torch.int16, device=DEV).view(dtype)
     return codes.view(torch.uint32), sc, sc.clone()
 
 
@@ -40,12 +40,12 @@ def page_tables(lens, npages, seed):
     return rows, torch.tensor(rows, dtype=torch.int32, device=DEV)
 
 
-def build(B, Hkv, lens, D, bits, dtype, seed, npages=None):
+def build(B, Hkv, lens, D, bits, dtype, seed, npages=None, group=64):
     """Paged pools and the equivalent contiguous caches (quantized by the same kernel)."""
     S = max(lens)
     npages = npages or sum(math.ceil(n / PAGE_ROWS) for n in lens) + 7
     rows, tables = page_tables(lens, npages, seed)
-    kp, vp = poisoned_pool(npages, Hkv, D, bits, dtype), poisoned_pool(npages, Hkv, D, bits, dtype)
+    kp, vp = poisoned_pool(npages, Hkv, D, bits, dtype, group), poisoned_pool(npages, Hkv, D, bits, dtype, group)
     k = seeded_normal((B, Hkv, S, D), seed, dtype, DEV)
     v = seeded_normal((B, Hkv, S, D), seed + 1, dtype, DEV)
     # append in two uneven pieces per sequence, as a prefill chunk and then decode steps would
@@ -53,16 +53,17 @@ def build(B, Hkv, lens, D, bits, dtype, seed, npages=None):
     for b in range(B):
         kb, vb = k[b:b + 1], v[b:b + 1]
         t = tables[b:b + 1]
-        kernels.paged_quantize_append(kb[:, :, :cut[b]], kp, vb[:, :, :cut[b]], vp, t, row_offset=0, bits=bits)
+        kernels.paged_quantize_append(kb[:, :, :cut[b]], kp, vb[:, :, :cut[b]], vp, t, row_offset=0, bits=bits,
+                                      group_size=group)
         if lens[b] > cut[b]:
             st = torch.full((1,), cut[b], dtype=torch.int32, device=DEV)
             kernels.paged_quantize_append(kb[:, :, cut[b]:lens[b]], kp, vb[:, :, cut[b]:lens[b]], vp, t, starts=st,
-                                          bits=bits)
+                                          bits=bits, group_size=group)
     kc = [torch.zeros((B, Hkv, S, D * bits // 32), dtype=torch.int32, device=DEV).view(torch.uint32),
-          torch.zeros((B, Hkv, S, D // 64), dtype=dtype, device=DEV), torch.zeros((B, Hkv, S, D // 64), dtype=dtype,
-                                                                                   device=DEV)]
+          torch.zeros((B, Hkv, S, D // group), dtype=dtype, device=DEV),
+          torch.zeros((B, Hkv, S, D // group), dtype=dtype, device=DEV)]
     vc = [x.clone() for x in kc]
-    kernels.quantize_append(k, kc, v, vc, row_offset=0, bits=bits)
+    kernels.quantize_append(k, kc, v, vc, row_offset=0, bits=bits, group_size=group)
     return rows, tables, kp, vp, tuple(kc), tuple(vc)
 
 
@@ -202,3 +203,25 @@ def test_prefix_sharing_through_the_radix():
                            y.view(torch.int32) if y.dtype == torch.uint32 else y)
     assert cache.total_prefix_hits == 512 and cache.cached_prefix_blocks == 10
     assert cache.kv_memory_bytes == 2 * 64 * Hkv * 64 * (128 + 2 * 2 * 2)  # K and V: codes, scales, biases
+
+
+@pytest.mark.parametrize("group", [32, 128])
+@pytest.mark.parametrize("bits", [8, 4])
+def test_paged_group_sizes(group, bits):
+    print(f"paged group={group} bits={bits}", flush=True)
+    B, Hq, Hkv, D, dtype = 2, 16, 4, 128, torch.bfloat16
+    lens = [2100, 517]
+    rows, tables, kp, vp, kc, vc = build(B, Hkv, lens, D, bits, dtype, 41 + group, group=group)
+    sl = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    scale = 1.0 / math.sqrt(D)
+    for L, kernel in ((1, "decode"), (2, "decode"), (120, "prefill")):
+        q = seeded_normal((B, Hq, L, D), 42 + L, dtype, DEV)
+        out_p = kernels.paged_attention(q, kp, vp, tables, sl, scale, causal=True, bits=bits, group_size=group,
+                                        max_len=max(lens), kernel=kernel)
+        out_c = kernels.attention(q, kc, vc, scale, causal=True, seq_lens=sl, bits=bits, group_size=group,
+                                  kernel=kernel)
+        torch.cuda.synchronize()
+        assert torch.isfinite(out_p.float()).all()
+        assert torch.equal(out_p, out_c), (L, kernel)
+        assert_close(out_p, exact_reference(q, kc, vc, scale, bits=bits, group_size=group, causal=True, seq_lens=sl),
+                     f"paged {kernel} group={group}")

@@ -20,17 +20,19 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda"
 
 
-def run_case(B, Hq, Hkv, L, S, bits, dtype, *, causal=True, window=0, seq_lens=None, seed=0, cap=None, what=""):
-    print(f"prefill case {what} B={B} Hq={Hq} Hkv={Hkv} L={L} S={S} bits={bits} {dtype} causal={causal} "
-          f"window={window} var={seq_lens is not None}", flush=True)
+def run_case(B, Hq, Hkv, L, S, bits, dtype, *, causal=True, window=0, seq_lens=None, seed=0, cap=None, group=64,
+             what=""):
+    print(f"prefill case {what} B={B} Hq={Hq} Hkv={Hkv} L={L} S={S} bits={bits} group={group} {dtype} "
+          f"causal={causal} window={window} var={seq_lens is not None}", flush=True)
     D = 128
-    kt, vt = make_cache(B, Hkv, S, D, bits, dtype, seed, cap=cap)
+    kt, vt = make_cache(B, Hkv, S, D, bits, dtype, seed, cap=cap, group=group)
     q = seeded_normal((B, Hq, L, D), seed + 2, dtype, DEV)
     sl = None if seq_lens is None else torch.tensor(seq_lens, dtype=torch.int32, device=DEV)
     scale = 1.0 / math.sqrt(D)
-    out = kernels.attention(q, kt, vt, scale, causal=causal, window=window, seq_lens=sl, bits=bits, kernel="prefill")
+    out = kernels.attention(q, kt, vt, scale, causal=causal, window=window, seq_lens=sl, bits=bits,
+                            group_size=group, kernel="prefill")
     torch.cuda.synchronize()
-    ref = exact_reference(q, kt, vt, scale, bits=bits, causal=causal, window=window, seq_lens=sl)
+    ref = exact_reference(q, kt, vt, scale, bits=bits, group_size=group, causal=causal, window=window, seq_lens=sl)
     return assert_close(out, ref, what)
 
 
@@ -39,6 +41,15 @@ def run_case(B, Hq, Hkv, L, S, bits, dtype, *, causal=True, window=0, seq_lens=N
 @pytest.mark.parametrize("Hq,Hkv", [(8, 8), (16, 8), (16, 4), (32, 4)])
 def test_gqa_ratios(dtype, bits, Hq, Hkv):
     run_case(1, Hq, Hkv, 96, 700, bits, dtype, seed=20 + Hq + Hkv, what="gqa")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("bits", [8, 4])
+@pytest.mark.parametrize("group", [32, 128])
+def test_group_sizes(dtype, bits, group):
+    run_case(2, 16, 4, 150, 1300, bits, dtype, seed=500 + group + bits, group=group, what="group")
+    run_case(2, 8, 2, 33, 5000, bits, dtype, window=1024, seq_lens=[5000, 700], seed=600 + group, group=group,
+             what="group-window")
 
 
 @pytest.mark.parametrize("L,S", [(1, 1), (2, 2), (5, 5), (17, 40), (64, 64), (65, 300), (128, 1000), (200, 2048)])
