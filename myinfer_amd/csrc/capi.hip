@@ -356,6 +356,17 @@ size_t kvq_prefill_workspace_size(int B, int Hq, int Hkv, int L, int D, int S, i
   return kvq::prefill_workspace_bytes(B, Hq, Hkv, L, D, S, window, 8);
 }
 
+// The prefill kernel loads two scale groups of a row at once when a row has several: scale and
+// bias rows then have to be 4-byte aligned.
+static int check_prefill_sb(const kvq_qtensor* k, const kvq_qtensor* v, int D, int group_size) {
+  if (D / group_size < 2) return KVQ_OK;
+  for (const kvq_qtensor* t : {k, v})
+    if (!aligned(t->scales, 4) || !aligned(t->biases, 4) || (t->sb_stride_s | t->sb_stride_h | t->sb_stride_b) & 1)
+      return fail(KVQ_ERR_INVALID, "prefill with %d scale groups per row needs 4-byte aligned scales and biases with "
+                  "even row, head and batch (page) strides", D / group_size);
+  return KVQ_OK;
+}
+
 int kvq_prefill_attn(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v, const int32_t* seq_lens,
                      const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int bits, int group_size,
                      int dtype, float scale, int causal, int window, void* workspace, size_t workspace_bytes,
@@ -365,6 +376,7 @@ int kvq_prefill_attn(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor*
                       kvq_prefill_workspace_size(B, Hq, Hkv, L, D, S, window), workspace, workspace_bytes);
   if (rc) return rc;
   if ((rc = check_rows(out, "out", D, true))) return rc;  // rows are written 8 bytes at a time
+  if ((rc = check_prefill_sb(k, v, D, group_size))) return rc;
   return hip_status(kvq::launch_prefill(q, k, v, seq_lens, out, B, Hq, Hkv, L, D, S, bits, group_size, dtype, scale,
                                         causal, window, workspace, (hipStream_t)stream),
                     "prefill_attn launch");
@@ -414,6 +426,8 @@ int kvq_paged_prefill_attn(const kvq_rows* q, const kvq_qtensor* k_pool, const k
                             group_size, dtype, scale, window, kvq_prefill_workspace_size(B, Hq, Hkv, L, D, S, window),
                             workspace, workspace_bytes);
   if (rc) return rc;
+  if ((rc = check_rows(out, "out", D, true))) return rc;  // rows are written 8 bytes at a time
+  if ((rc = check_prefill_sb(k_pool, v_pool, D, group_size))) return rc;
   return hip_status(kvq::launch_prefill_paged(q, k_pool, v_pool, num_pages, block_table, table_stride, seq_lens, out, B,
                                               Hq, Hkv, L, D, S, bits, group_size, dtype, scale, causal, window,
                                               workspace, (hipStream_t)stream),

@@ -52,8 +52,9 @@ constexpr int kXcds = 8;  // MI355X: 8 XCDs, each with its own L2
 
 // The raw tile ring. A slot holds one 64-key tile as loaded: [K codes][V codes][sK, bK, sV, bV],
 // code rows with their 16-byte chunks XOR-swizzled by row (chunk c of row r at position
-// c ^ (r % CPR)), each scale/bias array as 64 NG 4-byte cells (cell NG key + g holds group g of
-// the key in its low half; NG = 128 / G scale groups per row).
+// c ^ (r % CPR)), each scale/bias array as 64 PC 4-byte cells: with NG = 128 / G >= 2 scale groups
+// per row, cell PC key + c holds groups 2c and 2c + 1 of the key (PC = NG / 2); with one group,
+// cell key holds it in its low half (PC = 1).
 // BITS == 16 is the unquantized cache: raw T rows, no scales or biases.
 template <int BITS, int G = 64>
 struct RawCfg {
@@ -65,14 +66,18 @@ struct RawCfg {
   static constexpr int RPI = 64 / CPR;              // rows per 1 KiB DMA instruction
   static constexpr int CI = kPT / RPI;              // DMA instructions per K (or V) code tile
   static constexpr int KB = kPT * ROWB;             // bytes of a K (or V) code tile
-  static constexpr int SBB = DENSE ? 0 : 256 * NG;  // bytes of one scale/bias array
+  static constexpr int PC = NG >= 2 ? NG / 2 : 1;  // 4-byte cells per key in a scale/bias array
+  static constexpr int SBB = DENSE ? 0 : 256 * PC;  // bytes of one scale/bias array
   static constexpr int SLOT = 2 * KB + 4 * SBB;
   static constexpr int CPW = 2 * CI / kPW;          // code DMA instructions per wave
-  // 64-cell scale/bias DMA instructions per wave: 4 NG of them fill the four arrays (with NG = 1
-  // two waves fill the same cells), spread evenly over the 8 waves
-  static constexpr int SBW = DENSE ? 0 : (NG > 2 ? NG / 2 : 1);
+  // 64-cell scale/bias DMA instructions per wave: 4 PC of them fill the four arrays, one per wave
+  // (with PC = 1 two waves fill the same cells)
+  static constexpr int SBW = DENSE ? 0 : 1;
   static constexpr int IPT = CPW + SBW;             // DMA instructions per wave per tile
   static_assert(CPW * kPW == 2 * CI, "code DMAs divide evenly over the waves");
+  static_assert(DENSE || 4 * PC <= kPW, "scale/bias DMAs fit one per wave");
+  // byte offset of group g of key `key` inside a scale/bias array
+  static __host__ __device__ constexpr int sb_off(int key, int g) { return 4 * (PC * key + g / 2) + 2 * (g & 1); }
 };
 
 typedef _Float16 h4 __attribute__((ext_vector_type(4)));
@@ -138,6 +143,13 @@ __device__ __forceinline__ void dma_b128(__amdgpu_buffer_rsrc_t r, uint32_t lds,
                : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(vo), "s"(r), "s"(__builtin_amdgcn_readfirstlane(so))
                : "memory");
 }
+__device__ __forceinline__ void dma_b32(__amdgpu_buffer_rsrc_t r, uint32_t lds, uint32_t vo, uint32_t so) {
+  uint32_t m0;
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\tbuffer_load_dword %2, %3, %4 offen lds\n\ts_mov_b32 m0, %0"
+               : "=&s"(m0)
+               : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(vo), "s"(r), "s"(__builtin_amdgcn_readfirstlane(so))
+               : "memory");
+}
 __device__ __forceinline__ void dma_b16(__amdgpu_buffer_rsrc_t r, uint32_t lds, uint32_t vo, uint32_t so) {
   uint32_t m0;
   asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\tbuffer_load_ushort %2, %3, %4 offen lds\n\ts_mov_b32 m0, %0"
@@ -154,10 +166,17 @@ __device__ __forceinline__ void wait_vm() {
 __device__ __forceinline__ uint32_t lds_addr(const void* ptr) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)ptr;
 }
+// A wave-uniform value the compiler treats as unknown. A buffer chosen by it is addressed as the
+// lane's offset plus this scalar, rather than by one precomputed vector address per buffer held in
+// registers through the loop (the LDS arrays extend past the 64 KiB immediate-offset range).
+__device__ __forceinline__ int opaque(int x) {
+  asm("" : "+s"(x));
+  return x;
+}
 
-// This wave's share of a raw tile: CPW 1 KiB code loads (K instructions first, then V) and SBW
-// 64-cell scale/bias loads (load li = SBW wave + j of the 8 SBW: array li / (2 SBW), cells
-// 64 part .. with part = (li % (2 SBW)) % NG).
+// This wave's share of a raw tile: CPW 1 KiB code loads (K instructions first, then V) and one
+// 64-cell scale/bias load (array wave / 2, cells 64 part .. with part = (wave % 2) % PC; 4-byte
+// cells, or 2-byte values into the low halves when PC = 1 holds a single group).
 template <int BITS, int G = 64>
 struct RawShare {
   using C = RawCfg<BITS, G>;
@@ -182,11 +201,11 @@ struct RawShare {
     }
 #pragma unroll
     for (int j = 0; j < SBN; ++j) {
-      const int li = wave * C::SBW + j, a = li / (2 * SBN), part = (li % (2 * SBN)) % C::NG;
-      const int cell = 64 * part + lane;  // group cell % NG of key cell / NG
+      const int li = wave * C::SBW + j, a = li / 2, part = (li % 2) % C::PC;
+      const int cell = 64 * part + lane;  // cell cell % PC of key cell / PC
       sb_r[j] = a == 0 ? sr[0] : a == 1 ? sr[1] : a == 2 ? sr[2] : sr[3];
       sb_ss[j] = C::DENSE ? 0 : 2 * (a < 2 ? p.ksb_ss : p.vsb_ss);
-      sb_vo[j] = (uint32_t)((cell / C::NG) * sb_ss[j] + 2 * (cell % C::NG));
+      sb_vo[j] = (uint32_t)((cell / C::PC) * sb_ss[j] + 4 * (cell % C::PC));
       sb_lds[j] = 2 * C::KB + C::SBB * a + 256 * part;
     }
   }
@@ -195,7 +214,14 @@ struct RawShare {
 #pragma unroll
     for (int j = 0; j < C::CPW; ++j) dma_b128(code_r[j], slot + code_lds[j], code_vo[j], (uint32_t)(k0 * code_ss[j]));
 #pragma unroll
-    for (int j = 0; j < C::SBW; ++j) dma_b16(sb_r[j], slot + sb_lds[j], sb_vo[j], (uint32_t)(k0 * sb_ss[j]));
+    for (int j = 0; j < C::SBW; ++j) dma_sb(sb_r[j], slot + sb_lds[j], sb_vo[j], (uint32_t)(k0 * sb_ss[j]));
+  }
+  static __device__ __forceinline__ void dma_sb(__amdgpu_buffer_rsrc_t r, uint32_t lds, uint32_t vo, uint32_t so) {
+    if constexpr (C::NG >= 2) {
+      dma_b32(r, lds, vo, so);
+    } else {
+      dma_b16(r, lds, vo, so);
+    }
   }
 
   // Paged cache: the wave's arrays at page 0 of this KV head, and their page strides (bytes).
@@ -211,7 +237,7 @@ struct RawShare {
     }
 #pragma unroll
     for (int j = 0; j < SBN; ++j) {
-      const int a = (wave * C::SBW + j) / (2 * SBN);
+      const int a = (wave * C::SBW + j) / 2;
       const uint16_t* arr = a == 0 ? p.ks : a == 1 ? p.kb : a == 2 ? p.vs : p.vb;
       sb_base[j] = (const uint8_t*)(arr + (int64_t)kvh * (a < 2 ? p.ksb_sh : p.vsb_sh));
       sb_ps[j] = 2 * (a < 2 ? p.ksb_sb : p.vsb_sb);
@@ -225,8 +251,8 @@ struct RawShare {
                code_vo[j], 0u);
 #pragma unroll
     for (int j = 0; j < C::SBW; ++j)
-      dma_b16(make_rsrc(sb_base[j] + (int64_t)pg * sb_ps[j], (uint32_t)(nv * sb_ss[j])), slot + sb_lds[j], sb_vo[j],
-              0u);
+      dma_sb(make_rsrc(sb_base[j] + (int64_t)pg * sb_ps[j], (uint32_t)(nv * sb_ss[j])), slot + sb_lds[j], sb_vo[j],
+             0u);
   }
 };
 
@@ -263,85 +289,100 @@ __device__ __forceinline__ void dequant8(const uint32_t* w, h2 s2, h2 b2, uint32
 // Dequantize the raw tile at `raw` into the fp16 operands. Threads 0-255 build V^T: thread t takes
 // the 8 keys of slot chunk t % 8 at dims [4 (t / 8), +4) and writes 4 V^T rows of 8 slots. Threads
 // 256-511 build K: thread t takes dims [32 q, +32) of key t % 64, q = (t - 256) / 64.
+//
+// V^T, first part: the wave's lanes convert the scale and bias of the wave's group (dims
+// [32 w, 32 w + 32) lie in one group) for the 64 keys (lane = key) into a per-wave table of fp16
+// (scale, bias) pairs, which stage_v then reads for its 8 keys. Only this wave touches its table,
+// and the LDS operations of one wave complete in program order, so a wave barrier (which keeps
+// the compiler from moving the lanes' accesses across it) is all the ordering the reads need.
+template <typename T, int BITS, int G>
+__device__ __forceinline__ void stage_v_table(const uint8_t* raw, uint32_t* sbt, int tid, bool& range_bad) {
+  using C = RawCfg<BITS, G>;
+  const int key = tid & 63, g = (4 * (tid >> 3)) / G;
+  const uint8_t* sbase = raw + 2 * C::KB + C::sb_off(key, g);
+  const h2 sbp = {to_half(*(const uint16_t*)(sbase + 2 * C::SBB), T{}), to_half(*(const uint16_t*)(sbase + 3 * C::SBB), T{})};
+  sbt[key] = __builtin_bit_cast(uint32_t, sbp);
+  // a bf16 group beyond the fp16 range has a bias (its largest-magnitude element) that converts to
+  // inf; the operands cannot hold it
+  if constexpr (T::id == KVQ_DTYPE_BF16) range_bad |= __builtin_isinf((float)sbp[1]);
+}
+
+// V^T, second part (threads 0-255, after stage_v_table of the same tile), in two halves: half H
+// builds dims 4 d4 + 2H and + 2H + 1 (V^T rows 2H, 2H + 1 of the thread's four).
+template <int BITS, int G, int H>
+__device__ __forceinline__ void stage_v(const uint8_t* raw, _Float16* vlds, const uint32_t* sbt, int tid) {
+  using C = RawCfg<BITS, G>;
+  const int c8 = tid & 7, d4 = tid >> 3;
+  // key i of the chunk is kb + v_key_offset(i), and its swizzle key % CPR is (kb % CPR) | (i & 3)
+  // (kb has its low two bits clear, the offsets are i & 3 modulo 8): four code addresses per
+  // lane; everything else is an immediate offset
+  const int kb = v_base_key(c8);
+  const uint8_t* vr = raw + C::KB + kb * C::ROWB;
+  uint32_t x[8];  // key i: the dim pair of this half
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int ko = v_key_offset(i);
+    const int sw = (kb % C::CPR) | (i & 3);
+    uint32_t bytes;  // codes of dims 4 d4 .. 4 d4 + 3 as 4 bytes
+    if constexpr (BITS == 8) {
+      bytes = *(const uint32_t*)(vr + ko * C::ROWB + 16 * ((d4 >> 2) ^ sw) + 4 * (d4 & 3));
+    } else {
+      const uint32_t h = *(const uint16_t*)(vr + ko * C::ROWB + 16 * ((d4 >> 3) ^ sw) + 2 * (d4 & 7));
+      bytes = perm((h >> 4) & 0x0F0Fu, h & 0x0F0Fu, 0x05010400u);
+    }
+    const h2 sbp = __builtin_bit_cast(h2, sbt[kb + ko]);
+    const _Float16 sh = sbp[0], bh = sbp[1];
+    x[i] = dequant_pair(bytes, H == 0 ? 0x04010400u : 0x04030402u, h2{sh, sh}, h2{bh, bh});
+  }
+#pragma unroll
+  for (int e = 2 * H; e < 2 * H + 2; ++e) {
+    const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
+    u4 v;
+#pragma unroll
+    for (int ip = 0; ip < 4; ++ip) v[ip] = perm(x[2 * ip + 1], x[2 * ip], sel);
+    *(u4*)&vlds[(4 * d4 + e) * kVS + 8 * c8] = v;
+  }
+}
+
+// K (threads 256-511), in two halves: half H builds dims [32 q + 16 H, +16) of key t % 64.
+template <typename T, int BITS, int G, int H>
+__device__ __forceinline__ void stage_k(const uint8_t* raw, _Float16* klds, int tid, bool& range_bad) {
+  using C = RawCfg<BITS, G>;
+  const int key = tid & 63, q = (tid - 256) >> 6;
+  const uint8_t* kr = raw + key * C::ROWB;
+  uint32_t w[4];  // the half's 16 codes
+  if constexpr (BITS == 8) {
+    const u4 a = *(const u4*)(kr + 16 * ((2 * q + H) ^ (key % C::CPR)));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w[i] = a[i];
+  } else {
+    const u2 a = *(const u2*)(kr + 16 * (q ^ (key % C::CPR)) + 8 * H);
+    w[0] = a[0];
+    w[1] = a[1];
+  }
+  const uint8_t* sbase = raw + 2 * C::KB + C::sb_off(key, (32 * q + 16 * H) / G);
+  const _Float16 sh = to_half(*(const uint16_t*)sbase, T{}), bh = to_half(*(const uint16_t*)(sbase + C::SBB), T{});
+  if constexpr (T::id == KVQ_DTYPE_BF16) range_bad |= __builtin_isinf((float)bh);
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    uint32_t x[4];
+    dequant8<BITS>(&w[(BITS / 4) * c], h2{sh, sh}, h2{bh, bh}, x);
+    *(u4*)&klds[key * kKS + 32 * q + 16 * H + 8 * c] = u4{x[0], x[1], x[2], x[3]};
+  }
+}
+
+// The whole tile, all 512 threads.
 template <typename T, int BITS, int G>
 __device__ __forceinline__ void stage_from_raw(const uint8_t* raw, _Float16* klds, _Float16* vlds, uint32_t* sbt,
                                                int tid, bool& range_bad) {
-  using C = RawCfg<BITS, G>;
-  const uint8_t* sbase = raw + 2 * C::KB;
-  auto sb_at = [&](int a, int key, int g) -> _Float16 {
-    return to_half(*(const uint16_t*)(sbase + C::SBB * a + 4 * (C::NG * key + g)), T{});
-  };
   if (tid < 256) {
-    const int c8 = tid & 7, d4 = tid >> 3, g = (4 * d4) / G;
-    // key i of the chunk is kb + v_key_offset(i), and its swizzle key % CPR is (kb % CPR) | (i & 3)
-    // (kb has its low two bits clear, the offsets are i & 3 modulo 8): four code addresses per
-    // lane, one per i & 3, and one scale/bias address; everything else is an immediate offset
-    const int kb = v_base_key(c8);
-    const uint8_t* vr = raw + C::KB + kb * C::ROWB;
-    // the wave's lanes convert the scale and bias of its group g for the 64 keys once (lane = key)
-    // into a per-wave table of (scale, bias) fp16 pairs; each lane then reads the pairs of its 8
-    // keys. Only this wave touches its table and LDS operations of a wave execute in order, so no
-    // barrier is needed.
-    {
-      const int key = tid & 63;
-      const h2 sbp = {sb_at(2, key, g), sb_at(3, key, g)};
-      sbt[key] = __builtin_bit_cast(uint32_t, sbp);
-      // a bf16 group beyond the fp16 range has a bias (its largest-magnitude element) that
-      // converts to inf; the operands cannot hold it
-      if constexpr (T::id == KVQ_DTYPE_BF16) range_bad |= __builtin_isinf((float)sbp[1]);
-    }
+    stage_v_table<T, BITS, G>(raw, sbt, tid, range_bad);
     __builtin_amdgcn_wave_barrier();
-    uint32_t x[8][2];  // key i, dim pair m
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int ko = v_key_offset(i);
-      const int sw = (kb % C::CPR) | (i & 3);
-      uint32_t bytes;  // codes of dims 4 d4 .. 4 d4 + 3 as 4 bytes
-      if constexpr (BITS == 8) {
-        bytes = *(const uint32_t*)(vr + ko * C::ROWB + 16 * ((d4 >> 2) ^ sw) + 4 * (d4 & 3));
-      } else {
-        const uint32_t h = *(const uint16_t*)(vr + ko * C::ROWB + 16 * ((d4 >> 3) ^ sw) + 2 * (d4 & 7));
-        bytes = perm((h >> 4) & 0x0F0Fu, h & 0x0F0Fu, 0x05010400u);
-      }
-      const h2 sbp = __builtin_bit_cast(h2, sbt[kb + ko]);
-      const _Float16 sh = sbp[0], bh = sbp[1];
-      x[i][0] = dequant_pair(bytes, 0x04010400u, h2{sh, sh}, h2{bh, bh});
-      x[i][1] = dequant_pair(bytes, 0x04030402u, h2{sh, sh}, h2{bh, bh});
-    }
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
-      u4 v;
-#pragma unroll
-      for (int ip = 0; ip < 4; ++ip) v[ip] = perm(x[2 * ip + 1][e >> 1], x[2 * ip][e >> 1], sel);
-      *(u4*)&vlds[(4 * d4 + e) * kVS + 8 * c8] = v;
-    }
+    stage_v<BITS, G, 0>(raw, vlds, sbt, tid);
+    stage_v<BITS, G, 1>(raw, vlds, sbt, tid);
   } else {
-    constexpr int W = BITS / 4;  // words per 8 codes
-    const int key = tid & 63, q = (tid - 256) >> 6;
-    const uint8_t* kr = raw + key * C::ROWB;
-    uint32_t w[4 * W];
-    if constexpr (BITS == 8) {
-      const u4 a0 = *(const u4*)(kr + 16 * ((2 * q) ^ (key % C::CPR)));
-      const u4 a1 = *(const u4*)(kr + 16 * ((2 * q + 1) ^ (key % C::CPR)));
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        w[i] = a0[i];
-        w[4 + i] = a1[i];
-      }
-    } else {
-      const u4 a0 = *(const u4*)(kr + 16 * (q ^ (key % C::CPR)));
-#pragma unroll
-      for (int i = 0; i < 4; ++i) w[i] = a0[i];
-    }
-    const _Float16 sh = sb_at(0, key, (32 * q) / G), bh = sb_at(1, key, (32 * q) / G);
-    if constexpr (T::id == KVQ_DTYPE_BF16) range_bad |= __builtin_isinf((float)bh);
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      uint32_t x[4];
-      dequant8<BITS>(&w[W * c], h2{sh, sh}, h2{bh, bh}, x);
-      *(u4*)&klds[key * kKS + 32 * q + 8 * c] = u4{x[0], x[1], x[2], x[3]};
-    }
+    stage_k<T, BITS, G, 0>(raw, klds, tid, range_bad);
+    stage_k<T, BITS, G, 1>(raw, klds, tid, range_bad);
   }
 }
 
@@ -372,14 +413,15 @@ template <typename T, int BITS, bool PAGED = false, int G = 64>
 __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) {
   using RC = RawCfg<BITS, G>;
   constexpr bool DENSE = RC::DENSE;  // unquantized cache: K operands are read from the raw ring
-  __shared__ __align__(16) _Float16 k_lds[DENSE ? 1 : 2][DENSE ? 8 : kPT * kKS];
-  __shared__ __align__(16) _Float16 v_lds[2][128 * kVS];
+  __shared__ __align__(16) _Float16 k_lds[DENSE ? 1 : 3][DENSE ? 8 : kPT * kKS];
+  __shared__ __align__(16) _Float16 v_lds[DENSE ? 2 : 3][128 * kVS];
   __shared__ __align__(16) uint8_t raw[kRawSlots][RC::SLOT];
   __shared__ uint32_t sb_tab[DENSE ? 1 : kPW / 2][64];  // per V^T-building wave: (scale, bias) pairs
-  __shared__ unsigned s_arrived;
-  __shared__ unsigned s_range_bad;  // some staged tile held a group beyond the fp16 range
-  bool range_bad = false;
-  if (threadIdx.x == 0) s_range_bad = 0;  // ordered before any staging by the prologue's barrier
+  // after the tile loop the table's storage holds per-wave flags (words 0-7) and the split arrival
+  // count (word 8): the LDS budget has no room for more
+  unsigned* const s_flags = &sb_tab[0][0];
+  unsigned* const s_arrived = &sb_tab[0][8];
+  bool range_bad = false;  // some tile this lane staged held a group beyond the fp16 range
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -478,9 +520,7 @@ __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) 
       share.issue(slot, k0);
     }
   };
-  // Quantized cache: the ring runs three tiles ahead (tile t + 3 is issued into the slot of tile t,
-  // which was dequantized in the previous step). Unquantized cache: K is read from the ring while
-  // tile t is computed, so tile t + 2 is issued into the slot of tile t - 1 and lands within the step.
+  // the first tiles of the ring (the tile loops below say how far ahead each runs)
   if (ntile > 0) {
 #pragma unroll
     for (int j = 0; j < (DENSE ? 2 : kRawSlots); ++j) issue_raw(j);
@@ -530,77 +570,11 @@ __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) 
 #pragma unroll
   for (int db = 0; db < 4; ++db) oacc[db] = f16v{};
 
-  // ---- prologue: tile 0 staged, tile 1 landed
-  if (ntile > 0) {
-    if constexpr (DENSE) {
-      wait_vm<0>();
-      __syncthreads();
-      stage_v_raw(raw[0], v_lds[0], tid & 255, tid >> 8);
-      __syncthreads();
-    } else {
-      wait_vm<2 * RC::IPT>();
-      __syncthreads();
-      stage_from_raw<T, BITS, G>(raw[0], k_lds[0], v_lds[0], sb_tab[wave & 3], tid, range_bad);
-      wait_vm<RC::IPT>();
-      __syncthreads();
-    }
-  }
-
-  // this lane's K operand bytes within a raw slot (unquantized cache): key row 32 (i & 1) + qc,
-  // 16-byte chunk 2 (i >> 1) + hh at its swizzled position
-  const int kswz = qc % RawCfg<16>::CPR;
-
-  for (int t = 0; t < ntile; ++t) {
-    const int cur = t & 1;
-    const int k0 = k_begin + kPT * t;
-    if constexpr (DENSE) {
-      if (t + 2 < ntile) issue_raw(t + 2);
-    } else {
-      issue_raw(t + kRawSlots);  // into the slot of tile t, dequantized before the last barrier
-    }
-    // waves 4-7 stage tile t + 1 before their MFMAs, waves 0-3 after theirs: the two waves that
-    // share a SIMD (w and w + 4) are in opposite phases, one on the MFMA pipe while the other is on
-    // the VALU (quantized cache: 4-7 dequantize K, 0-3 V; unquantized: each half of V^T)
-    if (t + 1 < ntile && wave >= kPW / 2) {
-      if constexpr (DENSE) {
-        stage_v_raw(raw[(t + 1) % kRawSlots], v_lds[cur ^ 1], tid - 256, 0);
-      } else {
-        stage_from_raw<T, BITS, G>(raw[(t + 1) % kRawSlots], k_lds[cur ^ 1], v_lds[cur ^ 1], sb_tab[wave & 3], tid,
-                                 range_bad);
-      }
-    }
-
-    // S^T = K Q^T for the two 32-key blocks of the tile (scores in log2 units times 2^qe)
-    // the 16 K operands stream through a 4-deep register ring, so each MFMA's LDS read was issued
-    // four MFMAs earlier; the two 32-key blocks alternate
-    f16v sacc[2] = {f16v{}, f16v{}};
-    {
-      const _Float16* kl = &k_lds[0][0];
-      const uint8_t* kraw = raw[t % kRawSlots] + qc * RawCfg<16>::ROWB;
-      if constexpr (!DENSE) kl = &k_lds[cur][qc * kKS + 8 * hh];
-      auto kop = [&](int i) -> u4 {
-        if constexpr (DENSE) {
-          return *(const u4*)(kraw + (i & 1) * 32 * RawCfg<16>::ROWB + 16 * ((2 * (i >> 1) + hh) ^ kswz));
-        } else {
-          return *(const u4*)(kl + (i & 1) * 32 * kKS + 16 * (i >> 1));
-        }
-      };
-      u4 ring[4] = {kop(0), kop(1), kop(2), kop(3)};
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        sacc[i & 1] = mfma_32x32x16(ring[i & 3], qop[i >> 1], sacc[i & 1], OT{});
-        if (i + 4 < 16) ring[i & 3] = kop(i + 4);
-      }
-    }
-    if constexpr (DENSE) {
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) sacc[kb][i] *= p.scale_log2;
-    }
-    // this lane's query sees keys k0 + 32kb + 8(i/4) + 4hh + i%4. Only tiles on a causal diagonal
-    // or window edge need a mask (a branch the whole workgroup takes or skips); there, each element's
-    // offset c = 32kb + 8(i/4) + i%4 is a constant compared with the lane's bounds
+  // ---- the pieces of a tile step
+  // this lane's query sees keys k0 + 32kb + 8(i/4) + 4hh + i%4. Only tiles on a causal diagonal or
+  // window edge need a mask (a branch the whole workgroup takes or skips); there, each element's
+  // offset c = 32kb + 8(i/4) + i%4 is a constant compared with the lane's bounds
+  auto mask_tile = [&](f16v (&acc)[2], int k0) {
     const bool need_mask = !(k0 >= lo_all && k0 + kPT <= hi_all);
     if (__builtin_expect(need_mask, 0)) {
       const int lo = lo_r - k0 - 4 * hh, hi = hi_r - k0 - 4 * hh;
@@ -609,22 +583,26 @@ __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) 
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
           for (int i = 0; i < 16; ++i)
-            if (32 * kb + 8 * (i >> 2) + (i & 3) >= hi) sacc[kb][i] = -INFINITY;
+            if (32 * kb + 8 * (i >> 2) + (i & 3) >= hi) acc[kb][i] = -INFINITY;
       } else {
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
           for (int i = 0; i < 16; ++i) {
             const int c = 32 * kb + 8 * (i >> 2) + (i & 3);
-            if (c < lo || c >= hi) sacc[kb][i] = -INFINITY;
+            if (c < lo || c >= hi) acc[kb][i] = -INFINITY;
           }
       }
     }
+  };
+  // the tile's row maximum in log2 units; the running maximum moves (and the accumulators are
+  // rescaled) only when it exceeds the running one by more than the slack
+  auto update_max = [&](const f16v (&acc)[2]) {
     float tm = -INFINITY;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) tm = fmaxf(tm, sacc[kb][i]);
+      for (int i = 0; i < 16; ++i) tm = fmaxf(tm, acc[kb][i]);
     tm = max_xor32(tm) * inv2;
     if (__builtin_amdgcn_ballot_w64(tm > m_run + kPSlack) != 0) {
       const float m_new = tm > m_run + kPSlack ? fmaxf(m_run, tm) : m_run;
@@ -636,59 +614,270 @@ __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) 
         for (int i = 0; i < 16; ++i) oacc[db][i] *= corr;
       m_run = m_new;
     }
-    // p = 2^(acc * inv2 - m): rounded to the operand type it is the B operand of O^T = V^T P^T;
-    // the row sum is kept in fp32 (of the rounded values for bf16 operands, so the output stays a
-    // convex combination of V rows)
+  };
+  // p = 2^(acc * inv2 - m): rounded to the operand type it is the B operand of O^T = V^T P^T; the
+  // row sum is kept in fp32 (of the rounded values, so the output stays a convex combination of V
+  // rows), in two chains
+  auto probs = [&](const f16v (&acc)[2], u4 (&pop)[4]) {
     const float nm = m_run == -INFINITY ? 0.0f : -m_run;
-    // the row sum of the rounded probabilities, in two chains
     float lsum[2] = {0.0f, 0.0f};
-    u4 pop[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const float p0 = exp2_fast(fmaf(sacc[j >> 1][8 * (j & 1) + 2 * e], inv2, nm));
-        const float p1 = exp2_fast(fmaf(sacc[j >> 1][8 * (j & 1) + 2 * e + 1], inv2, nm));
+        const float p0 = exp2_fast(fmaf(acc[j >> 1][8 * (j & 1) + 2 * e], inv2, nm));
+        const float p1 = exp2_fast(fmaf(acc[j >> 1][8 * (j & 1) + 2 * e + 1], inv2, nm));
         pop[j][e] = pack2(p0, p1, OT{});
         lsum[e & 1] = add_pair(pop[j][e], lsum[e & 1], OT{});
       }
     }
     l_run += lsum[0] + lsum[1];
-    // O^T += V^T P^T
-    {
-      // the 16 V^T operands stream through a 4-deep register ring; the 4 dim blocks alternate
-      const _Float16* vl = &v_lds[cur][qc * kVS + 8 * hh];
-      auto vop = [&](int i) { return *(const u4*)(vl + (i & 3) * 32 * kVS + 16 * (i >> 2)); };
+  };
+  // O^T += V^T P^T: the 16 V^T operands stream through a 4-deep register ring; the 4 dim blocks
+  // alternate. vl = this lane's start in a V^T buffer.
+  auto pv = [&](const _Float16* vl, const u4 (&pop)[4]) {
+    auto vop = [&](int i) { return *(const u4*)(vl + (i & 3) * 32 * kVS + 16 * (i >> 2)); };
+    u4 ring[4] = {vop(0), vop(1), vop(2), vop(3)};
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      oacc[i & 3] = mfma_32x32x16(ring[i & 3], pop[i >> 2], oacc[i & 3], OT{});
+      if (i + 4 < 16) ring[i & 3] = vop(i + 4);
+    }
+  };
+
+  if constexpr (DENSE) {
+    // ---- unquantized cache: K operands are read from the raw ring while tile t is computed, so
+    // tile t + 2 is issued into the slot of tile t - 1 and lands within the step; V^T is built from
+    // the raw rows into a double buffer, half by waves 4-7 before their MFMAs and half by waves 0-3
+    // after theirs (the two waves that share a SIMD are in opposite phases)
+    if (ntile > 0) {
+      wait_vm<0>();
+      __syncthreads();
+      stage_v_raw(raw[0], v_lds[0], tid & 255, tid >> 8);
+      __syncthreads();
+    }
+    // this lane's K operand bytes within a raw slot: key row 32 (i & 1) + qc, 16-byte chunk
+    // 2 (i >> 1) + hh at its swizzled position
+    const int kswz = qc % RawCfg<16>::CPR;
+    for (int t = 0; t < ntile; ++t) {
+      const int cur = t & 1;
+      const int k0 = k_begin + kPT * t;
+      if (t + 2 < ntile) issue_raw(t + 2);
+      if (t + 1 < ntile && wave >= kPW / 2) stage_v_raw(raw[(t + 1) % kRawSlots], v_lds[cur ^ 1], tid - 256, 0);
+      f16v sacc[2] = {f16v{}, f16v{}};
+      {
+        const uint8_t* kraw = raw[t % kRawSlots] + qc * RawCfg<16>::ROWB;
+        auto kop = [&](int i) -> u4 {
+          return *(const u4*)(kraw + (i & 1) * 32 * RawCfg<16>::ROWB + 16 * ((2 * (i >> 1) + hh) ^ kswz));
+        };
+        u4 ring[4] = {kop(0), kop(1), kop(2), kop(3)};
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          sacc[i & 1] = mfma_32x32x16(ring[i & 3], qop[i >> 1], sacc[i & 1], OT{});
+          if (i + 4 < 16) ring[i & 3] = kop(i + 4);
+        }
+      }
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) sacc[kb][i] *= p.scale_log2;
+      mask_tile(sacc, k0);
+      update_max(sacc);
+      u4 pop[4];
+      probs(sacc, pop);
+      pv(&v_lds[cur][qc * kVS + 8 * hh], pop);
+      if (t + 1 < ntile && wave < kPW / 2) stage_v_raw(raw[(t + 1) % kRawSlots], v_lds[cur ^ 1], tid, 1);
+      wait_vm<0>();  // tile t + 2 has landed
+      __syncthreads();
+    }
+  } else if (ntile > 0) {
+    // ---- quantized cache, software-pipelined over 32-key blocks. Step t (tile t) runs two halves;
+    // half h takes the scores of block h of the tile, already computed, and
+    //  * runs their softmax while the MFMAs of the next block's scores execute (block 1 of tile t,
+    //    then block 0 of tile t + 1), then
+    //  * accumulates O += V P for the block while the waves dequantize half of tile t + 2 (waves
+    //    0-3 its V^T, waves 4-7 its K),
+    // so every wave always has MFMA work beside its VALU work, and two 16-register score blocks are
+    // live rather than two tiles.
+    //  * fp16 operands: tile j in k_lds[j % 3] and v_lds[j % 3] (step t reads K of tiles t and
+    //    t + 1 and V of tile t, and writes tile t + 2);
+    //  * raw ring: tile j in slot j % 3; step t reads tile t + 2 and issues tile t + 4 into the slot
+    //    of tile t + 1 (dequantized in step t - 1), so every tile is loaded two steps ahead;
+    //  * one barrier per step orders all of it.
+    constexpr int KBUF = kPT * kKS, VBUF = 128 * kVS;
+    const _Float16* kl_lane = &k_lds[0][qc * kKS + 8 * hh];  // this lane's K operands, V^T operands
+    const _Float16* vl_lane = &v_lds[0][qc * kVS + 8 * hh];
+    // S^T = K Q^T for the 32-key block whose K rows start at kl (this lane's offset included): 8
+    // MFMAs over the head dimension, the K operands streamed through a 4-deep register ring; MFMAs
+    // [J0, J1) of the 8
+    auto qk_ring = [&](u4 (&ring)[4], const _Float16* kl) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) ring[j] = *(const u4*)(kl + 16 * j);
+    };
+    auto qk_run = [&](auto j0, auto j1, f16v& acc, u4 (&ring)[4], const _Float16* kl) {
+#pragma unroll
+      for (int j = decltype(j0)::value; j < decltype(j1)::value; ++j) {
+        acc = mfma_32x32x16(ring[j & 3], qop[j], j == 0 ? f16v{} : acc, OT{});
+        if (j + 4 < 8) ring[j & 3] = *(const u4*)(kl + 16 * (j + 4));
+      }
+    };
+    using J0 = std::integral_constant<int, 0>;
+    using J2 = std::integral_constant<int, 2>;
+    using J8 = std::integral_constant<int, 8>;
+    // the block's keys [k, k + 32): mask (only on a causal diagonal or window edge), row maximum
+    auto mask_blk = [&](f16v& acc, int k) {
+      if (__builtin_expect(!(k >= lo_all && k + 32 <= hi_all), 0)) {
+        const int lo = lo_r - k - 4 * hh, hi = hi_r - k - 4 * hh;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int c = 8 * (i >> 2) + (i & 3);
+          if (c < lo || c >= hi) acc[i] = -INFINITY;
+        }
+      }
+    };
+    auto max_blk = [&](const f16v& acc) {
+      float tm = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) tm = fmaxf(tm, acc[i]);
+      return max_xor32(tm) * inv2;
+    };
+    auto rescale = [&](float tm) {
+      if (__builtin_amdgcn_ballot_w64(tm > m_run + kPSlack) != 0) {
+        const float m_new = tm > m_run + kPSlack ? fmaxf(m_run, tm) : m_run;
+        const float corr = m_new == m_run ? 1.0f : exp2_fast(m_run - m_new);
+        l_run *= corr;
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) oacc[db][i] *= corr;
+        m_run = m_new;
+      }
+    };
+    // p = 2^(acc * inv2 - m) for the block's 32 keys: the B operands of its two PV k-steps
+    auto probs_blk = [&](const f16v& acc, u4 (&pop)[2]) {
+      const float nm = m_run == -INFINITY ? 0.0f : -m_run;
+      float lsum[2] = {0.0f, 0.0f};
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float p0 = exp2_fast(fmaf(acc[8 * j + 2 * e], inv2, nm));
+          const float p1 = exp2_fast(fmaf(acc[8 * j + 2 * e + 1], inv2, nm));
+          pop[j][e] = pack2(p0, p1, OT{});
+          lsum[e & 1] = add_pair(pop[j][e], lsum[e & 1], OT{});
+        }
+      l_run += lsum[0] + lsum[1];
+    };
+    // O^T += V^T P^T over block kb's two k-steps (V^T slots 32 kb .. 32 kb + 31): 8 MFMAs, the 4
+    // dim blocks alternating, V^T operands through a 4-deep ring
+    auto pv_blk = [&](const _Float16* vl, const u4 (&pop)[2], auto kb) {
+      constexpr int KB = decltype(kb)::value;
+      auto vop = [&](int i) { return *(const u4*)(vl + (i & 3) * 32 * kVS + 16 * (2 * KB + (i >> 2))); };
       u4 ring[4] = {vop(0), vop(1), vop(2), vop(3)};
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
+      for (int i = 0; i < 8; ++i) {
         oacc[i & 3] = mfma_32x32x16(ring[i & 3], pop[i >> 2], oacc[i & 3], OT{});
-        if (i + 4 < 16) ring[i & 3] = vop(i + 4);
+        if (i + 4 < 8) ring[i & 3] = vop(i + 4);
       }
-    }
+    };
+    using B0 = std::integral_constant<int, 0>;
+    using B1 = std::integral_constant<int, 1>;
 
-    if (t + 1 < ntile && wave < kPW / 2) {
-      if constexpr (DENSE) {
-        stage_v_raw(raw[(t + 1) % kRawSlots], v_lds[cur ^ 1], tid, 1);
-      } else {
-        stage_from_raw<T, BITS, G>(raw[(t + 1) % kRawSlots], k_lds[cur ^ 1], v_lds[cur ^ 1], sb_tab[wave & 3], tid,
-                                 range_bad);
+    f16v sX, sY;  // the scores of block 0 (entering a step: tile t's) and block 1 of a tile
+    // VW: this wave builds V^T (waves 0-3) rather than K (waves 4-7); the loop is compiled once per
+    // role, so each copy keeps only its own staging addresses live
+    auto step = [&](auto vw, auto qkn, auto stg, int t) {
+      constexpr bool VW = decltype(vw)::value, QKN = decltype(qkn)::value, STG = decltype(stg)::value;
+      issue_raw(t + 4);
+      // the step's buffers, as element (byte, for the raw ring) offsets from each array's start
+      const int k_t = opaque((t % 3) * KBUF), k_t1 = opaque(((t + 1) % 3) * KBUF);
+      const int k_w = opaque(((t + 2) % 3) * KBUF);
+      const int v_t = opaque((t % 3) * VBUF), v_w = opaque(((t + 2) % 3) * VBUF);
+      const uint8_t* raw2 = &raw[0][0] + opaque(((t + 2) % kRawSlots) * RC::SLOT);
+      if constexpr (STG && VW) {
+        stage_v_table<T, BITS, G>(raw2, sb_tab[wave & 3], tid, range_bad);
+        __builtin_amdgcn_wave_barrier();
       }
-    }
-    if constexpr (DENSE) {
-      wait_vm<0>();  // tile t + 2 has landed
-    } else {
-      wait_vm<RC::IPT>();  // tile t + 2 has landed (tile t + 3 may be in flight)
-    }
+      const int k0 = k_begin + kPT * t;
+      const _Float16* vl = vl_lane + v_t;
+      u4 ring[4];
+      u4 pop[2];
+      // half 0: softmax of block 0 beside S(block 1) = K(t) rows 32-63 Q^T
+      {
+        const _Float16* kl = kl_lane + k_t + 32 * kKS;
+        mask_blk(sX, k0);
+        qk_ring(ring, kl);
+        qk_run(J0{}, J2{}, sY, ring, kl);
+        const float tm = max_blk(sX);
+        rescale(tm);
+        qk_run(J2{}, J8{}, sY, ring, kl);
+        probs_blk(sX, pop);
+      }
+      pv_blk(vl, pop, B0{});
+      if constexpr (STG && VW) stage_v<BITS, G, 0>(raw2, &v_lds[0][0] + v_w, sb_tab[wave & 3], tid);
+      if constexpr (STG && !VW) stage_k<T, BITS, G, 0>(raw2, &k_lds[0][0] + k_w, tid, range_bad);
+      // half 1: softmax of block 1 beside S(block 0 of tile t + 1) = K(t + 1) rows 0-31 Q^T
+      {
+        const _Float16* kl = kl_lane + k_t1;
+        mask_blk(sY, k0 + 32);
+        if constexpr (QKN) {
+          qk_ring(ring, kl);
+          qk_run(J0{}, J2{}, sX, ring, kl);
+        }
+        const float tm = max_blk(sY);
+        rescale(tm);
+        if constexpr (QKN) qk_run(J2{}, J8{}, sX, ring, kl);
+        probs_blk(sY, pop);
+      }
+      pv_blk(vl, pop, B1{});
+      if constexpr (STG && VW) stage_v<BITS, G, 1>(raw2, &v_lds[0][0] + v_w, sb_tab[wave & 3], tid);
+      if constexpr (STG && !VW) stage_k<T, BITS, G, 1>(raw2, &k_lds[0][0] + k_w, tid, range_bad);
+      wait_vm<RC::IPT>();  // tile t + 3 has landed (tile t + 4 may be in flight)
+      __syncthreads();
+    };
+    using Y = std::true_type;
+    using N = std::false_type;
+
+    // prologue: tiles 0 and 1 dequantized, S(tile 0, block 0) computed, tile 2 landed, tile 3 in
+    // flight
+    wait_vm<2 * RC::IPT>();
     __syncthreads();
+    stage_from_raw<T, BITS, G>(raw[0], k_lds[0], v_lds[0], sb_tab[wave & 3], tid, range_bad);
+    wait_vm<RC::IPT>();
+    __syncthreads();
+    issue_raw(3);  // into the slot of tile 0
+    stage_from_raw<T, BITS, G>(raw[1], k_lds[1], v_lds[1], sb_tab[wave & 3], tid, range_bad);
+    {
+      u4 ring[4];
+      qk_ring(ring, kl_lane);
+      qk_run(J0{}, J8{}, sX, ring, kl_lane);
+    }
+    wait_vm<RC::IPT>();
+    __syncthreads();
+    auto run = [&](auto vw) {
+      int t = 0;
+      for (; t + 2 < ntile; ++t) step(vw, Y{}, Y{}, t);
+      if (t + 1 < ntile) step(vw, Y{}, N{}, t++);
+      step(vw, N{}, N{}, t);
+    };
+    if (wave < kPW / 2) {
+      run(Y{});
+    } else {
+      run(N{});
+    }
   }
   wait_vm<0>();  // no load into this workgroup's LDS outlives it
   if constexpr (!DENSE && T::id == KVQ_DTYPE_BF16) {
     // a group beyond the fp16 range poisons the workgroup's rows: NaN propagates through the split
-    // merge (0 * NaN is NaN) to every output row of the row block
-    if (range_bad) s_range_bad = 1;
+    // merge (0 * NaN is NaN) to every output row of the row block. (The tables are free: the last
+    // tile step staged nothing and ended with a barrier.)
+    const bool wave_bad = __builtin_amdgcn_ballot_w64(range_bad) != 0;
+    if (lane == 0) s_flags[wave] = wave_bad;
     __syncthreads();
-    if (s_range_bad) {
+    unsigned any_bad = 0;
+#pragma unroll
+    for (int w = 0; w < kPW; ++w) any_bad |= s_flags[w];
+    if (any_bad) {
 #pragma unroll
       for (int db = 0; db < 4; ++db)
 #pragma unroll
@@ -750,9 +939,9 @@ __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) 
     // arrival is counted, so the last arrival sees every split's partials.
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    if (tid == 0) s_arrived = __hip_atomic_fetch_add(&p.counters[unit], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid == 0) *s_arrived = __hip_atomic_fetch_add(&p.counters[unit], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
-    if (s_arrived != (unsigned)(p.nsplit - 1)) return;
+    if (*s_arrived != (unsigned)(p.nsplit - 1)) return;
     if (tid == 0) __hip_atomic_store(&p.counters[unit], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
     // M = max over the splits that saw a key; weights 2^(m_s - M)

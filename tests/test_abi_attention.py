@@ -144,3 +144,14 @@ def test_paged_append_rejects_bad_arguments():
     _expect(call(row_offset=255, L=2), _lib.ERR_INVALID, "cannot hold")
     _expect(call(bits=3), _lib.ERR_UNSUPPORTED, "bits")
     _expect(call(row_offset=-1), _lib.ERR_INVALID, "row_offset")
+
+
+@pytest.mark.parametrize("field,value", [("sb_stride_s", 3), ("sb_stride_h", 8 * 256 + 1), ("scales", (1 << 16) + 2)])
+def test_prefill_rejects_unaligned_scale_rows(field, value):
+    # with two or more scale groups per row the prefill kernel loads a row's groups in pairs
+    # (4 bytes): scale and bias rows must be 4-byte aligned
+    n = _lib.lib().kvq_prefill_workspace_size(1, 8, 1, 1, 128, 256, 0)
+    k = _fake_q()
+    setattr(k, field, value)
+    _expect(_prefill(k=k, ws=WS, wsb=n), _lib.ERR_INVALID, "4-byte aligned")
+    _expect(_paged(_lib.lib().kvq_paged_prefill_attn, k=k, ws=WS, wsb=n), _lib.ERR_INVALID, "4-byte aligned")
