@@ -127,9 +127,9 @@ int kvq_rope_quantize_append(const kvq_rows* k_src, const kvq_qtensor* k_dst,
  * out = softmax(scale * q K^T + mask) V over the dequantized K/V.
  * Replaces: m5engine/attention.py:42-45 (the L == 1 hand-off to mlx-lm's
  * quantized_scaled_dot_product_attention) and, for L > 1, the blocked loop at :64-103.
- * Requirements: D in {64, 128}; group_size in {32, 64, 128} and <= D; bits in {4, 8}. One pass of
- *   the kernel serves 16 * group_size / D query rows ((Hq / Hkv) * L) of a KV head; more rows take
- *   more passes over the keys.
+ * Requirements: D in {64, 128, 256}; group_size in {32, 64, 128} with D / 4 <= group_size <= D;
+ *   bits in {4, 8}. One pass of the kernel serves 16 * group_size / D query rows ((Hq / Hkv) * L)
+ *   of a KV head; more rows take more passes over the keys.
  *   seq_lens: NULL (every sequence has S keys) or device int32[B] with 1 <= seq_lens[b] <= S.
  *   causal:   query l of sequence b sits at position seq_len_b - L + l and sees keys <= it.
  *   window:   0 = none; otherwise keys k > position - window only (sliding window).

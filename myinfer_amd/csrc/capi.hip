@@ -98,10 +98,12 @@ int check_workspace(size_t ws_needed, void* workspace, size_t workspace_bytes) {
   return KVQ_OK;
 }
 
-// Scale-group sizes the attention kernels are built for: 32, 64 and 128, at most D.
+// Scale-group sizes the attention kernels are built for: 32, 64 and 128, at most D and at least D / 4
+// (a decode lane's quarter of a row lies in one group).
 int check_attn_group(int group_size, int D) {
-  if ((group_size != 32 && group_size != 64 && group_size != 128) || group_size > D)
-    return fail(KVQ_ERR_UNSUPPORTED, "attention supports group_size 32, 64 and 128 (at most head_dim %d), got %d", D,
+  if ((group_size != 32 && group_size != 64 && group_size != 128) || group_size > D || 4 * group_size < D)
+    return fail(KVQ_ERR_UNSUPPORTED,
+                "attention supports group_size 32, 64 and 128 between head_dim/4 and head_dim (%d), got %d", D,
                 group_size);
   return KVQ_OK;
 }
@@ -308,13 +310,13 @@ int kvq_paged_quantize_append(const kvq_rows* k_src, const kvq_qtensor* k_pool, 
 }
 
 size_t kvq_decode_workspace_size(int B, int Hq, int Hkv, int L, int D, int S, int window) {
-  if (B <= 0 || Hq <= 0 || Hkv <= 0 || L <= 0 || S <= 0 || (D != 64 && D != 128) || window < 0) return 0;
+  if (B <= 0 || Hq <= 0 || Hkv <= 0 || L <= 0 || S <= 0 || (D != 64 && D != 128 && D != 256) || window < 0) return 0;
   // one size serves every cache format: the quantized (8-, 4-bit) and the unquantized (16) plans
   // and every scale-group size (the group sets the query rows per workgroup)
   size_t n = 0;
   for (int bits : {8, 4, 16})
     for (int G : {32, 64, 128}) {
-      if (G > D) continue;
+      if (G > D || 4 * G < D || (bits == 16 && D > 128)) continue;
       const size_t x = kvq::decode_workspace_bytes(B, Hq, Hkv, L, D, S, window, bits, G);
       n = x > n ? x : n;
     }
@@ -325,7 +327,8 @@ int kvq_decode_attn(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* 
                     const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int bits, int group_size,
                     int dtype, float scale, int causal, int window, void* workspace, size_t workspace_bytes,
                     void* stream) {
-  if (D != 64 && D != 128) return fail(KVQ_ERR_UNSUPPORTED, "decode supports head_dim 64 and 128, got %d", D);
+  if (D != 64 && D != 128 && D != 256)
+    return fail(KVQ_ERR_UNSUPPORTED, "decode supports head_dim 64, 128 and 256, got %d", D);
   int rc = check_attn(q, k, v, out, B, Hq, Hkv, L, D, S, bits, group_size, dtype, scale, window,
                       kvq_decode_workspace_size(B, Hq, Hkv, L, D, S, window), workspace, workspace_bytes);
   if (rc) return rc;
@@ -337,7 +340,8 @@ int kvq_decode_attn(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* 
 int kvq_decode_attn_static(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v, const int32_t* seq_lens,
                            const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int bits, int group_size,
                            int dtype, float scale, int causal, int window, void* stream) {
-  if (D != 64 && D != 128) return fail(KVQ_ERR_UNSUPPORTED, "decode supports head_dim 64 and 128, got %d", D);
+  if (D != 64 && D != 128 && D != 256)
+    return fail(KVQ_ERR_UNSUPPORTED, "decode supports head_dim 64, 128 and 256, got %d", D);
   int rc = check_attn_args(q, k, v, out, B, Hq, Hkv, L, D, S, bits, group_size, dtype, scale, window);
   if (rc) return rc;
   const size_t need = kvq_decode_workspace_size(B, Hq, Hkv, L, D, S, window);
@@ -405,7 +409,8 @@ int kvq_paged_decode_attn(const kvq_rows* q, const kvq_qtensor* k_pool, const kv
                           const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int bits, int group_size,
                           int dtype, float scale, int causal, int window, void* workspace, size_t workspace_bytes,
                           void* stream) {
-  if (D != 64 && D != 128) return fail(KVQ_ERR_UNSUPPORTED, "decode supports head_dim 64 and 128, got %d", D);
+  if (D != 64 && D != 128 && D != 256)
+    return fail(KVQ_ERR_UNSUPPORTED, "decode supports head_dim 64, 128 and 256, got %d", D);
   int rc = check_paged_attn(q, k_pool, v_pool, num_pages, block_table, table_stride, out, B, Hq, Hkv, L, D, S, bits,
                             group_size, dtype, scale, window, kvq_decode_workspace_size(B, Hq, Hkv, L, D, S, window),
                             workspace, workspace_bytes);
@@ -437,7 +442,7 @@ int kvq_paged_prefill_attn(const kvq_rows* q, const kvq_qtensor* k_pool, const k
 int kvq_decode_attn_dense(const kvq_rows* q, const kvq_rows* k, const kvq_rows* v, const int32_t* seq_lens,
                           const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int dtype, float scale,
                           int causal, int window, void* workspace, size_t workspace_bytes, void* stream) {
-  if (D != 64 && D != 128) return fail(KVQ_ERR_UNSUPPORTED, "decode supports head_dim 64 and 128, got %d", D);
+  if (D != 64 && D != 128) return fail(KVQ_ERR_UNSUPPORTED, "unquantized decode supports head_dim 64 and 128, got %d", D);
   int rc = check_attn_dense(q, k, v, out, B, Hq, Hkv, L, D, S, dtype, scale, window,
                             kvq_decode_workspace_size(B, Hq, Hkv, L, D, S, window), workspace, workspace_bytes);
   if (rc) return rc;

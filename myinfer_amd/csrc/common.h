@@ -232,6 +232,26 @@ struct Bytes<32> {
     w[7] = b[3];
   }
 };
+template <>
+struct Bytes<64> {
+  uint32_t w[16];
+  __device__ __forceinline__ void load(const uint8_t* p) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const u4 v = *(const u4*)(p + 16 * c);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) w[4 * c + i] = v[i];
+    }
+  }
+  __device__ __forceinline__ void load_buf(__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const u4 v = __builtin_amdgcn_raw_buffer_load_b128(r, vo + 16 * c, so, 0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) w[4 * c + i] = v[i];
+    }
+  }
+};
 
 }  // namespace kvq
 

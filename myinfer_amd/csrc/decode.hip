@@ -6,7 +6,7 @@
 // i.e. the quantity m5engine/attention.py:29-103 evaluates (blocked online softmax, :64-100)
 // and that its L == 1 branch (:42-45) hands to mlx-lm's quantized SDPA.
 //
-// Design (one wave = 16 MFMA columns; group size 64, NG = D/64 groups per row):
+// Design (one wave = 16 MFMA columns; NG = D/G scale groups per row, head_dim 64, 128 or 256):
 //  * The rep*L query rows that share a KV head are the MFMA columns. Column n holds query row
 //    n % R (R = 16/NG) restricted to group n / R, so one accumulator yields per-group partial dot
 //    products and a DPP row rotation adds the groups; every lane then owns a complete score.
@@ -137,6 +137,12 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 template <int ROWB>
 struct TileOps;
 template <>
+struct TileOps<256> {
+  u4 k[2][4];
+  u4 sb[4][2];
+  u4 v[8];
+};
+template <>
 struct TileOps<128> {
   u4 k[2][2];
   u4 sb[4][2];
@@ -155,10 +161,48 @@ struct TileOps<32> {
   uint32_t v[8];
 };
 
-// ka0/ka1: the two K chunk addresses of key n (ka1 unused below 128-byte rows); sa: the sb base;
-// va: the V slice address of key 4 lg. AS: bytes between the scale/bias arrays of a slot.
+// ka: the K chunk addresses of key n (one per 16-byte chunk of the lane's quarter row; rows below
+// 128 bytes use the first); sa: the sb base; va: the V slice address of key 4 lg. AS: bytes between
+// the scale/bias arrays of a slot.
 template <int AS>
-__device__ __forceinline__ void read_tile(TileOps<128>& t, uint32_t ka0, uint32_t ka1, uint32_t sa, uint32_t va) {
+__device__ __forceinline__ void read_tile(TileOps<256>& t, const uint32_t (&ka)[4], uint32_t sa, uint32_t va) {
+  asm volatile(
+      "ds_read_b128 %0, %24\n"
+      "ds_read_b128 %1, %25\n"
+      "ds_read_b128 %2, %26\n"
+      "ds_read_b128 %3, %27\n"
+      "ds_read_b128 %4, %24 offset:4096\n"
+      "ds_read_b128 %5, %25 offset:4096\n"
+      "ds_read_b128 %6, %26 offset:4096\n"
+      "ds_read_b128 %7, %27 offset:4096\n"
+      "ds_read_b128 %8, %28\n"
+      "ds_read_b128 %9, %28 offset:64\n"
+      "ds_read_b128 %10, %28 offset:%30\n"
+      "ds_read_b128 %11, %28 offset:%31\n"
+      "ds_read_b128 %12, %28 offset:%32\n"
+      "ds_read_b128 %13, %28 offset:%33\n"
+      "ds_read_b128 %14, %28 offset:%34\n"
+      "ds_read_b128 %15, %28 offset:%35\n"
+      "ds_read_b128 %16, %29\n"
+      "ds_read_b128 %17, %29 offset:256\n"
+      "ds_read_b128 %18, %29 offset:512\n"
+      "ds_read_b128 %19, %29 offset:768\n"
+      "ds_read_b128 %20, %29 offset:4096\n"
+      "ds_read_b128 %21, %29 offset:4352\n"
+      "ds_read_b128 %22, %29 offset:4608\n"
+      "ds_read_b128 %23, %29 offset:4864\n"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(t.k[0][0]), "=&v"(t.k[0][1]), "=&v"(t.k[0][2]), "=&v"(t.k[0][3]), "=&v"(t.k[1][0]), "=&v"(t.k[1][1]),
+        "=&v"(t.k[1][2]), "=&v"(t.k[1][3]), "=&v"(t.sb[0][0]), "=&v"(t.sb[0][1]), "=&v"(t.sb[1][0]),
+        "=&v"(t.sb[1][1]), "=&v"(t.sb[2][0]), "=&v"(t.sb[2][1]), "=&v"(t.sb[3][0]), "=&v"(t.sb[3][1]), "=&v"(t.v[0]),
+        "=&v"(t.v[1]), "=&v"(t.v[2]), "=&v"(t.v[3]), "=&v"(t.v[4]), "=&v"(t.v[5]), "=&v"(t.v[6]), "=&v"(t.v[7])
+      : "v"(ka[0]), "v"(ka[1]), "v"(ka[2]), "v"(ka[3]), "v"(sa), "v"(va), "i"(AS), "i"(AS + 64), "i"(2 * AS),
+        "i"(2 * AS + 64), "i"(3 * AS), "i"(3 * AS + 64)
+      : "memory");
+}
+template <int AS>
+__device__ __forceinline__ void read_tile(TileOps<128>& t, const uint32_t (&ka)[4], uint32_t sa, uint32_t va) {
+  const uint32_t ka0 = ka[0], ka1 = ka[1];
   asm volatile(
       "ds_read_b128 %0, %20\n"
       "ds_read_b128 %1, %21\n"
@@ -190,7 +234,8 @@ __device__ __forceinline__ void read_tile(TileOps<128>& t, uint32_t ka0, uint32_
       : "memory");
 }
 template <int AS>
-__device__ __forceinline__ void read_tile(TileOps<64>& t, uint32_t ka0, uint32_t, uint32_t sa, uint32_t va) {
+__device__ __forceinline__ void read_tile(TileOps<64>& t, const uint32_t (&ka)[4], uint32_t sa, uint32_t va) {
+  const uint32_t ka0 = ka[0];
   asm volatile(
       "ds_read_b128 %0, %18\n"
       "ds_read_b128 %1, %18 offset:1024\n"
@@ -218,7 +263,8 @@ __device__ __forceinline__ void read_tile(TileOps<64>& t, uint32_t ka0, uint32_t
       : "memory");
 }
 template <int AS>
-__device__ __forceinline__ void read_tile(TileOps<32>& t, uint32_t ka0, uint32_t, uint32_t sa, uint32_t va) {
+__device__ __forceinline__ void read_tile(TileOps<32>& t, const uint32_t (&ka)[4], uint32_t sa, uint32_t va) {
+  const uint32_t ka0 = ka[0];
   asm volatile(
       "ds_read_b64 %0, %18\n"
       "ds_read_b64 %1, %18 offset:512\n"
@@ -604,14 +650,15 @@ __global__ __launch_bounds__(NW * 64, (dec_min_wgs<D, BITS, NW, NSLOT, G>())) vo
 
   // per-lane LDS offsets of the tile operands, relative to a slot
   const int sw = n % C::CPR;  // the swizzle of key n (and of key 16 + n)
-  uint32_t off_k0, off_k1;
-  if constexpr (C::KLB == 32) {
-    off_k0 = n * C::ROWB + 16 * ((2 * lg) ^ sw);
-    off_k1 = n * C::ROWB + 16 * ((2 * lg + 1) ^ sw);
-  } else if constexpr (C::KLB == 16) {
-    off_k0 = off_k1 = n * C::ROWB + 16 * (lg ^ sw);
-  } else {
-    off_k0 = off_k1 = n * C::ROWB + 16 * ((lg >> 1) ^ sw) + 8 * (lg & 1);
+  // K: chunk c of the lane's quarter row of key n (KLB / 16 chunks; below 16 bytes a half chunk)
+  uint32_t off_k[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    if constexpr (C::KLB >= 16) {
+      off_k[c] = n * C::ROWB + 16 * (((C::KLB / 16) * lg + min(c, C::KLB / 16 - 1)) ^ sw);
+    } else {
+      off_k[c] = n * C::ROWB + 16 * ((lg >> 1) ^ sw) + 8 * (lg & 1);
+    }
   }
   const uint32_t off_sb = 2 * C::TB + 4 * (32 * g + 4 * lg);
   const uint32_t off_v = C::TB + 4 * lg * C::ROWB + n * C::VLB;
@@ -646,7 +693,12 @@ __global__ __launch_bounds__(NW * 64, (dec_min_wgs<D, BITS, NW, NSLOT, G>())) vo
 #pragma unroll
       for (int beta = 0; beta < 2; ++beta) {
         Bytes<C::KLB> kc;
-        if constexpr (C::KLB == 32) {
+        if constexpr (C::KLB == 64) {
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+#pragma unroll
+            for (int w = 0; w < 4; ++w) kc.w[4 * c + w] = op.k[beta][c][w];
+        } else if constexpr (C::KLB == 32) {
 #pragma unroll
           for (int w = 0; w < 4; ++w) {
             kc.w[w] = op.k[beta][0][w];
@@ -739,7 +791,10 @@ __global__ __launch_bounds__(NW * 64, (dec_min_wgs<D, BITS, NW, NSLOT, G>())) vo
       Bytes<VB> vc[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        if constexpr (C::VLB == 8) {
+        if constexpr (C::VLB == 16) {
+#pragma unroll
+          for (int w = 0; w < 4; ++w) vc[i].w[w] = op.v[i][w];
+        } else if constexpr (C::VLB == 8) {
           vc[i].w[0] = op.v[i][0];
           vc[i].w[1] = op.v[i][1];
         } else {
@@ -769,7 +824,8 @@ __global__ __launch_bounds__(NW * 64, (dec_min_wgs<D, BITS, NW, NSLOT, G>())) vo
       compute(op, tile_k0(i));
     } else {
       TileOps<C::ROWB> op;
-      read_tile<C::AS>(op, sa + off_k0, sa + off_k1, sa + off_sb, sa + off_v);
+      const uint32_t ka[4] = {sa + off_k[0], sa + off_k[1], sa + off_k[2], sa + off_k[3]};
+      read_tile<C::AS>(op, ka, sa + off_sb, sa + off_v);
       issue(i + NSLOT, slot);
       compute(op, tile_k0(i));
     }
@@ -1113,21 +1169,27 @@ static DecParams decode_params(const kvq_rows* q, const int32_t* seq_lens, const
 }
 
 // Calls f(T{}, D, BITS, G) (the last three as std::integral_constant) for the quantized
-// instantiation that matches the runtime arguments: D in {64, 128}, bits in {4, 8}, G in {32, 64,
-// 128} with G <= D.
+// instantiation that matches the runtime arguments: D in {64, 128, 256}, bits in {4, 8}, G in {32,
+// 64, 128} with D / 4 <= G <= D.
 template <int N>
 using IC = std::integral_constant<int, N>;
 template <typename F>
 static hipError_t dispatch_quant(int dtype, int D, int bits, int G, F&& f) {
   auto by_g = [&](auto t, auto d, auto b) -> hipError_t {
-    if (G == 32) return f(t, d, b, IC<32>{});
-    if constexpr (decltype(d)::value >= 128) {
+    constexpr int DD = decltype(d)::value;
+    if constexpr (DD / 4 <= 32) {
+      if (G == 32) return f(t, d, b, IC<32>{});
+    }
+    if constexpr (DD >= 128) {
       if (G == 128) return f(t, d, b, IC<128>{});
     }
     return f(t, d, b, IC<64>{});
   };
   auto by_b = [&](auto t, auto d) -> hipError_t { return bits == 8 ? by_g(t, d, IC<8>{}) : by_g(t, d, IC<4>{}); };
-  auto by_d = [&](auto t) -> hipError_t { return D == 128 ? by_b(t, IC<128>{}) : by_b(t, IC<64>{}); };
+  auto by_d = [&](auto t) -> hipError_t {
+    if (D == 256) return by_b(t, IC<256>{});
+    return D == 128 ? by_b(t, IC<128>{}) : by_b(t, IC<64>{});
+  };
   return dtype == KVQ_DTYPE_BF16 ? by_d(BF16{}) : by_d(F16{});
 }
 

@@ -59,6 +59,8 @@ def _attn(fn, **kw):
     (dict(group=48), _lib.ERR_UNSUPPORTED, "group_size"),
     (dict(group=128, D=64, S=256), _lib.ERR_UNSUPPORTED, "group_size"),
     (dict(D=96), _lib.ERR_UNSUPPORTED, "head_dim"),
+    (dict(D=512), _lib.ERR_UNSUPPORTED, "head_dim"),
+    (dict(group=32, D=256, S=256), _lib.ERR_UNSUPPORTED, "group_size"),
     (dict(Hq=7, Hkv=2), _lib.ERR_INVALID, "multiple"),
     (dict(dtype=5), _lib.ERR_INVALID, "dtype"),
     (dict(S=0), _lib.ERR_INVALID, "positive"),
@@ -116,6 +118,7 @@ def test_workspace_sizes():
     # the split count targets a fixed number of workgroups, so the partials do not shrink with B
     assert 0 < a <= b
     assert lib.kvq_decode_workspace_size(1, 64, 8, 1, 96, 32768, 0) == 0
+    assert lib.kvq_decode_workspace_size(1, 64, 8, 1, 256, 32768, 0) > 0  # head_dim 256 (quantized caches)
     # a sliding window never needs more splits than the full context
     assert 0 < lib.kvq_decode_workspace_size(4, 32, 16, 1, 128, 8192, 1024) <= lib.kvq_decode_workspace_size(4, 32, 16, 1, 128, 8192, 0)
 

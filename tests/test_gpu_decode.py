@@ -84,6 +84,22 @@ def test_group_sizes(dtype, bits, group, D, Hq, Hkv, L, S):
     run_case(2, Hq, Hkv, L, S, D, bits, dtype, causal=L > 1, seed=400 + group + S, group=group, what="group")
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("bits", [8, 4])
+@pytest.mark.parametrize("group", [64, 128])
+@pytest.mark.parametrize("Hq,Hkv,L,S", [(8, 1, 1, 1000), (16, 2, 1, 4097), (4, 4, 1, 33), (8, 2, 3, 700)])
+def test_head_dim_256(dtype, bits, group, Hq, Hkv, L, S):
+    # head_dim 256 (Gemma-style): a pass serves 16*group/256 query rows
+    run_case(2, Hq, Hkv, L, S, 256, bits, dtype, causal=L > 1, seed=700 + group + S, group=group, what="d256")
+
+
+def test_head_dim_256_window_lengths_and_prompt():
+    run_case(3, 16, 2, 1, 3000, 256, 8, torch.bfloat16, window=700, seq_lens=[3000, 1, 1777], seed=81, group=64,
+             what="d256-window")
+    # a prompt chunk: many query rows take many decode passes over the keys
+    run_case(1, 8, 4, 70, 900, 256, 4, torch.float16, causal=True, seed=82, group=64, what="d256-chunk")
+
+
 def test_group_sizes_window_and_lengths():
     run_case(3, 16, 2, 1, 3000, 128, 4, torch.float16, window=700, seq_lens=[3000, 1, 1777], seed=77, group=32,
              what="group32-window")

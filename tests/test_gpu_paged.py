@@ -225,3 +225,23 @@ def test_paged_group_sizes(group, bits):
         assert torch.equal(out_p, out_c), (L, kernel)
         assert_close(out_p, exact_reference(q, kc, vc, scale, bits=bits, group_size=group, causal=True, seq_lens=sl),
                      f"paged {kernel} group={group}")
+
+
+@pytest.mark.parametrize("bits", [8, 4])
+def test_paged_head_dim_256(bits):
+    print(f"paged D=256 bits={bits}", flush=True)
+    B, Hq, Hkv, D, dtype = 2, 8, 2, 256, torch.float16
+    lens = [1500, 333]
+    rows, tables, kp, vp, kc, vc = build(B, Hkv, lens, D, bits, dtype, 51, group=64)
+    sl = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    scale = 1.0 / math.sqrt(D)
+    for L in (1, 3):
+        q = seeded_normal((B, Hq, L, D), 52 + L, dtype, DEV)
+        out_p = kernels.paged_attention(q, kp, vp, tables, sl, scale, causal=True, bits=bits, group_size=64,
+                                        max_len=max(lens))
+        out_c = kernels.attention(q, kc, vc, scale, causal=True, seq_lens=sl, bits=bits, group_size=64)
+        torch.cuda.synchronize()
+        assert torch.isfinite(out_p.float()).all()
+        assert torch.equal(out_p, out_c), L
+        assert_close(out_p, exact_reference(q, kc, vc, scale, bits=bits, group_size=64, causal=True, seq_lens=sl),
+                     f"paged D=256 L={L}")
