@@ -172,8 +172,9 @@ int kvq_decode_attn_static(const kvq_rows* q, const kvq_qtensor* k, const kvq_qt
 /*
  * Attention for prefill chunks (any L): same contract as kvq_decode_attn, MFMA tiles with
  * K/V tiles dequantized into LDS. Replaces m5engine/attention.py:29-103 for L > 1.
- * Requirements: D == 128; group_size in {32, 64, 128}; bits in {4, 8}; Hq a multiple of Hkv; with
- *   group_size < 128, scale and bias rows 4-byte aligned (even strides; MLX's contiguous layout is).
+ * Requirements: D in {64, 128}; group_size in {32, 64, 128}, at most D; bits in {4, 8}; Hq a multiple
+ *   of Hkv; with two or more scale groups per row, scale and bias rows 4-byte aligned (even
+ *   strides; MLX's contiguous layout is).
  */
 int kvq_prefill_attn(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v,
                      const int32_t* seq_lens, const kvq_rows* out,

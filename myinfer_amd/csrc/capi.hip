@@ -356,7 +356,7 @@ int kvq_decode_attn_static(const kvq_rows* q, const kvq_qtensor* k, const kvq_qt
 }
 
 size_t kvq_prefill_workspace_size(int B, int Hq, int Hkv, int L, int D, int S, int window) {
-  if (B <= 0 || Hq <= 0 || Hkv <= 0 || L <= 0 || S <= 0 || D != 128 || window < 0 || Hq % Hkv) return 0;
+  if (B <= 0 || Hq <= 0 || Hkv <= 0 || L <= 0 || S <= 0 || (D != 64 && D != 128) || window < 0 || Hq % Hkv) return 0;
   return kvq::prefill_workspace_bytes(B, Hq, Hkv, L, D, S, window, 8);
 }
 
@@ -375,7 +375,7 @@ int kvq_prefill_attn(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor*
                      const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int bits, int group_size,
                      int dtype, float scale, int causal, int window, void* workspace, size_t workspace_bytes,
                      void* stream) {
-  if (D != 128) return fail(KVQ_ERR_UNSUPPORTED, "prefill supports head_dim 128, got %d", D);
+  if (D != 64 && D != 128) return fail(KVQ_ERR_UNSUPPORTED, "prefill supports head_dim 64 and 128, got %d", D);
   int rc = check_attn(q, k, v, out, B, Hq, Hkv, L, D, S, bits, group_size, dtype, scale, window,
                       kvq_prefill_workspace_size(B, Hq, Hkv, L, D, S, window), workspace, workspace_bytes);
   if (rc) return rc;
@@ -426,7 +426,7 @@ int kvq_paged_prefill_attn(const kvq_rows* q, const kvq_qtensor* k_pool, const k
                            const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int bits, int group_size,
                            int dtype, float scale, int causal, int window, void* workspace, size_t workspace_bytes,
                            void* stream) {
-  if (D != 128) return fail(KVQ_ERR_UNSUPPORTED, "prefill supports head_dim 128, got %d", D);
+  if (D != 64 && D != 128) return fail(KVQ_ERR_UNSUPPORTED, "prefill supports head_dim 64 and 128, got %d", D);
   int rc = check_paged_attn(q, k_pool, v_pool, num_pages, block_table, table_stride, out, B, Hq, Hkv, L, D, S, bits,
                             group_size, dtype, scale, window, kvq_prefill_workspace_size(B, Hq, Hkv, L, D, S, window),
                             workspace, workspace_bytes);
@@ -454,7 +454,7 @@ int kvq_decode_attn_dense(const kvq_rows* q, const kvq_rows* k, const kvq_rows* 
 int kvq_prefill_attn_dense(const kvq_rows* q, const kvq_rows* k, const kvq_rows* v, const int32_t* seq_lens,
                            const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int dtype, float scale,
                            int causal, int window, void* workspace, size_t workspace_bytes, void* stream) {
-  if (D != 128) return fail(KVQ_ERR_UNSUPPORTED, "prefill supports head_dim 128, got %d", D);
+  if (D != 128) return fail(KVQ_ERR_UNSUPPORTED, "unquantized prefill supports head_dim 128, got %d", D);
   int rc = check_attn_dense(q, k, v, out, B, Hq, Hkv, L, D, S, dtype, scale, window,
                             kvq_prefill_workspace_size(B, Hq, Hkv, L, D, S, window), workspace, workspace_bytes);
   if (rc) return rc;

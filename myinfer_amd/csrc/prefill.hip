@@ -7,7 +7,7 @@
 // with query l at position S_b - L + l, keys <= position when causal, keys > position - window
 // when a sliding window is set.
 //
-// Design (head_dim 128, 64-key tiles, a workgroup = 8 waves = 256 query rows, one per CU):
+// Design (head_dim D = 128 or 64, 64-key tiles, a workgroup = 8 waves = 256 query rows, one per CU):
 //  * A workgroup serves 256 consecutive rows of one (sequence, KV head) in position-major order
 //    (row = position * rep + local head), so all rep query heads of a position share each K/V
 //    tile and a causal boundary cuts only a few positions.
@@ -43,7 +43,9 @@ namespace kvq {
 constexpr int kPT = 64;       // keys per tile
 constexpr int kPRows = 256;   // query rows per workgroup (8 waves x 32 MFMA columns)
 constexpr int kPW = 8;        // waves per workgroup
-constexpr int kKS = 136;      // fp16 per K row in LDS: 128 + 8 (rows shift by 4 banks)
+// fp16 per K row in LDS: D + 8 (rows shift by 4 banks)
+template <int D>
+constexpr int kKS = D + 8;
 constexpr int kVS = 72;       // fp16 per V^T row in LDS: 64 + 8
 constexpr float kPSlack = 6.0f;
 constexpr int kPTargetWgs = 256;  // one workgroup per CU
@@ -52,16 +54,18 @@ constexpr int kXcds = 8;  // MI355X: 8 XCDs, each with its own L2
 
 // The raw tile ring. A slot holds one 64-key tile as loaded: [K codes][V codes][sK, bK, sV, bV],
 // code rows with their 16-byte chunks XOR-swizzled by row (chunk c of row r at position
-// c ^ (r % CPR)), each scale/bias array as 64 PC 4-byte cells: with NG = 128 / G >= 2 scale groups
+// c ^ (r % CPR)), each scale/bias array as 64 PC 4-byte cells: with NG = D / G >= 2 scale groups
 // per row, cell PC key + c holds groups 2c and 2c + 1 of the key (PC = NG / 2); with one group,
 // cell key holds it in its low half (PC = 1).
 // BITS == 16 is the unquantized cache: raw T rows, no scales or biases.
-template <int BITS, int G = 64>
+template <int BITS, int G = 64, int D = 128>
 struct RawCfg {
   static constexpr bool DENSE = BITS == 16;
   static_assert(G == 32 || G == 64 || G == 128, "group sizes 32, 64, 128");
-  static constexpr int NG = 128 / G;                // scale groups per key row
-  static constexpr int ROWB = 128 * BITS / 8;       // code bytes per key row
+  static_assert(D == 128 || (D == 64 && !DENSE), "head_dim 128, or 64 for quantized caches");
+  static_assert(G <= D, "a group lies in one row");
+  static constexpr int NG = D / G;                  // scale groups per key row
+  static constexpr int ROWB = D * BITS / 8;         // code bytes per key row
   static constexpr int CPR = ROWB / 16;             // 16-byte chunks per row
   static constexpr int RPI = 64 / CPR;              // rows per 1 KiB DMA instruction
   static constexpr int CI = kPT / RPI;              // DMA instructions per K (or V) code tile
@@ -69,12 +73,20 @@ struct RawCfg {
   static constexpr int PC = NG >= 2 ? NG / 2 : 1;  // 4-byte cells per key in a scale/bias array
   static constexpr int SBB = DENSE ? 0 : 256 * PC;  // bytes of one scale/bias array
   static constexpr int SLOT = 2 * KB + 4 * SBB;
-  static constexpr int CPW = 2 * CI / kPW;          // code DMA instructions per wave
+  // code DMA instructions per wave: with fewer than one per wave (4-bit, D = 64) waves 0 .. 2 CI - 1
+  // issue one each and the others none
+  static constexpr int CPW = 2 * CI >= kPW ? 2 * CI / kPW : 1;
+  static constexpr int CODE_WAVES = 2 * CI >= kPW ? kPW : 2 * CI;
+  // the waves that dequantize: V^T in waves [0, NSW), K in [NSW, 2 NSW) (256 threads each for
+  // D = 128, 128 for D = 64); the other waves only compute
+  static constexpr int NSW = D / 32;
   // 64-cell scale/bias DMA instructions per wave: 4 PC of them fill the four arrays, one per wave
   // (with PC = 1 two waves fill the same cells)
   static constexpr int SBW = DENSE ? 0 : 1;
-  static constexpr int IPT = CPW + SBW;             // DMA instructions per wave per tile
-  static_assert(CPW * kPW == 2 * CI, "code DMAs divide evenly over the waves");
+  static constexpr int IPT = CPW + SBW;             // DMA instructions per tile of a wave that loads codes
+  static constexpr int IPT_NOCODE = SBW;            // ... and of one that does not
+  static_assert(CPW * CODE_WAVES == 2 * CI, "code DMAs divide evenly over the waves that issue them");
+  static_assert(CODE_WAVES >= 2 * NSW, "the dequantizing waves load codes");
   static_assert(DENSE || 4 * PC <= kPW, "scale/bias DMAs fit one per wave");
   // byte offset of group g of key `key` inside a scale/bias array
   static __host__ __device__ constexpr int sb_off(int key, int g) { return 4 * (PC * key + g / 2) + 2 * (g & 1); }
@@ -174,22 +186,25 @@ __device__ __forceinline__ int opaque(int x) {
   return x;
 }
 
-// This wave's share of a raw tile: CPW 1 KiB code loads (K instructions first, then V) and one
-// 64-cell scale/bias load (array wave / 2, cells 64 part .. with part = (wave % 2) % PC; 4-byte
-// cells, or 2-byte values into the low halves when PC = 1 holds a single group).
-template <int BITS, int G = 64>
+// This wave's share of a raw tile: CPW 1 KiB code loads (K instructions first, then V; none for
+// waves from CODE_WAVES on) and one 64-cell scale/bias load (array wave / 2, cells 64 part .. with
+// part = (wave % 2) % PC; 4-byte cells, or 2-byte values into the low halves when PC = 1 holds a
+// single group).
+template <int BITS, int G = 64, int D = 128>
 struct RawShare {
-  using C = RawCfg<BITS, G>;
+  using C = RawCfg<BITS, G, D>;
   static constexpr int SBN = C::SBW > 0 ? C::SBW : 1;
   __amdgpu_buffer_rsrc_t code_r[C::CPW], sb_r[SBN];
   uint32_t code_vo[C::CPW], code_lds[C::CPW], sb_vo[SBN], sb_lds[SBN];
   int64_t code_ss[C::CPW], sb_ss[SBN];  // bytes per key row
+  bool code_on;                         // this wave issues code loads (wave-uniform)
 
   __device__ __forceinline__ void init(const PreParams& p, __amdgpu_buffer_rsrc_t kr, __amdgpu_buffer_rsrc_t vr,
                                        const __amdgpu_buffer_rsrc_t (&sr)[4], int wave, int lane) {
+    code_on = wave < C::CODE_WAVES;
 #pragma unroll
     for (int j = 0; j < C::CPW; ++j) {
-      const int q = wave * C::CPW + j;
+      const int q = code_on ? wave * C::CPW + j : 0;
       const bool is_k = q < C::CI;
       const int i = is_k ? q : q - C::CI;
       const int r = i * C::RPI + lane / C::CPR;
@@ -211,8 +226,10 @@ struct RawShare {
   }
   // raw tile of keys [k0, k0 + 64) into the slot at LDS address `slot`
   __device__ __forceinline__ void issue(uint32_t slot, int k0) const {
+    if (code_on) {
 #pragma unroll
-    for (int j = 0; j < C::CPW; ++j) dma_b128(code_r[j], slot + code_lds[j], code_vo[j], (uint32_t)(k0 * code_ss[j]));
+      for (int j = 0; j < C::CPW; ++j) dma_b128(code_r[j], slot + code_lds[j], code_vo[j], (uint32_t)(k0 * code_ss[j]));
+    }
 #pragma unroll
     for (int j = 0; j < C::SBW; ++j) dma_sb(sb_r[j], slot + sb_lds[j], sb_vo[j], (uint32_t)(k0 * sb_ss[j]));
   }
@@ -231,7 +248,7 @@ struct RawShare {
   __device__ __forceinline__ void init_paged(const PreParams& p, int kvh, int wave) {
 #pragma unroll
     for (int j = 0; j < C::CPW; ++j) {
-      const bool is_k = wave * C::CPW + j < C::CI;
+      const bool is_k = (code_on ? wave * C::CPW + j : 0) < C::CI;
       code_base[j] = is_k ? p.kc + (int64_t)kvh * p.kc_sh : p.vc + (int64_t)kvh * p.vc_sh;
       code_ps[j] = is_k ? p.kc_sb : p.vc_sb;
     }
@@ -245,10 +262,12 @@ struct RawShare {
   }
   // raw tile of page `pg` (its first nv rows valid) into the slot at LDS address `slot`
   __device__ __forceinline__ void issue_paged(uint32_t slot, int pg, int nv) const {
+    if (code_on) {
 #pragma unroll
-    for (int j = 0; j < C::CPW; ++j)
-      dma_b128(make_rsrc(code_base[j] + (int64_t)pg * code_ps[j], (uint32_t)(nv * code_ss[j])), slot + code_lds[j],
-               code_vo[j], 0u);
+      for (int j = 0; j < C::CPW; ++j)
+        dma_b128(make_rsrc(code_base[j] + (int64_t)pg * code_ps[j], (uint32_t)(nv * code_ss[j])), slot + code_lds[j],
+                 code_vo[j], 0u);
+    }
 #pragma unroll
     for (int j = 0; j < C::SBW; ++j)
       dma_sb(make_rsrc(sb_base[j] + (int64_t)pg * sb_ps[j], (uint32_t)(nv * sb_ss[j])), slot + sb_lds[j], sb_vo[j],
@@ -286,18 +305,19 @@ __device__ __forceinline__ void dequant8(const uint32_t* w, h2 s2, h2 b2, uint32
   }
 }
 
-// Dequantize the raw tile at `raw` into the fp16 operands. Threads 0-255 build V^T: thread t takes
-// the 8 keys of slot chunk t % 8 at dims [4 (t / 8), +4) and writes 4 V^T rows of 8 slots. Threads
-// 256-511 build K: thread t takes dims [32 q, +32) of key t % 64, q = (t - 256) / 64.
+// Dequantize the raw tile at `raw` into the fp16 operands. Threads 0 .. 64 NSW - 1 (NSW = D / 32
+// waves) build V^T: thread t takes the 8 keys of slot chunk t % 8 at dims [4 (t / 8), +4) and writes
+// 4 V^T rows of 8 slots. The next 64 NSW threads build K: thread 64 NSW + u takes dims [32 q, +32)
+// of key u % 64, q = u / 64. Threads beyond take no part.
 //
 // V^T, first part: the wave's lanes convert the scale and bias of the wave's group (dims
 // [32 w, 32 w + 32) lie in one group) for the 64 keys (lane = key) into a per-wave table of fp16
 // (scale, bias) pairs, which stage_v then reads for its 8 keys. Only this wave touches its table,
 // and the LDS operations of one wave complete in program order, so a wave barrier (which keeps
 // the compiler from moving the lanes' accesses across it) is all the ordering the reads need.
-template <typename T, int BITS, int G>
+template <typename T, int BITS, int G, int D>
 __device__ __forceinline__ void stage_v_table(const uint8_t* raw, uint32_t* sbt, int tid, bool& range_bad) {
-  using C = RawCfg<BITS, G>;
+  using C = RawCfg<BITS, G, D>;
   const int key = tid & 63, g = (4 * (tid >> 3)) / G;
   const uint8_t* sbase = raw + 2 * C::KB + C::sb_off(key, g);
   const h2 sbp = {to_half(*(const uint16_t*)(sbase + 2 * C::SBB), T{}), to_half(*(const uint16_t*)(sbase + 3 * C::SBB), T{})};
@@ -307,22 +327,22 @@ __device__ __forceinline__ void stage_v_table(const uint8_t* raw, uint32_t* sbt,
   if constexpr (T::id == KVQ_DTYPE_BF16) range_bad |= __builtin_isinf((float)sbp[1]);
 }
 
-// V^T, second part (threads 0-255, after stage_v_table of the same tile), in two halves: half H
-// builds dims 4 d4 + 2H and + 2H + 1 (V^T rows 2H, 2H + 1 of the thread's four).
-template <int BITS, int G, int H>
+// V^T, second part (after stage_v_table of the same tile), in two halves: half H builds dims
+// 4 d4 + 2H and + 2H + 1 (V^T rows 2H, 2H + 1 of the thread's four).
+template <int BITS, int G, int D, int H>
 __device__ __forceinline__ void stage_v(const uint8_t* raw, _Float16* vlds, const uint32_t* sbt, int tid) {
-  using C = RawCfg<BITS, G>;
+  using C = RawCfg<BITS, G, D>;
   const int c8 = tid & 7, d4 = tid >> 3;
-  // key i of the chunk is kb + v_key_offset(i), and its swizzle key % CPR is (kb % CPR) | (i & 3)
-  // (kb has its low two bits clear, the offsets are i & 3 modulo 8): four code addresses per
-  // lane; everything else is an immediate offset
+  // key i of the chunk is kb + v_key_offset(i), and its swizzle key % CPR is ((kb % CPR) | (i & 3))
+  // % CPR (kb has its low two bits clear, the offsets are i & 3 modulo 8, CPR is a power of two):
+  // four code addresses per lane; everything else is an immediate offset
   const int kb = v_base_key(c8);
   const uint8_t* vr = raw + C::KB + kb * C::ROWB;
   uint32_t x[8];  // key i: the dim pair of this half
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int ko = v_key_offset(i);
-    const int sw = (kb % C::CPR) | (i & 3);
+    const int sw = ((kb % C::CPR) | (i & 3)) % C::CPR;
     uint32_t bytes;  // codes of dims 4 d4 .. 4 d4 + 3 as 4 bytes
     if constexpr (BITS == 8) {
       bytes = *(const uint32_t*)(vr + ko * C::ROWB + 16 * ((d4 >> 2) ^ sw) + 4 * (d4 & 3));
@@ -344,11 +364,12 @@ __device__ __forceinline__ void stage_v(const uint8_t* raw, _Float16* vlds, cons
   }
 }
 
-// K (threads 256-511), in two halves: half H builds dims [32 q + 16 H, +16) of key t % 64.
-template <typename T, int BITS, int G, int H>
+// K, in two halves: half H builds dims [32 q + 16 H, +16) of key u % 64.
+template <typename T, int BITS, int G, int D, int H>
 __device__ __forceinline__ void stage_k(const uint8_t* raw, _Float16* klds, int tid, bool& range_bad) {
-  using C = RawCfg<BITS, G>;
-  const int key = tid & 63, q = (tid - 256) >> 6;
+  using C = RawCfg<BITS, G, D>;
+  const int u = tid - 64 * C::NSW;
+  const int key = u & 63, q = u >> 6;
   const uint8_t* kr = raw + key * C::ROWB;
   uint32_t w[4];  // the half's 16 codes
   if constexpr (BITS == 8) {
@@ -367,22 +388,23 @@ __device__ __forceinline__ void stage_k(const uint8_t* raw, _Float16* klds, int 
   for (int c = 0; c < 2; ++c) {
     uint32_t x[4];
     dequant8<BITS>(&w[(BITS / 4) * c], h2{sh, sh}, h2{bh, bh}, x);
-    *(u4*)&klds[key * kKS + 32 * q + 16 * H + 8 * c] = u4{x[0], x[1], x[2], x[3]};
+    *(u4*)&klds[key * kKS<D> + 32 * q + 16 * H + 8 * c] = u4{x[0], x[1], x[2], x[3]};
   }
 }
 
-// The whole tile, all 512 threads.
-template <typename T, int BITS, int G>
+// The whole tile, all threads.
+template <typename T, int BITS, int G, int D>
 __device__ __forceinline__ void stage_from_raw(const uint8_t* raw, _Float16* klds, _Float16* vlds, uint32_t* sbt,
                                                int tid, bool& range_bad) {
-  if (tid < 256) {
-    stage_v_table<T, BITS, G>(raw, sbt, tid, range_bad);
+  constexpr int NST = 64 * RawCfg<BITS, G, D>::NSW;  // threads per operand
+  if (tid < NST) {
+    stage_v_table<T, BITS, G, D>(raw, sbt, tid, range_bad);
     __builtin_amdgcn_wave_barrier();
-    stage_v<BITS, G, 0>(raw, vlds, sbt, tid);
-    stage_v<BITS, G, 1>(raw, vlds, sbt, tid);
-  } else {
-    stage_k<T, BITS, G, 0>(raw, klds, tid, range_bad);
-    stage_k<T, BITS, G, 1>(raw, klds, tid, range_bad);
+    stage_v<BITS, G, D, 0>(raw, vlds, sbt, tid);
+    stage_v<BITS, G, D, 1>(raw, vlds, sbt, tid);
+  } else if (tid < 2 * NST) {
+    stage_k<T, BITS, G, D, 0>(raw, klds, tid, range_bad);
+    stage_k<T, BITS, G, D, 1>(raw, klds, tid, range_bad);
   }
 }
 
@@ -409,12 +431,16 @@ __device__ __forceinline__ void stage_v_raw(const uint8_t* raw, _Float16* vlds, 
   *(u4*)&vlds[(2 * d2 + 1) * kVS + 8 * c8] = hi;
 }
 
-template <typename T, int BITS, bool PAGED = false, int G = 64>
+template <typename T, int BITS, bool PAGED = false, int G = 64, int D = 128>
 __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) {
-  using RC = RawCfg<BITS, G>;
+  using RC = RawCfg<BITS, G, D>;
   constexpr bool DENSE = RC::DENSE;  // unquantized cache: K operands are read from the raw ring
-  __shared__ __align__(16) _Float16 k_lds[DENSE ? 1 : 3][DENSE ? 8 : kPT * kKS];
-  __shared__ __align__(16) _Float16 v_lds[DENSE ? 2 : 3][128 * kVS];
+  constexpr int KS = kKS<D>;
+  constexpr int KSTEPS = D / 16;   // k-steps of S^T = K Q^T over the head dimension
+  constexpr int NDB = D / 32;      // 32-dim blocks of O^T
+  constexpr int QW = D / 16;       // 16-byte words of a lane's packed output row
+  __shared__ __align__(16) _Float16 k_lds[DENSE ? 1 : 3][DENSE ? 8 : kPT * KS];
+  __shared__ __align__(16) _Float16 v_lds[DENSE ? 2 : 3][D * kVS];
   __shared__ __align__(16) uint8_t raw[kRawSlots][RC::SLOT];
   __shared__ uint32_t sb_tab[DENSE ? 1 : kPW / 2][64];  // per V^T-building wave: (scale, bias) pairs
   // after the tile loop the table's storage holds per-wave flags (words 0-7) and the split arrival
@@ -471,16 +497,16 @@ __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) 
 
   // ---- the raw query slice (loaded before the tile stream; row and head are clamped, so every
   // lane's load is in bounds)
-  u4 qraw[8];
+  u4 qraw[KSTEPS];
   {
     const uint16_t* qrow = p.q + (int64_t)b * p.q_sb + (int64_t)head * p.q_sh + (int64_t)lq * p.q_sl + 8 * hh;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) qraw[j] = *(const u4*)(qrow + 16 * j);
+    for (int j = 0; j < KSTEPS; ++j) qraw[j] = *(const u4*)(qrow + 16 * j);
   }
 
   // ---- raw tile stream: buffer resources over the S_b valid rows of this (sequence, KV head)
   // (the host checks S * row stride fits 32 bits); tiles past the last re-read the last one
-  RawShare<BITS, G> share;
+  RawShare<BITS, G, D> share;
   {
     const __amdgpu_buffer_rsrc_t kr =
         make_rsrc(p.kc + (int64_t)b * p.kc_sb + (int64_t)kvh * p.kc_sh, (uint32_t)((int64_t)S_b * p.kc_ss));
@@ -532,17 +558,17 @@ __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) 
   // bits), and the scores are multiplied by inv2 = scale * log2(e) * 2^-qe in fp32. Folding the
   // softmax scale into the fp16 operand instead would round every query element. Unquantized
   // cache: the raw query (exact), the scores multiplied by scale*log2(e) in fp32.
-  u4 qop[8];
+  u4 qop[KSTEPS];
   float inv2;
   if constexpr (DENSE) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) qop[j] = row_ok ? qraw[j] : u4{0, 0, 0, 0};
+    for (int j = 0; j < KSTEPS; ++j) qop[j] = row_ok ? qraw[j] : u4{0, 0, 0, 0};
     inv2 = 1.0f;
   } else {
-    float qv[8][8];
+    float qv[KSTEPS][8];
     float qmax = 0.0f;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
+    for (int j = 0; j < KSTEPS; ++j) {
       const u4 raw_q = row_ok ? qraw[j] : u4{0, 0, 0, 0};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -558,7 +584,7 @@ __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) 
     const float qmul = ldexpf(1.0f, qe);
     inv2 = ldexpf(p.scale_log2, -qe);
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
+    for (int j = 0; j < KSTEPS; ++j)
 #pragma unroll
       for (int i = 0; i < 4; ++i) qop[j][i] = pack_f16x2(qv[j][2 * i] * qmul, qv[j][2 * i + 1] * qmul);
   }
@@ -566,86 +592,86 @@ __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) 
   using OT = typename std::conditional<DENSE && T::id == KVQ_DTYPE_BF16, BF16, F16>::type;
 
   float m_run = -INFINITY, l_run = 0.0f;
-  f16v oacc[4];
+  f16v oacc[NDB];
 #pragma unroll
-  for (int db = 0; db < 4; ++db) oacc[db] = f16v{};
-
-  // ---- the pieces of a tile step
-  // this lane's query sees keys k0 + 32kb + 8(i/4) + 4hh + i%4. Only tiles on a causal diagonal or
-  // window edge need a mask (a branch the whole workgroup takes or skips); there, each element's
-  // offset c = 32kb + 8(i/4) + i%4 is a constant compared with the lane's bounds
-  auto mask_tile = [&](f16v (&acc)[2], int k0) {
-    const bool need_mask = !(k0 >= lo_all && k0 + kPT <= hi_all);
-    if (__builtin_expect(need_mask, 0)) {
-      const int lo = lo_r - k0 - 4 * hh, hi = hi_r - k0 - 4 * hh;
-      if (lo <= 0) {  // no key of the tile is below the lane's window
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int i = 0; i < 16; ++i)
-            if (32 * kb + 8 * (i >> 2) + (i & 3) >= hi) acc[kb][i] = -INFINITY;
-      } else {
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const int c = 32 * kb + 8 * (i >> 2) + (i & 3);
-            if (c < lo || c >= hi) acc[kb][i] = -INFINITY;
-          }
-      }
-    }
-  };
-  // the tile's row maximum in log2 units; the running maximum moves (and the accumulators are
-  // rescaled) only when it exceeds the running one by more than the slack
-  auto update_max = [&](const f16v (&acc)[2]) {
-    float tm = -INFINITY;
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) tm = fmaxf(tm, acc[kb][i]);
-    tm = max_xor32(tm) * inv2;
-    if (__builtin_amdgcn_ballot_w64(tm > m_run + kPSlack) != 0) {
-      const float m_new = tm > m_run + kPSlack ? fmaxf(m_run, tm) : m_run;
-      const float corr = m_new == m_run ? 1.0f : exp2_fast(m_run - m_new);
-      l_run *= corr;
-#pragma unroll
-      for (int db = 0; db < 4; ++db)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) oacc[db][i] *= corr;
-      m_run = m_new;
-    }
-  };
-  // p = 2^(acc * inv2 - m): rounded to the operand type it is the B operand of O^T = V^T P^T; the
-  // row sum is kept in fp32 (of the rounded values, so the output stays a convex combination of V
-  // rows), in two chains
-  auto probs = [&](const f16v (&acc)[2], u4 (&pop)[4]) {
-    const float nm = m_run == -INFINITY ? 0.0f : -m_run;
-    float lsum[2] = {0.0f, 0.0f};
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float p0 = exp2_fast(fmaf(acc[j >> 1][8 * (j & 1) + 2 * e], inv2, nm));
-        const float p1 = exp2_fast(fmaf(acc[j >> 1][8 * (j & 1) + 2 * e + 1], inv2, nm));
-        pop[j][e] = pack2(p0, p1, OT{});
-        lsum[e & 1] = add_pair(pop[j][e], lsum[e & 1], OT{});
-      }
-    }
-    l_run += lsum[0] + lsum[1];
-  };
-  // O^T += V^T P^T: the 16 V^T operands stream through a 4-deep register ring; the 4 dim blocks
-  // alternate. vl = this lane's start in a V^T buffer.
-  auto pv = [&](const _Float16* vl, const u4 (&pop)[4]) {
-    auto vop = [&](int i) { return *(const u4*)(vl + (i & 3) * 32 * kVS + 16 * (i >> 2)); };
-    u4 ring[4] = {vop(0), vop(1), vop(2), vop(3)};
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      oacc[i & 3] = mfma_32x32x16(ring[i & 3], pop[i >> 2], oacc[i & 3], OT{});
-      if (i + 4 < 16) ring[i & 3] = vop(i + 4);
-    }
-  };
+  for (int db = 0; db < NDB; ++db) oacc[db] = f16v{};
 
   if constexpr (DENSE) {
+    // ---- the pieces of a tile step (head_dim 128)
+    // this lane's query sees keys k0 + 32kb + 8(i/4) + 4hh + i%4. Only tiles on a causal diagonal or
+    // window edge need a mask (a branch the whole workgroup takes or skips); there, each element's
+    // offset c = 32kb + 8(i/4) + i%4 is a constant compared with the lane's bounds
+    auto mask_tile = [&](f16v (&acc)[2], int k0) {
+      const bool need_mask = !(k0 >= lo_all && k0 + kPT <= hi_all);
+      if (__builtin_expect(need_mask, 0)) {
+        const int lo = lo_r - k0 - 4 * hh, hi = hi_r - k0 - 4 * hh;
+        if (lo <= 0) {  // no key of the tile is below the lane's window
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int i = 0; i < 16; ++i)
+              if (32 * kb + 8 * (i >> 2) + (i & 3) >= hi) acc[kb][i] = -INFINITY;
+        } else {
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+              const int c = 32 * kb + 8 * (i >> 2) + (i & 3);
+              if (c < lo || c >= hi) acc[kb][i] = -INFINITY;
+            }
+        }
+      }
+    };
+    // the tile's row maximum in log2 units; the running maximum moves (and the accumulators are
+    // rescaled) only when it exceeds the running one by more than the slack
+    auto update_max = [&](const f16v (&acc)[2]) {
+      float tm = -INFINITY;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) tm = fmaxf(tm, acc[kb][i]);
+      tm = max_xor32(tm) * inv2;
+      if (__builtin_amdgcn_ballot_w64(tm > m_run + kPSlack) != 0) {
+        const float m_new = tm > m_run + kPSlack ? fmaxf(m_run, tm) : m_run;
+        const float corr = m_new == m_run ? 1.0f : exp2_fast(m_run - m_new);
+        l_run *= corr;
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) oacc[db][i] *= corr;
+        m_run = m_new;
+      }
+    };
+    // p = 2^(acc * inv2 - m): rounded to the operand type it is the B operand of O^T = V^T P^T; the
+    // row sum is kept in fp32 (of the rounded values, so the output stays a convex combination of V
+    // rows), in two chains
+    auto probs = [&](const f16v (&acc)[2], u4 (&pop)[4]) {
+      const float nm = m_run == -INFINITY ? 0.0f : -m_run;
+      float lsum[2] = {0.0f, 0.0f};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float p0 = exp2_fast(fmaf(acc[j >> 1][8 * (j & 1) + 2 * e], inv2, nm));
+          const float p1 = exp2_fast(fmaf(acc[j >> 1][8 * (j & 1) + 2 * e + 1], inv2, nm));
+          pop[j][e] = pack2(p0, p1, OT{});
+          lsum[e & 1] = add_pair(pop[j][e], lsum[e & 1], OT{});
+        }
+      }
+      l_run += lsum[0] + lsum[1];
+    };
+    // O^T += V^T P^T: the 16 V^T operands stream through a 4-deep register ring; the 4 dim blocks
+    // alternate. vl = this lane's start in a V^T buffer.
+    auto pv = [&](const _Float16* vl, const u4 (&pop)[4]) {
+      auto vop = [&](int i) { return *(const u4*)(vl + (i & 3) * 32 * kVS + 16 * (i >> 2)); };
+      u4 ring[4] = {vop(0), vop(1), vop(2), vop(3)};
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        oacc[i & 3] = mfma_32x32x16(ring[i & 3], pop[i >> 2], oacc[i & 3], OT{});
+        if (i + 4 < 16) ring[i & 3] = vop(i + 4);
+      }
+    };
+
     // ---- unquantized cache: K operands are read from the raw ring while tile t is computed, so
     // tile t + 2 is issued into the slot of tile t - 1 and lands within the step; V^T is built from
     // the raw rows into a double buffer, half by waves 4-7 before their MFMAs and half by waves 0-3
@@ -695,8 +721,8 @@ __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) 
     // half h takes the scores of block h of the tile, already computed, and
     //  * runs their softmax while the MFMAs of the next block's scores execute (block 1 of tile t,
     //    then block 0 of tile t + 1), then
-    //  * accumulates O += V P for the block while the waves dequantize half of tile t + 2 (waves
-    //    0-3 its V^T, waves 4-7 its K),
+    //  * accumulates O += V P for the block while the dequantizing waves build half of tile t + 2
+    //    (the V^T waves its V^T, the K waves its K),
     // so every wave always has MFMA work beside its VALU work, and two 16-register score blocks are
     // live rather than two tiles.
     //  * fp16 operands: tile j in k_lds[j % 3] and v_lds[j % 3] (step t reads K of tiles t and
@@ -704,12 +730,12 @@ __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) 
     //  * raw ring: tile j in slot j % 3; step t reads tile t + 2 and issues tile t + 4 into the slot
     //    of tile t + 1 (dequantized in step t - 1), so every tile is loaded two steps ahead;
     //  * one barrier per step orders all of it.
-    constexpr int KBUF = kPT * kKS, VBUF = 128 * kVS;
-    const _Float16* kl_lane = &k_lds[0][qc * kKS + 8 * hh];  // this lane's K operands, V^T operands
+    constexpr int KBUF = kPT * KS, VBUF = D * kVS;
+    const _Float16* kl_lane = &k_lds[0][qc * KS + 8 * hh];  // this lane's K operands, V^T operands
     const _Float16* vl_lane = &v_lds[0][qc * kVS + 8 * hh];
-    // S^T = K Q^T for the 32-key block whose K rows start at kl (this lane's offset included): 8
-    // MFMAs over the head dimension, the K operands streamed through a 4-deep register ring; MFMAs
-    // [J0, J1) of the 8
+    // S^T = K Q^T for the 32-key block whose K rows start at kl (this lane's offset included):
+    // KSTEPS MFMAs over the head dimension, the K operands streamed through a 4-deep register ring;
+    // MFMAs [J0, J1) of them
     auto qk_ring = [&](u4 (&ring)[4], const _Float16* kl) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) ring[j] = *(const u4*)(kl + 16 * j);
@@ -718,12 +744,12 @@ __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) 
 #pragma unroll
       for (int j = decltype(j0)::value; j < decltype(j1)::value; ++j) {
         acc = mfma_32x32x16(ring[j & 3], qop[j], j == 0 ? f16v{} : acc, OT{});
-        if (j + 4 < 8) ring[j & 3] = *(const u4*)(kl + 16 * (j + 4));
+        if (j + 4 < KSTEPS) ring[j & 3] = *(const u4*)(kl + 16 * (j + 4));
       }
     };
     using J0 = std::integral_constant<int, 0>;
     using J2 = std::integral_constant<int, 2>;
-    using J8 = std::integral_constant<int, 8>;
+    using JE = std::integral_constant<int, KSTEPS>;
     // the block's keys [k, k + 32): mask (only on a causal diagonal or window edge), row maximum
     auto mask_blk = [&](f16v& acc, int k) {
       if (__builtin_expect(!(k >= lo_all && k + 32 <= hi_all), 0)) {
@@ -747,7 +773,7 @@ __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) 
         const float corr = m_new == m_run ? 1.0f : exp2_fast(m_run - m_new);
         l_run *= corr;
 #pragma unroll
-        for (int db = 0; db < 4; ++db)
+        for (int db = 0; db < NDB; ++db)
 #pragma unroll
           for (int i = 0; i < 16; ++i) oacc[db][i] *= corr;
         m_run = m_new;
@@ -768,34 +794,38 @@ __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) 
         }
       l_run += lsum[0] + lsum[1];
     };
-    // O^T += V^T P^T over block kb's two k-steps (V^T slots 32 kb .. 32 kb + 31): 8 MFMAs, the 4
-    // dim blocks alternating, V^T operands through a 4-deep ring
+    // O^T += V^T P^T over block kb's two k-steps (V^T slots 32 kb .. 32 kb + 31): 2 NDB MFMAs, the
+    // NDB dim blocks alternating, V^T operands through a 4-deep ring
     auto pv_blk = [&](const _Float16* vl, const u4 (&pop)[2], auto kb) {
       constexpr int KB = decltype(kb)::value;
-      auto vop = [&](int i) { return *(const u4*)(vl + (i & 3) * 32 * kVS + 16 * (2 * KB + (i >> 2))); };
+      auto vop = [&](int i) { return *(const u4*)(vl + (i % NDB) * 32 * kVS + 16 * (2 * KB + i / NDB)); };
       u4 ring[4] = {vop(0), vop(1), vop(2), vop(3)};
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        oacc[i & 3] = mfma_32x32x16(ring[i & 3], pop[i >> 2], oacc[i & 3], OT{});
-        if (i + 4 < 8) ring[i & 3] = vop(i + 4);
+      for (int i = 0; i < 2 * NDB; ++i) {
+        oacc[i % NDB] = mfma_32x32x16(ring[i & 3], pop[i / NDB], oacc[i % NDB], OT{});
+        if (i + 4 < 2 * NDB) ring[i & 3] = vop(i + 4);
       }
     };
     using B0 = std::integral_constant<int, 0>;
     using B1 = std::integral_constant<int, 1>;
 
+    // The wave's role: 0 builds V^T (waves [0, NSW)), 1 builds K (waves [NSW, 2 NSW)), 2 only
+    // computes (head_dim 64: waves from 2 NSW on). The loop is compiled once per role, so each copy
+    // keeps only its own staging addresses live, and waits for its own number of loads per tile.
+    static_assert(RC::CODE_WAVES == kPW || RC::CODE_WAVES == 2 * RC::NSW, "computing-only waves all load codes or none");
     f16v sX, sY;  // the scores of block 0 (entering a step: tile t's) and block 1 of a tile
-    // VW: this wave builds V^T (waves 0-3) rather than K (waves 4-7); the loop is compiled once per
-    // role, so each copy keeps only its own staging addresses live
-    auto step = [&](auto vw, auto qkn, auto stg, int t) {
-      constexpr bool VW = decltype(vw)::value, QKN = decltype(qkn)::value, STG = decltype(stg)::value;
+    auto step = [&](auto role, auto qkn, auto stg, int t) {
+      constexpr int ROLE = decltype(role)::value;
+      constexpr bool QKN = decltype(qkn)::value, STG = decltype(stg)::value;
+      constexpr int IPT = (ROLE < 2 || RC::CODE_WAVES == kPW) ? RC::IPT : RC::IPT_NOCODE;
       issue_raw(t + 4);
       // the step's buffers, as element (byte, for the raw ring) offsets from each array's start
       const int k_t = opaque((t % 3) * KBUF), k_t1 = opaque(((t + 1) % 3) * KBUF);
       const int k_w = opaque(((t + 2) % 3) * KBUF);
       const int v_t = opaque((t % 3) * VBUF), v_w = opaque(((t + 2) % 3) * VBUF);
       const uint8_t* raw2 = &raw[0][0] + opaque(((t + 2) % kRawSlots) * RC::SLOT);
-      if constexpr (STG && VW) {
-        stage_v_table<T, BITS, G>(raw2, sb_tab[wave & 3], tid, range_bad);
+      if constexpr (STG && ROLE == 0) {
+        stage_v_table<T, BITS, G, D>(raw2, sb_tab[wave & 3], tid, range_bad);
         __builtin_amdgcn_wave_barrier();
       }
       const int k0 = k_begin + kPT * t;
@@ -804,18 +834,18 @@ __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) 
       u4 pop[2];
       // half 0: softmax of block 0 beside S(block 1) = K(t) rows 32-63 Q^T
       {
-        const _Float16* kl = kl_lane + k_t + 32 * kKS;
+        const _Float16* kl = kl_lane + k_t + 32 * KS;
         mask_blk(sX, k0);
         qk_ring(ring, kl);
         qk_run(J0{}, J2{}, sY, ring, kl);
         const float tm = max_blk(sX);
         rescale(tm);
-        qk_run(J2{}, J8{}, sY, ring, kl);
+        qk_run(J2{}, JE{}, sY, ring, kl);
         probs_blk(sX, pop);
       }
       pv_blk(vl, pop, B0{});
-      if constexpr (STG && VW) stage_v<BITS, G, 0>(raw2, &v_lds[0][0] + v_w, sb_tab[wave & 3], tid);
-      if constexpr (STG && !VW) stage_k<T, BITS, G, 0>(raw2, &k_lds[0][0] + k_w, tid, range_bad);
+      if constexpr (STG && ROLE == 0) stage_v<BITS, G, D, 0>(raw2, &v_lds[0][0] + v_w, sb_tab[wave & 3], tid);
+      if constexpr (STG && ROLE == 1) stage_k<T, BITS, G, D, 0>(raw2, &k_lds[0][0] + k_w, tid, range_bad);
       // half 1: softmax of block 1 beside S(block 0 of tile t + 1) = K(t + 1) rows 0-31 Q^T
       {
         const _Float16* kl = kl_lane + k_t1;
@@ -826,44 +856,52 @@ __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) 
         }
         const float tm = max_blk(sY);
         rescale(tm);
-        if constexpr (QKN) qk_run(J2{}, J8{}, sX, ring, kl);
+        if constexpr (QKN) qk_run(J2{}, JE{}, sX, ring, kl);
         probs_blk(sY, pop);
       }
       pv_blk(vl, pop, B1{});
-      if constexpr (STG && VW) stage_v<BITS, G, 1>(raw2, &v_lds[0][0] + v_w, sb_tab[wave & 3], tid);
-      if constexpr (STG && !VW) stage_k<T, BITS, G, 1>(raw2, &k_lds[0][0] + k_w, tid, range_bad);
-      wait_vm<RC::IPT>();  // tile t + 3 has landed (tile t + 4 may be in flight)
+      if constexpr (STG && ROLE == 0) stage_v<BITS, G, D, 1>(raw2, &v_lds[0][0] + v_w, sb_tab[wave & 3], tid);
+      if constexpr (STG && ROLE == 1) stage_k<T, BITS, G, D, 1>(raw2, &k_lds[0][0] + k_w, tid, range_bad);
+      wait_vm<IPT>();  // tile t + 3 has landed (tile t + 4 may be in flight)
       __syncthreads();
     };
     using Y = std::true_type;
     using N = std::false_type;
 
-    // prologue: tiles 0 and 1 dequantized, S(tile 0, block 0) computed, tile 2 landed, tile 3 in
-    // flight
-    wait_vm<2 * RC::IPT>();
-    __syncthreads();
-    stage_from_raw<T, BITS, G>(raw[0], k_lds[0], v_lds[0], sb_tab[wave & 3], tid, range_bad);
-    wait_vm<RC::IPT>();
-    __syncthreads();
-    issue_raw(3);  // into the slot of tile 0
-    stage_from_raw<T, BITS, G>(raw[1], k_lds[1], v_lds[1], sb_tab[wave & 3], tid, range_bad);
-    {
-      u4 ring[4];
-      qk_ring(ring, kl_lane);
-      qk_run(J0{}, J8{}, sX, ring, kl_lane);
-    }
-    wait_vm<RC::IPT>();
-    __syncthreads();
-    auto run = [&](auto vw) {
+    auto run = [&](auto role) {
+      constexpr int ROLE = decltype(role)::value;
+      constexpr int IPT = (ROLE < 2 || RC::CODE_WAVES == kPW) ? RC::IPT : RC::IPT_NOCODE;
+      // prologue: tiles 0 and 1 dequantized, S(tile 0, block 0) computed, tile 2 landed, tile 3 in
+      // flight
+      wait_vm<2 * IPT>();
+      __syncthreads();
+      stage_from_raw<T, BITS, G, D>(raw[0], k_lds[0], v_lds[0], sb_tab[wave & 3], tid, range_bad);
+      wait_vm<IPT>();
+      __syncthreads();
+      issue_raw(3);  // into the slot of tile 0
+      stage_from_raw<T, BITS, G, D>(raw[1], k_lds[1], v_lds[1], sb_tab[wave & 3], tid, range_bad);
+      {
+        u4 ring[4];
+        qk_ring(ring, kl_lane);
+        qk_run(J0{}, JE{}, sX, ring, kl_lane);
+      }
+      wait_vm<IPT>();
+      __syncthreads();
       int t = 0;
-      for (; t + 2 < ntile; ++t) step(vw, Y{}, Y{}, t);
-      if (t + 1 < ntile) step(vw, Y{}, N{}, t++);
-      step(vw, N{}, N{}, t);
+      for (; t + 2 < ntile; ++t) step(role, Y{}, Y{}, t);
+      if (t + 1 < ntile) step(role, Y{}, N{}, t++);
+      step(role, N{}, N{}, t);
     };
-    if (wave < kPW / 2) {
-      run(Y{});
+    if (wave < RC::NSW) {
+      run(std::integral_constant<int, 0>{});
+    } else if constexpr (2 * RC::NSW == kPW) {
+      run(std::integral_constant<int, 1>{});
     } else {
-      run(N{});
+      if (wave < 2 * RC::NSW) {
+        run(std::integral_constant<int, 1>{});
+      } else {
+        run(std::integral_constant<int, 2>{});
+      }
     }
   }
   wait_vm<0>();  // no load into this workgroup's LDS outlives it
@@ -879,7 +917,7 @@ __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) 
     for (int w = 0; w < kPW; ++w) any_bad |= s_flags[w];
     if (any_bad) {
 #pragma unroll
-      for (int db = 0; db < 4; ++db)
+      for (int db = 0; db < NDB; ++db)
 #pragma unroll
         for (int i = 0; i < 16; ++i) oacc[db][i] = __builtin_nanf("");
     }
@@ -896,23 +934,23 @@ __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) 
     //    term is formed from the same values whichever split merges: the result is
     //    bit-reproducible from call to call.
     //  * The packed row keeps the register image: lane `lane` of wave `wave` of split s holds words
-    //    u (0..7) of 16 bytes at byte ((s * kPW + wave) * 8 + u) * 1024 + 16 lane of the unit's o
+    //    u (0 .. QW - 1) of 16 bytes at byte ((s * kPW + wave) * QW + u) * 1024 + 16 lane of the unit's o
     //    block; word u packs value groups 2u and 2u + 1 (group 4 db + c = oacc[db][4c .. 4c+3]).
     //    Record of row r at byte 16 (s * kPRows + r) of the unit's record block.
-    const __amdgpu_buffer_rsrc_t ro = make_rsrc((const uint8_t*)p.part_o + (int64_t)unit * p.nsplit * (kPRows * 256),
-                                                (uint32_t)p.nsplit * (kPRows * 256));
+    const __amdgpu_buffer_rsrc_t ro = make_rsrc((const uint8_t*)p.part_o + (int64_t)unit * p.nsplit * (kPRows * 2 * D),
+                                                (uint32_t)p.nsplit * (kPRows * 2 * D));
     const __amdgpu_buffer_rsrc_t rm = make_rsrc(p.part_ml + (int64_t)unit * p.nsplit * (kPRows * 4),
                                                 (uint32_t)p.nsplit * (kPRows * 16));
-    const uint32_t lo = (uint32_t)wave * (8 * 1024) + 16 * lane;
-    const uint32_t split_o = kPW * 8 * 1024;
+    const uint32_t lo = (uint32_t)wave * (QW * 1024) + 16 * lane;
+    const uint32_t split_o = kPW * QW * 1024;
     const uint32_t row_ml = 16 * (wave * 32 + qc);
-    u4 own[8];
+    u4 own[QW];
     float own_sc;
     {
       const float inv_l = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
       float mx = 0.0f;
 #pragma unroll
-      for (int db = 0; db < 4; ++db)
+      for (int db = 0; db < NDB; ++db)
 #pragma unroll
         for (int i = 0; i < 16; ++i) mx = fmaxf(mx, fabsf(oacc[db][i]));
       mx = max_xor32(mx) * inv_l;
@@ -924,7 +962,7 @@ __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) 
       own_sc = ldexpf(1.0f, e);
       const float f = ldexpf(inv_l, -e);
 #pragma unroll
-      for (int u = 0; u < 8; ++u)
+      for (int u = 0; u < QW; ++u)
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
           const int g = 2 * u + h, db = g >> 2, c = g & 3;
@@ -933,7 +971,7 @@ __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) 
         }
     }
 #pragma unroll
-    for (int u = 0; u < 8; ++u) store_agent_b128(ro, lo + u * 1024 + split * split_o, __builtin_bit_cast(f4, own[u]));
+    for (int u = 0; u < QW; ++u) store_agent_b128(ro, lo + u * 1024 + split * split_o, __builtin_bit_cast(f4, own[u]));
     if (hh == 0) store_agent_b128(rm, row_ml + split * (kPRows * 16), f4{m_run, l_tot, own_sc, 0.0f});
     // The stores are acknowledged (written through to the device's coherence point) before the
     // arrival is counted, so the last arrival sees every split's partials.
@@ -952,27 +990,27 @@ __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) 
       if (rec[1] > 0.0f) M = fmaxf(M, rec[0]);
     }
     // the splits are summed in split order, each term one explicit fma
-    f16v macc[4];
+    f16v macc[NDB];
 #pragma unroll
-    for (int db = 0; db < 4; ++db) macc[db] = f16v{};
+    for (int db = 0; db < NDB; ++db) macc[db] = f16v{};
     float l_acc = 0.0f;
     for (int s2 = 0; s2 < p.nsplit; ++s2) {
       f4 rec;
-      u4 po[8];
+      u4 po[QW];
       if (s2 == split) {
         rec = f4{m_run, l_tot, own_sc, 0.0f};
 #pragma unroll
-        for (int u = 0; u < 8; ++u) po[u] = own[u];
+        for (int u = 0; u < QW; ++u) po[u] = own[u];
       } else {
         rec = load_agent_b128(rm, row_ml, s2 * (kPRows * 16));
 #pragma unroll
-        for (int u = 0; u < 8; ++u) po[u] = __builtin_bit_cast(u4, load_agent_b128(ro, lo + u * 1024, s2 * split_o));
+        for (int u = 0; u < QW; ++u) po[u] = __builtin_bit_cast(u4, load_agent_b128(ro, lo + u * 1024, s2 * split_o));
       }
       const float w = (M == -INFINITY || rec[1] <= 0.0f) ? 0.0f : exp2_fast(rec[0] - M);
       l_acc = fmaf(w, rec[1], l_acc);
       const float F = (w * rec[1]) * rec[2];
 #pragma unroll
-      for (int u = 0; u < 8; ++u)
+      for (int u = 0; u < QW; ++u)
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
           const int g = 2 * u + h, db = g >> 2, c = g & 3;
@@ -989,13 +1027,13 @@ __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) 
     }
     l_tot = l_acc;
 #pragma unroll
-    for (int db = 0; db < 4; ++db) oacc[db] = macc[db];
+    for (int db = 0; db < NDB; ++db) oacc[db] = macc[db];
   }
   if (!row_ok) return;
   const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
   uint16_t* orow = p.out + (int64_t)b * p.o_sb + (int64_t)head * p.o_sh + (int64_t)lq * p.o_sl;
 #pragma unroll
-  for (int db = 0; db < 4; ++db)
+  for (int db = 0; db < NDB; ++db)
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       const int d = 32 * db + 8 * c + 4 * hh;
@@ -1031,11 +1069,11 @@ static PrePlan prefill_plan(int B, int Hq, int Hkv, int L, int S, int window) {
 struct PreLayout {
   size_t o, ml, total;
 };
-static PreLayout prefill_layout(const PrePlan& pl) {
+static PreLayout prefill_layout(const PrePlan& pl, int D) {
   PreLayout l;
   const size_t slots = (size_t)pl.nunits * pl.nsplit * kPRows;
   l.o = kCounterBytes;
-  l.ml = l.o + slots * 128 * sizeof(uint16_t);  // fp16 rows
+  l.ml = l.o + slots * D * sizeof(uint16_t);  // fp16 rows
   l.total = l.ml + (slots * 4 * sizeof(float) + 255) / 256 * 256;  // (m, l, 2^e, -) records
   return l;
 }
@@ -1043,33 +1081,40 @@ static PreLayout prefill_layout(const PrePlan& pl) {
 size_t prefill_workspace_bytes(int B, int Hq, int Hkv, int L, int D, int S, int window, int) {
   const PrePlan pl = prefill_plan(B, Hq, Hkv, L, S, window);
   if (pl.nsplit == 1) return 256;
-  return prefill_layout(pl).total;
+  return prefill_layout(pl, D).total;
 }
 
-template <typename T, int BITS, bool PAGED = false, int G = 64>
+template <typename T, int BITS, bool PAGED = false, int G = 64, int D = 128>
 static hipError_t launch_prefill_t(const PreParams& p, hipStream_t stream) {
-  hipLaunchKernelGGL((prefill_attn_kernel<T, BITS, PAGED, G>), dim3(p.nunits * p.nsplit), dim3(kPW * 64), 0, stream, p);
+  hipLaunchKernelGGL((prefill_attn_kernel<T, BITS, PAGED, G, D>), dim3(p.nunits * p.nsplit), dim3(kPW * 64), 0, stream,
+                     p);
   return hipGetLastError();
 }
 
-// The quantized instantiation for (dtype, bits in {4, 8}, G in {32, 64, 128}).
+// The quantized instantiation for (dtype, D in {64, 128}, bits in {4, 8}, G in {32, 64, 128}, G <= D).
 template <bool PAGED>
-static hipError_t launch_prefill_quant(const PreParams& p, int dtype, int bits, int G, hipStream_t stream) {
-  auto by_g = [&](auto t, auto b) -> hipError_t {
+static hipError_t launch_prefill_quant(const PreParams& p, int dtype, int D, int bits, int G, hipStream_t stream) {
+  auto by_g = [&](auto t, auto d, auto b) -> hipError_t {
     using TT = decltype(t);
+    constexpr int DD = decltype(d)::value;
     constexpr int BB = decltype(b)::value;
-    if (G == 32) return launch_prefill_t<TT, BB, PAGED, 32>(p, stream);
-    if (G == 128) return launch_prefill_t<TT, BB, PAGED, 128>(p, stream);
-    return launch_prefill_t<TT, BB, PAGED, 64>(p, stream);
+    if (G == 32) return launch_prefill_t<TT, BB, PAGED, 32, DD>(p, stream);
+    if constexpr (DD >= 128) {
+      if (G == 128) return launch_prefill_t<TT, BB, PAGED, 128, DD>(p, stream);
+    }
+    return launch_prefill_t<TT, BB, PAGED, 64, DD>(p, stream);
+  };
+  auto by_d = [&](auto t, auto b) -> hipError_t {
+    return D == 64 ? by_g(t, std::integral_constant<int, 64>{}, b) : by_g(t, std::integral_constant<int, 128>{}, b);
   };
   auto by_b = [&](auto t) -> hipError_t {
-    return bits == 8 ? by_g(t, std::integral_constant<int, 8>{}) : by_g(t, std::integral_constant<int, 4>{});
+    return bits == 8 ? by_d(t, std::integral_constant<int, 8>{}) : by_d(t, std::integral_constant<int, 4>{});
   };
   return dtype == KVQ_DTYPE_BF16 ? by_b(BF16{}) : by_b(F16{});
 }
 
 // Everything but the K/V operands.
-static PreParams prefill_params(const kvq_rows* q, const int32_t* seq_lens, const kvq_rows* out, int Hq, int Hkv, int L,
+static PreParams prefill_params(const kvq_rows* q, const int32_t* seq_lens, const kvq_rows* out, int Hq, int Hkv, int L, int D,
                                 int S, float scale, int causal, int window, void* workspace, const PrePlan& pl) {
   PreParams p{};
   p.q = (const uint16_t*)q->data;
@@ -1081,7 +1126,7 @@ static PreParams prefill_params(const kvq_rows* q, const int32_t* seq_lens, cons
   p.o_sb = out->stride_b;
   p.o_sh = out->stride_h;
   p.o_sl = out->stride_l;
-  const PreLayout lay = prefill_layout(pl);
+  const PreLayout lay = prefill_layout(pl, D);
   p.counters = (unsigned*)workspace;
   p.part_o = (float*)((char*)workspace + lay.o);
   p.part_ml = (float*)((char*)workspace + lay.ml);
@@ -1105,8 +1150,7 @@ hipError_t launch_prefill(const kvq_rows* q, const kvq_qtensor* k, const kvq_qte
                           const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int bits, int G, int dtype,
                           float scale, int causal, int window, void* workspace, hipStream_t stream) {
   const PrePlan pl = prefill_plan(B, Hq, Hkv, L, S, window);
-  PreParams p = prefill_params(q, seq_lens, out, Hq, Hkv, L, S, scale, causal, window, workspace, pl);
-  (void)D;
+  PreParams p = prefill_params(q, seq_lens, out, Hq, Hkv, L, D, S, scale, causal, window, workspace, pl);
   p.kc = (const uint8_t*)k->codes;
   p.vc = (const uint8_t*)v->codes;
   p.kc_sb = k->codes_stride_b * 4;
@@ -1125,7 +1169,7 @@ hipError_t launch_prefill(const kvq_rows* q, const kvq_qtensor* k, const kvq_qte
   p.vsb_sb = v->sb_stride_b;
   p.vsb_sh = v->sb_stride_h;
   p.vsb_ss = v->sb_stride_s;
-  return launch_prefill_quant<false>(p, dtype, bits, G, stream);
+  return launch_prefill_quant<false>(p, dtype, D, bits, G, stream);
 }
 
 hipError_t launch_prefill_paged(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v, int num_pages,
@@ -1133,7 +1177,7 @@ hipError_t launch_prefill_paged(const kvq_rows* q, const kvq_qtensor* k, const k
                                 int B, int Hq, int Hkv, int L, int D, int S, int bits, int G, int dtype, float scale,
                                 int causal, int window, void* workspace, hipStream_t stream) {
   const PrePlan pl = prefill_plan(B, Hq, Hkv, L, S, window);
-  PreParams p = prefill_params(q, seq_lens, out, Hq, Hkv, L, S, scale, causal, window, workspace, pl);
+  PreParams p = prefill_params(q, seq_lens, out, Hq, Hkv, L, D, S, scale, causal, window, workspace, pl);
   p.kc = (const uint8_t*)k->codes;
   p.vc = (const uint8_t*)v->codes;
   p.kc_sb = k->codes_stride_b * 4;  // page strides
@@ -1155,15 +1199,14 @@ hipError_t launch_prefill_paged(const kvq_rows* q, const kvq_qtensor* k, const k
   p.table = table;
   p.table_stride = table_stride;
   p.num_pages = num_pages;
-  (void)D;
-  return launch_prefill_quant<true>(p, dtype, bits, G, stream);
+  return launch_prefill_quant<true>(p, dtype, D, bits, G, stream);
 }
 
 hipError_t launch_prefill_dense(const kvq_rows* q, const kvq_rows* k, const kvq_rows* v, const int32_t* seq_lens,
                                 const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int dtype,
                                 float scale, int causal, int window, void* workspace, hipStream_t stream) {
   const PrePlan pl = prefill_plan(B, Hq, Hkv, L, S, window);
-  PreParams p = prefill_params(q, seq_lens, out, Hq, Hkv, L, S, scale, causal, window, workspace, pl);
+  PreParams p = prefill_params(q, seq_lens, out, Hq, Hkv, L, D, S, scale, causal, window, workspace, pl);
   p.kc = (const uint8_t*)k->data;
   p.vc = (const uint8_t*)v->data;
   p.kc_sb = k->stride_b * 2;
@@ -1172,7 +1215,6 @@ hipError_t launch_prefill_dense(const kvq_rows* q, const kvq_rows* k, const kvq_
   p.vc_sb = v->stride_b * 2;
   p.vc_sh = v->stride_h * 2;
   p.vc_ss = v->stride_l * 2;
-  (void)D;
   if (dtype == KVQ_DTYPE_BF16) return launch_prefill_t<BF16, 16>(p, stream);
   return launch_prefill_t<F16, 16>(p, stream);
 }

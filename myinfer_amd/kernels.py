@@ -227,10 +227,12 @@ def decode_rows_per_pass(D: int, group_size: int = 64) -> int:
     return 16 * group_size // D
 
 
-def _auto_kernel(rep_rows: int, D: int, group_size: int) -> str:
+def _auto_kernel(rep_rows: int, D: int, group_size: int, dense: bool = False) -> str:
     """Decode while a KV head's query rows fit at most two decode passes over its keys (one pass for
-    group 64, where 8 rows fit one pass), the prefill kernel otherwise; decode for D != 128."""
-    return "decode" if (rep_rows <= max(decode_rows_per_pass(D, group_size), 8) or D != 128) else "prefill"
+    group 64, where 8 rows fit one pass), the prefill kernel otherwise; decode where the prefill
+    kernel has no build (head_dim 256, and head_dim 64 over an unquantized cache)."""
+    prefill_built = D == 128 or (D == 64 and not dense)
+    return "decode" if (rep_rows <= max(decode_rows_per_pass(D, group_size), 8) or not prefill_built) else "prefill"
 
 
 class AttentionCall:
@@ -327,7 +329,7 @@ def prepare_attention(queries: torch.Tensor, keys, values, scale: float, *, caus
         sl_ptr = seq_lens.data_ptr()
     rep = Hq // Hkv
     if kernel == "auto":
-        kernel = _auto_kernel(rep * L, D, 64 if dense else group_size)
+        kernel = _auto_kernel(rep * L, D, 64 if dense else group_size, dense)
     if kernel not in ("decode", "prefill"):
         raise ValueError(f"kernel must be 'decode', 'prefill' or 'auto', got {kernel!r}")
     lib = _lib.lib()

@@ -50,14 +50,16 @@ def test_prefill_workspace_size():
     # counter block
     assert lib.kvq_prefill_workspace_size(1, 32, 4, 128, 128, 128, 0) == 256
     assert lib.kvq_prefill_workspace_size(1, 32, 4, 512, 128, 512, 0) > 256
-    assert lib.kvq_prefill_workspace_size(1, 32, 4, 512, 64, 16384, 0) == 0  # head_dim 128 only
+    assert lib.kvq_prefill_workspace_size(1, 32, 4, 512, 96, 16384, 0) == 0  # head_dim 64 or 128 only
+    assert 0 < lib.kvq_prefill_workspace_size(1, 32, 4, 512, 64, 16384, 0) < c3  # half the dims per partial row
     assert lib.kvq_prefill_workspace_size(1, 30, 4, 512, 128, 16384, 0) == 0  # Hq not a multiple of Hkv
     assert lib.kvq_prefill_workspace_size(1, 32, 4, 0, 128, 16384, 0) == 0
     assert lib.kvq_prefill_workspace_size(1, 32, 4, 512, 128, 16384, -1) == 0
 
 
 @pytest.mark.parametrize("kw,code,needle", [
-    (dict(D=64), _lib.ERR_UNSUPPORTED, "head_dim 128"),
+    (dict(D=256), _lib.ERR_UNSUPPORTED, "head_dim 64 and 128"),
+    (dict(D=64, group=128), _lib.ERR_UNSUPPORTED, "group_size"),
     (dict(bits=3), _lib.ERR_UNSUPPORTED, "bits"),
     (dict(group=16), _lib.ERR_UNSUPPORTED, "group_size"),
     (dict(Hq=6, Hkv=4), _lib.ERR_INVALID, "multiple"),
@@ -155,3 +157,10 @@ def test_prefill_rejects_unaligned_scale_rows(field, value):
     setattr(k, field, value)
     _expect(_prefill(k=k, ws=WS, wsb=n), _lib.ERR_INVALID, "4-byte aligned")
     _expect(_paged(_lib.lib().kvq_paged_prefill_attn, k=k, ws=WS, wsb=n), _lib.ERR_INVALID, "4-byte aligned")
+
+
+def test_unquantized_head_dims():
+    # the unquantized kernels keep head_dim 64/128 (decode) and 128 (prefill)
+    lib = _lib.lib()
+    _expect(_dense(lib.kvq_prefill_attn_dense, D=64), _lib.ERR_UNSUPPORTED, "head_dim 128")
+    _expect(_dense(lib.kvq_decode_attn_dense, D=256), _lib.ERR_UNSUPPORTED, "head_dim 64 and 128")

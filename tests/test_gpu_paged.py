@@ -245,3 +245,23 @@ def test_paged_head_dim_256(bits):
         assert torch.equal(out_p, out_c), L
         assert_close(out_p, exact_reference(q, kc, vc, scale, bits=bits, group_size=64, causal=True, seq_lens=sl),
                      f"paged D=256 L={L}")
+
+
+@pytest.mark.parametrize("bits,group", [(8, 64), (4, 32)])
+def test_paged_prefill_head_dim_64(bits, group):
+    print(f"paged prefill D=64 bits={bits} group={group}", flush=True)
+    B, Hq, Hkv, D, L, dtype = 2, 16, 4, 64, 200, torch.bfloat16
+    lens = [2500, 901]
+    rows, tables, kp, vp, kc, vc = build(B, Hkv, lens, D, bits, dtype, 61, group=group)
+    q = seeded_normal((B, Hq, L, D), 62, dtype, DEV)
+    sl = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    scale = 1.0 / math.sqrt(D)
+    out_p = kernels.paged_attention(q, kp, vp, tables, sl, scale, causal=True, bits=bits, group_size=group,
+                                    max_len=max(lens), kernel="prefill")
+    out_c = kernels.attention(q, kc, vc, scale, causal=True, seq_lens=sl, bits=bits, group_size=group,
+                              kernel="prefill")
+    torch.cuda.synchronize()
+    assert torch.isfinite(out_p.float()).all()
+    assert torch.equal(out_p, out_c)
+    assert_close(out_p, exact_reference(q, kc, vc, scale, bits=bits, group_size=group, causal=True, seq_lens=sl),
+                 "paged prefill D=64")

@@ -21,10 +21,9 @@ DEV = "cuda"
 
 
 def run_case(B, Hq, Hkv, L, S, bits, dtype, *, causal=True, window=0, seq_lens=None, seed=0, cap=None, group=64,
-             what=""):
-    print(f"prefill case {what} B={B} Hq={Hq} Hkv={Hkv} L={L} S={S} bits={bits} group={group} {dtype} "
+             D=128, what=""):
+    print(f"prefill case {what} B={B} Hq={Hq} Hkv={Hkv} L={L} S={S} D={D} bits={bits} group={group} {dtype} "
           f"causal={causal} window={window} var={seq_lens is not None}", flush=True)
-    D = 128
     kt, vt = make_cache(B, Hkv, S, D, bits, dtype, seed, cap=cap, group=group)
     q = seeded_normal((B, Hq, L, D), seed + 2, dtype, DEV)
     sl = None if seq_lens is None else torch.tensor(seq_lens, dtype=torch.int32, device=DEV)
@@ -50,6 +49,32 @@ def test_group_sizes(dtype, bits, group):
     run_case(2, 16, 4, 150, 1300, bits, dtype, seed=500 + group + bits, group=group, what="group")
     run_case(2, 8, 2, 33, 5000, bits, dtype, window=1024, seq_lens=[5000, 700], seed=600 + group, group=group,
              what="group-window")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("bits", [8, 4])
+@pytest.mark.parametrize("group", [32, 64])
+def test_head_dim_64(dtype, bits, group):
+    # head_dim 64 (Llama-3.2-1B, Qwen2.5-0.5B shapes): half the MFMAs per tile, waves 0-3 dequantize
+    run_case(2, 16, 4, 150, 1300, bits, dtype, seed=800 + group + bits, group=group, D=64, what="d64")
+    run_case(2, 8, 2, 33, 5000, bits, dtype, window=1024, seq_lens=[5000, 700], seed=900 + group, group=group, D=64,
+             what="d64-window")
+
+
+@pytest.mark.parametrize("L,S", [(1, 1), (5, 5), (65, 300), (200, 2048)])
+def test_head_dim_64_ragged_and_full(L, S):
+    run_case(1, 8, 2, L, S, 8, torch.float16, seed=L + S + 64, D=64, what="d64-ragged")
+    run_case(2, 14, 2, L, S, 4, torch.bfloat16, causal=False, seed=L + S + 65, D=64, what="d64-full")
+
+
+def test_head_dim_64_long_context_and_auto_dispatch():
+    run_case(1, 16, 4, 512, 8192, 8, torch.bfloat16, seed=66, D=64, what="d64-long")
+    # kernel="auto" picks the prefill kernel for a D=64 prompt chunk
+    D = 64
+    kt, vt = make_cache(1, 2, 1000, D, 8, torch.float16, 67)
+    q = seeded_normal((1, 8, 100, D), 68, torch.float16, DEV)
+    call = kernels.prepare_attention(q, kt, vt, 0.125, causal=True, bits=8)
+    assert call.kernel == "prefill"
 
 
 @pytest.mark.parametrize("L,S", [(1, 1), (2, 2), (5, 5), (17, 40), (64, 64), (65, 300), (128, 1000), (200, 2048)])
