@@ -413,8 +413,8 @@ PREFILL = dict(desc="Qwen3-30B-A3B chunked prefill, 16384 tokens in 512-token ch
 
 # C5 (Gemma-3-27B shapes) prefill legs over the quantized cache: B=4 sequences of 8192 tokens in
 # 2048-token chunks, 32 query heads / 16 KV heads, bf16; the global causal layer and a window-1024
-# layer (5 of every 6 layers; quantized here as SURVEY's C5 configuration asks, although the
-# reference leaves sliding-window caches unquantized: m5engine/attention.py:106-112).
+# layer (5 of every 6 layers; quantized here, as the C5 workload's 8-bit KV cache states, although
+# the reference leaves sliding-window caches unquantized: m5engine/attention.py:106-112).
 PREFILL_C5 = {
     "C5-global-prefill": dict(desc="Gemma-3-27B global-layer chunked prefill, B=4 x 8192 tokens in 2048-token "
                                    "chunks, 8-bit KV, bf16", B=4, Hq=32, Hkv=16, D=128, N=8192, chunk=2048, bits=8,

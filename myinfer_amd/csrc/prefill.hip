@@ -12,11 +12,12 @@
 //    (row = position * rep + local head), so all rep query heads of a position share each K/V
 //    tile and a causal boundary cuts only a few positions.
 //  * The raw tiles (codes, scales, biases) stream into a 3-slot LDS ring by buffer->LDS DMA, two
-//    tiles ahead of their use, with no registers held in flight; rows past the sequence end read
+//    steps ahead of their use, with no registers held in flight; rows past the sequence end read
 //    as zero through the buffer range check (they are masked). Each 64-key tile is then
 //    dequantized once per workgroup, LDS to LDS, into fp16 operands: K row-major, V transposed
 //    (V^T[d][slot]) with its key slots permuted to match the score layout below. The fp16
-//    operands are double-buffered: tile t+1 is dequantized while tile t is computed.
+//    operands are triple-buffered: tile t + 2 is dequantized while tile t is computed (the
+//    quantized tile loop below says how the steps overlap).
 //  * Per wave (32 rows = the columns of a 32x32 MFMA): S^T = K Q^T (v_mfma_f32_32x32x16_f16;
 //    A = K rows from LDS, B = Q^T held in registers). In the MFMA result layout every lane holds
 //    16 keys of one query column, so the row max / sum are lane-local plus one permlane swap, and
