@@ -61,6 +61,39 @@ def test_prefill_fuzz(case):
                 seed=7200 + case, cap=cap, what=f"fuzz {case}")
 
 
+def _group(rng, D):
+    return rng.choice([g for g in (32, 64, 128) if D // 4 <= g <= D])
+
+
+@pytest.mark.parametrize("case", range(16))
+def test_decode_fuzz_groups_and_head_dims(case):
+    # group sizes 32/64/128 and head_dim 64/128/256, with the masks, lengths and views above
+    rng = random.Random(7500 + case)
+    D, bits, dtype = rng.choice([64, 128, 256]), rng.choice([4, 8]), rng.choice(DTYPES)
+    group = _group(rng, D)
+    Hkv, rep = rng.choice([1, 2, 4]), rng.choice([1, 2, 3, 4, 8])
+    B, L = rng.choice([1, 2, 3]), rng.choice([1, 1, 2, 5])
+    S = rng.randrange(L, 2500)
+    cap = S + rng.choice([0, 0, rng.randrange(1, 300)])
+    causal, window, seq_lens = _masks(rng, B, L, S)
+    TD.run_case(B, Hkv * rep, Hkv, L, S, D, bits, dtype, causal=causal, window=window, seq_lens=seq_lens,
+                seed=7500 + case, cap=cap, outliers=rng.random() < 0.3, group=group, what=f"fuzz-gd {case}")
+
+
+@pytest.mark.parametrize("case", range(16))
+def test_prefill_fuzz_groups_and_head_dims(case):
+    rng = random.Random(7600 + case)
+    D, bits, dtype = rng.choice([64, 128]), rng.choice([4, 8]), rng.choice(DTYPES)
+    group = _group(rng, D)
+    Hkv, rep = rng.choice([1, 2, 4, 8]), rng.choice([1, 2, 4, 8])
+    B, L = rng.choice([1, 2]), rng.randrange(1, 400)
+    S = rng.randrange(L, 3000)
+    cap = S + rng.choice([0, 0, rng.randrange(1, 300)])
+    causal, window, seq_lens = _masks(rng, B, L, S)
+    TP.run_case(B, Hkv * rep, Hkv, L, S, bits, dtype, causal=causal, window=window, seq_lens=seq_lens,
+                seed=7600 + case, cap=cap, group=group, D=D, what=f"fuzz-gd {case}")
+
+
 @pytest.mark.parametrize("case", range(24))
 def test_unquantized_fuzz(case):
     rng = random.Random(7300 + case)
