@@ -340,6 +340,14 @@ class QuantizedKVCache:
     def empty(self) -> bool:
         return self.keys is None
 
+    def fits_fp16_operands(self) -> bool:
+        """Whether the cached K and V rows dequantize inside the fp16 range, as the prefill kernel's
+        operands require (kernels.fits_fp16_operands); an empty cache fits."""
+        if self.keys is None or self.offset == 0:
+            return True
+        keys, values = self.fetch()
+        return kernels.fits_fp16_operands(keys, self.bits) and kernels.fits_fp16_operands(values, self.bits)
+
 
 def can_trim_prompt_cache(cache: List) -> bool:
     """mlx-lm's can_trim_prompt_cache, used at m5engine/prefix_cache.py:90."""

@@ -221,6 +221,24 @@ def quantize(x: torch.Tensor, group_size: int = 64, bits: int = 8) -> Triple:
     return (codes.reshape(*lead, -1), scales.reshape(*lead, -1), biases.reshape(*lead, -1))
 
 
+FP16_MAX = 65504.0
+
+
+def fits_fp16_operands(triple: Triple, bits: int) -> bool:
+    """Whether every dequantized value s * c + b (c in [0, 2^bits - 1]) of a (codes, scales,
+    biases) triple lies inside the fp16 range. The prefill kernel's dequantized operands are fp16:
+    for a bf16 cache with a group outside that range its query rows come back NaN (decode is exact
+    either way), so a caller whose bf16 K/V can exceed 65504 checks its cache once with this and
+    routes those layers through decode. Works on the triple's device; returns a Python bool (a
+    synchronisation on the GPU)."""
+    _check_triple(triple, "triple")
+    _, scales, biases = triple
+    s, b = scales.float(), biases.float()
+    hi = b + s * float((1 << bits) - 1)
+    worst = torch.maximum(b.abs(), hi.abs())
+    return bool(torch.isfinite(worst).all().item()) and bool((worst <= FP16_MAX).all().item())
+
+
 def decode_rows_per_pass(D: int, group_size: int = 64) -> int:
     """Query rows (heads of a GQA group x query positions) one decode pass serves: the 16 MFMA
     columns hold each row once per scale group (an unquantized cache counts as group 64)."""

@@ -43,6 +43,10 @@ def test_prefill_poisons_row_blocks_beyond_fp16(which, causal):
     kmul, vmul = (4e4, 1.0) if which == "keys" else (1.0, 4e4)  # about 1.6e5 at the extremes
     kt, vt = big_cache(B, Hkv, S, D, bits, 1, kmul, vmul, 300)
     assert float((kt[2] if which == "keys" else vt[2])[:, 1].float().abs().max()) > 65504
+    # the host-side check flags exactly the cache that prefill cannot hold
+    assert not kernels.fits_fp16_operands(kt if which == "keys" else vt, bits)
+    assert kernels.fits_fp16_operands(vt if which == "keys" else kt, bits)
+    assert kernels.fits_fp16_operands(tuple(t[:, :1] for t in kt), bits)
     q = seeded_normal((B, Hq, L, D), 302, torch.bfloat16, DEV)
     scale = 1.0 / math.sqrt(D)
     out = kernels.attention(q, kt, vt, scale, causal=causal, bits=bits, kernel="prefill")
