@@ -1113,6 +1113,7 @@ static hipError_t launch_decode_t(const DecParams& p, hipStream_t stream) {
   m.R = DecCfg<D, BITS, G>::R;
   m.rowblocks = p.rowblocks;
   m.nsplit = p.nsplit;
+  m.xcd_remap = p.xcd_remap;
   return launch_combine<T, D>(m, p.nunits / (p.Hkv * p.rowblocks), stream);
 }
 

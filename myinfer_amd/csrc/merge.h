@@ -45,6 +45,7 @@ struct MergeParams {
   uint16_t* out;
   int64_t o_sb, o_sh, o_sl;
   int Hq, Hkv, L, rep, R, rowblocks, nsplit;
+  int xcd_remap;  // 1: the decode launch numbered its workgroups by XCD (see decode_attn_kernel)
 };
 
 // Quad lane exchanges (lane i with lane i ^ 1, i ^ 2) through DPP quad permutes.
@@ -65,7 +66,10 @@ __device__ __forceinline__ float quad_sum(float v) {
 // loads its float4 and (m, l) of each in one round (a quarter of the loads a thread would issue
 // alone: the merge is bound by the latency of these loads), forms the split weights against the
 // quad's maximum, and the quad sums its terms with two DPP exchanges. Fixed order, so repeated
-// calls are bit-identical. 256 / D rows per workgroup of 256 threads.
+// calls are bit-identical. 256 / D rows per workgroup of 256 threads. When the decode launch
+// placed each unit's splits on one XCD, the workgroups here are numbered the same way (a grid that
+// is a multiple of 8, rows in unit order), so a unit's partials are merged on the XCD that wrote
+// them (+1% at 32 splits).
 template <typename T, int D, int R>
 __global__ __launch_bounds__(256) void combine_kernel(MergeParams p, int nrows) {
   constexpr int F4 = D / 4;              // float4s per row
@@ -73,7 +77,8 @@ __global__ __launch_bounds__(256) void combine_kernel(MergeParams p, int nrows) 
   constexpr int CH = 8;                  // splits per thread loaded in the first round
   const int t = threadIdx.x;
   const int q = t & 3, j = (t >> 2) % F4;
-  const int grow = blockIdx.x * RPB + t / (4 * F4);
+  const int bx = p.xcd_remap ? (blockIdx.x % 8) * (gridDim.x / 8) + blockIdx.x / 8 : blockIdx.x;
+  const int grow = bx * RPB + t / (4 * F4);
   const bool ok = grow < nrows;
   const int g = ok ? grow : 0;
   const int l = g % p.L, h = (g / p.L) % p.Hq, b = g / (p.L * p.Hq);
@@ -134,11 +139,13 @@ inline hipError_t launch_combine(const MergeParams& m, int B, hipStream_t stream
   const int nrows = B * m.Hq * m.L;
   constexpr int rpb = 256 / D;  // rows per 256-thread workgroup
   const dim3 grid((nrows + rpb - 1) / rpb);
+  MergeParams mm = m;
+  mm.xcd_remap = m.xcd_remap && grid.x % 8 == 0;
   // R (rows per decode unit, 16 / scale groups per row) fixes the kernel's split strides
   switch (m.R) {
-    case 4: hipLaunchKernelGGL((combine_kernel<T, D, 4>), grid, dim3(256), 0, stream, m, nrows); break;
-    case 8: hipLaunchKernelGGL((combine_kernel<T, D, 8>), grid, dim3(256), 0, stream, m, nrows); break;
-    case 16: hipLaunchKernelGGL((combine_kernel<T, D, 16>), grid, dim3(256), 0, stream, m, nrows); break;
+    case 4: hipLaunchKernelGGL((combine_kernel<T, D, 4>), grid, dim3(256), 0, stream, mm, nrows); break;
+    case 8: hipLaunchKernelGGL((combine_kernel<T, D, 8>), grid, dim3(256), 0, stream, mm, nrows); break;
+    case 16: hipLaunchKernelGGL((combine_kernel<T, D, 16>), grid, dim3(256), 0, stream, mm, nrows); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
