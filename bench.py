@@ -479,8 +479,9 @@ def time_prefill(cfg, steps, warmup, device, want_parity=False):
             f()
     torch.cuda.synchronize()
 
-    # attention-kernel time per chunk: event pairs around each attention call, all queued behind a
-    # spin kernel so the pairs bracket the kernels only
+    # per-chunk breakdown: event pairs around each append and attention call, all queued behind a
+    # spin kernel. Each pair also holds the gap between its event packets and the kernel (a few us),
+    # so the attention total below comes from a graph of the attention launches instead.
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(2 * nchunk)]
     cycles = calibrate_spin(torch, 30.0)
     torch.cuda.synchronize()
@@ -516,16 +517,47 @@ def time_prefill(cfg, steps, warmup, device, want_parity=False):
     e_.record()
     torch.cuda.synchronize()
     ms_per_step = s_.elapsed_time(e_) / steps
+    del graph
+
+    # The attention kernels' share of the timed step: the step minus the same appends replayed alone
+    # (a graph of the prompt's append launches; they rewrite the same rows). For reference, the
+    # attention launches replayed alone (the cache already holds every chunk's rows, and a chunk's
+    # call reads only the rows before its end). Each graph holds `steps` prompts and is timed by one
+    # event pair.
+    def replay_ms(body):
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr, stream=side):
+            for _ in range(steps):
+                body()
+        gr.replay()
+        torch.cuda.synchronize()
+        s_.record()
+        gr.replay()
+        e_.record()
+        torch.cuda.synchronize()
+        return s_.elapsed_time(e_) / steps
+
+    def appends_only():
+        for a in gappends:
+            kernels.quantize_append(a[0], (kc, ks, kb), a[1], (vc, vs, vb), row_offset=a[2], group_size=64, bits=bits)
+
+    def attns_only():
+        for f in gattns:
+            f()
+
+    append_graph_ms = replay_ms(appends_only)
+    attn_alone_ms = replay_ms(attns_only)
+    attn_step_ms = ms_per_step - append_graph_ms
     res = dict(flops=flops, ms_per_step=ms_per_step, tflops=flops / (ms_per_step * 1e-3) / 1e12,
-               attn_ms=sum(attn_ms), append_ms=sum(append_ms),
-               attn_tflops=flops / (sum(attn_ms) * 1e-3) / 1e12,
+               attn_ms=attn_step_ms, append_ms=append_graph_ms, attn_alone_ms=attn_alone_ms,
+               attn_events_ms=sum(attn_ms), append_events_ms=sum(append_ms),
+               attn_tflops=flops / (attn_step_ms * 1e-3) / 1e12,
                chunk_attn_us={c: round(1e3 * attn_ms[c], 2) for c in (0, nchunk // 2, nchunk - 1)})
     if want_parity:
         res["parity"], res["parity_arrays"] = prefill_parity(cfg, q, out, (kc, ks, kb), (vc, vs, vb), scale,
                                                              nchunk - 1)
         last = nchunk - 1
         res["cpu_inputs"] = (q[:, :, last * C:], (kc, ks, kb), (vc, vs, vb), scale)
-    del graph
     return res
 
 
@@ -826,8 +858,11 @@ def main():
                          "traffic": measured_traffic("prefill_c3_chunk"),
                          "kernel_ms": round(pr["attn_ms"], 4),
                          "kernel": "prefill_attn_kernel (one launch per chunk; split keys are merged inside it), "
-                                   "summed over the 32 chunks"},
+                                   "summed over the 32 chunks: the timed step's graph minus a graph of its "
+                                   "appends alone"},
             "append_ms": round(pr["append_ms"], 4),
+            "attn_alone_ms": round(pr["attn_alone_ms"], 4),
+            "attn_events_ms": round(pr["attn_events_ms"], 4),
             "chunk_attn_us": pr["chunk_attn_us"],
             "cpu_baseline": pcpu,
             "parity": pr.get("parity"),
