@@ -55,7 +55,7 @@ constexpr int kXcds = 8;  // MI355X: 8 XCDs, each with its own L2
 
 // The raw tile ring. A slot holds one 64-key tile as loaded: [K codes][V codes][sK, bK, sV, bV],
 // code rows with their 16-byte chunks XOR-swizzled by row (chunk c of row r at position
-// c ^ (r % CPR)), each scale/bias array as 64 PC 4-byte cells: with NG = D / G >= 2 scale groups
+// c ^ swz(r)), each scale/bias array as 64 PC 4-byte cells: with NG = D / G >= 2 scale groups
 // per row, cell PC key + c holds groups 2c and 2c + 1 of the key (PC = NG / 2); with one group,
 // cell key holds it in its low half (PC = 1).
 // BITS == 16 is the unquantized cache: raw T rows, no scales or biases.
@@ -78,6 +78,11 @@ struct RawCfg {
   // issue one each and the others none
   static constexpr int CPW = 2 * CI >= kPW ? 2 * CI / kPW : 1;
   static constexpr int CODE_WAVES = 2 * CI >= kPW ? kPW : 2 * CI;
+  // The chunk swizzle of row r. Quantized tiles fold in r / 16: the V^T staging reads one dim
+  // quad of 8 keys per lane, and keys 16 apart (the same key % CPR) would otherwise share LDS
+  // banks (a 4-way conflict at 8 bits); this spreads them over the banks. Unquantized rows keep
+  // r % CPR (their staging and operand reads index it directly).
+  static __device__ __forceinline__ constexpr int swz(int r) { return (DENSE ? r : r ^ (r >> 4)) % CPR; }
   // the waves that dequantize: V^T in waves [0, NSW), K in [NSW, 2 NSW) (256 threads each for
   // D = 128, 128 for D = 64); the other waves only compute
   static constexpr int NSW = D / 32;
@@ -138,11 +143,11 @@ constexpr bool v_keys_split() {
   for (int c8 = 0; c8 < 8; ++c8)
     for (int i = 0; i < 8; ++i)
       if (v_slot_key(8 * c8 + i) != v_base_key(c8) + v_key_offset(i) || (v_base_key(c8) & 3) != 0 ||
-          (v_key_offset(i) & 7) != (i & 3))
+          (v_key_offset(i) & 7) != (i & 3) || ((v_base_key(c8) + v_key_offset(i)) >> 4) != (v_base_key(c8) >> 4))
         return false;
   return true;
 }
-static_assert(v_keys_split(), "slot keys are a per-lane base (low two bits clear) plus i-dependent offsets");
+static_assert(v_keys_split(), "slot keys are a per-lane base (low two bits clear) plus i-dependent offsets below 16");
 
 // Buffer->LDS DMA issued from inline asm: the compiler does not model these loads, so it adds no
 // wait for them before the kernel's LDS accesses; the tile ring orders every slot with explicit
@@ -209,7 +214,7 @@ struct RawShare {
       const bool is_k = q < C::CI;
       const int i = is_k ? q : q - C::CI;
       const int r = i * C::RPI + lane / C::CPR;
-      const int c = (lane % C::CPR) ^ (r % C::CPR);
+      const int c = (lane % C::CPR) ^ C::swz(r);
       code_r[j] = is_k ? kr : vr;
       code_ss[j] = is_k ? p.kc_ss : p.vc_ss;
       code_vo[j] = (uint32_t)(r * code_ss[j] + 16 * c);
@@ -334,16 +339,17 @@ template <int BITS, int G, int D, int H>
 __device__ __forceinline__ void stage_v(const uint8_t* raw, _Float16* vlds, const uint32_t* sbt, int tid) {
   using C = RawCfg<BITS, G, D>;
   const int c8 = tid & 7, d4 = tid >> 3;
-  // key i of the chunk is kb + v_key_offset(i), and its swizzle key % CPR is ((kb % CPR) | (i & 3))
-  // % CPR (kb has its low two bits clear, the offsets are i & 3 modulo 8, CPR is a power of two):
-  // four code addresses per lane; everything else is an immediate offset
+  // key i of the chunk is kb + v_key_offset(i), and its swizzle swz(key) is
+  // (((kb % CPR) | (i & 3)) ^ (kb >> 4)) % CPR: kb has its low two bits clear and kb % 16 is 0 or
+  // 4, the offsets are i & 3 modulo 8 and below 12 (so key >> 4 == kb >> 4), CPR is a power of
+  // two. Four code addresses per lane; everything else is an immediate offset
   const int kb = v_base_key(c8);
   const uint8_t* vr = raw + C::KB + kb * C::ROWB;
   uint32_t x[8];  // key i: the dim pair of this half
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int ko = v_key_offset(i);
-    const int sw = ((kb % C::CPR) | (i & 3)) % C::CPR;
+    const int sw = (((kb % C::CPR) | (i & 3)) ^ (kb >> 4)) % C::CPR;
     uint32_t bytes;  // codes of dims 4 d4 .. 4 d4 + 3 as 4 bytes
     if constexpr (BITS == 8) {
       bytes = *(const uint32_t*)(vr + ko * C::ROWB + 16 * ((d4 >> 2) ^ sw) + 4 * (d4 & 3));
@@ -374,11 +380,11 @@ __device__ __forceinline__ void stage_k(const uint8_t* raw, _Float16* klds, int 
   const uint8_t* kr = raw + key * C::ROWB;
   uint32_t w[4];  // the half's 16 codes
   if constexpr (BITS == 8) {
-    const u4 a = *(const u4*)(kr + 16 * ((2 * q + H) ^ (key % C::CPR)));
+    const u4 a = *(const u4*)(kr + 16 * ((2 * q + H) ^ C::swz(key)));
 #pragma unroll
     for (int i = 0; i < 4; ++i) w[i] = a[i];
   } else {
-    const u2 a = *(const u2*)(kr + 16 * (q ^ (key % C::CPR)) + 8 * H);
+    const u2 a = *(const u2*)(kr + 16 * (q ^ C::swz(key)) + 8 * H);
     w[0] = a[0];
     w[1] = a[1];
   }
