@@ -825,7 +825,6 @@ __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) 
       constexpr int ROLE = decltype(role)::value;
       constexpr bool QKN = decltype(qkn)::value, STG = decltype(stg)::value;
       constexpr int IPT = (ROLE < 2 || RC::CODE_WAVES == kPW) ? RC::IPT : RC::IPT_NOCODE;
-      issue_raw(t + 4);
       // the step's buffers, as element (byte, for the raw ring) offsets from each array's start
       const int k_t = opaque((t % 3) * KBUF), k_t1 = opaque(((t + 1) % 3) * KBUF);
       const int k_w = opaque(((t + 2) % 3) * KBUF);
@@ -852,6 +851,9 @@ __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) 
       pv_blk(vl, pop, B0{});
       if constexpr (STG && ROLE == 0) stage_v<BITS, G, D, 0>(raw2, &v_lds[0][0] + v_w, sb_tab[wave & 3], tid);
       if constexpr (STG && ROLE == 1) stage_k<T, BITS, G, D, 0>(raw2, &k_lds[0][0] + k_w, tid, range_bad);
+      // tile t + 4 into the slot of tile t + 1, issued between the halves (at the step's start
+      // it delays the first half: about 2% slower on C3, as are the other positions tried)
+      issue_raw(t + 4);
       // half 1: softmax of block 1 beside S(block 0 of tile t + 1) = K(t + 1) rows 0-31 Q^T
       {
         const _Float16* kl = kl_lane + k_t1;
