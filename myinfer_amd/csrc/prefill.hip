@@ -30,6 +30,8 @@
 //    maximum exceeds it by more than 2^6), fp32 accumulators.
 //  * Long key ranges are split over several workgroups; the last split of a row block to finish
 //    merges the (m, l, o) partials of the others (log-sum-exp) and writes the output.
+//  * An unquantized fp16/bf16 cache (BITS == 16) takes a simpler loop: K operands straight from
+//    the raw ring, only V^T staged, the MFMAs in the cache's type.
 
 #include <math.h>
 
