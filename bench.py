@@ -17,6 +17,9 @@ Timing:
   * roofline.achieved: the average duration of one call (the decode kernel and the split-merge
     kernel it launches), from one HIP event pair around a batch of eager calls queued behind a
     spin kernel, so the GPU runs them back to back and the pair brackets their kernels only.
+  * prefill.roofline.achieved: the attention kernels' share of the graph-replayed prefill step,
+    that is the step minus the same appends replayed alone in a graph of their own (an event
+    pair around each eager launch, kept only for the per-chunk breakdown, adds a few us each).
   * roofline.traffic: HBM bytes per call (decode) / per chunk launch (prefill), read from the
     committed rocprofv3 FETCH_SIZE and WRITE_SIZE summary in profiles/, whose counters are scaled
     by what they read for a plain 256 MiB device copy (`bench.py --calibrate-copy`).
