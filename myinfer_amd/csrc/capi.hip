@@ -320,6 +320,10 @@ size_t kvq_decode_workspace_size(int B, int Hq, int Hkv, int L, int D, int S, in
       const size_t x = kvq::decode_workspace_bytes(B, Hq, Hkv, L, D, S, window, bits, G);
       n = x > n ? x : n;
     }
+  if (D == 256) {  // the unquantized cache at head_dim 256 runs through the head_dim-256 kernel
+    const size_t x = kvq::wide_workspace_bytes(B, Hq, Hkv, L, S, window);
+    n = x > n ? x : n;
+  }
   return n;
 }
 
@@ -356,7 +360,9 @@ int kvq_decode_attn_static(const kvq_rows* q, const kvq_qtensor* k, const kvq_qt
 }
 
 size_t kvq_prefill_workspace_size(int B, int Hq, int Hkv, int L, int D, int S, int window) {
-  if (B <= 0 || Hq <= 0 || Hkv <= 0 || L <= 0 || S <= 0 || (D != 64 && D != 128) || window < 0 || Hq % Hkv) return 0;
+  if (B <= 0 || Hq <= 0 || Hkv <= 0 || L <= 0 || S <= 0 || (D != 64 && D != 128 && D != 256) || window < 0 || Hq % Hkv)
+    return 0;
+  if (D == 256) return kvq::wide_workspace_bytes(B, Hq, Hkv, L, S, window);
   return kvq::prefill_workspace_bytes(B, Hq, Hkv, L, D, S, window, 8);
 }
 
@@ -375,10 +381,15 @@ int kvq_prefill_attn(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor*
                      const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int bits, int group_size,
                      int dtype, float scale, int causal, int window, void* workspace, size_t workspace_bytes,
                      void* stream) {
-  if (D != 64 && D != 128) return fail(KVQ_ERR_UNSUPPORTED, "prefill supports head_dim 64 and 128, got %d", D);
+  if (D != 64 && D != 128 && D != 256)
+    return fail(KVQ_ERR_UNSUPPORTED, "prefill supports head_dim 64, 128 and 256, got %d", D);
   int rc = check_attn(q, k, v, out, B, Hq, Hkv, L, D, S, bits, group_size, dtype, scale, window,
                       kvq_prefill_workspace_size(B, Hq, Hkv, L, D, S, window), workspace, workspace_bytes);
   if (rc) return rc;
+  if (D == 256)
+    return hip_status(kvq::launch_wide(q, k, v, seq_lens, out, B, Hq, Hkv, L, S, bits, group_size, dtype, scale, causal,
+                                       window, workspace, (hipStream_t)stream),
+                      "prefill_attn launch (head_dim 256)");
   if ((rc = check_rows(out, "out", D, true))) return rc;  // rows are written 8 bytes at a time
   if ((rc = check_prefill_sb(k, v, D, group_size))) return rc;
   return hip_status(kvq::launch_prefill(q, k, v, seq_lens, out, B, Hq, Hkv, L, D, S, bits, group_size, dtype, scale,
@@ -442,10 +453,15 @@ int kvq_paged_prefill_attn(const kvq_rows* q, const kvq_qtensor* k_pool, const k
 int kvq_decode_attn_dense(const kvq_rows* q, const kvq_rows* k, const kvq_rows* v, const int32_t* seq_lens,
                           const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int dtype, float scale,
                           int causal, int window, void* workspace, size_t workspace_bytes, void* stream) {
-  if (D != 64 && D != 128) return fail(KVQ_ERR_UNSUPPORTED, "unquantized decode supports head_dim 64 and 128, got %d", D);
+  if (D != 64 && D != 128 && D != 256)
+    return fail(KVQ_ERR_UNSUPPORTED, "unquantized decode supports head_dim 64, 128 and 256, got %d", D);
   int rc = check_attn_dense(q, k, v, out, B, Hq, Hkv, L, D, S, dtype, scale, window,
                             kvq_decode_workspace_size(B, Hq, Hkv, L, D, S, window), workspace, workspace_bytes);
   if (rc) return rc;
+  if (D == 256)
+    return hip_status(kvq::launch_wide_dense(q, k, v, seq_lens, out, B, Hq, Hkv, L, S, dtype, scale, causal, window,
+                                             workspace, (hipStream_t)stream),
+                      "decode_attn_dense launch (head_dim 256)");
   return hip_status(kvq::launch_decode_dense(q, k, v, seq_lens, out, B, Hq, Hkv, L, D, S, dtype, scale, causal, window,
                                              workspace, (hipStream_t)stream),
                     "decode_attn_dense launch");
@@ -454,10 +470,15 @@ int kvq_decode_attn_dense(const kvq_rows* q, const kvq_rows* k, const kvq_rows* 
 int kvq_prefill_attn_dense(const kvq_rows* q, const kvq_rows* k, const kvq_rows* v, const int32_t* seq_lens,
                            const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int dtype, float scale,
                            int causal, int window, void* workspace, size_t workspace_bytes, void* stream) {
-  if (D != 128) return fail(KVQ_ERR_UNSUPPORTED, "unquantized prefill supports head_dim 128, got %d", D);
+  if (D != 128 && D != 256)
+    return fail(KVQ_ERR_UNSUPPORTED, "unquantized prefill supports head_dim 128 and 256, got %d", D);
   int rc = check_attn_dense(q, k, v, out, B, Hq, Hkv, L, D, S, dtype, scale, window,
                             kvq_prefill_workspace_size(B, Hq, Hkv, L, D, S, window), workspace, workspace_bytes);
   if (rc) return rc;
+  if (D == 256)
+    return hip_status(kvq::launch_wide_dense(q, k, v, seq_lens, out, B, Hq, Hkv, L, S, dtype, scale, causal, window,
+                                             workspace, (hipStream_t)stream),
+                      "prefill_attn_dense launch (head_dim 256)");
   return hip_status(kvq::launch_prefill_dense(q, k, v, seq_lens, out, B, Hq, Hkv, L, D, S, dtype, scale, causal, window,
                                               workspace, (hipStream_t)stream),
                     "prefill_attn_dense launch");

@@ -141,11 +141,13 @@ inline hipError_t launch_combine(const MergeParams& m, int B, hipStream_t stream
   const dim3 grid((nrows + rpb - 1) / rpb);
   MergeParams mm = m;
   mm.xcd_remap = m.xcd_remap && grid.x % 8 == 0;
-  // R (rows per decode unit, 16 / scale groups per row) fixes the kernel's split strides
+  // R (rows per unit: 16 / scale groups per row for decode, 128 for the head_dim-256 kernel) fixes
+  // the kernel's split strides
   switch (m.R) {
     case 4: hipLaunchKernelGGL((combine_kernel<T, D, 4>), grid, dim3(256), 0, stream, mm, nrows); break;
     case 8: hipLaunchKernelGGL((combine_kernel<T, D, 8>), grid, dim3(256), 0, stream, mm, nrows); break;
     case 16: hipLaunchKernelGGL((combine_kernel<T, D, 16>), grid, dim3(256), 0, stream, mm, nrows); break;
+    case 128: hipLaunchKernelGGL((combine_kernel<T, D, 128>), grid, dim3(256), 0, stream, mm, nrows); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

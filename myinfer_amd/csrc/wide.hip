@@ -1,0 +1,571 @@
+// Attention at head_dim 256: the reference's blocked attention over a quantized cache
+// (m5engine/attention.py:29-103) for models whose heads are 256 wide, and every call over an
+// unquantized cache of that width (the plain KVCache before quantized_kv_start and the sliding-window
+// RotatingKVCache, which the reference leaves to mlx-lm's SDPA, attention.py:106-112).
+//
+//   out = softmax(scale * q K^T + mask) V,  K = sK * codesK + bK,  V = sV * codesV + bV
+//
+// Design (gfx950):
+//  * Workgroup: 4 waves, one per SIMD (up to 512 registers each: the 256-wide head needs 128
+//    accumulator registers per 32 query rows and 64 for the query operand), 128 query rows of one
+//    KV head, 32 per wave. Rows are head-major within the KV head (row r is position r % L of GQA
+//    head r / L), the order the split merge (combine_kernel) uses.
+//  * Keys stream in 32-key tiles through a ring of raw slots filled by buffer->LDS DMA (codes, and
+//    scales/biases into 4-byte cells, cell 32 g + k = group g of key k; raw T rows for an
+//    unquantized cache). Each tile is dequantized once per workgroup, LDS to LDS, into MFMA operands:
+//    K row-major with its 16-byte chunks XOR-swizzled by key, V transposed with its key slots
+//    permuted to the score layout. The staging of tile t + 1 runs beside the MFMAs of tile t, one
+//    barrier per tile.
+//  * Scores S^T = K Q^T with v_mfma_f32_32x32x16 (16 k-steps over the head): each lane holds 16
+//    keys of one query, so the row max / sum are lane-local plus one permlane swap; the packed
+//    probabilities are the B operand of O^T = V^T P^T (2 k-steps x 8 column blocks). The softmax
+//    scale is applied to the fp32 scores.
+//  * Operands: an unquantized cache's own rows (T, on the T MFMA); a quantized cache is dequantized
+//    to fp16 whatever T is (one fp32 FMA per element, rounded once), with the query entering the
+//    fp16 MFMA exactly as q * 2^qe (the power of two that puts the row's largest element in
+//    [2^13, 2^14)) and 2^-qe folded into the softmax scale. A bf16 cache group whose values do not
+//    fit fp16 dequantizes to inf and the rows that read it come out NaN, never a finite wrong value.
+//  * Online softmax in log2 units with threshold rescaling (the running maximum moves only when a
+//    tile's maximum exceeds it by more than 2^6, so probabilities stay below 64).
+//  * Keys are split over workgroups when the row blocks alone do not fill the GPU; the splits
+//    leave (m, l, o) partials that combine_kernel merges (merge.h).
+#include <math.h>
+
+#include <algorithm>
+#include <type_traits>
+
+#include "common.h"
+#include "dma.h"
+#include "launch.h"
+#include "merge.h"
+
+namespace kvq {
+
+constexpr int kWD = 256;     // head dim
+constexpr int kWT = 32;      // keys per tile
+constexpr int kWW = 4;       // waves per workgroup
+constexpr int kWRows = 128;  // query rows per workgroup
+constexpr float kWSlack = 6.0f;
+
+template <int BITS, int G>
+struct WideCfg {
+  static constexpr bool DENSE = BITS == 16;
+  static_assert(DENSE || ((BITS == 4 || BITS == 8) && (G == 64 || G == 128)), "4/8 bits, groups 64/128");
+  static constexpr int NG = DENSE ? 1 : kWD / G;           // scale groups per row
+  static constexpr int ROWB = kWD * BITS / 8;              // raw bytes per key row: 128, 256, 512
+  static constexpr int TB = kWT * ROWB;                    // raw bytes of a K (or V) tile
+  static constexpr int CI = TB / 1024;                     // 1 KiB DMAs per K (or V) tile
+  static constexpr int CPR = ROWB / 16;                    // 16-byte chunks per raw row
+  static constexpr int RPI = 64 / CPR;                     // raw rows per 1 KiB DMA
+  static constexpr int SBA = DENSE ? 0 : 4 * kWT * NG;     // bytes of one scale/bias cell array
+  static constexpr int NSB = DENSE ? 0 : NG / 2;           // 64-cell DMAs per array (2 groups x 32 keys)
+  static constexpr int SLOT = 2 * TB + 4 * SBA;            // [K raw][V raw][sK][bK][sV][bV]
+  static constexpr int NR = DENSE ? 2 : 3;                 // raw ring slots
+  static constexpr int CPW = 2 * CI / kWW;                 // code DMAs per wave per tile
+  static constexpr int IPW = CPW + NSB;                    // DMAs per wave per tile (wave a loads array a)
+  static constexpr int OPB = kWT * kWD * 2;                // bytes of a 16-bit operand tile (K or V^T)
+  static constexpr int LDS = NR * SLOT + 4 * OPB;          // ring + double-buffered K and V^T
+  static_assert(2 * CI % kWW == 0, "code DMAs divide over the waves");
+  static_assert(LDS <= 160 * 1024, "fits the LDS");
+};
+
+struct WideParams {
+  const uint16_t* q;
+  int64_t q_sb, q_sh, q_sl;  // elements
+  const uint8_t* kc;         // codes (quantized) or raw T rows (unquantized)
+  const uint8_t* vc;
+  int64_t kc_sb, kc_sh, kc_ss;  // bytes
+  int64_t vc_sb, vc_sh, vc_ss;  // bytes
+  const uint16_t* ks;
+  const uint16_t* kb;
+  const uint16_t* vs;
+  const uint16_t* vb;
+  int64_t ksb_sb, ksb_sh, ksb_ss;  // elements
+  int64_t vsb_sb, vsb_sh, vsb_ss;
+  const int32_t* seq_lens;
+  uint16_t* out;
+  int64_t o_sb, o_sh, o_sl;
+  float* part_o;   // nsplit > 1: o per (unit, split, row), D floats
+  float* part_ml;  // (m, l) pairs, same index
+  int Hq, Hkv, L, S, rep, nrows, rowblocks, nsplit, nunits;
+  float scale_log2;
+  int causal, window;
+};
+
+// The key held in V^T slot 8 c + e (c = 0..3, e = 0..7): PV k-step c / 2 takes, in lane half c % 2,
+// the probabilities the score layout gives that half as its values 8 (c / 2) + e, which are keys
+// 16 (c / 2) + 4 (c % 2) + (e < 4 ? e : e + 4).
+__host__ __device__ constexpr int w_slot_key(int c, int e) { return 16 * (c >> 1) + 4 * (c & 1) + (e < 4 ? e : e + 4); }
+
+template <typename T>
+__device__ __forceinline__ float dq(uint32_t code, uint32_t s_cell, uint32_t b_cell) {
+  return fmaf(to_float((uint16_t)(s_cell & 0xffffu), T{}), (float)code, to_float((uint16_t)(b_cell & 0xffffu), T{}));
+}
+
+// K of a raw tile into the K operand tile (OT elements): thread t dequantizes dims [32 p, 32 p + 32)
+// of key r (t = 8 r + p) and writes them as 4 chunks of 8 dims, chunk c of key r at position c ^ r.
+template <typename T, typename OT, int BITS, int G>
+__device__ __forceinline__ void wide_stage_k(const uint8_t* raw, uint8_t* kop, int t) {
+  using C = WideCfg<BITS, G>;
+  const int r = t >> 3, p = t & 7;
+  u4 w[4];
+  if constexpr (C::DENSE) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) w[c] = *(const u4*)(raw + r * C::ROWB + 16 * (4 * p + c));
+  } else {
+    const int g = 32 * p / G;
+    const uint32_t* cells = (const uint32_t*)(raw + 2 * C::TB);
+    const uint32_t sc = cells[32 * g + r], bc = cells[C::SBA / 4 + 32 * g + r];
+    uint32_t code[8];
+    if constexpr (BITS == 8) {
+      const u4 a = *(const u4*)(raw + r * C::ROWB + 32 * p), b = *(const u4*)(raw + r * C::ROWB + 32 * p + 16);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        code[i] = a[i];
+        code[4 + i] = b[i];
+      }
+    } else {
+      const u4 a = *(const u4*)(raw + r * C::ROWB + 16 * p);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) code[i] = a[i];
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int d = 8 * c + 2 * i;  // dims d, d + 1 of the thread's 32
+        uint32_t c0, c1;
+        if constexpr (BITS == 8) {
+          c0 = (code[d >> 2] >> (8 * (d & 3))) & 0xffu;
+          c1 = (code[(d + 1) >> 2] >> (8 * ((d + 1) & 3))) & 0xffu;
+        } else {
+          c0 = (code[d >> 3] >> (4 * (d & 7))) & 0xfu;
+          c1 = (code[(d + 1) >> 3] >> (4 * ((d + 1) & 7))) & 0xfu;
+        }
+        w[c][i] = pack2(dq<T>(c0, sc, bc), dq<T>(c1, sc, bc), OT{});
+      }
+  }
+#pragma unroll
+  for (int c = 0; c < 4; ++c) *(u4*)(kop + r * (kWD * 2) + 16 * ((4 * p + c) ^ r)) = w[c];
+}
+
+// V of a raw tile into the V^T operand tile: thread t = 64 c + j dequantizes dims [4 j, 4 j + 4) of
+// the 8 keys of slot chunk c and writes, for each of those dims, the chunk's 8 slots (16 bytes) to
+// row d at chunk position c ^ ((d >> 2) & 3) (rows are 64 bytes: 32 slots).
+template <typename T, typename OT, int BITS, int G>
+__device__ __forceinline__ void wide_stage_v(const uint8_t* raw, uint8_t* vop, int t) {
+  using C = WideCfg<BITS, G>;
+  const int c = t >> 6, j = t & 63;
+  const uint8_t* vraw = raw + C::TB;
+  float x[8][4];  // [slot e][dim i]
+  if constexpr (C::DENSE) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const u2 v = *(const u2*)(vraw + w_slot_key(c, e) * C::ROWB + 8 * j);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) x[e][i] = to_float((uint16_t)(v[i >> 1] >> (16 * (i & 1))), T{});
+    }
+  } else {
+    const int g = 4 * j / G;
+    const uint8_t* cells = raw + 2 * C::TB + 2 * C::SBA + 4 * 32 * g;  // sV, then bV one array later
+    const int kb0 = w_slot_key(c, 0);
+    const u4 s_lo = *(const u4*)(cells + 4 * kb0), s_hi = *(const u4*)(cells + 4 * (kb0 + 8));
+    const u4 b_lo = *(const u4*)(cells + C::SBA + 4 * kb0), b_hi = *(const u4*)(cells + C::SBA + 4 * (kb0 + 8));
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const uint32_t sc = e < 4 ? s_lo[e] : s_hi[e - 4], bc = e < 4 ? b_lo[e] : b_hi[e - 4];
+      uint32_t w;
+      if constexpr (BITS == 8) {
+        w = *(const uint32_t*)(vraw + w_slot_key(c, e) * C::ROWB + 4 * j);
+      } else {
+        w = *(const uint16_t*)(vraw + w_slot_key(c, e) * C::ROWB + 2 * j);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t code = BITS == 8 ? (w >> (8 * i)) & 0xffu : (w >> (4 * i)) & 0xfu;
+        x[e][i] = dq<T>(code, sc, bc);
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    u4 o;
+#pragma unroll
+    for (int a = 0; a < 4; ++a) o[a] = pack2(x[2 * a][i], x[2 * a + 1][i], OT{});
+    const int d = 4 * j + i;
+    *(u4*)(vop + d * (kWT * 2) + 16 * (c ^ ((d >> 2) & 3))) = o;
+  }
+}
+
+template <typename T, int BITS, int G>
+__global__ __launch_bounds__(kWW * 64, 1) void wide_attn_kernel(WideParams p) {
+  using C = WideCfg<BITS, G>;
+  using OT = std::conditional_t<C::DENSE, T, F16>;  // operand type
+  __shared__ __align__(16) uint8_t smem[C::LDS];
+  uint8_t* const ring = smem;
+  uint8_t* const kop = smem + C::NR * C::SLOT;  // [2][OPB]
+  uint8_t* const vop = kop + 2 * C::OPB;        // [2][OPB]
+
+  const int tid = threadIdx.x;
+  const int lane = __lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n = lane & 31, h = lane >> 5;
+
+  // ---- workgroup -> (unit, split); a unit is (sequence, KV head, row block)
+  const int unit = blockIdx.x / p.nsplit, split = blockIdx.x % p.nsplit;
+  const int b = unit / (p.Hkv * p.rowblocks);
+  const int kvh = (unit / p.rowblocks) % p.Hkv;
+  const int rb = unit % p.rowblocks;
+  const int S_b = p.seq_lens ? min(max(p.seq_lens[b], 0), p.S) : p.S;
+
+  // the row block's positions: one head's contiguous run, or every position when it spans heads
+  const int r0 = rb * kWRows, r1 = min(r0 + kWRows, p.nrows) - 1;
+  const bool one_head = r0 / p.L == r1 / p.L;
+  const int lq_min = one_head ? r0 % p.L : 0, lq_max = one_head ? r1 % p.L : p.L - 1;
+  const int key_hi = p.causal ? min(S_b, max(0, S_b - p.L + lq_max + 1)) : S_b;
+  const int key_lo = p.window > 0 ? min(key_hi, max(0, S_b - p.L + lq_min - p.window + 1)) : 0;
+  const int t_lo = key_lo / kWT, t_hi = (key_hi + kWT - 1) / kWT;
+  const int cps = (t_hi - t_lo + p.nsplit - 1) / p.nsplit;
+  const int t_begin = min(t_hi, t_lo + split * cps), t_end = min(t_hi, t_begin + cps);
+  const int ntile = t_end - t_begin;
+
+  // ---- raw tile DMAs: wave w issues code DMAs [w CPW, (w + 1) CPW) (K first, then V) and the NSB
+  // loads of scale/bias array w (sK, bK, sV, bV)
+  const uint8_t* kbase = p.kc + (int64_t)b * p.kc_sb + (int64_t)kvh * p.kc_sh;
+  const uint8_t* vbase = p.vc + (int64_t)b * p.vc_sb + (int64_t)kvh * p.vc_sh;
+  const __amdgpu_buffer_rsrc_t krs = make_rsrc(kbase, (uint32_t)((int64_t)S_b * p.kc_ss));
+  const __amdgpu_buffer_rsrc_t vrs = make_rsrc(vbase, (uint32_t)((int64_t)S_b * p.vc_ss));
+  __amdgpu_buffer_rsrc_t code_r[C::CPW];
+  uint32_t code_vo[C::CPW], code_lds[C::CPW];
+  int64_t code_ss[C::CPW];
+#pragma unroll
+  for (int j = 0; j < C::CPW; ++j) {
+    const int q = wave * C::CPW + j;
+    const bool is_k = q < C::CI;
+    const int i = is_k ? q : q - C::CI;
+    code_r[j] = is_k ? krs : vrs;
+    code_ss[j] = is_k ? p.kc_ss : p.vc_ss;
+    code_vo[j] = (uint32_t)((i * C::RPI + lane / C::CPR) * code_ss[j] + 16 * (lane % C::CPR));
+    code_lds[j] = (is_k ? 0 : C::TB) + 1024 * i;
+  }
+  __amdgpu_buffer_rsrc_t sb_r = krs;
+  int64_t sb_ss = 0;
+  uint32_t sb_vo[C::NSB > 0 ? C::NSB : 1] = {};
+  if constexpr (!C::DENSE) {
+    const uint16_t* arr = wave == 0 ? p.ks : wave == 1 ? p.kb : wave == 2 ? p.vs : p.vb;
+    const int64_t sb_b = wave < 2 ? p.ksb_sb : p.vsb_sb, sb_h = wave < 2 ? p.ksb_sh : p.vsb_sh;
+    sb_ss = wave < 2 ? p.ksb_ss : p.vsb_ss;
+    sb_r = make_rsrc(arr + (int64_t)b * sb_b + (int64_t)kvh * sb_h, (uint32_t)((int64_t)S_b * sb_ss * 2));
+#pragma unroll
+    for (int j = 0; j < C::NSB; ++j) sb_vo[j] = (uint32_t)(2 * ((lane & 31) * sb_ss + 2 * j + (lane >> 5)));
+  }
+  const uint32_t ring_lds = lds_addr(ring);
+  const int t_last = max(ntile - 1, 0);
+  // tile i of this split into ring slot i % NR; past the last tile it re-reads the last one, so every
+  // wait below sees the same number of loads in flight
+  auto issue = [&](int i) {
+    const int k0 = (t_begin + min(i, t_last)) * kWT;
+    const uint32_t slot = ring_lds + (uint32_t)((i % C::NR) * C::SLOT);
+#pragma unroll
+    for (int j = 0; j < C::CPW; ++j) dma_b128(code_r[j], slot + code_lds[j], code_vo[j], (uint32_t)(k0 * code_ss[j]));
+    if constexpr (!C::DENSE) {
+#pragma unroll
+      for (int j = 0; j < C::NSB; ++j)
+        dma_b16(sb_r, slot + 2 * C::TB + C::SBA * wave + 256 * j, sb_vo[j], (uint32_t)(2 * k0 * sb_ss));
+    }
+  };
+
+  // ---- this lane's query row and its operand (rows past the block's end read row 0 of the head
+  // and are never stored)
+  const int row = r0 + 32 * wave + n;
+  const bool row_ok = row < p.nrows;
+  const bool wave_on = r0 + 32 * wave < p.nrows;  // wave-uniform: the wave has rows to compute
+  const int hq = kvh * p.rep + (row_ok ? row / p.L : 0);
+  const int lq = row_ok ? row % p.L : 0;
+  const int qpos = S_b - p.L + lq;
+  const int lo_r = p.window > 0 ? max(0, qpos - p.window + 1) : 0;
+  const int hi_r = p.causal ? min(S_b, qpos + 1) : S_b;
+  // keys every row of the block sees: tiles inside need no mask
+  const int lo_all = p.window > 0 ? max(0, S_b - p.L + lq_max - p.window + 1) : 0;
+  const int hi_all = p.causal ? S_b - p.L + lq_min + 1 : S_b;
+
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int i = 0; i < C::NR; ++i) issue(i);
+  __builtin_amdgcn_sched_barrier(0);
+
+  u4 qop[16];
+  float kf = p.scale_log2;  // fp32 score -> log2 units
+  {
+    const uint16_t* qrow = p.q + (int64_t)b * p.q_sb + (int64_t)hq * p.q_sh + (int64_t)lq * p.q_sl + 8 * h;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) qop[j] = *(const u4*)(qrow + 16 * j);
+    if constexpr (!C::DENSE) {
+      // q * 2^qe in fp16, exact: the row's largest |q| lands in [2^13, 2^14)
+      float qmax = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+#pragma unroll
+        for (int a = 0; a < 8; ++a) qmax = fmaxf(qmax, fabsf(to_float((uint16_t)(qop[j][a >> 1] >> (16 * (a & 1))), T{})));
+      qmax = max_xor32(qmax);
+      int qe = 0;
+      if (qmax > 0.0f) {
+        frexpf(qmax, &qe);
+        qe = 14 - qe;
+      }
+      const float qs = ldexpf(1.0f, qe);
+      kf = ldexpf(p.scale_log2, -qe);
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+          qop[j][a] = pack_f16x2(to_float((uint16_t)(qop[j][a] & 0xffffu), T{}) * qs,
+                                 to_float((uint16_t)(qop[j][a] >> 16), T{}) * qs);
+    }
+  }
+
+  float m_run = -INFINITY, l_run = 0.0f;
+  f16v oacc[8];
+#pragma unroll
+  for (int db = 0; db < 8; ++db) oacc[db] = f16v{};
+
+  // K operand of k-step j: key n, dims 16 j + 8 h .. + 8, at chunk position (2 j + h) ^ n; V^T
+  // operand of column block db, k-step s: row d = 32 db + n, chunk position (2 s + h) ^ ((n >> 2) & 3)
+  const uint32_t k_off = (uint32_t)(n * (kWD * 2));
+  const uint32_t v_off = (uint32_t)(n * (kWT * 2));
+  const int v_sw = (n >> 2) & 3;
+
+  auto compute = [&](const uint8_t* kt, const uint8_t* vt, int k0) {
+    f16v s = f16v{};
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const u4 a = *(const u4*)(kt + k_off + 16 * ((2 * j + h) ^ n));
+      s = mfma_32x32x16(a, qop[j], s, OT{});
+    }
+    // value i of the lane is key k0 + 8 (i / 4) + 4 h + i % 4 of query row n
+    if (!(k0 >= lo_all && k0 + kWT <= hi_all)) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int k = k0 + 8 * (i >> 2) + 4 * h + (i & 3);
+        if (k < lo_r || k >= hi_r) s[i] = -INFINITY;
+      }
+    }
+    float tm = s[0];
+#pragma unroll
+    for (int i = 1; i < 16; ++i) tm = fmaxf(tm, s[i]);
+    tm = max_xor32(tm) * kf;
+    if (__builtin_amdgcn_ballot_w64(tm > m_run + kWSlack) != 0) {
+      const float m_new = tm > m_run + kWSlack ? fmaxf(m_run, tm) : m_run;
+      const float corr = m_new == m_run ? 1.0f : exp2_fast(m_run - m_new);
+      l_run *= corr;
+#pragma unroll
+      for (int db = 0; db < 8; ++db) oacc[db] *= corr;
+      m_run = m_new;
+    }
+    const float nm = m_run == -INFINITY ? 0.0f : -m_run;
+    u4 pop[2];
+#pragma unroll
+    for (int st = 0; st < 2; ++st)
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        const float p0 = exp2_fast(fmaf(s[8 * st + 2 * a], kf, nm));
+        const float p1 = exp2_fast(fmaf(s[8 * st + 2 * a + 1], kf, nm));
+        pop[st][a] = pack2(p0, p1, OT{});
+        l_run = add_pair(pop[st][a], l_run, OT{});
+      }
+#pragma unroll
+    for (int db = 0; db < 8; ++db)
+#pragma unroll
+      for (int st = 0; st < 2; ++st) {
+        const u4 a = *(const u4*)(vt + 32 * db * (kWT * 2) + v_off + 16 * ((2 * st + h) ^ v_sw));
+        oacc[db] = mfma_32x32x16(a, pop[st], oacc[db], OT{});
+      }
+  };
+
+  // ---- the tile loop: tile t is computed from operand buffer t % 2 while tile t + 1 is staged into
+  // the other; raw slot t % NR is refilled with tile t + NR once tile t is staged
+  if (ntile > 0) {
+    wait_vm<0>();  // the query and the first NR raw tiles
+    __syncthreads();
+    wide_stage_k<T, OT, BITS, G>(ring, kop, tid);
+    wide_stage_v<T, OT, BITS, G>(ring, vop, tid);
+    for (int t = 0; t < ntile; ++t) {
+      if constexpr (C::NR == 3) {
+        wait_vm<C::IPW>();  // tile t + 1 has landed (tile t + 2 may be in flight)
+      } else {
+        wait_vm<0>();
+      }
+      __syncthreads();  // operand buffer t % 2 is complete; raw slot t % NR is free
+      issue(t + C::NR);
+      const int nb = (t + 1) & 1;
+      if (t + 1 < ntile) {
+        const uint8_t* raw1 = ring + opaque(((t + 1) % C::NR) * C::SLOT);
+        wide_stage_k<T, OT, BITS, G>(raw1, kop + opaque(nb * C::OPB), tid);
+        wide_stage_v<T, OT, BITS, G>(raw1, vop + opaque(nb * C::OPB), tid);
+      }
+      if (wave_on) compute(kop + opaque((t & 1) * C::OPB), vop + opaque((t & 1) * C::OPB), (t_begin + t) * kWT);
+    }
+  }
+  wait_vm<0>();  // the look-ahead loads land before the workgroup's LDS is released
+
+  // ---- epilogue: lane (n, h) holds O^T rows 32 db + 8 i + 4 h + j (j = 0..3) of query row n
+  const float l_tot = add_xor32(l_run);
+  if (!row_ok) return;
+  if (p.nsplit == 1) {
+    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+    uint16_t* orow = p.out + (int64_t)b * p.o_sb + (int64_t)hq * p.o_sh + (int64_t)lq * p.o_sl + 4 * h;
+#pragma unroll
+    for (int db = 0; db < 8; ++db)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        u2 w;
+        w[0] = pack2(oacc[db][4 * i] * inv, oacc[db][4 * i + 1] * inv, T{});
+        w[1] = pack2(oacc[db][4 * i + 2] * inv, oacc[db][4 * i + 3] * inv, T{});
+        *(u2*)(orow + 32 * db + 8 * i) = w;
+      }
+  } else {
+    const int64_t pi = ((int64_t)unit * p.nsplit + split) * kWRows + (row - r0);
+    float* po = p.part_o + pi * kWD + 4 * h;
+#pragma unroll
+    for (int db = 0; db < 8; ++db)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        *(f4*)(po + 32 * db + 8 * i) = f4{oacc[db][4 * i], oacc[db][4 * i + 1], oacc[db][4 * i + 2], oacc[db][4 * i + 3]};
+    if (h == 0) ((float2*)p.part_ml)[pi] = make_float2(m_run, l_tot);
+  }
+}
+
+// ------------------------------------------------------------------------------------------
+// Host side: plan, workspace, launch.
+
+struct WidePlan {
+  int rowblocks, nunits, nsplit;
+};
+
+// Splits fill about 256 workgroups when the row blocks alone do not; each split keeps at least two
+// tiles of the widest row block's keys.
+static WidePlan wide_plan(int B, int Hq, int Hkv, int L, int S, int window) {
+  WidePlan pl;
+  const int nrows = (Hq / Hkv) * L;
+  pl.rowblocks = (nrows + kWRows - 1) / kWRows;
+  pl.nunits = B * Hkv * pl.rowblocks;
+  const int span = window > 0 ? std::min(S, window + std::min(L, kWRows) - 1 + kWT) : S;
+  const int tiles = (span + kWT - 1) / kWT;
+  pl.nsplit = 1;
+  if (pl.nunits < 192) pl.nsplit = std::max(1, std::min({(256 + pl.nunits - 1) / pl.nunits, tiles / 2, kMaxSplit}));
+  return pl;
+}
+
+// Workspace: [the arrival counter block every launch reserves (merge.h), left untouched][(m, l) per
+// row and split][o per row and split]; a launch without splits writes none of it.
+size_t wide_workspace_bytes(int B, int Hq, int Hkv, int L, int S, int window) {
+  const WidePlan pl = wide_plan(B, Hq, Hkv, L, S, window);
+  if (pl.nsplit == 1) return kCounterBytes;
+  auto up = [](size_t x) { return (x + 255) / 256 * 256; };
+  const size_t rows = (size_t)pl.nunits * pl.nsplit * kWRows;
+  return kCounterBytes + up(rows * sizeof(float2)) + up(rows * kWD * sizeof(float));
+}
+
+template <typename T, int BITS, int G>
+static hipError_t launch_wide_t(const WideParams& p, hipStream_t stream) {
+  hipLaunchKernelGGL((wide_attn_kernel<T, BITS, G>), dim3(p.nunits * p.nsplit), dim3(kWW * 64), 0, stream, p);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || p.nsplit == 1) return e;
+  MergeParams m;
+  m.part_o = p.part_o;
+  m.part_ml = p.part_ml;
+  m.out = p.out;
+  m.o_sb = p.o_sb;
+  m.o_sh = p.o_sh;
+  m.o_sl = p.o_sl;
+  m.Hq = p.Hq;
+  m.Hkv = p.Hkv;
+  m.L = p.L;
+  m.rep = p.rep;
+  m.R = kWRows;
+  m.rowblocks = p.rowblocks;
+  m.nsplit = p.nsplit;
+  m.xcd_remap = 0;
+  return launch_combine<T, kWD>(m, p.nunits / (p.Hkv * p.rowblocks), stream);
+}
+
+static WideParams wide_params(const kvq_rows* q, const int32_t* seq_lens, const kvq_rows* out, int B, int Hq, int Hkv,
+                              int L, int S, float scale, int causal, int window, void* workspace) {
+  const WidePlan pl = wide_plan(B, Hq, Hkv, L, S, window);
+  WideParams p{};
+  p.q = (const uint16_t*)q->data;
+  p.q_sb = q->stride_b;
+  p.q_sh = q->stride_h;
+  p.q_sl = q->stride_l;
+  p.seq_lens = seq_lens;
+  p.out = (uint16_t*)out->data;
+  p.o_sb = out->stride_b;
+  p.o_sh = out->stride_h;
+  p.o_sl = out->stride_l;
+  const size_t rows = (size_t)pl.nunits * pl.nsplit * kWRows;
+  p.part_ml = (float*)((char*)workspace + kCounterBytes);
+  p.part_o = (float*)((char*)workspace + kCounterBytes + (rows * sizeof(float2) + 255) / 256 * 256);
+  p.Hq = Hq;
+  p.Hkv = Hkv;
+  p.L = L;
+  p.S = S;
+  p.rep = Hq / Hkv;
+  p.nrows = p.rep * L;
+  p.rowblocks = pl.rowblocks;
+  p.nsplit = pl.nsplit;
+  p.nunits = pl.nunits;
+  p.scale_log2 = scale * 1.4426950408889634f;
+  p.causal = causal;
+  p.window = window;
+  return p;
+}
+
+hipError_t launch_wide(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v, const int32_t* seq_lens,
+                       const kvq_rows* out, int B, int Hq, int Hkv, int L, int S, int bits, int G, int dtype,
+                       float scale, int causal, int window, void* workspace, hipStream_t stream) {
+  WideParams p = wide_params(q, seq_lens, out, B, Hq, Hkv, L, S, scale, causal, window, workspace);
+  p.kc = (const uint8_t*)k->codes;
+  p.vc = (const uint8_t*)v->codes;
+  p.kc_sb = k->codes_stride_b * 4;
+  p.kc_sh = k->codes_stride_h * 4;
+  p.kc_ss = k->codes_stride_s * 4;
+  p.vc_sb = v->codes_stride_b * 4;
+  p.vc_sh = v->codes_stride_h * 4;
+  p.vc_ss = v->codes_stride_s * 4;
+  p.ks = (const uint16_t*)k->scales;
+  p.kb = (const uint16_t*)k->biases;
+  p.vs = (const uint16_t*)v->scales;
+  p.vb = (const uint16_t*)v->biases;
+  p.ksb_sb = k->sb_stride_b;
+  p.ksb_sh = k->sb_stride_h;
+  p.ksb_ss = k->sb_stride_s;
+  p.vsb_sb = v->sb_stride_b;
+  p.vsb_sh = v->sb_stride_h;
+  p.vsb_ss = v->sb_stride_s;
+  auto go = [&](auto t) -> hipError_t {
+    using T = decltype(t);
+    if (bits == 8 && G == 64) return launch_wide_t<T, 8, 64>(p, stream);
+    if (bits == 8 && G == 128) return launch_wide_t<T, 8, 128>(p, stream);
+    if (bits == 4 && G == 64) return launch_wide_t<T, 4, 64>(p, stream);
+    if (bits == 4 && G == 128) return launch_wide_t<T, 4, 128>(p, stream);
+    return hipErrorInvalidValue;
+  };
+  return dtype == KVQ_DTYPE_BF16 ? go(BF16{}) : go(F16{});
+}
+
+hipError_t launch_wide_dense(const kvq_rows* q, const kvq_rows* k, const kvq_rows* v, const int32_t* seq_lens,
+                             const kvq_rows* out, int B, int Hq, int Hkv, int L, int S, int dtype, float scale,
+                             int causal, int window, void* workspace, hipStream_t stream) {
+  WideParams p = wide_params(q, seq_lens, out, B, Hq, Hkv, L, S, scale, causal, window, workspace);
+  p.kc = (const uint8_t*)k->data;
+  p.vc = (const uint8_t*)v->data;
+  p.kc_sb = k->stride_b * 2;
+  p.kc_sh = k->stride_h * 2;
+  p.kc_ss = k->stride_l * 2;
+  p.vc_sb = v->stride_b * 2;
+  p.vc_sh = v->stride_h * 2;
+  p.vc_ss = v->stride_l * 2;
+  return dtype == KVQ_DTYPE_BF16 ? launch_wide_t<BF16, 16, 64>(p, stream) : launch_wide_t<F16, 16, 64>(p, stream);
+}
+
+}  // namespace kvq

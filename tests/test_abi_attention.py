@@ -58,7 +58,8 @@ def test_prefill_workspace_size():
 
 
 @pytest.mark.parametrize("kw,code,needle", [
-    (dict(D=256), _lib.ERR_UNSUPPORTED, "head_dim 64 and 128"),
+    (dict(D=512), _lib.ERR_UNSUPPORTED, "head_dim 64, 128 and 256"),
+    (dict(D=256, group=32), _lib.ERR_UNSUPPORTED, "group_size"),
     (dict(D=64, group=128), _lib.ERR_UNSUPPORTED, "group_size"),
     (dict(bits=3), _lib.ERR_UNSUPPORTED, "bits"),
     (dict(group=16), _lib.ERR_UNSUPPORTED, "group_size"),
@@ -160,7 +161,11 @@ def test_prefill_rejects_unaligned_scale_rows(field, value):
 
 
 def test_unquantized_head_dims():
-    # the unquantized kernels keep head_dim 64/128 (decode) and 128 (prefill)
+    # the unquantized kernels take head_dim 64/128/256 (decode) and 128/256 (prefill)
     lib = _lib.lib()
-    _expect(_dense(lib.kvq_prefill_attn_dense, D=64), _lib.ERR_UNSUPPORTED, "head_dim 128")
-    _expect(_dense(lib.kvq_decode_attn_dense, D=256), _lib.ERR_UNSUPPORTED, "head_dim 64 and 128")
+    _expect(_dense(lib.kvq_prefill_attn_dense, D=64), _lib.ERR_UNSUPPORTED, "head_dim 128 and 256")
+    _expect(_dense(lib.kvq_decode_attn_dense, D=512), _lib.ERR_UNSUPPORTED, "head_dim 64, 128 and 256")
+    # head_dim 256 needs a workspace from both size queries
+    assert lib.kvq_prefill_workspace_size(1, 8, 4, 512, 256, 4096, 0) >= 256
+    assert lib.kvq_decode_workspace_size(1, 8, 4, 1, 256, 4096, 0) >= lib.kvq_prefill_workspace_size(1, 8, 4, 1, 256,
+                                                                                                    4096, 0)

@@ -94,6 +94,31 @@ def test_prefill_fuzz_groups_and_head_dims(case):
                 seed=7600 + case, cap=cap, group=group, D=D, what=f"fuzz-gd {case}")
 
 
+@pytest.mark.parametrize("case", range(16))
+def test_head_dim_256_fuzz(case):
+    # the head_dim-256 kernel: quantized prefill (groups 64/128) and unquantized decode / prefill
+    rng = random.Random(7700 + case)
+    dtype = rng.choice(DTYPES)
+    Hkv, rep = rng.choice([1, 2, 4, 8]), rng.choice([1, 2, 4])
+    B = rng.choice([1, 2])
+    if case % 2 == 0:
+        bits, group = rng.choice([4, 8]), rng.choice([64, 128])
+        L = rng.randrange(1, 300)
+        S = rng.randrange(L, 3000)
+        cap = S + rng.choice([0, 0, rng.randrange(1, 300)])
+        causal, window, seq_lens = _masks(rng, B, L, S)
+        TP.run_case(B, Hkv * rep, Hkv, L, S, bits, dtype, causal=causal, window=window, seq_lens=seq_lens,
+                    seed=7700 + case, cap=cap, group=group, D=256, what=f"fuzz-d256 {case}")
+    else:
+        kernel = rng.choice(["decode", "prefill"])
+        L = rng.choice([1, 2, 4]) if kernel == "decode" else rng.randrange(1, 300)
+        S = rng.randrange(L, 2500)
+        cap = S + rng.choice([0, 0, rng.randrange(1, 300)])
+        causal, window, seq_lens = _masks(rng, B, L, S)
+        TN.run_case(kernel, B, Hkv * rep, Hkv, L, S, 256, dtype, causal=causal, window=window, seq_lens=seq_lens,
+                    seed=7700 + case, cap=cap, what=f"fuzz-d256 {case}")
+
+
 @pytest.mark.parametrize("case", range(24))
 def test_unquantized_fuzz(case):
     rng = random.Random(7300 + case)
