@@ -38,7 +38,8 @@ The "extra" object also times the other decode configurations, C2 at batch 8 ove
 without fused RoPE (device time from a graph replay, and the host time of an eager call), and,
 over unquantized caches, the
 C5 window layer's decode step and prefill chunk and a C3 chunk (attention FLOPs: 4 * D * Hq per
-unmasked query-key pair).
+unmasked query-key pair), and head_dim-256 legs (Gemma-3-12B heads: a quantized and an unquantized
+window prefill chunk, an unquantized decode step).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra] [--no-parity]
                        [--no-prefill | --prefill-only] [--calibrate-copy]
@@ -565,8 +566,9 @@ def time_prefill(cfg, steps, warmup, device, want_parity=False):
 
 
 def time_attention_shape(desc, q, k, v, scale, flops, steps, device, **mask):
-    """Attention-kernel TFLOP/s of one call shape over an unquantized cache: `steps` calls captured
-    in a HIP graph and replayed once, timed with events."""
+    """Attention-kernel TFLOP/s of one prefill call shape (k, v: unquantized tensors, or quantized
+    triples with bits / group_size among the keyword arguments): `steps` calls captured in a HIP
+    graph and replayed once, timed with events."""
     import torch
 
     from myinfer_amd import kernels
@@ -619,6 +621,69 @@ def dense_prefill_extras(steps, device):
     res["C3-last-chunk-dense"] = time_attention_shape(
         "C3 last chunk over an unquantized bf16 cache (512 queries, 16384 keys, causal)", q, k, v,
         1.0 / math.sqrt(D), prefill_flops(N, Hq, D, N - C, N), steps, device, causal=True)
+    return res
+
+
+def wide_extras(steps, device):
+    """Head_dim 256 (Gemma-3-12B attention: 16 query / 8 KV heads): a 2048-token prefill chunk after
+    6144 earlier tokens over an 8-bit quantized bf16 cache, a sliding-window (1024) chunk of the same
+    size over an unquantized cache, and a batch-4 decode step over 8192 unquantized rows (graph
+    replay; HBM bytes = the K/V rows read plus the query and output)."""
+    import torch
+
+    from myinfer_amd import kernels
+
+    g = torch.Generator(device=device).manual_seed(1010)
+    res = {}
+    B, Hq, Hkv, D, S, C = 1, 16, 8, 256, 8192, 2048
+    T = torch.bfloat16
+    k = torch.randn((B, Hkv, S, D), generator=g, device=device).to(T)
+    v = torch.randn((B, Hkv, S, D), generator=g, device=device).to(T)
+    q = torch.randn((B, Hq, C, D), generator=g, device=device).to(T)
+    trip = []
+    for x in (k, v):
+        c = torch.zeros((B, Hkv, S, D // 4), dtype=torch.int32, device=device).view(torch.uint32)
+        sc = torch.zeros((B, Hkv, S, D // 64), dtype=T, device=device)
+        bi = torch.zeros_like(sc)
+        kernels.quantize_append(x, (c, sc, bi), group_size=64, bits=8)
+        trip.append((c, sc, bi))
+    res["D256-prefill-q8"] = time_attention_shape(
+        "head_dim 256 prefill chunk over an 8-bit cache (Gemma-3-12B heads, 2048 queries, 8192 keys, causal)",
+        q, trip[0], trip[1], 1.0 / math.sqrt(D), prefill_flops(S, Hq, D, S - C, S), steps, device, causal=True,
+        bits=8, group_size=64)
+    W = 1024
+    res["D256-window-prefill-dense"] = time_attention_shape(
+        "head_dim 256 window-1024 prefill chunk over an unquantized bf16 cache (2048 queries, 8192 keys)",
+        q, k, v, 1.0 / math.sqrt(D), prefill_flops(S, Hq, D, S - C, S, window=W), steps, device, causal=True,
+        window=W)
+    del trip
+    B = 4
+    k = torch.randn((B, Hkv, S, D), generator=g, device=device).to(T)
+    v = torch.randn((B, Hkv, S, D), generator=g, device=device).to(T)
+    q = torch.randn((B, Hq, 1, D), generator=g, device=device).to(T)
+    out = torch.empty_like(q)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        call = kernels.prepare_attention(q, k, v, 1.0 / math.sqrt(D), out=out)
+    call()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        for _ in range(steps):
+            call()
+    graph.replay()
+    torch.cuda.synchronize()
+    s_, e_ = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s_.record()
+    graph.replay()
+    e_.record()
+    torch.cuda.synchronize()
+    us = s_.elapsed_time(e_) / steps * 1e3
+    nbytes = 2 * k.numel() * 2 + 2 * q.numel() * 2
+    res["D256-decode-dense-b4"] = {"gbs": round(nbytes / us / 1e3, 1), "frac": round(nbytes / us / 1e3 / PEAK_HBM_GBS, 4),
+                                   "us_per_step": round(us, 3), "bytes": nbytes, "kernel": call.symbol}
+    del graph
     return res
 
 
@@ -925,6 +990,11 @@ def main():
         for name, r in dense_prefill_extras(min(args.steps, 20), device).items():
             extra[name] = r
             log(f"[bench] {name}: {r['tflops']:.1f} TFLOP/s ({r['us_per_call']:.1f} us/call)")
+        torch.cuda.empty_cache()
+        for name, r in wide_extras(min(args.steps, 20), device).items():
+            extra[name] = r
+            log(f"[bench] {name}: " + (f"{r['tflops']:.1f} TFLOP/s ({r['us_per_call']:.1f} us/call)" if "tflops" in r
+                                       else f"{r['gbs']:.1f} GB/s ({r['us_per_step']:.2f} us/step)"))
         torch.cuda.empty_cache()
 
     cpu = None

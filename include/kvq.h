@@ -172,9 +172,11 @@ int kvq_decode_attn_static(const kvq_rows* q, const kvq_qtensor* k, const kvq_qt
 /*
  * Attention for prefill chunks (any L): same contract as kvq_decode_attn, MFMA tiles with
  * K/V tiles dequantized into LDS. Replaces m5engine/attention.py:29-103 for L > 1.
- * Requirements: D in {64, 128}; group_size in {32, 64, 128}, at most D; bits in {4, 8}; Hq a multiple
- *   of Hkv; with two or more scale groups per row, scale and bias rows 4-byte aligned (even
- *   strides; MLX's contiguous layout is).
+ * Requirements: D in {64, 128, 256}; group_size in {32, 64, 128} with D / 4 <= group_size <= D;
+ *   bits in {4, 8}; Hq a multiple of Hkv; at D = 64 or 128 with two or more scale groups per row,
+ *   scale and bias rows 4-byte aligned (even strides; MLX's contiguous layout is).
+ * D = 256 runs a kernel of its own (128 query rows per workgroup, 32-key tiles) whose split key
+ * ranges are merged by a second, small launch on the same stream.
  */
 int kvq_prefill_attn(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v,
                      const int32_t* seq_lens, const kvq_rows* out,
@@ -195,8 +197,9 @@ size_t kvq_prefill_workspace_size(int B, int Hq, int Hkv, int L, int D, int S, i
  * unquantized.
  * The products run on MFMA in the cache's own type (fp16 or bf16, exact operands) with fp32
  * accumulation; the probabilities enter the PV product in that type.
- * Requirements: decode D in {64, 128}, prefill D == 128; rows 16-byte aligned with strides that are
- * multiples of 8 elements.
+ * Requirements: decode D in {64, 128, 256}, prefill D in {128, 256}; rows 16-byte aligned with
+ * strides that are multiples of 8 elements. At D = 256 both entry points run the head_dim-256
+ * prefill kernel (any L).
  */
 int kvq_decode_attn_dense(const kvq_rows* q, const kvq_rows* k, const kvq_rows* v,
                           const int32_t* seq_lens, const kvq_rows* out,
