@@ -279,7 +279,6 @@ __global__ __launch_bounds__(kWW * 64, 1) void wide_attn_kernel(WideParams p) {
   // and are never stored)
   const int row = r0 + 32 * wave + n;
   const bool row_ok = row < p.nrows;
-  const bool wave_on = r0 + 32 * wave < p.nrows;  // wave-uniform: the wave has rows to compute
   const int hq = kvh * p.rep + (row_ok ? row / p.L : 0);
   const int lq = row_ok ? row % p.L : 0;
   const int qpos = S_b - p.L + lq;
@@ -335,13 +334,17 @@ __global__ __launch_bounds__(kWW * 64, 1) void wide_attn_kernel(WideParams p) {
   const uint32_t v_off = (uint32_t)(n * (kWT * 2));
   const int v_sw = (n >> 2) & 3;
 
-  auto compute = [&](const uint8_t* kt, const uint8_t* vt, int k0) {
+  // One step: tile t's products from operand buffers (kt, vt), and tile t + 1's staging from raw
+  // slot raw1 into (kd, vd). The step is one basic block: each product's operand reads are issued
+  // ahead of its MFMA chain, and the staging's independent VALU work fills the chain's issue slots.
+  auto step = [&](const uint8_t* kt, const uint8_t* vt, int k0, const uint8_t* raw1, uint8_t* kd, uint8_t* vd) {
+    u4 ka[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) ka[j] = *(const u4*)(kt + k_off + 16 * ((2 * j + h) ^ n));
+    wide_stage_k<T, OT, BITS, G>(raw1, kd, tid);
     f16v s = f16v{};
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const u4 a = *(const u4*)(kt + k_off + 16 * ((2 * j + h) ^ n));
-      s = mfma_32x32x16(a, qop[j], s, OT{});
-    }
+    for (int j = 0; j < 16; ++j) s = mfma_32x32x16(ka[j], qop[j], s, OT{});
     // value i of the lane is key k0 + 8 (i / 4) + 4 h + i % 4 of query row n
     if (!(k0 >= lo_all && k0 + kWT <= hi_all)) {
 #pragma unroll
@@ -373,17 +376,18 @@ __global__ __launch_bounds__(kWW * 64, 1) void wide_attn_kernel(WideParams p) {
         pop[st][a] = pack2(p0, p1, OT{});
         l_run = add_pair(pop[st][a], l_run, OT{});
       }
+    u4 va[16];
 #pragma unroll
-    for (int db = 0; db < 8; ++db)
+    for (int i = 0; i < 16; ++i) va[i] = *(const u4*)(vt + 32 * (i >> 1) * (kWT * 2) + v_off + 16 * ((2 * (i & 1) + h) ^ v_sw));
+    wide_stage_v<T, OT, BITS, G>(raw1, vd, tid);
 #pragma unroll
-      for (int st = 0; st < 2; ++st) {
-        const u4 a = *(const u4*)(vt + 32 * db * (kWT * 2) + v_off + 16 * ((2 * st + h) ^ v_sw));
-        oacc[db] = mfma_32x32x16(a, pop[st], oacc[db], OT{});
-      }
+    for (int i = 0; i < 16; ++i) oacc[i >> 1] = mfma_32x32x16(va[i], pop[i & 1], oacc[i >> 1], OT{});
   };
 
   // ---- the tile loop: tile t is computed from operand buffer t % 2 while tile t + 1 is staged into
-  // the other; raw slot t % NR is refilled with tile t + NR once tile t is staged
+  // the other; raw slot t % NR is refilled with tile t + NR once tile t is staged. Every step stages:
+  // past the last tile the raw slot holds a re-read of the last tile, staged into a buffer no step
+  // reads. Every wave computes (rows past the block's end are clamped and never stored).
   if (ntile > 0) {
     wait_vm<0>();  // the query and the first NR raw tiles
     __syncthreads();
@@ -397,13 +401,8 @@ __global__ __launch_bounds__(kWW * 64, 1) void wide_attn_kernel(WideParams p) {
       }
       __syncthreads();  // operand buffer t % 2 is complete; raw slot t % NR is free
       issue(t + C::NR);
-      const int nb = (t + 1) & 1;
-      if (t + 1 < ntile) {
-        const uint8_t* raw1 = ring + opaque(((t + 1) % C::NR) * C::SLOT);
-        wide_stage_k<T, OT, BITS, G>(raw1, kop + opaque(nb * C::OPB), tid);
-        wide_stage_v<T, OT, BITS, G>(raw1, vop + opaque(nb * C::OPB), tid);
-      }
-      if (wave_on) compute(kop + opaque((t & 1) * C::OPB), vop + opaque((t & 1) * C::OPB), (t_begin + t) * kWT);
+      const int cb = opaque((t & 1) * C::OPB), nb = opaque(((t + 1) & 1) * C::OPB);
+      step(kop + cb, vop + cb, (t_begin + t) * kWT, ring + opaque(((t + 1) % C::NR) * C::SLOT), kop + nb, vop + nb);
     }
   }
   wait_vm<0>();  // the look-ahead loads land before the workgroup's LDS is released
