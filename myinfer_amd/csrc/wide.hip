@@ -13,8 +13,7 @@
 //  * Keys stream in 32-key tiles through a ring of raw slots filled by buffer->LDS DMA (codes, and
 //    scales/biases into 4-byte cells, cell 32 g + k = group g of key k; raw T rows for an
 //    unquantized cache). Each tile is dequantized once per workgroup, LDS to LDS, into MFMA operands:
-//    K row-major with its 16-byte chunks XOR-swizzled by key, V transposed with its key slots
-//    permuted to the score layout. The staging of tile t + 1 runs beside the MFMAs of tile t, one
+//    K row-major with padded rows, V transposed with its key slots permuted to the score layout. The staging of tile t + 1 runs beside the MFMAs of tile t, one
 //    barrier per tile.
 //  * Scores S^T = K Q^T with v_mfma_f32_32x32x16 (16 k-steps over the head): each lane holds 16
 //    keys of one query, so the row max / sum are lane-local plus one permlane swap; the packed
@@ -63,8 +62,10 @@ struct WideCfg {
   static constexpr int NR = DENSE ? 2 : 3;                 // raw ring slots
   static constexpr int CPW = 2 * CI / kWW;                 // code DMAs per wave per tile
   static constexpr int IPW = CPW + NSB;                    // DMAs per wave per tile (wave a loads array a)
-  static constexpr int OPB = kWT * kWD * 2;                // bytes of a 16-bit operand tile (K or V^T)
-  static constexpr int LDS = NR * SLOT + 4 * OPB;          // ring + double-buffered K and V^T
+  static constexpr int KROW = kWD * 2 + 16;                // K operand row pitch: 512 bytes + 16 of padding
+  static constexpr int KOPB = kWT * KROW;                  // bytes of a K operand tile
+  static constexpr int VOPB = kWD * kWT * 2;               // bytes of a V^T operand tile
+  static constexpr int LDS = NR * SLOT + 2 * (KOPB + VOPB);  // ring + double-buffered K and V^T
   static_assert(2 * CI % kWW == 0, "code DMAs divide over the waves");
   static_assert(LDS <= 160 * 1024, "fits the LDS");
 };
@@ -103,7 +104,9 @@ __device__ __forceinline__ float dq(uint32_t code, uint32_t s_cell, uint32_t b_c
 }
 
 // K of a raw tile into the K operand tile (OT elements): thread t dequantizes dims [32 p, 32 p + 32)
-// of key r (t = 8 r + p) and writes them as 4 chunks of 8 dims, chunk c of key r at position c ^ r.
+// of key r (t = 8 r + p) and writes them as 4 chunks of 8 dims. Rows are 528 bytes apart (16 bytes of
+// padding), so the 32 lanes that read one 16-byte column of 32 keys hit distinct banks and a lane's
+// 16 reads of one row are one base address plus immediate offsets.
 template <typename T, typename OT, int BITS, int G>
 __device__ __forceinline__ void wide_stage_k(const uint8_t* raw, uint8_t* kop, int t) {
   using C = WideCfg<BITS, G>;
@@ -146,7 +149,7 @@ __device__ __forceinline__ void wide_stage_k(const uint8_t* raw, uint8_t* kop, i
       }
   }
 #pragma unroll
-  for (int c = 0; c < 4; ++c) *(u4*)(kop + r * (kWD * 2) + 16 * ((4 * p + c) ^ r)) = w[c];
+  for (int c = 0; c < 4; ++c) *(u4*)(kop + r * C::KROW + 16 * (4 * p + c)) = w[c];
 }
 
 // V of a raw tile into the V^T operand tile: thread t = 64 c + j dequantizes dims [4 j, 4 j + 4) of
@@ -203,8 +206,8 @@ __global__ __launch_bounds__(kWW * 64, 1) void wide_attn_kernel(WideParams p) {
   using OT = std::conditional_t<C::DENSE, T, F16>;  // operand type
   __shared__ __align__(16) uint8_t smem[C::LDS];
   uint8_t* const ring = smem;
-  uint8_t* const kop = smem + C::NR * C::SLOT;  // [2][OPB]
-  uint8_t* const vop = kop + 2 * C::OPB;        // [2][OPB]
+  uint8_t* const kop = smem + C::NR * C::SLOT;  // [2][KOPB]
+  uint8_t* const vop = kop + 2 * C::KOPB;       // [2][VOPB]
 
   const int tid = threadIdx.x;
   const int lane = __lane_id();
@@ -328,9 +331,9 @@ __global__ __launch_bounds__(kWW * 64, 1) void wide_attn_kernel(WideParams p) {
 #pragma unroll
   for (int db = 0; db < 8; ++db) oacc[db] = f16v{};
 
-  // K operand of k-step j: key n, dims 16 j + 8 h .. + 8, at chunk position (2 j + h) ^ n; V^T
-  // operand of column block db, k-step s: row d = 32 db + n, chunk position (2 s + h) ^ ((n >> 2) & 3)
-  const uint32_t k_off = (uint32_t)(n * (kWD * 2));
+  // K operand of k-step j: key n, dims 16 j + 8 h .. + 8; V^T operand of column block db, k-step s:
+  // row d = 32 db + n, chunk position (2 s + h) ^ ((n >> 2) & 3)
+  const uint32_t k_off = (uint32_t)(n * C::KROW + 16 * h);
   const uint32_t v_off = (uint32_t)(n * (kWT * 2));
   const int v_sw = (n >> 2) & 3;
 
@@ -340,7 +343,7 @@ __global__ __launch_bounds__(kWW * 64, 1) void wide_attn_kernel(WideParams p) {
   auto step = [&](const uint8_t* kt, const uint8_t* vt, int k0, const uint8_t* raw1, uint8_t* kd, uint8_t* vd) {
     u4 ka[16];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) ka[j] = *(const u4*)(kt + k_off + 16 * ((2 * j + h) ^ n));
+    for (int j = 0; j < 16; ++j) ka[j] = *(const u4*)(kt + k_off + 32 * j);
     wide_stage_k<T, OT, BITS, G>(raw1, kd, tid);
     f16v s = f16v{};
 #pragma unroll
@@ -401,8 +404,9 @@ __global__ __launch_bounds__(kWW * 64, 1) void wide_attn_kernel(WideParams p) {
       }
       __syncthreads();  // operand buffer t % 2 is complete; raw slot t % NR is free
       issue(t + C::NR);
-      const int cb = opaque((t & 1) * C::OPB), nb = opaque(((t + 1) & 1) * C::OPB);
-      step(kop + cb, vop + cb, (t_begin + t) * kWT, ring + opaque(((t + 1) % C::NR) * C::SLOT), kop + nb, vop + nb);
+      const int ck = opaque((t & 1) * C::KOPB), nk = opaque(((t + 1) & 1) * C::KOPB);
+      const int cv = opaque((t & 1) * C::VOPB), nv = opaque(((t + 1) & 1) * C::VOPB);
+      step(kop + ck, vop + cv, (t_begin + t) * kWT, ring + opaque(((t + 1) % C::NR) * C::SLOT), kop + nk, vop + nv);
     }
   }
   wait_vm<0>();  // the look-ahead loads land before the workgroup's LDS is released
