@@ -687,6 +687,45 @@ def wide_extras(steps, device):
     return res
 
 
+def plain_read_reference(nbytes, steps, device):
+    """What a plain read of the same number of bytes costs on this GPU, for reading the decode
+    roofline fraction against: torch's own reduction kernel (an fp32 sum) and its
+    device copy (nbytes read and nbytes written), each timed like the decode call (one event pair
+    around a batch of eager calls queued behind a spin kernel) over buffers that rotate past the
+    MALL like the decode caches. A reference point, not a bound."""
+    import torch
+
+    nbuf = max(3, math.ceil(2.5 * MALL_BYTES / nbytes))
+    bufs = [torch.ones(nbytes // 4, dtype=torch.float32, device=device) for _ in range(nbuf)]
+    dsts = [torch.empty_like(b) for b in bufs]
+    acc = torch.zeros((), dtype=torch.float32, device=device)
+
+    n = min(steps, 100)
+
+    def timed(fn):
+        for i in range(3):
+            fn(i)
+        cycles = calibrate_spin(torch, 20.0 + 0.05 * n)
+        torch.cuda.synchronize()
+        s_, e_ = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(cycles)
+        s_.record()
+        for i in range(n):
+            fn(i)
+        e_.record()
+        torch.cuda.synchronize()
+        return s_.elapsed_time(e_) / n * 1e3  # us
+
+    sum_us = timed(lambda i: torch.sum(bufs[i % nbuf], dim=0, out=acc))
+    copy_us = timed(lambda i: dsts[i % nbuf].copy_(bufs[i % nbuf]))
+    del bufs, dsts
+    torch.cuda.empty_cache()
+    return {"bytes": nbytes, "torch_sum_us": round(sum_us, 3), "torch_sum_gbs": round(nbytes / sum_us / 1e3, 1),
+            "torch_copy_us": round(copy_us, 3), "torch_copy_gbs": round(2 * nbytes / copy_us / 1e3, 1),
+            "note": "torch's fp32 sum and device copy over buffers of the call's size rotated past the MALL, "
+                    "timed like the decode call; copy counts read + write bytes"}
+
+
 def append_extras(device, calls=200):
     """The C3 chunk's cache update: quantize-append of 512 rows x 4 KV heads (bf16, 8-bit), plain and
     with the keys rotated in the same launch (kvq_rope_quantize_append); device microseconds per call
@@ -1008,6 +1047,9 @@ def main():
         log(f"[bench] CPU baseline: {cpu['value']} GB/s on {cpu['cores']} cores")
 
     achieved = res["kernel_gbs"]
+    read_ref = plain_read_reference(res["bytes"], args.steps, device)
+    log(f"[bench] plain read of {res['bytes']} B: torch sum {read_ref['torch_sum_us']} us "
+        f"({read_ref['torch_sum_gbs']} GB/s), torch copy {read_ref['torch_copy_gbs']} GB/s")
     line = {
         "metric": METRIC,
         "value": round(res["gbs"], 2),
@@ -1036,6 +1078,7 @@ def main():
             "traffic": measured_traffic("decode_c2_b1"),
             "kernel_us": round(res["call_us_mean"], 3),
             "kernel": "decode_attn_kernel + combine_kernel (the two launches of one kvq_decode_attn call)",
+            "plain_read_reference": read_ref,
         },
         "cpu_baseline": cpu,
         "parity": res.get("parity"),
