@@ -891,7 +891,7 @@ def main():
     ap.add_argument("--prefill-only", action="store_true", help="time only the C3 chunked-prefill leg")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run 10 device copies of 256 MiB (reference for rocprofv3 FETCH_SIZE/WRITE_SIZE)")
-    ap.add_argument("--config", choices=sorted(DECODE) + sorted(PREFILL_C5) + ["C3"],
+    ap.add_argument("--config", choices=sorted(DECODE) + sorted(PREFILL_C5) + ["C3", "D256"],
                     help="time only this workload (no CPU leg, no parity) and print its numbers: for profiling")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -927,6 +927,9 @@ def main():
 
     if args.config:
         # one workload alone, as a profiler run needs it
+        if args.config == "D256":
+            print(json.dumps({"config": "D256", **wide_extras(min(args.steps, 20), device)}), flush=True)
+            return
         if args.config in DECODE:
             r = time_decode(DECODE[args.config], args.steps, args.warmup, device)
             out = {"config": args.config, "gbs": round(r["gbs"], 1), "frac": round(r["gbs"] / PEAK_HBM_GBS, 4),
