@@ -197,9 +197,9 @@ size_t kvq_prefill_workspace_size(int B, int Hq, int Hkv, int L, int D, int S, i
  * unquantized.
  * The products run on MFMA in the cache's own type (fp16 or bf16, exact operands) with fp32
  * accumulation; the probabilities enter the PV product in that type.
- * Requirements: decode D in {64, 128, 256}, prefill D in {128, 256}; rows 16-byte aligned with
- * strides that are multiples of 8 elements. At D = 256 both entry points run the head_dim-256
- * prefill kernel (any L).
+ * Requirements: D in {64, 128, 256}; rows 16-byte aligned with strides that are multiples of 8
+ * elements. At D = 256 both entry points run the head_dim-256 prefill kernel (any L); the prefill
+ * entry point runs the same kernel at D = 64.
  */
 int kvq_decode_attn_dense(const kvq_rows* q, const kvq_rows* k, const kvq_rows* v,
                           const int32_t* seq_lens, const kvq_rows* out,

@@ -321,7 +321,7 @@ size_t kvq_decode_workspace_size(int B, int Hq, int Hkv, int L, int D, int S, in
       n = x > n ? x : n;
     }
   if (D == 256) {  // the unquantized cache at head_dim 256 runs through the head_dim-256 kernel
-    const size_t x = kvq::wide_workspace_bytes(B, Hq, Hkv, L, S, window);
+    const size_t x = kvq::wide_workspace_bytes(B, Hq, Hkv, L, D, S, window);
     n = x > n ? x : n;
   }
   return n;
@@ -362,8 +362,13 @@ int kvq_decode_attn_static(const kvq_rows* q, const kvq_qtensor* k, const kvq_qt
 size_t kvq_prefill_workspace_size(int B, int Hq, int Hkv, int L, int D, int S, int window) {
   if (B <= 0 || Hq <= 0 || Hkv <= 0 || L <= 0 || S <= 0 || (D != 64 && D != 128 && D != 256) || window < 0 || Hq % Hkv)
     return 0;
-  if (D == 256) return kvq::wide_workspace_bytes(B, Hq, Hkv, L, S, window);
-  return kvq::prefill_workspace_bytes(B, Hq, Hkv, L, D, S, window, 8);
+  if (D == 256) return kvq::wide_workspace_bytes(B, Hq, Hkv, L, D, S, window);
+  const size_t n = kvq::prefill_workspace_bytes(B, Hq, Hkv, L, D, S, window, 8);
+  if (D == 64) {  // the unquantized cache at head_dim 64 runs through wide.hip's kernel
+    const size_t x = kvq::wide_workspace_bytes(B, Hq, Hkv, L, D, S, window);
+    return x > n ? x : n;
+  }
+  return n;
 }
 
 // The prefill kernel loads two scale groups of a row at once when a row has several: scale and
@@ -459,7 +464,7 @@ int kvq_decode_attn_dense(const kvq_rows* q, const kvq_rows* k, const kvq_rows* 
                             kvq_decode_workspace_size(B, Hq, Hkv, L, D, S, window), workspace, workspace_bytes);
   if (rc) return rc;
   if (D == 256)
-    return hip_status(kvq::launch_wide_dense(q, k, v, seq_lens, out, B, Hq, Hkv, L, S, dtype, scale, causal, window,
+    return hip_status(kvq::launch_wide_dense(q, k, v, seq_lens, out, B, Hq, Hkv, L, D, S, dtype, scale, causal, window,
                                              workspace, (hipStream_t)stream),
                       "decode_attn_dense launch (head_dim 256)");
   return hip_status(kvq::launch_decode_dense(q, k, v, seq_lens, out, B, Hq, Hkv, L, D, S, dtype, scale, causal, window,
@@ -470,15 +475,15 @@ int kvq_decode_attn_dense(const kvq_rows* q, const kvq_rows* k, const kvq_rows* 
 int kvq_prefill_attn_dense(const kvq_rows* q, const kvq_rows* k, const kvq_rows* v, const int32_t* seq_lens,
                            const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int dtype, float scale,
                            int causal, int window, void* workspace, size_t workspace_bytes, void* stream) {
-  if (D != 128 && D != 256)
-    return fail(KVQ_ERR_UNSUPPORTED, "unquantized prefill supports head_dim 128 and 256, got %d", D);
+  if (D != 64 && D != 128 && D != 256)
+    return fail(KVQ_ERR_UNSUPPORTED, "unquantized prefill supports head_dim 64, 128 and 256, got %d", D);
   int rc = check_attn_dense(q, k, v, out, B, Hq, Hkv, L, D, S, dtype, scale, window,
                             kvq_prefill_workspace_size(B, Hq, Hkv, L, D, S, window), workspace, workspace_bytes);
   if (rc) return rc;
-  if (D == 256)
-    return hip_status(kvq::launch_wide_dense(q, k, v, seq_lens, out, B, Hq, Hkv, L, S, dtype, scale, causal, window,
+  if (D != 128)
+    return hip_status(kvq::launch_wide_dense(q, k, v, seq_lens, out, B, Hq, Hkv, L, D, S, dtype, scale, causal, window,
                                              workspace, (hipStream_t)stream),
-                      "prefill_attn_dense launch (head_dim 256)");
+                      "prefill_attn_dense launch (head_dim 64 / 256)");
   return hip_status(kvq::launch_prefill_dense(q, k, v, seq_lens, out, B, Hq, Hkv, L, D, S, dtype, scale, causal, window,
                                               workspace, (hipStream_t)stream),
                     "prefill_attn_dense launch");

@@ -40,13 +40,14 @@ hipError_t launch_prefill_paged(const kvq_rows* q, const kvq_qtensor* k, const k
                                 const int32_t* table, int64_t table_stride, const int32_t* seq_lens, const kvq_rows* out,
                                 int B, int Hq, int Hkv, int L, int D, int S, int bits, int G, int dtype, float scale,
                                 int causal, int window, void* workspace, hipStream_t stream);
-// head_dim 256 (wide.hip): quantized (4/8 bits, groups 64/128) and unquantized caches, any query length
-size_t wide_workspace_bytes(int B, int Hq, int Hkv, int L, int S, int window);
+// wide.hip: head_dim 256 over quantized (4/8 bits, groups 64/128) and unquantized caches, and head_dim 64
+// over unquantized caches, any query length
+size_t wide_workspace_bytes(int B, int Hq, int Hkv, int L, int D, int S, int window);
 hipError_t launch_wide(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v, const int32_t* seq_lens,
                        const kvq_rows* out, int B, int Hq, int Hkv, int L, int S, int bits, int G, int dtype,
                        float scale, int causal, int window, void* workspace, hipStream_t stream);
 hipError_t launch_wide_dense(const kvq_rows* q, const kvq_rows* k, const kvq_rows* v, const int32_t* seq_lens,
-                             const kvq_rows* out, int B, int Hq, int Hkv, int L, int S, int dtype, float scale,
+                             const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int dtype, float scale,
                              int causal, int window, void* workspace, hipStream_t stream);
 hipError_t launch_prefill_dense(const kvq_rows* q, const kvq_rows* k, const kvq_rows* v, const int32_t* seq_lens,
                                 const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int dtype,

@@ -1,7 +1,8 @@
 // Attention at head_dim 256: the reference's blocked attention over a quantized cache
 // (m5engine/attention.py:29-103) for models whose heads are 256 wide, and every call over an
 // unquantized cache of that width (the plain KVCache before quantized_kv_start and the sliding-window
-// RotatingKVCache, which the reference leaves to mlx-lm's SDPA, attention.py:106-112).
+// RotatingKVCache, which the reference leaves to mlx-lm's SDPA, attention.py:106-112). The same
+// kernel at head_dim 64 serves prefill over unquantized caches of that width.
 //
 //   out = softmax(scale * q K^T + mask) V,  K = sK * codesK + bK,  V = sV * codesV + bV
 //
@@ -40,18 +41,22 @@
 
 namespace kvq {
 
-constexpr int kWD = 256;     // head dim
 constexpr int kWT = 32;      // keys per tile
 constexpr int kWW = 4;       // waves per workgroup
 constexpr int kWRows = 128;  // query rows per workgroup
 constexpr float kWSlack = 6.0f;
 
-template <int BITS, int G>
+template <int D, int BITS, int G>
 struct WideCfg {
   static constexpr bool DENSE = BITS == 16;
   static_assert(DENSE || ((BITS == 4 || BITS == 8) && (G == 64 || G == 128)), "4/8 bits, groups 64/128");
-  static constexpr int NG = DENSE ? 1 : kWD / G;           // scale groups per row
-  static constexpr int ROWB = kWD * BITS / 8;              // raw bytes per key row: 128, 256, 512
+  static_assert(D == 256 || (D == 64 && DENSE), "head_dim 256, or 64 over an unquantized cache");
+  static constexpr int NG = DENSE ? 1 : D / G;             // scale groups per row
+  static constexpr int KSTEPS = D / 16;                    // QK MFMA k-steps
+  static constexpr int NDB = D / 32;                       // PV MFMA column blocks
+  static constexpr int KCH = D / 64;                       // K staging: 16-byte chunks per thread
+  static constexpr int VPT = D / 64;                       // V^T staging: dims per thread
+  static constexpr int ROWB = D * BITS / 8;                // raw bytes per key row: 128, 256, 512 (D 256)
   static constexpr int TB = kWT * ROWB;                    // raw bytes of a K (or V) tile
   static constexpr int CI = TB / 1024;                     // 1 KiB DMAs per K (or V) tile
   static constexpr int CPR = ROWB / 16;                    // 16-byte chunks per raw row
@@ -62,9 +67,9 @@ struct WideCfg {
   static constexpr int NR = DENSE ? 2 : 3;                 // raw ring slots
   static constexpr int CPW = 2 * CI / kWW;                 // code DMAs per wave per tile
   static constexpr int IPW = CPW + NSB;                    // DMAs per wave per tile (wave a loads array a)
-  static constexpr int KROW = kWD * 2 + 16;                // K operand row pitch: 512 bytes + 16 of padding
+  static constexpr int KROW = D * 2 + 16;                  // K operand row pitch: the row + 16 bytes of padding
   static constexpr int KOPB = kWT * KROW;                  // bytes of a K operand tile
-  static constexpr int VOPB = kWD * kWT * 2;               // bytes of a V^T operand tile
+  static constexpr int VOPB = D * kWT * 2;                 // bytes of a V^T operand tile
   static constexpr int LDS = NR * SLOT + 2 * (KOPB + VOPB);  // ring + double-buffered K and V^T
   static_assert(2 * CI % kWW == 0, "code DMAs divide over the waves");
   static_assert(LDS <= 160 * 1024, "fits the LDS");
@@ -103,18 +108,18 @@ __device__ __forceinline__ float dq(uint32_t code, uint32_t s_cell, uint32_t b_c
   return fmaf(to_float((uint16_t)(s_cell & 0xffffu), T{}), (float)code, to_float((uint16_t)(b_cell & 0xffffu), T{}));
 }
 
-// K of a raw tile into the K operand tile (OT elements): thread t dequantizes dims [32 p, 32 p + 32)
-// of key r (t = 8 r + p) and writes them as 4 chunks of 8 dims. Rows are 528 bytes apart (16 bytes of
-// padding), so the 32 lanes that read one 16-byte column of 32 keys hit distinct banks and a lane's
-// 16 reads of one row are one base address plus immediate offsets.
-template <typename T, typename OT, int BITS, int G>
+// K of a raw tile into the K operand tile (OT elements): thread t dequantizes dims
+// [D/8 p, D/8 (p + 1)) of key r (t = 8 r + p) and writes them as KCH chunks of 8 dims. Rows are 16
+// bytes longer than the data (528 bytes at D = 256), so the 32 lanes that read one 16-byte column of
+// 32 keys hit distinct banks and a lane's reads of one row are one base address plus immediates.
+template <typename T, typename OT, int D, int BITS, int G>
 __device__ __forceinline__ void wide_stage_k(const uint8_t* raw, uint8_t* kop, int t) {
-  using C = WideCfg<BITS, G>;
+  using C = WideCfg<D, BITS, G>;
   const int r = t >> 3, p = t & 7;
-  u4 w[4];
+  u4 w[C::KCH];
   if constexpr (C::DENSE) {
 #pragma unroll
-    for (int c = 0; c < 4; ++c) w[c] = *(const u4*)(raw + r * C::ROWB + 16 * (4 * p + c));
+    for (int c = 0; c < C::KCH; ++c) w[c] = *(const u4*)(raw + r * C::ROWB + 16 * (C::KCH * p + c));
   } else {
     const int g = 32 * p / G;
     const uint32_t* cells = (const uint32_t*)(raw + 2 * C::TB);
@@ -149,24 +154,29 @@ __device__ __forceinline__ void wide_stage_k(const uint8_t* raw, uint8_t* kop, i
       }
   }
 #pragma unroll
-  for (int c = 0; c < 4; ++c) *(u4*)(kop + r * C::KROW + 16 * (4 * p + c)) = w[c];
+  for (int c = 0; c < C::KCH; ++c) *(u4*)(kop + r * C::KROW + 16 * (C::KCH * p + c)) = w[c];
 }
 
-// V of a raw tile into the V^T operand tile: thread t = 64 c + j dequantizes dims [4 j, 4 j + 4) of
-// the 8 keys of slot chunk c and writes, for each of those dims, the chunk's 8 slots (16 bytes) to
-// row d at chunk position c ^ ((d >> 2) & 3) (rows are 64 bytes: 32 slots).
-template <typename T, typename OT, int BITS, int G>
+// V of a raw tile into the V^T operand tile: thread t = 64 c + j dequantizes dims
+// [VPT j, VPT (j + 1)) (VPT = D / 64) of the 8 keys of slot chunk c and writes, for each of those
+// dims, the chunk's 8 slots (16 bytes) to row d at chunk position c ^ ((d >> 2) & 3) (rows are 64
+// bytes: 32 slots).
+template <typename T, typename OT, int D, int BITS, int G>
 __device__ __forceinline__ void wide_stage_v(const uint8_t* raw, uint8_t* vop, int t) {
-  using C = WideCfg<BITS, G>;
+  using C = WideCfg<D, BITS, G>;
   const int c = t >> 6, j = t & 63;
   const uint8_t* vraw = raw + C::TB;
-  float x[8][4];  // [slot e][dim i]
+  float x[8][C::VPT];  // [slot e][dim i]
   if constexpr (C::DENSE) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const u2 v = *(const u2*)(vraw + w_slot_key(c, e) * C::ROWB + 8 * j);
+      if constexpr (C::VPT == 4) {
+        const u2 v = *(const u2*)(vraw + w_slot_key(c, e) * C::ROWB + 8 * j);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) x[e][i] = to_float((uint16_t)(v[i >> 1] >> (16 * (i & 1))), T{});
+        for (int i = 0; i < 4; ++i) x[e][i] = to_float((uint16_t)(v[i >> 1] >> (16 * (i & 1))), T{});
+      } else {
+        x[e][0] = to_float(*(const uint16_t*)(vraw + w_slot_key(c, e) * C::ROWB + 2 * j), T{});
+      }
     }
   } else {
     const int g = 4 * j / G;
@@ -191,18 +201,18 @@ __device__ __forceinline__ void wide_stage_v(const uint8_t* raw, uint8_t* vop, i
     }
   }
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < C::VPT; ++i) {
     u4 o;
 #pragma unroll
     for (int a = 0; a < 4; ++a) o[a] = pack2(x[2 * a][i], x[2 * a + 1][i], OT{});
-    const int d = 4 * j + i;
+    const int d = C::VPT * j + i;
     *(u4*)(vop + d * (kWT * 2) + 16 * (c ^ ((d >> 2) & 3))) = o;
   }
 }
 
-template <typename T, int BITS, int G>
+template <typename T, int D, int BITS, int G>
 __global__ __launch_bounds__(kWW * 64, 1) void wide_attn_kernel(WideParams p) {
-  using C = WideCfg<BITS, G>;
+  using C = WideCfg<D, BITS, G>;
   using OT = std::conditional_t<C::DENSE, T, F16>;  // operand type
   __shared__ __align__(16) uint8_t smem[C::LDS];
   uint8_t* const ring = smem;
@@ -296,17 +306,17 @@ __global__ __launch_bounds__(kWW * 64, 1) void wide_attn_kernel(WideParams p) {
   for (int i = 0; i < C::NR; ++i) issue(i);
   __builtin_amdgcn_sched_barrier(0);
 
-  u4 qop[16];
+  u4 qop[C::KSTEPS];
   float kf = p.scale_log2;  // fp32 score -> log2 units
   {
     const uint16_t* qrow = p.q + (int64_t)b * p.q_sb + (int64_t)hq * p.q_sh + (int64_t)lq * p.q_sl + 8 * h;
 #pragma unroll
-    for (int j = 0; j < 16; ++j) qop[j] = *(const u4*)(qrow + 16 * j);
+    for (int j = 0; j < C::KSTEPS; ++j) qop[j] = *(const u4*)(qrow + 16 * j);
     if constexpr (!C::DENSE) {
       // q * 2^qe in fp16, exact: the row's largest |q| lands in [2^13, 2^14)
       float qmax = 0.0f;
 #pragma unroll
-      for (int j = 0; j < 16; ++j)
+      for (int j = 0; j < C::KSTEPS; ++j)
 #pragma unroll
         for (int a = 0; a < 8; ++a) qmax = fmaxf(qmax, fabsf(to_float((uint16_t)(qop[j][a >> 1] >> (16 * (a & 1))), T{})));
       qmax = max_xor32(qmax);
@@ -318,7 +328,7 @@ __global__ __launch_bounds__(kWW * 64, 1) void wide_attn_kernel(WideParams p) {
       const float qs = ldexpf(1.0f, qe);
       kf = ldexpf(p.scale_log2, -qe);
 #pragma unroll
-      for (int j = 0; j < 16; ++j)
+      for (int j = 0; j < C::KSTEPS; ++j)
 #pragma unroll
         for (int a = 0; a < 4; ++a)
           qop[j][a] = pack_f16x2(to_float((uint16_t)(qop[j][a] & 0xffffu), T{}) * qs,
@@ -327,9 +337,9 @@ __global__ __launch_bounds__(kWW * 64, 1) void wide_attn_kernel(WideParams p) {
   }
 
   float m_run = -INFINITY, l_run = 0.0f;
-  f16v oacc[8];
+  f16v oacc[C::NDB];
 #pragma unroll
-  for (int db = 0; db < 8; ++db) oacc[db] = f16v{};
+  for (int db = 0; db < C::NDB; ++db) oacc[db] = f16v{};
 
   // K operand of k-step j: key n, dims 16 j + 8 h .. + 8; V^T operand of column block db, k-step s:
   // row d = 32 db + n, chunk position (2 s + h) ^ ((n >> 2) & 3)
@@ -341,13 +351,13 @@ __global__ __launch_bounds__(kWW * 64, 1) void wide_attn_kernel(WideParams p) {
   // slot raw1 into (kd, vd). The step is one basic block: each product's operand reads are issued
   // ahead of its MFMA chain, and the staging's independent VALU work fills the chain's issue slots.
   auto step = [&](const uint8_t* kt, const uint8_t* vt, int k0, const uint8_t* raw1, uint8_t* kd, uint8_t* vd) {
-    u4 ka[16];
+    u4 ka[C::KSTEPS];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) ka[j] = *(const u4*)(kt + k_off + 32 * j);
-    wide_stage_k<T, OT, BITS, G>(raw1, kd, tid);
+    for (int j = 0; j < C::KSTEPS; ++j) ka[j] = *(const u4*)(kt + k_off + 32 * j);
+    wide_stage_k<T, OT, D, BITS, G>(raw1, kd, tid);
     f16v s = f16v{};
 #pragma unroll
-    for (int j = 0; j < 16; ++j) s = mfma_32x32x16(ka[j], qop[j], s, OT{});
+    for (int j = 0; j < C::KSTEPS; ++j) s = mfma_32x32x16(ka[j], qop[j], s, OT{});
     // value i of the lane is key k0 + 8 (i / 4) + 4 h + i % 4 of query row n
     if (!(k0 >= lo_all && k0 + kWT <= hi_all)) {
 #pragma unroll
@@ -365,7 +375,7 @@ __global__ __launch_bounds__(kWW * 64, 1) void wide_attn_kernel(WideParams p) {
       const float corr = m_new == m_run ? 1.0f : exp2_fast(m_run - m_new);
       l_run *= corr;
 #pragma unroll
-      for (int db = 0; db < 8; ++db) oacc[db] *= corr;
+      for (int db = 0; db < C::NDB; ++db) oacc[db] *= corr;
       m_run = m_new;
     }
     const float nm = m_run == -INFINITY ? 0.0f : -m_run;
@@ -379,12 +389,13 @@ __global__ __launch_bounds__(kWW * 64, 1) void wide_attn_kernel(WideParams p) {
         pop[st][a] = pack2(p0, p1, OT{});
         l_run = add_pair(pop[st][a], l_run, OT{});
       }
-    u4 va[16];
+    u4 va[2 * C::NDB];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) va[i] = *(const u4*)(vt + 32 * (i >> 1) * (kWT * 2) + v_off + 16 * ((2 * (i & 1) + h) ^ v_sw));
-    wide_stage_v<T, OT, BITS, G>(raw1, vd, tid);
+    for (int i = 0; i < 2 * C::NDB; ++i)
+      va[i] = *(const u4*)(vt + 32 * (i >> 1) * (kWT * 2) + v_off + 16 * ((2 * (i & 1) + h) ^ v_sw));
+    wide_stage_v<T, OT, D, BITS, G>(raw1, vd, tid);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) oacc[i >> 1] = mfma_32x32x16(va[i], pop[i & 1], oacc[i >> 1], OT{});
+    for (int i = 0; i < 2 * C::NDB; ++i) oacc[i >> 1] = mfma_32x32x16(va[i], pop[i & 1], oacc[i >> 1], OT{});
   };
 
   // ---- the tile loop: tile t is computed from operand buffer t % 2 while tile t + 1 is staged into
@@ -394,8 +405,8 @@ __global__ __launch_bounds__(kWW * 64, 1) void wide_attn_kernel(WideParams p) {
   if (ntile > 0) {
     wait_vm<0>();  // the query and the first NR raw tiles
     __syncthreads();
-    wide_stage_k<T, OT, BITS, G>(ring, kop, tid);
-    wide_stage_v<T, OT, BITS, G>(ring, vop, tid);
+    wide_stage_k<T, OT, D, BITS, G>(ring, kop, tid);
+    wide_stage_v<T, OT, D, BITS, G>(ring, vop, tid);
     for (int t = 0; t < ntile; ++t) {
       if constexpr (C::NR == 3) {
         wait_vm<C::IPW>();  // tile t + 1 has landed (tile t + 2 may be in flight)
@@ -418,7 +429,7 @@ __global__ __launch_bounds__(kWW * 64, 1) void wide_attn_kernel(WideParams p) {
     const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
     uint16_t* orow = p.out + (int64_t)b * p.o_sb + (int64_t)hq * p.o_sh + (int64_t)lq * p.o_sl + 4 * h;
 #pragma unroll
-    for (int db = 0; db < 8; ++db)
+    for (int db = 0; db < C::NDB; ++db)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         u2 w;
@@ -428,9 +439,9 @@ __global__ __launch_bounds__(kWW * 64, 1) void wide_attn_kernel(WideParams p) {
       }
   } else {
     const int64_t pi = ((int64_t)unit * p.nsplit + split) * kWRows + (row - r0);
-    float* po = p.part_o + pi * kWD + 4 * h;
+    float* po = p.part_o + pi * D + 4 * h;
 #pragma unroll
-    for (int db = 0; db < 8; ++db)
+    for (int db = 0; db < C::NDB; ++db)
 #pragma unroll
       for (int i = 0; i < 4; ++i)
         *(f4*)(po + 32 * db + 8 * i) = f4{oacc[db][4 * i], oacc[db][4 * i + 1], oacc[db][4 * i + 2], oacc[db][4 * i + 3]};
@@ -461,17 +472,17 @@ static WidePlan wide_plan(int B, int Hq, int Hkv, int L, int S, int window) {
 
 // Workspace: [the arrival counter block every launch reserves (merge.h), left untouched][(m, l) per
 // row and split][o per row and split]; a launch without splits writes none of it.
-size_t wide_workspace_bytes(int B, int Hq, int Hkv, int L, int S, int window) {
+size_t wide_workspace_bytes(int B, int Hq, int Hkv, int L, int D, int S, int window) {
   const WidePlan pl = wide_plan(B, Hq, Hkv, L, S, window);
   if (pl.nsplit == 1) return kCounterBytes;
   auto up = [](size_t x) { return (x + 255) / 256 * 256; };
   const size_t rows = (size_t)pl.nunits * pl.nsplit * kWRows;
-  return kCounterBytes + up(rows * sizeof(float2)) + up(rows * kWD * sizeof(float));
+  return kCounterBytes + up(rows * sizeof(float2)) + up(rows * D * sizeof(float));
 }
 
-template <typename T, int BITS, int G>
+template <typename T, int D, int BITS, int G>
 static hipError_t launch_wide_t(const WideParams& p, hipStream_t stream) {
-  hipLaunchKernelGGL((wide_attn_kernel<T, BITS, G>), dim3(p.nunits * p.nsplit), dim3(kWW * 64), 0, stream, p);
+  hipLaunchKernelGGL((wide_attn_kernel<T, D, BITS, G>), dim3(p.nunits * p.nsplit), dim3(kWW * 64), 0, stream, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || p.nsplit == 1) return e;
   MergeParams m;
@@ -489,7 +500,7 @@ static hipError_t launch_wide_t(const WideParams& p, hipStream_t stream) {
   m.rowblocks = p.rowblocks;
   m.nsplit = p.nsplit;
   m.xcd_remap = 0;
-  return launch_combine<T, kWD>(m, p.nunits / (p.Hkv * p.rowblocks), stream);
+  return launch_combine<T, D>(m, p.nunits / (p.Hkv * p.rowblocks), stream);
 }
 
 static WideParams wide_params(const kvq_rows* q, const int32_t* seq_lens, const kvq_rows* out, int B, int Hq, int Hkv,
@@ -547,17 +558,17 @@ hipError_t launch_wide(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtenso
   p.vsb_ss = v->sb_stride_s;
   auto go = [&](auto t) -> hipError_t {
     using T = decltype(t);
-    if (bits == 8 && G == 64) return launch_wide_t<T, 8, 64>(p, stream);
-    if (bits == 8 && G == 128) return launch_wide_t<T, 8, 128>(p, stream);
-    if (bits == 4 && G == 64) return launch_wide_t<T, 4, 64>(p, stream);
-    if (bits == 4 && G == 128) return launch_wide_t<T, 4, 128>(p, stream);
+    if (bits == 8 && G == 64) return launch_wide_t<T, 256, 8, 64>(p, stream);
+    if (bits == 8 && G == 128) return launch_wide_t<T, 256, 8, 128>(p, stream);
+    if (bits == 4 && G == 64) return launch_wide_t<T, 256, 4, 64>(p, stream);
+    if (bits == 4 && G == 128) return launch_wide_t<T, 256, 4, 128>(p, stream);
     return hipErrorInvalidValue;
   };
   return dtype == KVQ_DTYPE_BF16 ? go(BF16{}) : go(F16{});
 }
 
 hipError_t launch_wide_dense(const kvq_rows* q, const kvq_rows* k, const kvq_rows* v, const int32_t* seq_lens,
-                             const kvq_rows* out, int B, int Hq, int Hkv, int L, int S, int dtype, float scale,
+                             const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int dtype, float scale,
                              int causal, int window, void* workspace, hipStream_t stream) {
   WideParams p = wide_params(q, seq_lens, out, B, Hq, Hkv, L, S, scale, causal, window, workspace);
   p.kc = (const uint8_t*)k->data;
@@ -568,7 +579,12 @@ hipError_t launch_wide_dense(const kvq_rows* q, const kvq_rows* k, const kvq_row
   p.vc_sb = v->stride_b * 2;
   p.vc_sh = v->stride_h * 2;
   p.vc_ss = v->stride_l * 2;
-  return dtype == KVQ_DTYPE_BF16 ? launch_wide_t<BF16, 16, 64>(p, stream) : launch_wide_t<F16, 16, 64>(p, stream);
+  if (D == 64)
+    return dtype == KVQ_DTYPE_BF16 ? launch_wide_t<BF16, 64, 16, 64>(p, stream) : launch_wide_t<F16, 64, 16, 64>(p, stream);
+  if (D == 256)
+    return dtype == KVQ_DTYPE_BF16 ? launch_wide_t<BF16, 256, 16, 64>(p, stream)
+                                   : launch_wide_t<F16, 256, 16, 64>(p, stream);
+  return hipErrorInvalidValue;
 }
 
 }  // namespace kvq

@@ -248,9 +248,9 @@ def decode_rows_per_pass(D: int, group_size: int = 64) -> int:
 def _auto_kernel(rep_rows: int, D: int, group_size: int, dense: bool = False, paged: bool = False) -> str:
     """Decode while a KV head's query rows fit at most two decode passes over its keys (one pass for
     group 64, where 8 rows fit one pass), the prefill kernel otherwise; decode where the prefill
-    kernel has no build (head_dim 64 over an unquantized cache, head_dim 256 over a paged pool). At
-    head_dim 256 the unquantized entry points run the head_dim-256 kernel for every query length."""
-    prefill_built = D == 128 or (D == 64 and not dense) or (D == 256 and not paged)
+    kernel has no build (head_dim 256 over a paged pool). At head_dim 256 the unquantized entry
+    points run the head_dim-256 kernel for every query length."""
+    prefill_built = D in (64, 128) or (D == 256 and not paged)
     return "decode" if (rep_rows <= max(decode_rows_per_pass(D, group_size), 8) or not prefill_built) else "prefill"
 
 

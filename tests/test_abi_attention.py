@@ -161,9 +161,9 @@ def test_prefill_rejects_unaligned_scale_rows(field, value):
 
 
 def test_unquantized_head_dims():
-    # the unquantized kernels take head_dim 64/128/256 (decode) and 128/256 (prefill)
+    # the unquantized kernels take head_dim 64/128/256 (decode and prefill)
     lib = _lib.lib()
-    _expect(_dense(lib.kvq_prefill_attn_dense, D=64), _lib.ERR_UNSUPPORTED, "head_dim 128 and 256")
+    _expect(_dense(lib.kvq_prefill_attn_dense, D=512), _lib.ERR_UNSUPPORTED, "head_dim 64, 128 and 256")
     _expect(_dense(lib.kvq_decode_attn_dense, D=512), _lib.ERR_UNSUPPORTED, "head_dim 64, 128 and 256")
     # head_dim 256 needs a workspace from both size queries
     assert lib.kvq_prefill_workspace_size(1, 8, 4, 512, 256, 4096, 0) >= 256

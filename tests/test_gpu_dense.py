@@ -127,8 +127,8 @@ def test_rejects_bad_dense_arguments():
         kernels.attention(q, k[:, :, :, :64], k[:, :, :, :64], 0.1)
     with pytest.raises(ValueError):
         kernels.attention(q, k, (k, k, k), 0.1)
-    with pytest.raises(NotImplementedError):
-        kernels.attention(q[..., :64].contiguous(), k[..., :64].contiguous(), k[..., :64].contiguous(), 0.1,
+    with pytest.raises(NotImplementedError):  # no kernel at head_dim 32
+        kernels.attention(q[..., :32].contiguous(), k[..., :32].contiguous(), k[..., :32].contiguous(), 0.1,
                           kernel="prefill")
 
 

@@ -1,8 +1,9 @@
-"""GPU attention at head_dim 256 (wide_attn_kernel) vs the exact fp64 oracle.
+"""GPU attention through wide_attn_kernel vs the exact fp64 oracle.
 
 Head_dim 256 is the Gemma family's width (Gemma-2 and the smaller Gemma-3 models). The kernel
 serves prefill over quantized caches (4/8-bit, groups 64 and 128) and every call, decode included,
 over unquantized caches (the plain cache before quantized_kv_start and the sliding-window layers).
+At head_dim 64 (Llama-3.2-1B, Qwen2.5-0.5B) it serves prefill over unquantized caches.
 Covers GQA ratios, causal / full / sliding-window masks, variable-length batches, ragged query and
 key counts (partial tiles and row blocks, row blocks spanning two heads), capacity-padded views,
 split key ranges merged by combine_kernel, a Gemma-3-12B prefill chunk, and the public API's
@@ -40,13 +41,14 @@ def quant_case(B, Hq, Hkv, L, S, bits, dtype, *, group=64, causal=True, window=0
     return assert_close(out, ref, what)
 
 
-def dense_case(kernel, B, Hq, Hkv, L, S, dtype, *, causal=False, window=0, seq_lens=None, seed=0, cap=None, what=""):
-    print(f"wide dense {kernel} case {what} B={B} Hq={Hq} Hkv={Hkv} L={L} S={S} {dtype} causal={causal} "
+def dense_case(kernel, B, Hq, Hkv, L, S, dtype, *, causal=False, window=0, seq_lens=None, seed=0, cap=None, what="",
+               head_dim=D):
+    print(f"wide dense {kernel} case {what} B={B} Hq={Hq} Hkv={Hkv} L={L} S={S} D={head_dim} {dtype} causal={causal} "
           f"window={window} var={seq_lens is not None}", flush=True)
-    k, v = make_kv(B, Hkv, S, D, dtype, seed, cap=cap)
-    q = seeded_normal((B, Hq, L, D), seed + 2, dtype, DEV)
+    k, v = make_kv(B, Hkv, S, head_dim, dtype, seed, cap=cap)
+    q = seeded_normal((B, Hq, L, head_dim), seed + 2, dtype, DEV)
     sl = None if seq_lens is None else torch.tensor(seq_lens, dtype=torch.int32, device=DEV)
-    scale = 1.0 / math.sqrt(D)
+    scale = 1.0 / math.sqrt(head_dim)
     out = kernels.attention(q, k, v, scale, causal=causal, window=window, seq_lens=sl, kernel=kernel)
     torch.cuda.synchronize()
     ref = exact(q, k, v, scale, causal=causal, window=window, seq_lens=sl)
@@ -118,6 +120,31 @@ def test_dense_prefill(dtype, L, S, causal, window):
 def test_dense_gemma3_window_chunk():
     # a sliding-window layer of Gemma-3-12B: 512 queries, window 1024, after 3584 earlier tokens
     dense_case("prefill", 1, 16, 8, 512, 4096, torch.bfloat16, causal=True, window=1024, seed=95, what="gemma3-window")
+
+
+# ---- unquantized caches at head_dim 64 (prefill)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("Hq,Hkv,L,S,causal,window", [(32, 8, 150, 1300, True, 0), (8, 8, 64, 64, True, 0),
+                                                      (14, 2, 100, 2100, False, 0), (16, 4, 300, 3000, True, 1024),
+                                                      (8, 2, 7, 9000, True, 0), (32, 8, 33, 5000, True, 0)])
+def test_dense_prefill_head_dim_64(dtype, Hq, Hkv, L, S, causal, window):
+    dense_case("prefill", 1, Hq, Hkv, L, S, dtype, causal=causal, window=window, seed=110 + L + S, what="d64",
+               head_dim=64)
+
+
+def test_dense_head_dim_64_varlen_capacity_and_dispatch():
+    dense_case("prefill", 3, 16, 4, 40, 900, torch.bfloat16, causal=True, seq_lens=[900, 41, 333], seed=121, cap=1280,
+               what="d64-varlen-cap", head_dim=64)
+    # the public entry point sends a head_dim-64 prompt chunk over an unquantized cache here
+    k, v = make_kv(1, 8, 600, 64, torch.float16, 122)
+    q = seeded_normal((1, 32, 128, 64), 124, torch.float16, DEV)
+    call = kernels.prepare_attention(q, k, v, 0.125, causal=True)
+    assert call.symbol == "kvq_prefill_attn_dense"
+    out = call()
+    torch.cuda.synchronize()
+    assert_close(out, exact(q, k, v, 0.125, causal=True), "d64 dispatch")
 
 
 # ---- the public API routes head_dim 256 here
