@@ -442,11 +442,17 @@ int kvq_paged_prefill_attn(const kvq_rows* q, const kvq_qtensor* k_pool, const k
                            const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int bits, int group_size,
                            int dtype, float scale, int causal, int window, void* workspace, size_t workspace_bytes,
                            void* stream) {
-  if (D != 64 && D != 128) return fail(KVQ_ERR_UNSUPPORTED, "prefill supports head_dim 64 and 128, got %d", D);
+  if (D != 64 && D != 128 && D != 256)
+    return fail(KVQ_ERR_UNSUPPORTED, "prefill supports head_dim 64, 128 and 256, got %d", D);
   int rc = check_paged_attn(q, k_pool, v_pool, num_pages, block_table, table_stride, out, B, Hq, Hkv, L, D, S, bits,
                             group_size, dtype, scale, window, kvq_prefill_workspace_size(B, Hq, Hkv, L, D, S, window),
                             workspace, workspace_bytes);
   if (rc) return rc;
+  if (D == 256)
+    return hip_status(kvq::launch_wide_paged(q, k_pool, v_pool, num_pages, block_table, table_stride, seq_lens, out, B,
+                                             Hq, Hkv, L, S, bits, group_size, dtype, scale, causal, window, workspace,
+                                             (hipStream_t)stream),
+                      "paged_prefill_attn launch (head_dim 256)");
   if ((rc = check_rows(out, "out", D, true))) return rc;  // rows are written 8 bytes at a time
   if ((rc = check_prefill_sb(k_pool, v_pool, D, group_size))) return rc;
   return hip_status(kvq::launch_prefill_paged(q, k_pool, v_pool, num_pages, block_table, table_stride, seq_lens, out, B,

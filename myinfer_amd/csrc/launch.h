@@ -46,6 +46,10 @@ size_t wide_workspace_bytes(int B, int Hq, int Hkv, int L, int D, int S, int win
 hipError_t launch_wide(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v, const int32_t* seq_lens,
                        const kvq_rows* out, int B, int Hq, int Hkv, int L, int S, int bits, int G, int dtype,
                        float scale, int causal, int window, void* workspace, hipStream_t stream);
+hipError_t launch_wide_paged(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v, int num_pages,
+                             const int32_t* table, int64_t table_stride, const int32_t* seq_lens, const kvq_rows* out,
+                             int B, int Hq, int Hkv, int L, int S, int bits, int G, int dtype, float scale, int causal,
+                             int window, void* workspace, hipStream_t stream);
 hipError_t launch_wide_dense(const kvq_rows* q, const kvq_rows* k, const kvq_rows* v, const int32_t* seq_lens,
                              const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int dtype, float scale,
                              int causal, int window, void* workspace, hipStream_t stream);

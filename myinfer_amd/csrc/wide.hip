@@ -96,6 +96,11 @@ struct WideParams {
   int Hq, Hkv, L, S, rep, nrows, rowblocks, nsplit, nunits;
   float scale_log2;
   int causal, window;
+  // paged pools (PAGED kernels): rows of sequence b live in 64-row pages, page table[b][r / 64]; the
+  // codes / scales / biases batch strides above are then page strides
+  const int32_t* table;
+  int64_t table_stride;
+  int num_pages;
 };
 
 // The key held in V^T slot 8 c + e (c = 0..3, e = 0..7): PV k-step c / 2 takes, in lane half c % 2,
@@ -210,9 +215,10 @@ __device__ __forceinline__ void wide_stage_v(const uint8_t* raw, uint8_t* vop, i
   }
 }
 
-template <typename T, int D, int BITS, int G>
+template <typename T, int D, int BITS, int G, bool PAGED = false>
 __global__ __launch_bounds__(kWW * 64, 1) void wide_attn_kernel(WideParams p) {
   using C = WideCfg<D, BITS, G>;
+  static_assert(!PAGED || !C::DENSE, "paged pools hold quantized caches");
   using OT = std::conditional_t<C::DENSE, T, F16>;  // operand type
   __shared__ __align__(16) uint8_t smem[C::LDS];
   uint8_t* const ring = smem;
@@ -264,27 +270,58 @@ __global__ __launch_bounds__(kWW * 64, 1) void wide_attn_kernel(WideParams p) {
   __amdgpu_buffer_rsrc_t sb_r = krs;
   int64_t sb_ss = 0;
   uint32_t sb_vo[C::NSB > 0 ? C::NSB : 1] = {};
+  const uint8_t* sb_page0 = nullptr;  // paged pools: the wave's scale/bias array at page 0 of this head
+  int64_t sb_ps = 0;                  // ... and its page stride in bytes
   if constexpr (!C::DENSE) {
     const uint16_t* arr = wave == 0 ? p.ks : wave == 1 ? p.kb : wave == 2 ? p.vs : p.vb;
     const int64_t sb_b = wave < 2 ? p.ksb_sb : p.vsb_sb, sb_h = wave < 2 ? p.ksb_sh : p.vsb_sh;
     sb_ss = wave < 2 ? p.ksb_ss : p.vsb_ss;
     sb_r = make_rsrc(arr + (int64_t)b * sb_b + (int64_t)kvh * sb_h, (uint32_t)((int64_t)S_b * sb_ss * 2));
+    sb_page0 = (const uint8_t*)(arr + (int64_t)kvh * sb_h);
+    sb_ps = 2 * sb_b;
 #pragma unroll
     for (int j = 0; j < C::NSB; ++j) sb_vo[j] = (uint32_t)(2 * ((lane & 31) * sb_ss + 2 * j + (lane >> 5)));
   }
   const uint32_t ring_lds = lds_addr(ring);
   const int t_last = max(ntile - 1, 0);
+  // paged pools: a 32-key tile (32-aligned) lies in one 64-row page; its page number is read one
+  // tile ahead (a scalar load that the next issue consumes), clamped to the pool, and the tile's
+  // buffer resources span only that page's valid rows, so rows past S_b still read as zero
+  auto page_of = [&](int i) -> int {
+    const int k0 = (t_begin + min(i, t_last)) * kWT;
+    const int pi = min(k0, max(S_b - 1, 0)) >> 6;
+    return __builtin_amdgcn_readfirstlane(min(max(p.table[(int64_t)b * p.table_stride + pi], 0), p.num_pages - 1));
+  };
+  int pg_next = PAGED ? page_of(0) : 0;
   // tile i of this split into ring slot i % NR; past the last tile it re-reads the last one, so every
   // wait below sees the same number of loads in flight
   auto issue = [&](int i) {
     const int k0 = (t_begin + min(i, t_last)) * kWT;
     const uint32_t slot = ring_lds + (uint32_t)((i % C::NR) * C::SLOT);
+    if constexpr (PAGED) {
+      const int pg = pg_next;
+      pg_next = page_of(i + 1);
+      const int nv = __builtin_amdgcn_readfirstlane(max(min(64, S_b - (k0 & ~63)), 0));  // valid rows of the page
+      const int r0p = k0 & 63;                                                          // the tile's first row in it
 #pragma unroll
-    for (int j = 0; j < C::CPW; ++j) dma_b128(code_r[j], slot + code_lds[j], code_vo[j], (uint32_t)(k0 * code_ss[j]));
-    if constexpr (!C::DENSE) {
+      for (int j = 0; j < C::CPW; ++j) {
+        const bool is_k = wave * C::CPW + j < C::CI;
+        const uint8_t* base = is_k ? p.kc + (int64_t)kvh * p.kc_sh + (int64_t)pg * p.kc_sb
+                                   : p.vc + (int64_t)kvh * p.vc_sh + (int64_t)pg * p.vc_sb;
+        dma_b128(make_rsrc(base, (uint32_t)(nv * code_ss[j])), slot + code_lds[j], code_vo[j], (uint32_t)(r0p * code_ss[j]));
+      }
+      const __amdgpu_buffer_rsrc_t r = make_rsrc(sb_page0 + (int64_t)pg * sb_ps, (uint32_t)(nv * sb_ss * 2));
 #pragma unroll
       for (int j = 0; j < C::NSB; ++j)
-        dma_b16(sb_r, slot + 2 * C::TB + C::SBA * wave + 256 * j, sb_vo[j], (uint32_t)(2 * k0 * sb_ss));
+        dma_b16(r, slot + 2 * C::TB + C::SBA * wave + 256 * j, sb_vo[j], (uint32_t)(2 * r0p * sb_ss));
+    } else {
+#pragma unroll
+      for (int j = 0; j < C::CPW; ++j) dma_b128(code_r[j], slot + code_lds[j], code_vo[j], (uint32_t)(k0 * code_ss[j]));
+      if constexpr (!C::DENSE) {
+#pragma unroll
+        for (int j = 0; j < C::NSB; ++j)
+          dma_b16(sb_r, slot + 2 * C::TB + C::SBA * wave + 256 * j, sb_vo[j], (uint32_t)(2 * k0 * sb_ss));
+      }
     }
   };
 
@@ -480,9 +517,9 @@ size_t wide_workspace_bytes(int B, int Hq, int Hkv, int L, int D, int S, int win
   return kCounterBytes + up(rows * sizeof(float2)) + up(rows * D * sizeof(float));
 }
 
-template <typename T, int D, int BITS, int G>
+template <typename T, int D, int BITS, int G, bool PAGED = false>
 static hipError_t launch_wide_t(const WideParams& p, hipStream_t stream) {
-  hipLaunchKernelGGL((wide_attn_kernel<T, D, BITS, G>), dim3(p.nunits * p.nsplit), dim3(kWW * 64), 0, stream, p);
+  hipLaunchKernelGGL((wide_attn_kernel<T, D, BITS, G, PAGED>), dim3(p.nunits * p.nsplit), dim3(kWW * 64), 0, stream, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || p.nsplit == 1) return e;
   MergeParams m;
@@ -534,10 +571,7 @@ static WideParams wide_params(const kvq_rows* q, const int32_t* seq_lens, const 
   return p;
 }
 
-hipError_t launch_wide(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v, const int32_t* seq_lens,
-                       const kvq_rows* out, int B, int Hq, int Hkv, int L, int S, int bits, int G, int dtype,
-                       float scale, int causal, int window, void* workspace, hipStream_t stream) {
-  WideParams p = wide_params(q, seq_lens, out, B, Hq, Hkv, L, S, scale, causal, window, workspace);
+static void wide_quant_params(WideParams& p, const kvq_qtensor* k, const kvq_qtensor* v) {
   p.kc = (const uint8_t*)k->codes;
   p.vc = (const uint8_t*)v->codes;
   p.kc_sb = k->codes_stride_b * 4;
@@ -556,15 +590,40 @@ hipError_t launch_wide(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtenso
   p.vsb_sb = v->sb_stride_b;
   p.vsb_sh = v->sb_stride_h;
   p.vsb_ss = v->sb_stride_s;
+}
+
+template <bool PAGED>
+static hipError_t launch_wide_quant(const WideParams& p, int bits, int G, int dtype, hipStream_t stream) {
   auto go = [&](auto t) -> hipError_t {
     using T = decltype(t);
-    if (bits == 8 && G == 64) return launch_wide_t<T, 256, 8, 64>(p, stream);
-    if (bits == 8 && G == 128) return launch_wide_t<T, 256, 8, 128>(p, stream);
-    if (bits == 4 && G == 64) return launch_wide_t<T, 256, 4, 64>(p, stream);
-    if (bits == 4 && G == 128) return launch_wide_t<T, 256, 4, 128>(p, stream);
+    if (bits == 8 && G == 64) return launch_wide_t<T, 256, 8, 64, PAGED>(p, stream);
+    if (bits == 8 && G == 128) return launch_wide_t<T, 256, 8, 128, PAGED>(p, stream);
+    if (bits == 4 && G == 64) return launch_wide_t<T, 256, 4, 64, PAGED>(p, stream);
+    if (bits == 4 && G == 128) return launch_wide_t<T, 256, 4, 128, PAGED>(p, stream);
     return hipErrorInvalidValue;
   };
   return dtype == KVQ_DTYPE_BF16 ? go(BF16{}) : go(F16{});
+}
+
+hipError_t launch_wide(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v, const int32_t* seq_lens,
+                       const kvq_rows* out, int B, int Hq, int Hkv, int L, int S, int bits, int G, int dtype,
+                       float scale, int causal, int window, void* workspace, hipStream_t stream) {
+  WideParams p = wide_params(q, seq_lens, out, B, Hq, Hkv, L, S, scale, causal, window, workspace);
+  wide_quant_params(p, k, v);
+  return launch_wide_quant<false>(p, bits, G, dtype, stream);
+}
+
+// Paged pools: the k / v descriptors' batch strides are page strides (include/kvq.h "Paged layout").
+hipError_t launch_wide_paged(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v, int num_pages,
+                             const int32_t* table, int64_t table_stride, const int32_t* seq_lens, const kvq_rows* out,
+                             int B, int Hq, int Hkv, int L, int S, int bits, int G, int dtype, float scale, int causal,
+                             int window, void* workspace, hipStream_t stream) {
+  WideParams p = wide_params(q, seq_lens, out, B, Hq, Hkv, L, S, scale, causal, window, workspace);
+  wide_quant_params(p, k, v);
+  p.table = table;
+  p.table_stride = table_stride;
+  p.num_pages = num_pages;
+  return launch_wide_quant<true>(p, bits, G, dtype, stream);
 }
 
 hipError_t launch_wide_dense(const kvq_rows* q, const kvq_rows* k, const kvq_rows* v, const int32_t* seq_lens,

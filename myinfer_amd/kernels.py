@@ -245,13 +245,11 @@ def decode_rows_per_pass(D: int, group_size: int = 64) -> int:
     return 16 * group_size // D
 
 
-def _auto_kernel(rep_rows: int, D: int, group_size: int, dense: bool = False, paged: bool = False) -> str:
+def _auto_kernel(rep_rows: int, D: int, group_size: int) -> str:
     """Decode while a KV head's query rows fit at most two decode passes over its keys (one pass for
-    group 64, where 8 rows fit one pass), the prefill kernel otherwise; decode where the prefill
-    kernel has no build (head_dim 256 over a paged pool). At head_dim 256 the unquantized entry
-    points run the head_dim-256 kernel for every query length."""
-    prefill_built = D in (64, 128) or (D == 256 and not paged)
-    return "decode" if (rep_rows <= max(decode_rows_per_pass(D, group_size), 8) or not prefill_built) else "prefill"
+    group 64, where 8 rows fit one pass), the prefill kernel otherwise (every head dim has one). At
+    head_dim 256 the unquantized entry points run the head_dim-256 kernel for every query length."""
+    return "decode" if rep_rows <= max(decode_rows_per_pass(D, group_size), 8) else "prefill"
 
 
 class AttentionCall:
@@ -348,7 +346,7 @@ def prepare_attention(queries: torch.Tensor, keys, values, scale: float, *, caus
         sl_ptr = seq_lens.data_ptr()
     rep = Hq // Hkv
     if kernel == "auto":
-        kernel = _auto_kernel(rep * L, D, 64 if dense else group_size, dense)
+        kernel = _auto_kernel(rep * L, D, 64 if dense else group_size)
     if kernel not in ("decode", "prefill"):
         raise ValueError(f"kernel must be 'decode', 'prefill' or 'auto', got {kernel!r}")
     lib = _lib.lib()
@@ -473,7 +471,7 @@ def paged_attention(queries: torch.Tensor, k_pool: Triple, v_pool: Triple, block
         queries = queries.contiguous()
     out = _check_out(out, queries, dev)
     if kernel == "auto":
-        kernel = _auto_kernel((Hq // Hkv) * L, D, group_size, paged=True)
+        kernel = _auto_kernel((Hq // Hkv) * L, D, group_size)
     lib = _lib.lib()
     ws_fn = lib.kvq_decode_workspace_size if kernel == "decode" else lib.kvq_prefill_workspace_size
     nbytes = ws_fn(B, Hq, Hkv, L, D, S, int(window))

@@ -235,14 +235,12 @@ def test_paged_head_dim_256(bits):
     rows, tables, kp, vp, kc, vc = build(B, Hkv, lens, D, bits, dtype, 51, group=64)
     sl = torch.tensor(lens, dtype=torch.int32, device=DEV)
     scale = 1.0 / math.sqrt(D)
-    for L in (1, 3):
+    for L in (1, 3, 200):
         q = seeded_normal((B, Hq, L, D), 52 + L, dtype, DEV)
         out_p = kernels.paged_attention(q, kp, vp, tables, sl, scale, causal=True, bits=bits, group_size=64,
                                         max_len=max(lens))
-        # paged pools at head_dim 256 run the decode kernel for every query length; the contiguous
-        # cache through the same kernel gives the same bits
-        out_c = kernels.attention(q, kc, vc, scale, causal=True, seq_lens=sl, bits=bits, group_size=64,
-                                  kernel="decode")
+        # L = 1 runs the decode kernel, L = 3 and 200 the head_dim-256 prefill kernel, on both layouts
+        out_c = kernels.attention(q, kc, vc, scale, causal=True, seq_lens=sl, bits=bits, group_size=64)
         torch.cuda.synchronize()
         assert torch.isfinite(out_p.float()).all()
         assert torch.equal(out_p, out_c), L
