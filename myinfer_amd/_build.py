@@ -39,6 +39,11 @@ HIPCC_FLAGS = [
 ]
 
 
+# Per-source additions. wide.hip keeps its MFMA accumulators in VGPRs: one wave per SIMD has 512
+# registers, and with AGPR accumulators the compiler copied all 128 of them between the two files on
+# every tile step.
+SOURCE_FLAGS = {"wide.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
 HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall"]
 
 
@@ -83,7 +88,8 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
     host_objs = [OBJ / (s.stem + ".host.o") for s in host_sources]
     jobs = jobs or min(len(sources) + len(host_sources), max(1, os.cpu_count() or 1), 8)
     with cf.ThreadPoolExecutor(jobs) as ex:
-        futs = [ex.submit(_run, [hipcc, *HIPCC_FLAGS, "-c", str(s), "-o", str(o)], verbose) for s, o in zip(sources, objs)]
+        futs = [ex.submit(_run, [hipcc, *HIPCC_FLAGS, *SOURCE_FLAGS.get(s.name, []), "-c", str(s), "-o", str(o)], verbose)
+                for s, o in zip(sources, objs)]
         futs += [ex.submit(_run, ["g++", *HOST_FLAGS, "-c", str(s), "-o", str(o)], verbose)
                  for s, o in zip(host_sources, host_objs)]
         for f in futs:

@@ -388,13 +388,18 @@ __global__ __launch_bounds__(kWW * 64, 1) void wide_attn_kernel(WideParams p) {
   // slot raw1 into (kd, vd). The step is one basic block: each product's operand reads are issued
   // ahead of its MFMA chain, and the staging's independent VALU work fills the chain's issue slots.
   auto step = [&](const uint8_t* kt, const uint8_t* vt, int k0, const uint8_t* raw1, uint8_t* kd, uint8_t* vd) {
-    u4 ka[C::KSTEPS];
+    // K operands through a ring of KR registers, read KR MFMAs ahead
+    constexpr int KR = C::KSTEPS < 8 ? C::KSTEPS : 8;
+    u4 ka[KR];
 #pragma unroll
-    for (int j = 0; j < C::KSTEPS; ++j) ka[j] = *(const u4*)(kt + k_off + 32 * j);
+    for (int j = 0; j < KR; ++j) ka[j] = *(const u4*)(kt + k_off + 32 * j);
     wide_stage_k<T, OT, D, BITS, G>(raw1, kd, tid);
     f16v s = f16v{};
 #pragma unroll
-    for (int j = 0; j < C::KSTEPS; ++j) s = mfma_32x32x16(ka[j], qop[j], s, OT{});
+    for (int j = 0; j < C::KSTEPS; ++j) {
+      s = mfma_32x32x16(ka[j % KR], qop[j], s, OT{});
+      if (j + KR < C::KSTEPS) ka[j % KR] = *(const u4*)(kt + k_off + 32 * (j + KR));
+    }
     // value i of the lane is key k0 + 8 (i / 4) + 4 h + i % 4 of query row n
     if (!(k0 >= lo_all && k0 + kWT <= hi_all)) {
 #pragma unroll
@@ -426,13 +431,20 @@ __global__ __launch_bounds__(kWW * 64, 1) void wide_attn_kernel(WideParams p) {
         pop[st][a] = pack2(p0, p1, OT{});
         l_run = add_pair(pop[st][a], l_run, OT{});
       }
-    u4 va[2 * C::NDB];
+    // V^T operands likewise, VR MFMAs ahead
+    constexpr int NV = 2 * C::NDB, VR = NV < 8 ? NV : 8;
+    auto vop_at = [&](int i) {
+      return *(const u4*)(vt + 32 * (i >> 1) * (kWT * 2) + v_off + 16 * ((2 * (i & 1) + h) ^ v_sw));
+    };
+    u4 va[VR];
 #pragma unroll
-    for (int i = 0; i < 2 * C::NDB; ++i)
-      va[i] = *(const u4*)(vt + 32 * (i >> 1) * (kWT * 2) + v_off + 16 * ((2 * (i & 1) + h) ^ v_sw));
+    for (int i = 0; i < VR; ++i) va[i] = vop_at(i);
     wide_stage_v<T, OT, D, BITS, G>(raw1, vd, tid);
 #pragma unroll
-    for (int i = 0; i < 2 * C::NDB; ++i) oacc[i >> 1] = mfma_32x32x16(va[i], pop[i & 1], oacc[i >> 1], OT{});
+    for (int i = 0; i < NV; ++i) {
+      oacc[i >> 1] = mfma_32x32x16(va[i % VR], pop[i & 1], oacc[i >> 1], OT{});
+      if (i + VR < NV) va[i % VR] = vop_at(i + VR);
+    }
   };
 
   // ---- the tile loop: tile t is computed from operand buffer t % 2 while tile t + 1 is staged into
