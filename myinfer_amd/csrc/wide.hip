@@ -108,9 +108,26 @@ struct WideParams {
 // 16 (c / 2) + 4 (c % 2) + (e < 4 ? e : e + 4).
 __host__ __device__ constexpr int w_slot_key(int c, int e) { return 16 * (c >> 1) + 4 * (c & 1) + (e < 4 ? e : e + 4); }
 
-template <typename T>
-__device__ __forceinline__ float dq(uint32_t code, uint32_t s_cell, uint32_t b_cell) {
-  return fmaf(to_float((uint16_t)(s_cell & 0xffffu), T{}), (float)code, to_float((uint16_t)(b_cell & 0xffffu), T{}));
+// A scale/bias cell (the value in its low half, the cache's dtype) as fp16. A bf16 value beyond the
+// fp16 range becomes inf, and the rows that read the group come out non-finite.
+__device__ __forceinline__ _Float16 cell_half(uint32_t cell, F16) { return __builtin_bit_cast(_Float16, (uint16_t)cell); }
+__device__ __forceinline__ _Float16 cell_half(uint32_t cell, BF16) { return (_Float16)__uint_as_float(cell << 16); }
+
+// Two codes as fp16 s * c + b in packed arithmetic: the code bytes `sel` picks become the low
+// mantissa bytes of 0x64xx (1024 + c, exact), then one packed subtract and one packed FMA (rounded
+// once to fp16).
+__device__ __forceinline__ uint32_t dq_pair(uint32_t bytes, uint32_t sel, h2 s2, h2 b2) {
+  h2 x = __builtin_bit_cast(h2, perm(0x64646464u, bytes, sel)) - h2{(_Float16)1024.0f, (_Float16)1024.0f};
+  return __builtin_bit_cast(uint32_t, x * s2 + b2);
+}
+constexpr uint32_t kSelLo = 0x04010400u;  // bytes 0, 1 -> fp16 pair
+constexpr uint32_t kSelHi = 0x04030402u;  // bytes 2, 3 -> fp16 pair
+// 4-bit codes 0..3 (or 4..7) of a word as one byte each
+__device__ __forceinline__ uint32_t nibbles_lo(uint32_t w) {
+  return perm((w >> 4) & 0x0F0F0F0Fu, w & 0x0F0F0F0Fu, 0x05010400u);
+}
+__device__ __forceinline__ uint32_t nibbles_hi(uint32_t w) {
+  return perm((w >> 4) & 0x0F0F0F0Fu, w & 0x0F0F0F0Fu, 0x07030602u);
 }
 
 // K of a raw tile into the K operand tile (OT elements): thread t dequantizes dims
@@ -128,35 +145,25 @@ __device__ __forceinline__ void wide_stage_k(const uint8_t* raw, uint8_t* kop, i
   } else {
     const int g = 32 * p / G;
     const uint32_t* cells = (const uint32_t*)(raw + 2 * C::TB);
-    const uint32_t sc = cells[32 * g + r], bc = cells[C::SBA / 4 + 32 * g + r];
-    uint32_t code[8];
+    const _Float16 sh = cell_half(cells[32 * g + r], T{}), bh = cell_half(cells[C::SBA / 4 + 32 * g + r], T{});
+    const h2 s2 = {sh, sh}, b2 = {bh, bh};
     if constexpr (BITS == 8) {
       const u4 a = *(const u4*)(raw + r * C::ROWB + 32 * p), b = *(const u4*)(raw + r * C::ROWB + 32 * p + 16);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        code[i] = a[i];
-        code[4 + i] = b[i];
+        const uint32_t wa = i < 2 ? a[2 * i] : b[2 * (i - 2)], wb = i < 2 ? a[2 * i + 1] : b[2 * (i - 2) + 1];
+        w[i] = u4{dq_pair(wa, kSelLo, s2, b2), dq_pair(wa, kSelHi, s2, b2), dq_pair(wb, kSelLo, s2, b2),
+                  dq_pair(wb, kSelHi, s2, b2)};
       }
     } else {
       const u4 a = *(const u4*)(raw + r * C::ROWB + 16 * p);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) code[i] = a[i];
-    }
-#pragma unroll
-    for (int c = 0; c < 4; ++c)
-#pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int d = 8 * c + 2 * i;  // dims d, d + 1 of the thread's 32
-        uint32_t c0, c1;
-        if constexpr (BITS == 8) {
-          c0 = (code[d >> 2] >> (8 * (d & 3))) & 0xffu;
-          c1 = (code[(d + 1) >> 2] >> (8 * ((d + 1) & 3))) & 0xffu;
-        } else {
-          c0 = (code[d >> 3] >> (4 * (d & 7))) & 0xfu;
-          c1 = (code[(d + 1) >> 3] >> (4 * ((d + 1) & 7))) & 0xfu;
-        }
-        w[c][i] = pack2(dq<T>(c0, sc, bc), dq<T>(c1, sc, bc), OT{});
+        const uint32_t lo = nibbles_lo(a[i]), hi = nibbles_hi(a[i]);
+        w[i] = u4{dq_pair(lo, kSelLo, s2, b2), dq_pair(lo, kSelHi, s2, b2), dq_pair(hi, kSelLo, s2, b2),
+                  dq_pair(hi, kSelHi, s2, b2)};
       }
+    }
   }
 #pragma unroll
   for (int c = 0; c < C::KCH; ++c) *(u4*)(kop + r * C::KROW + 16 * (C::KCH * p + c)) = w[c];
@@ -171,19 +178,22 @@ __device__ __forceinline__ void wide_stage_v(const uint8_t* raw, uint8_t* vop, i
   using C = WideCfg<D, BITS, G>;
   const int c = t >> 6, j = t & 63;
   const uint8_t* vraw = raw + C::TB;
-  float x[8][C::VPT];  // [slot e][dim i]
+  // xp[e][q]: key e's dims 2q, 2q + 1 of the thread's VPT as a packed pair (one 16-bit value when
+  // VPT is 1)
+  uint32_t xp[8][(C::VPT + 1) / 2];
   if constexpr (C::DENSE) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       if constexpr (C::VPT == 4) {
         const u2 v = *(const u2*)(vraw + w_slot_key(c, e) * C::ROWB + 8 * j);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) x[e][i] = to_float((uint16_t)(v[i >> 1] >> (16 * (i & 1))), T{});
+        xp[e][0] = v[0];
+        xp[e][1] = v[1];
       } else {
-        x[e][0] = to_float(*(const uint16_t*)(vraw + w_slot_key(c, e) * C::ROWB + 2 * j), T{});
+        xp[e][0] = *(const uint16_t*)(vraw + w_slot_key(c, e) * C::ROWB + 2 * j);
       }
     }
   } else {
+    static_assert(C::VPT == 4, "quantized caches at head_dim 256");
     const int g = 4 * j / G;
     const uint8_t* cells = raw + 2 * C::TB + 2 * C::SBA + 4 * 32 * g;  // sV, then bV one array later
     const int kb0 = w_slot_key(c, 0);
@@ -191,25 +201,30 @@ __device__ __forceinline__ void wide_stage_v(const uint8_t* raw, uint8_t* vop, i
     const u4 b_lo = *(const u4*)(cells + C::SBA + 4 * kb0), b_hi = *(const u4*)(cells + C::SBA + 4 * (kb0 + 8));
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const uint32_t sc = e < 4 ? s_lo[e] : s_hi[e - 4], bc = e < 4 ? b_lo[e] : b_hi[e - 4];
-      uint32_t w;
+      const _Float16 sh = cell_half(e < 4 ? s_lo[e] : s_hi[e - 4], T{});
+      const _Float16 bh = cell_half(e < 4 ? b_lo[e] : b_hi[e - 4], T{});
+      uint32_t bytes;  // codes of the thread's 4 dims, one byte each
       if constexpr (BITS == 8) {
-        w = *(const uint32_t*)(vraw + w_slot_key(c, e) * C::ROWB + 4 * j);
+        bytes = *(const uint32_t*)(vraw + w_slot_key(c, e) * C::ROWB + 4 * j);
       } else {
-        w = *(const uint16_t*)(vraw + w_slot_key(c, e) * C::ROWB + 2 * j);
+        bytes = nibbles_lo(*(const uint16_t*)(vraw + w_slot_key(c, e) * C::ROWB + 2 * j));
       }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint32_t code = BITS == 8 ? (w >> (8 * i)) & 0xffu : (w >> (4 * i)) & 0xfu;
-        x[e][i] = dq<T>(code, sc, bc);
-      }
+      xp[e][0] = dq_pair(bytes, kSelLo, h2{sh, sh}, h2{bh, bh});
+      xp[e][1] = dq_pair(bytes, kSelHi, h2{sh, sh}, h2{bh, bh});
     }
   }
+  // V^T row of dim i: slots e = 0..7, packed (2a, 2a + 1): the matching halves of two keys' pairs
 #pragma unroll
   for (int i = 0; i < C::VPT; ++i) {
     u4 o;
 #pragma unroll
-    for (int a = 0; a < 4; ++a) o[a] = pack2(x[2 * a][i], x[2 * a + 1][i], OT{});
+    for (int a = 0; a < 4; ++a) {
+      if constexpr (C::VPT == 1) {
+        o[a] = (xp[2 * a][0] & 0xffffu) | (xp[2 * a + 1][0] << 16);
+      } else {
+        o[a] = perm(xp[2 * a + 1][i >> 1], xp[2 * a][i >> 1], (i & 1) ? 0x07060302u : 0x05040100u);
+      }
+    }
     const int d = C::VPT * j + i;
     *(u4*)(vop + d * (kWT * 2) + 16 * (c ^ ((d >> 2) & 3))) = o;
   }
