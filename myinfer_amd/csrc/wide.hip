@@ -135,7 +135,7 @@ __device__ __forceinline__ uint32_t nibbles_hi(uint32_t w) {
 // bytes longer than the data (528 bytes at D = 256), so the 32 lanes that read one 16-byte column of
 // 32 keys hit distinct banks and a lane's reads of one row are one base address plus immediates.
 template <typename T, typename OT, int D, int BITS, int G>
-__device__ __forceinline__ void wide_stage_k(const uint8_t* raw, uint8_t* kop, int t) {
+__device__ __forceinline__ void wide_stage_k(const uint8_t* raw, uint8_t* kop, int t, bool& range_bad) {
   using C = WideCfg<D, BITS, G>;
   const int r = t >> 3, p = t & 7;
   u4 w[C::KCH];
@@ -146,6 +146,9 @@ __device__ __forceinline__ void wide_stage_k(const uint8_t* raw, uint8_t* kop, i
     const int g = 32 * p / G;
     const uint32_t* cells = (const uint32_t*)(raw + 2 * C::TB);
     const _Float16 sh = cell_half(cells[32 * g + r], T{}), bh = cell_half(cells[C::SBA / 4 + 32 * g + r], T{});
+    // MLX's bias is the group's larger-magnitude extreme: it converts to inf exactly when some
+    // value of the group lies beyond the fp16 range
+    if constexpr (T::id == KVQ_DTYPE_BF16) range_bad |= __builtin_isinf((float)bh);
     const h2 s2 = {sh, sh}, b2 = {bh, bh};
     if constexpr (BITS == 8) {
       const u4 a = *(const u4*)(raw + r * C::ROWB + 32 * p), b = *(const u4*)(raw + r * C::ROWB + 32 * p + 16);
@@ -174,7 +177,7 @@ __device__ __forceinline__ void wide_stage_k(const uint8_t* raw, uint8_t* kop, i
 // dims, the chunk's 8 slots (16 bytes) to row d at chunk position c ^ ((d >> 2) & 3) (rows are 64
 // bytes: 32 slots).
 template <typename T, typename OT, int D, int BITS, int G>
-__device__ __forceinline__ void wide_stage_v(const uint8_t* raw, uint8_t* vop, int t) {
+__device__ __forceinline__ void wide_stage_v(const uint8_t* raw, uint8_t* vop, int t, bool& range_bad) {
   using C = WideCfg<D, BITS, G>;
   const int c = t >> 6, j = t & 63;
   const uint8_t* vraw = raw + C::TB;
@@ -203,6 +206,7 @@ __device__ __forceinline__ void wide_stage_v(const uint8_t* raw, uint8_t* vop, i
     for (int e = 0; e < 8; ++e) {
       const _Float16 sh = cell_half(e < 4 ? s_lo[e] : s_hi[e - 4], T{});
       const _Float16 bh = cell_half(e < 4 ? b_lo[e] : b_hi[e - 4], T{});
+      if constexpr (T::id == KVQ_DTYPE_BF16) range_bad |= __builtin_isinf((float)bh);
       uint32_t bytes;  // codes of the thread's 4 dims, one byte each
       if constexpr (BITS == 8) {
         bytes = *(const uint32_t*)(vraw + w_slot_key(c, e) * C::ROWB + 4 * j);
@@ -389,6 +393,7 @@ __global__ __launch_bounds__(kWW * 64, 1) void wide_attn_kernel(WideParams p) {
   }
 
   float m_run = -INFINITY, l_run = 0.0f;
+  bool range_bad = false;  // a tile this thread staged holds a bf16 group beyond the fp16 range
   f16v oacc[C::NDB];
 #pragma unroll
   for (int db = 0; db < C::NDB; ++db) oacc[db] = f16v{};
@@ -408,7 +413,7 @@ __global__ __launch_bounds__(kWW * 64, 1) void wide_attn_kernel(WideParams p) {
     u4 ka[KR];
 #pragma unroll
     for (int j = 0; j < KR; ++j) ka[j] = *(const u4*)(kt + k_off + 32 * j);
-    wide_stage_k<T, OT, D, BITS, G>(raw1, kd, tid);
+    wide_stage_k<T, OT, D, BITS, G>(raw1, kd, tid, range_bad);
     f16v s = f16v{};
 #pragma unroll
     for (int j = 0; j < C::KSTEPS; ++j) {
@@ -454,7 +459,7 @@ __global__ __launch_bounds__(kWW * 64, 1) void wide_attn_kernel(WideParams p) {
     u4 va[VR];
 #pragma unroll
     for (int i = 0; i < VR; ++i) va[i] = vop_at(i);
-    wide_stage_v<T, OT, D, BITS, G>(raw1, vd, tid);
+    wide_stage_v<T, OT, D, BITS, G>(raw1, vd, tid, range_bad);
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       oacc[i >> 1] = mfma_32x32x16(va[i % VR], pop[i & 1], oacc[i >> 1], OT{});
@@ -469,8 +474,8 @@ __global__ __launch_bounds__(kWW * 64, 1) void wide_attn_kernel(WideParams p) {
   if (ntile > 0) {
     wait_vm<0>();  // the query and the first NR raw tiles
     __syncthreads();
-    wide_stage_k<T, OT, D, BITS, G>(ring, kop, tid);
-    wide_stage_v<T, OT, D, BITS, G>(ring, vop, tid);
+    wide_stage_k<T, OT, D, BITS, G>(ring, kop, tid, range_bad);
+    wide_stage_v<T, OT, D, BITS, G>(ring, vop, tid, range_bad);
     for (int t = 0; t < ntile; ++t) {
       if constexpr (C::NR == 3) {
         wait_vm<C::IPW>();  // tile t + 1 has landed (tile t + 2 may be in flight)
@@ -485,9 +490,20 @@ __global__ __launch_bounds__(kWW * 64, 1) void wide_attn_kernel(WideParams p) {
     }
   }
   wait_vm<0>();  // the look-ahead loads land before the workgroup's LDS is released
+  float l_tot = add_xor32(l_run);
+  if constexpr (!C::DENSE && T::id == KVQ_DTYPE_BF16) {
+    // a group beyond the fp16 range poisons every row of the workgroup: NaN output rows, or NaN
+    // partials with (m, l) = (0, 1), which the split merge counts and carries to the output rows
+    // (its weight times NaN is NaN, zero weight included)
+    if (__syncthreads_or(range_bad)) {
+#pragma unroll
+      for (int db = 0; db < C::NDB; ++db) oacc[db] = f16v{} + __builtin_nanf("");
+      m_run = 0.0f;
+      l_tot = 1.0f;
+    }
+  }
 
   // ---- epilogue: lane (n, h) holds O^T rows 32 db + 8 i + 4 h + j (j = 0..3) of query row n
-  const float l_tot = add_xor32(l_run);
   if (!row_ok) return;
   if (p.nsplit == 1) {
     const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;

@@ -1,8 +1,9 @@
 """bf16 caches whose values leave the fp16 range.
 
 MLX stores a bf16 cache's scales and biases in bf16, so a group may hold values beyond 65504. The
-prefill kernel's dequantized operands are fp16: a row block that reads such a group returns NaN
-(not finite wrong values), and every other row block stays exact. The decode kernel applies key
+prefill kernels' dequantized operands are fp16 (head_dim 64/128 and head_dim 256 alike): a row
+block that reads such a group returns NaN (not finite wrong values), and every other row block
+stays exact. The decode kernel applies key
 scales and biases in fp32 and takes |x| up to about 1.3e5 in values (the probability times value
 scale is an fp16 operand), so it stays exact for the same cache.
 """
@@ -72,3 +73,24 @@ def test_decode_exact_beyond_fp16():
     ref = exact_reference(q, kt, vt, scale, bits=bits)
     assert np.isfinite(out.cpu().float().numpy()).all()
     assert_close(out, ref, "decode beyond fp16")
+
+
+@pytest.mark.parametrize("which", ["keys", "values"])
+@pytest.mark.parametrize("L,S,causal", [(64, 700, True), (200, 900, False), (16, 12000, True)])
+def test_head_dim_256_poisons_beyond_fp16(which, L, S, causal):
+    # wide_attn_kernel (head_dim 256) dequantizes to fp16 operands as well; (16, 12000) splits the
+    # key range over workgroups, so the poisoned partials must reach the output through the merge
+    print(f"range wide which={which} L={L} S={S} causal={causal}", flush=True)
+    B, Hq, Hkv, D, bits = 1, 8, 2, 256, 8
+    kmul, vmul = (4e4, 1.0) if which == "keys" else (1.0, 4e4)
+    kt, vt = big_cache(B, Hkv, S, D, bits, 1, kmul, vmul, 320 + L)
+    assert not kernels.fits_fp16_operands(kt if which == "keys" else vt, bits)
+    q = seeded_normal((B, Hq, L, D), 322 + L, torch.bfloat16, DEV)
+    scale = 1.0 / math.sqrt(D)
+    out = kernels.attention(q, kt, vt, scale, causal=causal, bits=bits, kernel="prefill")
+    torch.cuda.synchronize()
+    o = out.cpu().float()
+    assert torch.isnan(o[:, 4:]).all()
+    ref = exact_reference(q[:, :4], tuple(t[:, :1] for t in kt), tuple(t[:, :1] for t in vt), scale, bits=bits,
+                          causal=causal)
+    assert_close(out[:, :4], ref, "wide in-range head")
