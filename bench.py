@@ -565,10 +565,11 @@ def time_prefill(cfg, steps, warmup, device, want_parity=False):
     return res
 
 
-def time_attention_shape(desc, q, k, v, scale, flops, steps, device, **mask):
+def time_attention_shape(desc, q, k, v, scale, flops, steps, device, check=None, **mask):
     """Attention-kernel TFLOP/s of one prefill call shape (k, v: unquantized tensors, or quantized
     triples with bits / group_size among the keyword arguments): `steps` calls captured in a HIP
-    graph and replayed once, timed with events."""
+    graph and replayed once, timed with events. `check(out)`, when given, judges the output the
+    timed replay left and its record goes in as "parity"."""
     import torch
 
     from myinfer_amd import kernels
@@ -594,8 +595,39 @@ def time_attention_shape(desc, q, k, v, scale, flops, steps, device, **mask):
     torch.cuda.synchronize()
     ms = s_.elapsed_time(e_) / steps
     del graph
-    return {"tflops": round(flops / (ms * 1e-3) / 1e12, 2), "frac": round(flops / (ms * 1e-3) / 1e12 / PEAK_MFMA_TFLOPS, 4),
-            "us_per_call": round(ms * 1e3, 2), "flops": flops}
+    res = {"tflops": round(flops / (ms * 1e-3) / 1e12, 2), "frac": round(flops / (ms * 1e-3) / 1e12 / PEAK_MFMA_TFLOPS, 4),
+           "us_per_call": round(ms * 1e3, 2), "flops": flops}
+    if check is not None:
+        res["parity"] = check(out)
+    return res
+
+
+def tail_parity(q, k, v, out, scale, rows=128, bits=None, window=0):
+    """The last `rows` queries of a causal call (all heads) against the exact fp64 oracle: queries
+    align to the end of the keys, as in the kernels. k, v: unquantized tensors, or quantized
+    triples of group 64 with `bits`."""
+    import numpy as np
+    import torch
+
+    from oracle import attention as OA
+    from oracle import quantize as OQ
+
+    dt = str(q.dtype).replace("torch.", "")
+
+    def host(x):
+        if bits is None:
+            return x.float().cpu().double().numpy()
+        cc, ss, bb = x
+        return OQ.dequantize(cc.cpu().view(torch.int32).numpy().view(np.uint32),
+                             ss.cpu().view(torch.int16).numpy().view(np.uint16),
+                             bb.cpu().view(torch.int16).numpy().view(np.uint16), dt, 64, bits)
+
+    L = q.shape[2]
+    r = min(rows, L)
+    qs = q[:, :, L - r:].float().cpu().double().numpy()
+    ref = OA.exact_attention(qs, host(k), host(v), scale, causal=True, window=window)
+    got = out[:, :, L - r:].float().cpu().double().numpy()
+    return parity_record(got, ref, dt, rows=f"last {r} of {L} queries")
 
 
 def dense_prefill_extras(steps, device):
@@ -650,12 +682,12 @@ def wide_extras(steps, device):
     res["D256-prefill-q8"] = time_attention_shape(
         "head_dim 256 prefill chunk over an 8-bit cache (Gemma-3-12B heads, 2048 queries, 8192 keys, causal)",
         q, trip[0], trip[1], 1.0 / math.sqrt(D), prefill_flops(S, Hq, D, S - C, S), steps, device, causal=True,
-        bits=8, group_size=64)
+        bits=8, group_size=64, check=lambda out: tail_parity(q, trip[0], trip[1], out, 1.0 / math.sqrt(D), bits=8))
     W = 1024
     res["D256-window-prefill-dense"] = time_attention_shape(
         "head_dim 256 window-1024 prefill chunk over an unquantized bf16 cache (2048 queries, 8192 keys)",
         q, k, v, 1.0 / math.sqrt(D), prefill_flops(S, Hq, D, S - C, S, window=W), steps, device, causal=True,
-        window=W)
+        window=W, check=lambda out: tail_parity(q, k, v, out, 1.0 / math.sqrt(D), window=W))
     del trip
     B = 4
     k = torch.randn((B, Hkv, S, D), generator=g, device=device).to(T)
@@ -682,7 +714,8 @@ def wide_extras(steps, device):
     us = s_.elapsed_time(e_) / steps * 1e3
     nbytes = 2 * k.numel() * 2 + 2 * q.numel() * 2
     res["D256-decode-dense-b4"] = {"gbs": round(nbytes / us / 1e3, 1), "frac": round(nbytes / us / 1e3 / PEAK_HBM_GBS, 4),
-                                   "us_per_step": round(us, 3), "bytes": nbytes, "kernel": call.symbol}
+                                   "us_per_step": round(us, 3), "bytes": nbytes, "kernel": call.symbol,
+                                   "parity": tail_parity(q, k, v, out, 1.0 / math.sqrt(D))}
     del graph
     return res
 
