@@ -309,18 +309,23 @@ def parity_check(cfg, q, cache, sl, scale):
     from oracle import attention as OA
     from oracle import quantize as OQ
 
+    dense = cfg["bits"] == 16
     out = kernels.attention(q, cache[0], cache[1], scale, causal=cfg.get("causal", False),
-                            window=cfg.get("window", 0), seq_lens=sl, bits=cfg["bits"], kernel="decode")
+                            window=cfg.get("window", 0), seq_lens=sl, kernel="decode",
+                            **({} if dense else {"bits": cfg["bits"]}))
     torch.cuda.synchronize()
     dt = cfg["dtype"]
 
     def trip(tr):
+        if dense:  # an unquantized cache: the tensor itself
+            return tr.float().cpu().double().numpy()
         c, s, b = tr
-        return (c.cpu().view(torch.int32).numpy().view(np.uint32), s.cpu().view(torch.int16).numpy().view(np.uint16),
-                b.cpu().view(torch.int16).numpy().view(np.uint16))
+        return OQ.dequantize(c.cpu().view(torch.int32).numpy().view(np.uint32),
+                             s.cpu().view(torch.int16).numpy().view(np.uint16),
+                             b.cpu().view(torch.int16).numpy().view(np.uint16), dt, 64, cfg["bits"])
 
-    kdq = OQ.dequantize(*trip(cache[0]), dt, 64, cfg["bits"])
-    vdq = OQ.dequantize(*trip(cache[1]), dt, 64, cfg["bits"])
+    kdq = trip(cache[0])
+    vdq = trip(cache[1])
     ref = OA.exact_attention(q.cpu().double().numpy(), kdq, vdq, scale, causal=cfg.get("causal", False),
                              window=cfg.get("window", 0), seq_lens=None if sl is None else sl.cpu().tolist())
     got = out.cpu().double().numpy()
@@ -645,14 +650,16 @@ def dense_prefill_extras(steps, device):
     v = torch.randn((B, Hkv, W - 1 + C, D), generator=g, device=device).to(T)
     res["C5-window-prefill-dense"] = time_attention_shape(
         "C5 window-layer prefill chunk, unquantized bf16 (B=4, 2048 queries, window 1024)", q, k, v,
-        1.0 / math.sqrt(D), 4 * D * Hq * B * C * W, steps, device, causal=True, window=W)
+        1.0 / math.sqrt(D), 4 * D * Hq * B * C * W, steps, device, causal=True, window=W,
+        check=lambda out: tail_parity(q, k, v, out, 1.0 / math.sqrt(D), window=W))
     B, Hq, Hkv, N, C = 1, 32, 4, 16384, 512
     q = torch.randn((B, Hq, C, D), generator=g, device=device).to(T)
     k = torch.randn((B, Hkv, N, D), generator=g, device=device).to(T)
     v = torch.randn((B, Hkv, N, D), generator=g, device=device).to(T)
     res["C3-last-chunk-dense"] = time_attention_shape(
         "C3 last chunk over an unquantized bf16 cache (512 queries, 16384 keys, causal)", q, k, v,
-        1.0 / math.sqrt(D), prefill_flops(N, Hq, D, N - C, N), steps, device, causal=True)
+        1.0 / math.sqrt(D), prefill_flops(N, Hq, D, N - C, N), steps, device, causal=True,
+        check=lambda out: tail_parity(q, k, v, out, 1.0 / math.sqrt(D)))
     return res
 
 
@@ -1025,7 +1032,7 @@ def main():
         for name in ("C1", "C2-b8", "C4", "C5-global", "C5-window", "C5-window-dense"):
             cfg = DECODE[name]
             quantized = cfg["bits"] != 16
-            r = time_decode(cfg, args.steps, args.warmup, device, want_parity=quantized)
+            r = time_decode(cfg, args.steps, args.warmup, device, want_parity=True)
             extra[name] = {"gbs": round(r["gbs"], 1), "frac": round(r["gbs"] / PEAK_HBM_GBS, 4),
                            "us_per_step": round(r["ms_per_step"] * 1e3, 3), "bytes": r["bytes"],
                            "kernel_us": round(r["call_us_mean"], 3), "parity": r.get("parity")}
