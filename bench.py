@@ -297,7 +297,19 @@ def time_paged_decode(cfg, steps, warmup, device):
     torch.cuda.synchronize()
     ms = s_.elapsed_time(e_) / steps
     del graph
-    return dict(bytes=nbytes, ms_per_step=ms, gbs=nbytes / (ms * 1e-3) / 1e9)
+    # the last replayed call read page set (steps - 1) % ncache: its first sequence, gathered out of
+    # the pools through its block table, against the exact fp64 oracle
+    t = tables[(steps - 1) % ncache]
+    n0 = lens[0]
+    pages = t[0, :math.ceil(n0 / PAGE)].long()
+
+    def gather(pool):  # (codes indexed as int32: torch has no uint32 gather on the device)
+        return tuple((x.view(torch.int32) if x.dtype == torch.uint32 else x)[pages].permute(1, 0, 2, 3)
+                     .reshape(1, Hkv, -1, x.shape[-1])[:, :, :n0] for x in pool)
+
+    parity = tail_parity(q[:1], gather(pools[0]), gather(pools[1]), out[:1], scale, bits=bits)
+    parity["rows"] = "sequence 0 of the last page set"
+    return dict(bytes=nbytes, ms_per_step=ms, gbs=nbytes / (ms * 1e-3) / 1e9, parity=parity)
 
 
 def parity_check(cfg, q, cache, sl, scale):
@@ -1062,7 +1074,8 @@ def main():
             torch.cuda.empty_cache()
         r = time_paged_decode(DECODE["C2-b8"], args.steps, args.warmup, device)
         extra["C2-b8-paged"] = {"gbs": round(r["gbs"], 1), "frac": round(r["gbs"] / PEAK_HBM_GBS, 4),
-                                "us_per_step": round(r["ms_per_step"] * 1e3, 3), "bytes": r["bytes"]}
+                                "us_per_step": round(r["ms_per_step"] * 1e3, 3), "bytes": r["bytes"],
+                                "parity": r["parity"]}
         log(f"[bench] C2-b8-paged: {r['gbs']:.1f} GB/s ({r['ms_per_step'] * 1e3:.2f} us/step)")
         torch.cuda.empty_cache()
         for name, r in append_extras(device).items():
