@@ -50,3 +50,30 @@ def test_measured_traffic_reads_the_committed_summary():
     # the cache is read once: within a few percent of the algorithmic bytes
     assert 1.0 <= decode / bench.decode_bytes([32768], 64, 8, 128, 8) < 1.1
     assert bench.measured_traffic("no_such_kernel") is None
+
+
+def test_tail_parity_judges_the_last_rows():
+    # the bench's parity record of a prefill shape: an output formed by the oracle itself is within
+    # the bar, and one whose last rows are perturbed by 1% fails it; rows before the checked tail
+    # are not looked at
+    import numpy as np
+    import torch
+
+    from oracle import attention as OA
+
+    g = torch.Generator().manual_seed(5)
+    q = torch.randn((1, 4, 40, 64), generator=g).to(torch.float16)
+    k = torch.randn((1, 2, 90, 64), generator=g).to(torch.float16)
+    v = torch.randn((1, 2, 90, 64), generator=g).to(torch.float16)
+    ref = OA.exact_attention(q.double().numpy(), k.double().numpy(), v.double().numpy(), 0.125, causal=True, window=30)
+    out = torch.from_numpy(ref).to(torch.float16)
+    rec = bench.tail_parity(q, k, v, out, 0.125, rows=16, window=30)
+    assert rec["within_bar"] and rec["rows"] == "last 16 of 40 queries"
+    bad = out.clone()
+    bad[:, :, :24] = 7.0  # outside the checked tail
+    assert bench.tail_parity(q, k, v, bad, 0.125, rows=16, window=30)["within_bar"]
+    bad[:, :, -1] *= 1.01
+    assert not bench.tail_parity(q, k, v, bad, 0.125, rows=16, window=30)["within_bar"]
+    # a window the oracle is not told about changes the reference: the record catches it
+    assert not bench.tail_parity(q, k, v, out, 0.125, rows=16)["within_bar"]
+    assert np.isfinite(rec["max_abs"])
