@@ -392,11 +392,11 @@ def cpu_trip(tr):
     return (c.cpu().view(torch.int32).to(torch.int64) & 0xFFFFFFFF, s.cpu(), b.cpu())
 
 
-def cpu_baseline(cfg, q, cache, scale, lens, budget_s=15.0, max_calls=8):
+def cpu_baseline(cfg, q, cache, scale, lens, budget_s=15.0, max_calls=8, min_calls=5):
     """The reference algorithm restated for the CPU (oracle.attention.reference_sdpa: mlx-lm's
     quantized SDPA for L == 1 with the reference's dtype casts and masks), timed on the host's
-    cores over the same workload (one cache, every sequence of the batch) for a bounded number of
-    calls."""
+    cores over the same workload (one cache, every sequence of the batch): at least `min_calls`
+    calls, more while the time budget lasts, up to `max_calls`; the median is reported."""
     import torch
 
     from oracle import attention as OA
@@ -409,7 +409,7 @@ def cpu_baseline(cfg, q, cache, scale, lens, budget_s=15.0, max_calls=8):
     OA.reference_sdpa(qc, kt, vt, scale, mask, 64, cfg["bits"])  # warm-up (allocator, threads)
     times = []
     t_all = time.perf_counter()
-    while len(times) < max_calls and (time.perf_counter() - t_all) < budget_s:
+    while len(times) < max_calls and (len(times) < min_calls or (time.perf_counter() - t_all) < budget_s):
         t0 = time.perf_counter()
         ref_out = OA.reference_sdpa(qc, kt, vt, scale, mask, 64, cfg["bits"])
         times.append(time.perf_counter() - t0)
@@ -1051,7 +1051,7 @@ def main():
             log(f"[bench] {name}: {r['gbs']:.1f} GB/s ({r['ms_per_step'] * 1e3:.2f} us/step)")
             if quantized and not args.no_cpu:
                 q, cache, scale = r["cpu_inputs"]
-                c, faithful = cpu_baseline(cfg, q, cache, scale, r["seq_lens"], budget_s=6.0, max_calls=3)
+                c, faithful = cpu_baseline(cfg, q, cache, scale, r["seq_lens"], budget_s=6.0, max_calls=5)
                 add_faithful(extra[name]["parity"], r.get("parity_arrays"), faithful)
                 extra[name]["cpu_baseline"] = c
                 log(f"[bench] {name} CPU baseline: {c['value']} GB/s on {c['cores']} cores")

@@ -83,8 +83,10 @@ def mask_structure(mask, B: int, n_q_heads: int, L: int, S: int, device=None):
 
     String and None masks cost nothing. An array mask is analysed on the host (a device mask is
     copied there once) and the result is cached for that mask object until it is modified, so the
-    layers of one forward pass share one analysis. seq_lens comes back as an int32 tensor on
-    `device` (default: the mask's device)."""
+    layers of one forward pass share one analysis. A mask created under torch.inference_mode() has
+    no version counter and is analysed on every call (callers in a serving loop pass ``window=`` /
+    ``seq_lens=`` to skip the analysis). seq_lens comes back as an int32 tensor on `device`
+    (default: the mask's device)."""
     if mask is None:
         return False, 0, None
     if isinstance(mask, str):
@@ -92,15 +94,20 @@ def mask_structure(mask, B: int, n_q_heads: int, L: int, S: int, device=None):
     if not torch.is_tensor(mask):
         raise NotImplementedError(f"unsupported mask type {type(mask)}")
     device = torch.device(device) if device is not None else mask.device
+    # A tensor made under torch.inference_mode() has no version counter, so an in-place edit of it
+    # could not be told from the cached analysis: such masks are analysed on every call.
+    versioned = not mask.is_inference()
     key = (B, n_q_heads, L, S, str(device))
-    hit = _mask_cache.get(id(mask))
-    if hit is not None and hit[0]() is mask and hit[1] == mask._version and hit[2] == key:
-        return hit[3]
+    if versioned:
+        hit = _mask_cache.get(id(mask))
+        if hit is not None and hit[0]() is mask and hit[1] == mask._version and hit[2] == key:
+            return hit[3]
     causal, window, seq = _analyse_mask(mask.detach().cpu(), B, n_q_heads, L, S)
     res = (causal, window, None if seq is None else seq.to(device))
-    if len(_mask_cache) > 64:
-        _mask_cache.clear()
-    _mask_cache[id(mask)] = (weakref.ref(mask), mask._version, key, res)
+    if versioned:
+        if len(_mask_cache) > 64:
+            _mask_cache.clear()
+        _mask_cache[id(mask)] = (weakref.ref(mask), mask._version, key, res)
     return res
 
 

@@ -348,7 +348,9 @@ int kvq_decode_attn_static(const kvq_rows* q, const kvq_qtensor* k, const kvq_qt
     return fail(KVQ_ERR_UNSUPPORTED, "decode supports head_dim 64, 128 and 256, got %d", D);
   int rc = check_attn_args(q, k, v, out, B, Hq, Hkv, L, D, S, bits, group_size, dtype, scale, window);
   if (rc) return rc;
-  const size_t need = kvq_decode_workspace_size(B, Hq, Hkv, L, D, S, window);
+  // the scratch has to hold this call's own plan (its format and group size), not the largest plan
+  // any cache format could need at these shapes
+  const size_t need = kvq::decode_workspace_bytes(B, Hq, Hkv, L, D, S, window, bits, group_size);
   if (need > (size_t)KVQ_STATIC_SCRATCH_BYTES)
     return fail(KVQ_ERR_WORKSPACE, "this call needs %zu bytes of scratch; the static scratch holds %zu (use kvq_decode_attn "
                 "with a workspace)", need, (size_t)KVQ_STATIC_SCRATCH_BYTES);

@@ -21,7 +21,8 @@
 //    probabilities are the B operand of O^T = V^T P^T (2 k-steps x 8 column blocks). The softmax
 //    scale is applied to the fp32 scores.
 //  * Operands: an unquantized cache's own rows (T, on the T MFMA); a quantized cache is dequantized
-//    to fp16 whatever T is (one fp32 FMA per element, rounded once), with the query entering the
+//    to fp16 whatever T is (a packed fp16 subtract and FMA per pair of elements: the code enters
+//    exactly as 1024 + c, the FMA rounds once), with the query entering the
 //    fp16 MFMA exactly as q * 2^qe (the power of two that puts the row's largest element in
 //    [2^13, 2^14)) and 2^-qe folded into the softmax scale. A bf16 cache group whose values do not
 //    fit fp16 dequantizes to inf and the rows that read it come out NaN, never a finite wrong value.

@@ -296,11 +296,26 @@ def _check_out(out: Optional[torch.Tensor], queries: torch.Tensor, dev) -> torch
     return out
 
 
+def _copy_for_one_shot(t: torch.Tensor, name: str, one_shot: bool) -> torch.Tensor:
+    """A contiguous copy of a tensor the kernels cannot read in place. Only a one-shot call may take
+    it: a prepared call holds its tensors by reference, so a copy would silently freeze them."""
+    if not one_shot:
+        raise ValueError(
+            f"prepare_attention: {name} need unit stride along D, 16-byte alignment and strides that are multiples "
+            f"of 8 elements (got strides {tuple(t.stride())}); a prepared call reads its tensors in place on every "
+            f"launch, so pass .contiguous() tensors (and refill those)")
+    return t.contiguous()
+
+
 def prepare_attention(queries: torch.Tensor, keys, values, scale: float, *, causal: bool = False,
                       window: int = 0, seq_lens: Optional[torch.Tensor] = None, group_size: int = 64,
                       bits: int = 8, out: Optional[torch.Tensor] = None, kernel: str = "auto",
-                      workspace: Optional[torch.Tensor] = None) -> AttentionCall:
-    """Validate one attention launch and return it as an ``AttentionCall`` (see ``attention``)."""
+                      workspace: Optional[torch.Tensor] = None, _one_shot: bool = False) -> AttentionCall:
+    """Validate one attention launch and return it as an ``AttentionCall`` (see ``attention``).
+
+    The queries and unquantized keys/values must be readable in place (unit stride along D, 16-byte
+    aligned, strides in multiples of 8 elements): a prepared call reads the same memory on every
+    launch, so a tensor that would need a copy raises ValueError rather than being snapshotted."""
     if queries.dim() != 4:
         raise ValueError(f"queries must be [B, Hq, L, D], got {tuple(queries.shape)}")
     B, Hq, L, D = queries.shape
@@ -316,9 +331,9 @@ def prepare_attention(queries: torch.Tensor, keys, values, scale: float, *, caus
             if t.dtype != queries.dtype:
                 raise ValueError(f"{name} are {t.dtype}, queries are {queries.dtype}")
         if not _rows_ok(keys):
-            keys = keys.contiguous()
+            keys = _copy_for_one_shot(keys, "keys", _one_shot)
         if not _rows_ok(values):
-            values = values.contiguous()
+            values = _copy_for_one_shot(values, "values", _one_shot)
     else:
         _check_triple(keys, "keys")
         _check_triple(values, "values")
@@ -337,7 +352,7 @@ def prepare_attention(queries: torch.Tensor, keys, values, scale: float, *, caus
     if Hq % Hkv:
         raise ValueError(f"Hq={Hq} is not a multiple of Hkv={Hkv}")
     if not _rows_ok(queries):
-        queries = queries.contiguous()
+        queries = _copy_for_one_shot(queries, "queries", _one_shot)
     out = _check_out(out, queries, dev)
     sl_ptr = None
     if seq_lens is not None:
@@ -387,7 +402,7 @@ def attention(queries: torch.Tensor, keys, values, scale: float, *, causal: bool
     "prefill" or "auto" (decode while a KV head's query rows fit max(16*G/D, 8) columns, that is
     at most two decode passes over its keys, prefill otherwise)."""
     return prepare_attention(queries, keys, values, scale, causal=causal, window=window, seq_lens=seq_lens,
-                             group_size=group_size, bits=bits, out=out, kernel=kernel)()
+                             group_size=group_size, bits=bits, out=out, kernel=kernel, _one_shot=True)()
 
 
 # ---- paged pools (64-row pages; include/kvq.h "Paged layout")
@@ -468,7 +483,7 @@ def paged_attention(queries: torch.Tensor, k_pool: Triple, v_pool: Triple, block
         raise ValueError(f"Hq={Hq} is not a multiple of Hkv={Hkv}")
     S = int(max_len) if max_len is not None else block_tables.shape[1] * PAGE_ROWS
     if not _rows_ok(queries):
-        queries = queries.contiguous()
+        queries = _copy_for_one_shot(queries, "queries", _one_shot)
     out = _check_out(out, queries, dev)
     if kernel == "auto":
         kernel = _auto_kernel((Hq // Hkv) * L, D, group_size)

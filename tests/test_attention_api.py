@@ -140,3 +140,51 @@ def test_mask_analysis_runs_once_per_mask(monkeypatch):
     m.fill_(True)  # modified in place: a new analysis, a new answer (every key visible)
     assert A.mask_structure(m, 1, 8, L, S) == (False, 0, None)
     assert len(calls) == 2
+
+
+def test_mask_structure_under_inference_mode(monkeypatch):
+    """A mask built under torch.inference_mode() has no version counter: it is analysed on every
+    call (no cache entry), gives the same answers, and an in-place edit is seen."""
+    calls = []
+    real = A._analyse_mask
+
+    def counting(*a):
+        calls.append(1)
+        return real(*a)
+
+    monkeypatch.setattr(A, "_analyse_mask", counting)
+    monkeypatch.setattr(A, "_mask_cache", {})
+    L, S = 4, 50
+    with torch.inference_mode():
+        m = torch.ones(1, 1, L, S, dtype=torch.bool).tril(S - L)
+        assert m.is_inference()
+        assert A.mask_structure(m, 1, 8, L, S) == (True, 0, None)
+        assert A.mask_structure(m, 1, 8, L, S) == (True, 0, None)
+        w = A.mask_structure(m & ~torch.ones(L, S, dtype=torch.bool).tril(S - L - 3), 1, 8, L, S)
+        assert w == (True, 3, None)
+        m.fill_(True)
+        assert A.mask_structure(m, 1, 8, L, S) == (False, 0, None)
+    assert len(calls) == 4 and A._mask_cache == {}
+    # outside inference mode too (the tensor is still an inference tensor)
+    assert A.mask_structure(m, 1, 8, L, S) == (False, 0, None)
+
+
+def test_prepared_call_rejects_inputs_it_would_copy(monkeypatch):
+    """A prepared call reads its tensors in place on every launch; a query or unquantized K/V that
+    the kernels cannot read directly (here: strided along D) raises instead of being snapshotted.
+    The checks run on the host before any library call (the device check is stubbed to run here)."""
+    from myinfer_amd import kernels as K
+
+    monkeypatch.setattr(K, "_require_cuda", lambda *t: t[0].device)
+    B, Hq, Hkv, L, S, D = 1, 8, 2, 4, 64, 128
+    q = torch.zeros(B, Hq, L, 2 * D, dtype=torch.float16)[..., ::2]  # stride 2 along D
+    k = torch.zeros(B, Hkv, S, D, dtype=torch.float16)
+    v = torch.zeros(B, Hkv, S, D, dtype=torch.float16)
+    with pytest.raises(ValueError, match="queries need unit stride"):
+        K.prepare_attention(q, k, v, 0.1)
+    with pytest.raises(ValueError, match="keys need unit stride"):
+        K.prepare_attention(q.contiguous(), torch.zeros(B, Hkv, S, 2 * D, dtype=torch.float16)[..., ::2], v, 0.1)
+    codes = torch.zeros(B, Hkv, S, D // 4, dtype=torch.int32).view(torch.uint32)
+    sb = torch.zeros(B, Hkv, S, D // 64, dtype=torch.float16)
+    with pytest.raises(ValueError, match="queries need unit stride"):
+        K.prepare_attention(q, (codes, sb, sb), (codes, sb, sb), 0.1)
