@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define KVQ_ABI_VERSION 4
+#define KVQ_ABI_VERSION 5
 
 /* Element types of queries, K/V rows, outputs, scales and biases. */
 #define KVQ_DTYPE_F16 0
@@ -61,13 +61,27 @@ typedef struct kvq_rows {
   int64_t stride_b, stride_h, stride_l;
 } kvq_rows;
 
-/* A quantized K or V cache view: the (codes, scales, biases) triple of the reference. */
+/* A quantized K or V cache view: the (codes, scales, biases) triple of the reference.
+ *
+ * range_exp (may be NULL) is the cache's range exponent E, one int32 in device memory, kept by
+ * the appends and read by the quantized prefill kernels:
+ *   - kvq_*quantize_append raise it (atomic max) to the smallest E >= 0 with every dequantized
+ *     value s * c + b of every group they write at most 2^15 * 2^E in magnitude (it starts at 0
+ *     and never decreases: a trimmed cache keeps it);
+ *   - the quantized prefill kernels stage their fp16 MFMA operands as (s * c + b) * 2^-E and fold
+ *     2^E back into the fp32 scores (K) and the output (V), so a bf16 cache whose values leave the
+ *     fp16 range still gives finite results (values below 2^(E - 24) then lose precision in the
+ *     operands). E = 0 (or NULL) stages the values as they are: there a bf16 group beyond the fp16
+ *     range makes the row blocks that read it return NaN, never a finite wrong value;
+ *   - decode ignores it: it applies scales and biases in fp32.
+ * This field has no counterpart in the reference, whose MLX kernels dequantize in bf16. */
 typedef struct kvq_qtensor {
   uint32_t* codes;
   void* scales;
   void* biases;
   int64_t codes_stride_b, codes_stride_h, codes_stride_s; /* in uint32 words; the row itself is contiguous */
   int64_t sb_stride_b, sb_stride_h, sb_stride_s;          /* in T elements; shared by scales and biases    */
+  int32_t* range_exp;                                     /* the range exponent E above, or NULL           */
 } kvq_qtensor;
 
 /* ABI version the library was built with (KVQ_ABI_VERSION). */

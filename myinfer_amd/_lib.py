@@ -16,7 +16,7 @@ import torch  # noqa: F401  (binds the HIP runtime before libkvq.so is loaded)
 
 # The in-tree build, the only library this package loads.
 LIB_PATH = Path(__file__).resolve().parent / "libkvq.so"
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 DTYPE_F16 = 0
 DTYPE_BF16 = 1
@@ -51,6 +51,7 @@ class QTensor(ctypes.Structure):
         ("sb_stride_b", c_int64),
         ("sb_stride_h", c_int64),
         ("sb_stride_s", c_int64),
+        ("range_exp", c_void_p),  # int32 range exponent in device memory, or NULL (include/kvq.h)
     ]
 
 
@@ -195,8 +196,10 @@ def rows(t: torch.Tensor) -> Rows:
     return Rows(t.data_ptr(), t.stride(0), t.stride(1), t.stride(2))
 
 
-def qtensor(codes: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor) -> QTensor:
-    """Descriptor of a quantized [B, H, S, *] triple (codes uint32, scales/biases in T)."""
+def qtensor(codes: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
+            range_exp: torch.Tensor | None = None) -> QTensor:
+    """Descriptor of a quantized [B, H, S, *] triple (codes uint32, scales/biases in T), with the
+    cache's range exponent (a one-element int32 device tensor) when it keeps one."""
     for name, t in (("codes", codes), ("scales", scales), ("biases", biases)):
         if t.dim() != 4:
             raise ValueError(f"{name} must be 4-D [B, H, S, *], got shape {tuple(t.shape)}")
@@ -208,10 +211,14 @@ def qtensor(codes: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor) -> 
         raise ValueError("scales and biases must share a dtype")
     if scales.stride() != biases.stride() or scales.shape != biases.shape:
         raise ValueError("scales and biases must have identical shapes and strides")
+    if range_exp is not None and (range_exp.dtype != torch.int32 or range_exp.numel() < 1
+                                  or range_exp.device != codes.device):
+        raise ValueError("range_exp must be an int32 tensor on the cache's device")
     return QTensor(
         codes.data_ptr(), scales.data_ptr(), biases.data_ptr(),
         codes.stride(0), codes.stride(1), codes.stride(2),
         scales.stride(0), scales.stride(1), scales.stride(2),
+        None if range_exp is None else range_exp.data_ptr(),
     )
 
 

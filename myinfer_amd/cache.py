@@ -113,8 +113,7 @@ class KVCache:
         qc = QuantizedKVCache(group_size=group_size, bits=bits)
         qc.offset = self.offset
         if self.keys is not None:
-            qc.keys = qc._alloc_like(self.keys, self.keys.shape[2])
-            qc.values = qc._alloc_like(self.values, self.values.shape[2])
+            qc.keys, qc.values = qc._buffers_like(self.keys, self.values, self.keys.shape[2])
             kernels.quantize_append(self.keys, qc.keys, self.values, qc.values, row_offset=0,
                                     group_size=group_size, bits=bits)
         return qc
@@ -263,6 +262,18 @@ class QuantizedKVCache:
         self.offset = 0
         self.group_size = group_size
         self.bits = bits
+        # the K and V range exponents (kernels.register_range_word): int32 [2] on the cache's device,
+        # raised by the appends, read by the prefill kernels; it outlives buffer growth
+        self.range_exp: Optional[torch.Tensor] = None
+
+    def _buffers_like(self, like_k: torch.Tensor, like_v: torch.Tensor, cap: int):
+        """New K and V buffers of `cap` rows, registered with the cache's range words."""
+        if self.range_exp is None:
+            self.range_exp = torch.zeros(2, dtype=torch.int32, device=like_k.device)
+        nk, nv = self._alloc_like(like_k, cap), self._alloc_like(like_v, cap)
+        kernels.register_range_word(nk[0], self.range_exp[0:1])
+        kernels.register_range_word(nv[0], self.range_exp[1:2])
+        return nk, nv
 
     def _alloc_like(self, rows: torch.Tensor, cap: int):
         B, H, _, D = rows.shape
@@ -279,8 +290,7 @@ class QuantizedKVCache:
             keep, new_cap = _grow_rows(self.offset, cap, L, self.step)
         else:
             keep, new_cap = (self.offset if self.keys is not None else 0), capacity
-        nk = self._alloc_like(keys, new_cap)
-        nv = self._alloc_like(values, new_cap)
+        nk, nv = self._buffers_like(keys, values, new_cap)
         if self.keys is not None:
             for dst, src in zip(nk + nv, self.keys + self.values):
                 _copy_rows(dst, src, keep)
@@ -340,9 +350,18 @@ class QuantizedKVCache:
     def empty(self) -> bool:
         return self.keys is None
 
+    def range_exponents(self) -> Tuple[int, int]:
+        """The K and V range exponents the appends have raised (0, 0 while every value fits the fp16
+        operands as it is). Reads device memory: a synchronization."""
+        if self.range_exp is None:
+            return 0, 0
+        k, v = self.range_exp.tolist()
+        return int(k), int(v)
+
     def fits_fp16_operands(self) -> bool:
-        """Whether the cached K and V rows dequantize inside the fp16 range, as the prefill kernel's
-        operands require (kernels.fits_fp16_operands); an empty cache fits."""
+        """Whether the cached K and V rows dequantize inside the fp16 range as they are
+        (kernels.fits_fp16_operands); an empty cache fits. A cache that does not still gives finite
+        prefill results: its range words scale the operands."""
         if self.keys is None or self.offset == 0:
             return True
         keys, values = self.fetch()

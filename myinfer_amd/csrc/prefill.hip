@@ -131,6 +131,10 @@ struct PreParams {
   const int32_t* table;
   int64_t table_stride;
   int num_pages;
+  // the caches' range exponents (kvq_qtensor.range_exp), or null: the fp16 operands are staged
+  // times 2^-E, and 2^E returns in the score scale (K) and the output (V)
+  const int32_t* k_rexp;
+  const int32_t* v_rexp;
 };
 
 // V^T slot of key `kk` (0..63) inside a tile: the 16 keys of PV k-step j = kk / 16 are stored so
@@ -244,6 +248,12 @@ struct RawShare {
 
 __device__ __forceinline__ _Float16 to_half(uint16_t r, F16) { return __builtin_bit_cast(_Float16, r); }
 __device__ __forceinline__ _Float16 to_half(uint16_t r, BF16) { return (_Float16)__uint_as_float((uint32_t)r << 16); }
+// A scale or bias as its fp16 operand value times m = 2^-E (the cache's range exponent, include/kvq.h):
+// exact in fp32, rounded once. An fp16 cache never needs the factor (its values fit the operands).
+__device__ __forceinline__ _Float16 to_half_scaled(uint16_t r, float, F16) { return __builtin_bit_cast(_Float16, r); }
+__device__ __forceinline__ _Float16 to_half_scaled(uint16_t r, float m, BF16) {
+  return (_Float16)(__uint_as_float((uint32_t)r << 16) * m);
+}
 
 // 1024 + c as fp16 for two codes: the code bytes selected by `sel` become the low mantissa bytes of
 // 0x64xx (= 1024 + c exactly); subtracting 1024 and one packed FMA give c * s + b in fp16.
@@ -283,11 +293,12 @@ __device__ __forceinline__ void dequant8(const uint32_t* w, h2 s2, h2 b2, uint32
 // and the LDS operations of one wave complete in program order, so a wave barrier (which keeps
 // the compiler from moving the lanes' accesses across it) is all the ordering the reads need.
 template <typename T, int BITS, int G, int D>
-__device__ __forceinline__ void stage_v_table(const uint8_t* raw, uint32_t* sbt, int tid, bool& range_bad) {
+__device__ __forceinline__ void stage_v_table(const uint8_t* raw, uint32_t* sbt, int tid, bool& range_bad, float vmul) {
   using C = RawCfg<BITS, G, D>;
   const int key = tid & 63, g = (4 * (tid >> 3)) / G;
   const uint8_t* sbase = raw + 2 * C::KB + C::sb_off(key, g);
-  const h2 sbp = {to_half(*(const uint16_t*)(sbase + 2 * C::SBB), T{}), to_half(*(const uint16_t*)(sbase + 3 * C::SBB), T{})};
+  const uint16_t sv = *(const uint16_t*)(sbase + 2 * C::SBB), bv = *(const uint16_t*)(sbase + 3 * C::SBB);
+  const h2 sbp = {to_half_scaled(sv, vmul, T{}), to_half_scaled(bv, vmul, T{})};
   sbt[key] = __builtin_bit_cast(uint32_t, sbp);
   // a bf16 group beyond the fp16 range has a bias (its largest-magnitude element) that converts to
   // inf; the operands cannot hold it
@@ -334,7 +345,7 @@ __device__ __forceinline__ void stage_v(const uint8_t* raw, _Float16* vlds, cons
 
 // K, in two halves: half H builds dims [32 q + 16 H, +16) of key u % 64.
 template <typename T, int BITS, int G, int D, int H>
-__device__ __forceinline__ void stage_k(const uint8_t* raw, _Float16* klds, int tid, bool& range_bad) {
+__device__ __forceinline__ void stage_k(const uint8_t* raw, _Float16* klds, int tid, bool& range_bad, float kmul) {
   using C = RawCfg<BITS, G, D>;
   const int u = tid - 64 * C::NSW;
   const int key = u & 63, q = u >> 6;
@@ -350,7 +361,8 @@ __device__ __forceinline__ void stage_k(const uint8_t* raw, _Float16* klds, int 
     w[1] = a[1];
   }
   const uint8_t* sbase = raw + 2 * C::KB + C::sb_off(key, (32 * q + 16 * H) / G);
-  const _Float16 sh = to_half(*(const uint16_t*)sbase, T{}), bh = to_half(*(const uint16_t*)(sbase + C::SBB), T{});
+  const _Float16 sh = to_half_scaled(*(const uint16_t*)sbase, kmul, T{});
+  const _Float16 bh = to_half_scaled(*(const uint16_t*)(sbase + C::SBB), kmul, T{});
   if constexpr (T::id == KVQ_DTYPE_BF16) range_bad |= __builtin_isinf((float)bh);
 #pragma unroll
   for (int c = 0; c < 2; ++c) {
@@ -363,16 +375,16 @@ __device__ __forceinline__ void stage_k(const uint8_t* raw, _Float16* klds, int 
 // The whole tile, all threads.
 template <typename T, int BITS, int G, int D>
 __device__ __forceinline__ void stage_from_raw(const uint8_t* raw, _Float16* klds, _Float16* vlds, uint32_t* sbt,
-                                               int tid, bool& range_bad) {
+                                               int tid, bool& range_bad, float kmul, float vmul) {
   constexpr int NST = 64 * RawCfg<BITS, G, D>::NSW;  // threads per operand
   if (tid < NST) {
-    stage_v_table<T, BITS, G, D>(raw, sbt, tid, range_bad);
+    stage_v_table<T, BITS, G, D>(raw, sbt, tid, range_bad, vmul);
     __builtin_amdgcn_wave_barrier();
     stage_v<BITS, G, D, 0>(raw, vlds, sbt, tid);
     stage_v<BITS, G, D, 1>(raw, vlds, sbt, tid);
   } else if (tid < 2 * NST) {
-    stage_k<T, BITS, G, D, 0>(raw, klds, tid, range_bad);
-    stage_k<T, BITS, G, D, 1>(raw, klds, tid, range_bad);
+    stage_k<T, BITS, G, D, 0>(raw, klds, tid, range_bad, kmul);
+    stage_k<T, BITS, G, D, 1>(raw, klds, tid, range_bad, kmul);
   }
 }
 
@@ -416,7 +428,6 @@ __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) 
   unsigned* const s_flags = &sb_tab[0][0];
   unsigned* const s_arrived = &sb_tab[0][8];
   bool range_bad = false;  // some tile this lane staged held a group beyond the fp16 range
-
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -520,6 +531,22 @@ __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) 
     for (int j = 0; j < (DENSE ? 2 : kRawSlots); ++j) issue_raw(j);
   }
 
+  // ---- range exponents of the K and V caches (0 for an unquantized cache, an fp16 cache -- whose
+  // values always fit the fp16 operands -- or a null pointer) and the factors 2^-E the staging
+  // applies to the scales and biases; 2^E_K returns in the score scale, 2^E_V in the output. Read
+  // here, after the first tile loads are issued, so that waiting for the word delays no load. (The
+  // factors are held in VGPRs: the tile loop has spare vector registers and no spare scalar ones.)
+  float kmul = 1.0f, vmul = 1.0f, kback = 1.0f, vback = 1.0f;
+  if constexpr (!DENSE && T::id == KVQ_DTYPE_BF16) {
+    const int ek = p.k_rexp ? min(max(*p.k_rexp, 0), 127) : 0;
+    const int ev = p.v_rexp ? min(max(*p.v_rexp, 0), 127) : 0;
+    kmul = ldexpf(1.0f, -ek);
+    vmul = ldexpf(1.0f, -ev);
+    kback = ldexpf(1.0f, ek);
+    vback = ldexpf(1.0f, ev);
+    asm volatile("" : "+v"(kmul), "+v"(vmul), "+v"(kback), "+v"(vback));
+  }
+
   // ---- Q^T operand: k-step j holds dims 16j + 8hh .. +7. Quantized cache: the query times 2^qe in
   // fp16 (exact: a power of two, with qe chosen so the row's largest element lands in [2^13, 2^14);
   // a bf16 query has 8 significant bits, so only elements below 2^-14 of the operand's scale lose
@@ -550,7 +577,7 @@ __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) 
     if (qmax > 0.0f) frexpf(qmax, &e);
     const int qe = 14 - e;  // |q| * 2^qe < 2^14
     const float qmul = ldexpf(1.0f, qe);
-    inv2 = ldexpf(p.scale_log2, -qe);
+    inv2 = ldexpf(p.scale_log2, -qe) * kback;  // the K operands are staged times 2^-E_K
 #pragma unroll
     for (int j = 0; j < KSTEPS; ++j)
 #pragma unroll
@@ -789,7 +816,7 @@ __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) 
       const int v_t = opaque((t % 3) * VBUF), v_w = opaque(((t + 2) % 3) * VBUF);
       const uint8_t* raw2 = &raw[0][0] + opaque(((t + 2) % kRawSlots) * RC::SLOT);
       if constexpr (STG && ROLE == 0) {
-        stage_v_table<T, BITS, G, D>(raw2, sb_tab[wave & 3], tid, range_bad);
+        stage_v_table<T, BITS, G, D>(raw2, sb_tab[wave & 3], tid, range_bad, vmul);
         __builtin_amdgcn_wave_barrier();
       }
       const int k0 = k_begin + kPT * t;
@@ -808,7 +835,7 @@ __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) 
       }
       pv_blk(vl, pop, B0{});
       if constexpr (STG && ROLE == 0) stage_v<BITS, G, D, 0>(raw2, &v_lds[0][0] + v_w, sb_tab[wave & 3], tid);
-      if constexpr (STG && ROLE == 1) stage_k<T, BITS, G, D, 0>(raw2, &k_lds[0][0] + k_w, tid, range_bad);
+      if constexpr (STG && ROLE == 1) stage_k<T, BITS, G, D, 0>(raw2, &k_lds[0][0] + k_w, tid, range_bad, kmul);
       // tile t + 4 into the slot of tile t + 1, issued between the halves (at the step's start
       // it delays the first half: about 2% slower on C3, as are the other positions tried)
       issue_raw(t + 4);
@@ -826,7 +853,7 @@ __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) 
       }
       pv_blk(vl, pop, B1{});
       if constexpr (STG && ROLE == 0) stage_v<BITS, G, D, 1>(raw2, &v_lds[0][0] + v_w, sb_tab[wave & 3], tid);
-      if constexpr (STG && ROLE == 1) stage_k<T, BITS, G, D, 1>(raw2, &k_lds[0][0] + k_w, tid, range_bad);
+      if constexpr (STG && ROLE == 1) stage_k<T, BITS, G, D, 1>(raw2, &k_lds[0][0] + k_w, tid, range_bad, kmul);
       wait_vm<IPT>();  // tile t + 3 has landed (tile t + 4 may be in flight)
       __syncthreads();
     };
@@ -840,11 +867,11 @@ __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) 
       // flight
       wait_vm<2 * IPT>();
       __syncthreads();
-      stage_from_raw<T, BITS, G, D>(raw[0], k_lds[0], v_lds[0], sb_tab[wave & 3], tid, range_bad);
+      stage_from_raw<T, BITS, G, D>(raw[0], k_lds[0], v_lds[0], sb_tab[wave & 3], tid, range_bad, kmul, vmul);
       wait_vm<IPT>();
       __syncthreads();
       issue_raw(3);  // into the slot of tile 0
-      stage_from_raw<T, BITS, G, D>(raw[1], k_lds[1], v_lds[1], sb_tab[wave & 3], tid, range_bad);
+      stage_from_raw<T, BITS, G, D>(raw[1], k_lds[1], v_lds[1], sb_tab[wave & 3], tid, range_bad, kmul, vmul);
       {
         u4 ring[4];
         qk_ring(ring, kl_lane);
@@ -924,7 +951,7 @@ __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) 
       int ex = 0;
       if (mx > 0.0f) frexpf(mx, &ex);
       const int e = mx > 0.0f ? min(max(ex - 14, -100), 100) : 0;
-      own_sc = ldexpf(1.0f, e);
+      own_sc = ldexpf(1.0f, e) * vback;  // the V operands were staged times 2^-E_V
       const float f = ldexpf(inv_l, -e);
 #pragma unroll
       for (int u = 0; u < QW; ++u)
@@ -995,7 +1022,8 @@ __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) 
     for (int db = 0; db < NDB; ++db) oacc[db] = macc[db];
   }
   if (!row_ok) return;
-  const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+  // (after a split merge l_tot and oacc are in true units; else the V operands' 2^-ev returns here)
+  const float inv = l_tot > 0.0f ? (1.0f / l_tot) * (p.nsplit > 1 ? 1.0f : vback) : 0.0f;
   uint16_t* orow = p.out + (int64_t)b * p.o_sb + (int64_t)head * p.o_sh + (int64_t)lq * p.o_sl;
 #pragma unroll
   for (int db = 0; db < NDB; ++db)
@@ -1134,6 +1162,8 @@ hipError_t launch_prefill(const kvq_rows* q, const kvq_qtensor* k, const kvq_qte
   p.vsb_sb = v->sb_stride_b;
   p.vsb_sh = v->sb_stride_h;
   p.vsb_ss = v->sb_stride_s;
+  p.k_rexp = k->range_exp;
+  p.v_rexp = v->range_exp;
   return launch_prefill_quant<false>(p, dtype, D, bits, G, stream);
 }
 
@@ -1161,6 +1191,8 @@ hipError_t launch_prefill_paged(const kvq_rows* q, const kvq_qtensor* k, const k
   p.vsb_sb = v->sb_stride_b;
   p.vsb_sh = v->sb_stride_h;
   p.vsb_ss = v->sb_stride_s;
+  p.k_rexp = k->range_exp;
+  p.v_rexp = v->range_exp;
   p.table = table;
   p.table_stride = table_stride;
   p.num_pages = num_pages;

@@ -101,7 +101,21 @@ struct QuantJob {
   uint16_t* biases;
   int64_t c_b, c_h, c_s;
   int64_t g_b, g_h, g_s;
+  int32_t* range_exp;  // the destination cache's range exponent (kvq_qtensor), or null
 };
+
+// The range exponent a group needs: the smallest E >= 0 with max(|b|, |b + n s|) <= 2^15 * 2^E,
+// from the stored (rounded) scale and bias, whose dequantized values s * c + b (c in [0, n]) have
+// their extremes at c = 0 and c = n.
+__device__ __forceinline__ int group_range_exp(float s, float b, float n) {
+#pragma clang fp contract(off)
+  const float bound = fmaxf(fabsf(b), fabsf(b + n * s));
+  if (!(bound > 32768.0f)) return 0;           // within range (or a NaN group, which no scale mends)
+  if (__builtin_isinf(bound)) return 127;      // the largest exponent the kernels accept
+  int k;
+  const float m = frexpf(bound * (1.0f / 32768.0f), &k);  // bound / 2^15 = m 2^k, m in [0.5, 1)
+  return m == 0.5f ? k - 1 : k;
+}
 
 // Paged destination: row r of sequence b goes to row r % 64 of page table[b][r / 64] (the job's
 // batch strides are then page strides); r = starts[b] + l when `starts` is given, else
@@ -199,8 +213,13 @@ __global__ __launch_bounds__(256) void quantize_append_kernel(QuantJob job0, Qua
   }
   if (chunk % (G / 8) == 0) {
     const int64_t gi = bb * job.g_b + h * job.g_h + drow * job.g_s + chunk / (G / 8);
-    job.scales[gi] = from_float(s, T{});
-    job.biases[gi] = from_float(bias, T{});
+    const uint16_t sT = from_float(s, T{}), bT = from_float(bias, T{});
+    job.scales[gi] = sT;
+    job.biases[gi] = bT;
+    if (job.range_exp) {
+      const int e = group_range_exp(to_float(sT, T{}), to_float(bT, T{}), n_bins);
+      if (e > 0) atomicMax(job.range_exp, e);
+    }
   }
 }
 
@@ -253,6 +272,7 @@ static QuantJob make_job(const kvq_rows* src, const kvq_qtensor* dst) {
   j.g_b = dst->sb_stride_b;
   j.g_h = dst->sb_stride_h;
   j.g_s = dst->sb_stride_s;
+  j.range_exp = dst->range_exp;
   return j;
 }
 

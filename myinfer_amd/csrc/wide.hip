@@ -102,6 +102,10 @@ struct WideParams {
   const int32_t* table;
   int64_t table_stride;
   int num_pages;
+  // the caches' range exponents (kvq_qtensor.range_exp), or null: the fp16 operands are staged
+  // times 2^-E, and 2^E returns in the score scale (K) and the output (V)
+  const int32_t* k_rexp;
+  const int32_t* v_rexp;
 };
 
 // The key held in V^T slot 8 c + e (c = 0..3, e = 0..7): PV k-step c / 2 takes, in lane half c % 2,
@@ -113,6 +117,16 @@ __host__ __device__ constexpr int w_slot_key(int c, int e) { return 16 * (c >> 1
 // fp16 range becomes inf, and the rows that read the group come out non-finite.
 __device__ __forceinline__ _Float16 cell_half(uint32_t cell, F16) { return __builtin_bit_cast(_Float16, (uint16_t)cell); }
 __device__ __forceinline__ _Float16 cell_half(uint32_t cell, BF16) { return (_Float16)__uint_as_float(cell << 16); }
+// The same times m = 2^-E (the cache's range exponent) when SCALED, exact in fp32 and rounded once
+// to fp16.
+template <typename T, bool SCALED>
+__device__ __forceinline__ _Float16 cell_half_e(uint32_t cell, float m) {
+  if constexpr (!SCALED) {
+    return cell_half(cell, T{});
+  } else {
+    return (_Float16)(to_float((uint16_t)cell, T{}) * m);
+  }
+}
 
 // Two codes as fp16 s * c + b in packed arithmetic: the code bytes `sel` picks become the low
 // mantissa bytes of 0x64xx (1024 + c, exact), then one packed subtract and one packed FMA (rounded
@@ -135,8 +149,8 @@ __device__ __forceinline__ uint32_t nibbles_hi(uint32_t w) {
 // [D/8 p, D/8 (p + 1)) of key r (t = 8 r + p) and writes them as KCH chunks of 8 dims. Rows are 16
 // bytes longer than the data (528 bytes at D = 256), so the 32 lanes that read one 16-byte column of
 // 32 keys hit distinct banks and a lane's reads of one row are one base address plus immediates.
-template <typename T, typename OT, int D, int BITS, int G>
-__device__ __forceinline__ void wide_stage_k(const uint8_t* raw, uint8_t* kop, int t, bool& range_bad) {
+template <typename T, typename OT, int D, int BITS, int G, bool SCALED = false>
+__device__ __forceinline__ void wide_stage_k(const uint8_t* raw, uint8_t* kop, int t, bool& range_bad, float kmul) {
   using C = WideCfg<D, BITS, G>;
   const int r = t >> 3, p = t & 7;
   u4 w[C::KCH];
@@ -146,7 +160,8 @@ __device__ __forceinline__ void wide_stage_k(const uint8_t* raw, uint8_t* kop, i
   } else {
     const int g = 32 * p / G;
     const uint32_t* cells = (const uint32_t*)(raw + 2 * C::TB);
-    const _Float16 sh = cell_half(cells[32 * g + r], T{}), bh = cell_half(cells[C::SBA / 4 + 32 * g + r], T{});
+    const _Float16 sh = cell_half_e<T, SCALED>(cells[32 * g + r], kmul);
+    const _Float16 bh = cell_half_e<T, SCALED>(cells[C::SBA / 4 + 32 * g + r], kmul);
     // MLX's bias is the group's larger-magnitude extreme: it converts to inf exactly when some
     // value of the group lies beyond the fp16 range
     if constexpr (T::id == KVQ_DTYPE_BF16) range_bad |= __builtin_isinf((float)bh);
@@ -177,8 +192,8 @@ __device__ __forceinline__ void wide_stage_k(const uint8_t* raw, uint8_t* kop, i
 // [VPT j, VPT (j + 1)) (VPT = D / 64) of the 8 keys of slot chunk c and writes, for each of those
 // dims, the chunk's 8 slots (16 bytes) to row d at chunk position c ^ ((d >> 2) & 3) (rows are 64
 // bytes: 32 slots).
-template <typename T, typename OT, int D, int BITS, int G>
-__device__ __forceinline__ void wide_stage_v(const uint8_t* raw, uint8_t* vop, int t, bool& range_bad) {
+template <typename T, typename OT, int D, int BITS, int G, bool SCALED = false>
+__device__ __forceinline__ void wide_stage_v(const uint8_t* raw, uint8_t* vop, int t, bool& range_bad, float vmul) {
   using C = WideCfg<D, BITS, G>;
   const int c = t >> 6, j = t & 63;
   const uint8_t* vraw = raw + C::TB;
@@ -205,8 +220,8 @@ __device__ __forceinline__ void wide_stage_v(const uint8_t* raw, uint8_t* vop, i
     const u4 b_lo = *(const u4*)(cells + C::SBA + 4 * kb0), b_hi = *(const u4*)(cells + C::SBA + 4 * (kb0 + 8));
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const _Float16 sh = cell_half(e < 4 ? s_lo[e] : s_hi[e - 4], T{});
-      const _Float16 bh = cell_half(e < 4 ? b_lo[e] : b_hi[e - 4], T{});
+      const _Float16 sh = cell_half_e<T, SCALED>(e < 4 ? s_lo[e] : s_hi[e - 4], vmul);
+      const _Float16 bh = cell_half_e<T, SCALED>(e < 4 ? b_lo[e] : b_hi[e - 4], vmul);
       if constexpr (T::id == KVQ_DTYPE_BF16) range_bad |= __builtin_isinf((float)bh);
       uint32_t bytes;  // codes of the thread's 4 dims, one byte each
       if constexpr (BITS == 8) {
@@ -365,10 +380,18 @@ __global__ __launch_bounds__(kWW * 64, 1) void wide_attn_kernel(WideParams p) {
 
   u4 qop[C::KSTEPS];
   float kf = p.scale_log2;  // fp32 score -> log2 units
+  // range exponents of the K and V caches (0 for an unquantized cache, an fp16 cache -- whose
+  // values always fit the fp16 operands -- or a null pointer), read after the query and the first
+  // tiles are requested, so that waiting for the word delays no load
+  int ek = 0, ev = 0;
   {
     const uint16_t* qrow = p.q + (int64_t)b * p.q_sb + (int64_t)hq * p.q_sh + (int64_t)lq * p.q_sl + 8 * h;
 #pragma unroll
     for (int j = 0; j < C::KSTEPS; ++j) qop[j] = *(const u4*)(qrow + 16 * j);
+    if constexpr (!C::DENSE && T::id == KVQ_DTYPE_BF16) {
+      if (p.k_rexp) ek = min(max(*p.k_rexp, 0), 127);
+      if (p.v_rexp) ev = min(max(*p.v_rexp, 0), 127);
+    }
     if constexpr (!C::DENSE) {
       // q * 2^qe in fp16, exact: the row's largest |q| lands in [2^13, 2^14)
       float qmax = 0.0f;
@@ -383,7 +406,7 @@ __global__ __launch_bounds__(kWW * 64, 1) void wide_attn_kernel(WideParams p) {
         qe = 14 - qe;
       }
       const float qs = ldexpf(1.0f, qe);
-      kf = ldexpf(p.scale_log2, -qe);
+      kf = ldexpf(p.scale_log2, ek - qe);  // the K operands are staged times 2^-ek
 #pragma unroll
       for (int j = 0; j < C::KSTEPS; ++j)
 #pragma unroll
@@ -393,6 +416,7 @@ __global__ __launch_bounds__(kWW * 64, 1) void wide_attn_kernel(WideParams p) {
     }
   }
 
+  const float kmul = ldexpf(1.0f, -ek), vmul = ldexpf(1.0f, -ev);  // the staging's factors 2^-E
   float m_run = -INFINITY, l_run = 0.0f;
   bool range_bad = false;  // a tile this thread staged holds a bf16 group beyond the fp16 range
   f16v oacc[C::NDB];
@@ -408,13 +432,15 @@ __global__ __launch_bounds__(kWW * 64, 1) void wide_attn_kernel(WideParams p) {
   // One step: tile t's products from operand buffers (kt, vt), and tile t + 1's staging from raw
   // slot raw1 into (kd, vd). The step is one basic block: each product's operand reads are issued
   // ahead of its MFMA chain, and the staging's independent VALU work fills the chain's issue slots.
-  auto step = [&](const uint8_t* kt, const uint8_t* vt, int k0, const uint8_t* raw1, uint8_t* kd, uint8_t* vd) {
+  auto step = [&](auto scaled, const uint8_t* kt, const uint8_t* vt, int k0, const uint8_t* raw1, uint8_t* kd,
+                  uint8_t* vd) {
+    constexpr bool SC = decltype(scaled)::value;
     // K operands through a ring of KR registers, read KR MFMAs ahead
     constexpr int KR = C::KSTEPS < 8 ? C::KSTEPS : 8;
     u4 ka[KR];
 #pragma unroll
     for (int j = 0; j < KR; ++j) ka[j] = *(const u4*)(kt + k_off + 32 * j);
-    wide_stage_k<T, OT, D, BITS, G>(raw1, kd, tid, range_bad);
+    wide_stage_k<T, OT, D, BITS, G, SC>(raw1, kd, tid, range_bad, kmul);
     f16v s = f16v{};
 #pragma unroll
     for (int j = 0; j < C::KSTEPS; ++j) {
@@ -460,7 +486,7 @@ __global__ __launch_bounds__(kWW * 64, 1) void wide_attn_kernel(WideParams p) {
     u4 va[VR];
 #pragma unroll
     for (int i = 0; i < VR; ++i) va[i] = vop_at(i);
-    wide_stage_v<T, OT, D, BITS, G>(raw1, vd, tid, range_bad);
+    wide_stage_v<T, OT, D, BITS, G, SC>(raw1, vd, tid, range_bad, vmul);
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       oacc[i >> 1] = mfma_32x32x16(va[i % VR], pop[i & 1], oacc[i >> 1], OT{});
@@ -472,11 +498,14 @@ __global__ __launch_bounds__(kWW * 64, 1) void wide_attn_kernel(WideParams p) {
   // the other; raw slot t % NR is refilled with tile t + NR once tile t is staged. Every step stages:
   // past the last tile the raw slot holds a re-read of the last tile, staged into a buffer no step
   // reads. Every wave computes (rows past the block's end are clamped and never stored).
-  if (ntile > 0) {
+  // The loop is compiled twice: staging the cache as it is, and staging it times 2^-E (a bf16 cache
+  // whose range exponent is not 0), so that the common case carries no scaling work.
+  auto tile_loop = [&](auto scaled) {
+    constexpr bool SC = decltype(scaled)::value;
     wait_vm<0>();  // the query and the first NR raw tiles
     __syncthreads();
-    wide_stage_k<T, OT, D, BITS, G>(ring, kop, tid, range_bad);
-    wide_stage_v<T, OT, D, BITS, G>(ring, vop, tid, range_bad);
+    wide_stage_k<T, OT, D, BITS, G, SC>(ring, kop, tid, range_bad, kmul);
+    wide_stage_v<T, OT, D, BITS, G, SC>(ring, vop, tid, range_bad, vmul);
     for (int t = 0; t < ntile; ++t) {
       if constexpr (C::NR == 3) {
         wait_vm<C::IPW>();  // tile t + 1 has landed (tile t + 2 may be in flight)
@@ -487,7 +516,19 @@ __global__ __launch_bounds__(kWW * 64, 1) void wide_attn_kernel(WideParams p) {
       issue(t + C::NR);
       const int ck = opaque((t & 1) * C::KOPB), nk = opaque(((t + 1) & 1) * C::KOPB);
       const int cv = opaque((t & 1) * C::VOPB), nv = opaque(((t + 1) & 1) * C::VOPB);
-      step(kop + ck, vop + cv, (t_begin + t) * kWT, ring + opaque(((t + 1) % C::NR) * C::SLOT), kop + nk, vop + nv);
+      step(scaled, kop + ck, vop + cv, (t_begin + t) * kWT, ring + opaque(((t + 1) % C::NR) * C::SLOT), kop + nk,
+           vop + nv);
+    }
+  };
+  if (ntile > 0) {
+    if constexpr (!C::DENSE && T::id == KVQ_DTYPE_BF16) {
+      if (ek != 0 || ev != 0) {
+        tile_loop(std::integral_constant<bool, true>{});
+      } else {
+        tile_loop(std::integral_constant<bool, false>{});
+      }
+    } else {
+      tile_loop(std::integral_constant<bool, false>{});
     }
   }
   wait_vm<0>();  // the look-ahead loads land before the workgroup's LDS is released
@@ -507,7 +548,7 @@ __global__ __launch_bounds__(kWW * 64, 1) void wide_attn_kernel(WideParams p) {
   // ---- epilogue: lane (n, h) holds O^T rows 32 db + 8 i + 4 h + j (j = 0..3) of query row n
   if (!row_ok) return;
   if (p.nsplit == 1) {
-    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+    const float inv = l_tot > 0.0f ? ldexpf(1.0f / l_tot, ev) : 0.0f;  // the V operands were staged times 2^-ev
     uint16_t* orow = p.out + (int64_t)b * p.o_sb + (int64_t)hq * p.o_sh + (int64_t)lq * p.o_sl + 4 * h;
 #pragma unroll
     for (int db = 0; db < C::NDB; ++db)
@@ -521,11 +562,13 @@ __global__ __launch_bounds__(kWW * 64, 1) void wide_attn_kernel(WideParams p) {
   } else {
     const int64_t pi = ((int64_t)unit * p.nsplit + split) * kWRows + (row - r0);
     float* po = p.part_o + pi * D + 4 * h;
+    const float vs = ldexpf(1.0f, ev);  // the partial in the cache's units (the V operands were staged times 2^-ev)
 #pragma unroll
     for (int db = 0; db < C::NDB; ++db)
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        *(f4*)(po + 32 * db + 8 * i) = f4{oacc[db][4 * i], oacc[db][4 * i + 1], oacc[db][4 * i + 2], oacc[db][4 * i + 3]};
+        *(f4*)(po + 32 * db + 8 * i) =
+            f4{oacc[db][4 * i] * vs, oacc[db][4 * i + 1] * vs, oacc[db][4 * i + 2] * vs, oacc[db][4 * i + 3] * vs};
     if (h == 0) ((float2*)p.part_ml)[pi] = make_float2(m_run, l_tot);
   }
 }
@@ -634,6 +677,8 @@ static void wide_quant_params(WideParams& p, const kvq_qtensor* k, const kvq_qte
   p.vsb_sb = v->sb_stride_b;
   p.vsb_sh = v->sb_stride_h;
   p.vsb_ss = v->sb_stride_s;
+  p.k_rexp = k->range_exp;
+  p.v_rexp = v->range_exp;
 }
 
 template <bool PAGED>

@@ -8,6 +8,7 @@ zero-filled torch allocation cached per (device, stream); the library itself all
 from __future__ import annotations
 
 import ctypes
+import weakref
 from dataclasses import dataclass
 from typing import Optional, Sequence, Tuple
 
@@ -48,6 +49,57 @@ def _require_cuda(*tensors: torch.Tensor) -> torch.device:
 def _check_triple(tr: Sequence[torch.Tensor], name: str) -> None:
     if len(tr) != 3:
         raise ValueError(f"{name} must be a (codes, scales, biases) triple")
+
+
+# ---- range exponents (include/kvq.h, kvq_qtensor.range_exp)
+#
+# A quantized cache keeps one int32 in device memory, its range exponent E: the appends raise it to
+# the smallest E >= 0 with every dequantized value within 2^15 * 2^E, and the quantized prefill
+# kernels stage their fp16 operands times 2^-E, so a bf16 cache whose values leave the fp16 range
+# still gives finite results. The word belongs to the cache's buffers: it is registered here under
+# the storage of the codes buffer, and every call that is handed a view of those buffers (the
+# reference-style entry points pass only the (codes, scales, biases) views) finds it again.
+
+_range_words: dict = {}  # codes storage address -> (weak reference to the codes buffer, int32 word)
+
+
+def register_range_word(codes: torch.Tensor, word: torch.Tensor) -> None:
+    """Attach a cache's range word (a one-element int32 tensor on the codes' device) to the codes
+    buffer: appends into views of it raise the word, attention over views of it reads it."""
+    if word.dtype != torch.int32 or word.numel() != 1 or word.device != codes.device:
+        raise ValueError("a range word is a one-element int32 tensor on the cache's device")
+    key = codes.untyped_storage().data_ptr()
+    if len(_range_words) > 4096:  # drop entries whose buffers are gone
+        for k in [k for k, (ref, _) in _range_words.items() if ref() is None]:
+            del _range_words[k]
+    _range_words[key] = (weakref.ref(codes), word)
+
+
+def range_word(codes: torch.Tensor) -> Optional[torch.Tensor]:
+    """The range word registered for the buffer `codes` is a view of, or None."""
+    hit = _range_words.get(codes.untyped_storage().data_ptr())
+    if hit is None:
+        return None
+    buf = hit[0]()
+    if buf is None or buf.untyped_storage().data_ptr() != codes.untyped_storage().data_ptr():
+        return None
+    return hit[1]
+
+
+def range_exponent(triple: Triple, bits: int) -> torch.Tensor:
+    """The range exponent of a (codes, scales, biases) triple computed from its scales and biases on
+    its device (no host synchronization): the smallest E >= 0 with max(|b|, |b + (2^bits - 1) s|)
+    <= 2^15 * 2^E over every group, as a one-element int32 tensor. For triples that carry no
+    registered word."""
+    _, scales, biases = triple
+    s, b = scales.float(), biases.float()
+    if s.numel() == 0:
+        return torch.zeros(1, dtype=torch.int32, device=scales.device)
+    top = b + float((1 << bits) - 1) * s
+    bound = torch.nan_to_num(torch.maximum(b.abs(), top.abs()), nan=0.0, posinf=float("inf")).amax()
+    e = torch.ceil(torch.log2(bound * (1.0 / 32768.0)))
+    e = torch.nan_to_num(e, nan=127.0, posinf=127.0, neginf=0.0).clamp(0.0, 127.0)
+    return e.to(torch.int32).reshape(1)
 
 
 @dataclass(frozen=True)
@@ -108,9 +160,9 @@ def quantize_append(k: torch.Tensor, k_dst: Triple, v: Optional[torch.Tensor] = 
         if scales.dtype != k.dtype:
             raise ValueError("scales/biases must have the dtype of the rows (MLX stores them in T)")
     L_ = _lib.lib()
-    kr, kq = _lib.rows(k), _lib.qtensor(*k_dst)
+    kr, kq = _lib.rows(k), _lib.qtensor(*k_dst, range_exp=range_word(k_dst[0]))
     if v is not None:
-        vr, vq = _lib.rows(v), _lib.qtensor(*v_dst)
+        vr, vq = _lib.rows(v), _lib.qtensor(*v_dst, range_exp=range_word(v_dst[0]))
         vr_p, vq_p = ctypes.byref(vr), ctypes.byref(vq)
     else:
         vr_p = vq_p = None
@@ -153,8 +205,8 @@ class AppendCall:
                 raise ValueError("k_dst and v_dst must have the same shapes")
             if v_dst[1].dtype != scales.dtype:
                 raise ValueError("k_dst and v_dst must share a dtype")
-        self._kq = _lib.qtensor(*k_dst)
-        self._vq = _lib.qtensor(*v_dst) if v_dst is not None else None
+        self._kq = _lib.qtensor(*k_dst, range_exp=range_word(k_dst[0]))
+        self._vq = _lib.qtensor(*v_dst, range_exp=range_word(v_dst[0])) if v_dst is not None else None
         self._kr, self._vr = _lib.Rows(), _lib.Rows()
         self._dtype = k_dst[1].dtype
         self._code = _lib.dtype_code(self._dtype)
@@ -386,10 +438,18 @@ def prepare_attention(queries: torch.Tensor, keys, values, scale: float, *, caus
         args = (ctypes.byref(qr), ctypes.byref(kq), ctypes.byref(vq), sl_ptr, ctypes.byref(orr), B, Hq, Hkv, L, D, S,
                 *tail)
     else:
-        kq, vq = _lib.qtensor(*keys), _lib.qtensor(*values)
+        # the caches' range words: registered with their buffers, else (one-shot prefill calls)
+        # computed from the scales and biases on the device; decode applies scales in fp32 and
+        # reads none
+        kw, vw = range_word(keys[0]), range_word(values[0])
+        if kernel == "prefill" and _one_shot:
+            kw = range_exponent(keys, bits) if kw is None else kw
+            vw = range_exponent(values, bits) if vw is None else vw
+        kq, vq = _lib.qtensor(*keys, range_exp=kw), _lib.qtensor(*values, range_exp=vw)
         args = (ctypes.byref(qr), ctypes.byref(kq), ctypes.byref(vq), sl_ptr, ctypes.byref(orr), B, Hq, Hkv, L, D, S,
                 int(bits), int(group_size), *tail)
-    keep = (queries, keys, values, seq_lens, ws, qr, orr, kq, vq)
+        keep_words = (kw, vw)
+    keep = (queries, keys, values, seq_lens, ws, qr, orr, kq, vq) + (() if dense else keep_words)
     return AttentionCall(fn, args, keep, kernel, out, symbol)
 
 
@@ -437,10 +497,10 @@ def paged_quantize_append(k: torch.Tensor, k_pool: Triple, v: Optional[torch.Ten
         if starts.dtype != torch.int32 or starts.numel() != B or starts.device != dev:
             raise ValueError("starts must be an int32 tensor of B entries on the same device")
         st_ptr = starts.data_ptr()
-    kr, kq = _lib.rows(k), _lib.qtensor(*k_pool)
+    kr, kq = _lib.rows(k), _lib.qtensor(*k_pool, range_exp=range_word(k_pool[0]))
     vr_p = vq_p = None
     if v is not None:
-        vr, vq = _lib.rows(v), _lib.qtensor(*v_pool)
+        vr, vq = _lib.rows(v), _lib.qtensor(*v_pool, range_exp=range_word(v_pool[0]))
         vr_p, vq_p = ctypes.byref(vr), ctypes.byref(vq)
     rp = None
     if rope is not None:
@@ -483,7 +543,7 @@ def paged_attention(queries: torch.Tensor, k_pool: Triple, v_pool: Triple, block
         raise ValueError(f"Hq={Hq} is not a multiple of Hkv={Hkv}")
     S = int(max_len) if max_len is not None else block_tables.shape[1] * PAGE_ROWS
     if not _rows_ok(queries):
-        queries = _copy_for_one_shot(queries, "queries", _one_shot)
+        queries = _copy_for_one_shot(queries, "queries", True)
     out = _check_out(out, queries, dev)
     if kernel == "auto":
         kernel = _auto_kernel((Hq // Hkv) * L, D, group_size)
@@ -495,7 +555,9 @@ def paged_attention(queries: torch.Tensor, k_pool: Triple, v_pool: Triple, block
     stream = _lib.stream_ptr(dev)
     ws = _workspace(dev, stream, nbytes)
     qr, orr = _lib.rows(queries), _lib.rows(out)
-    kq, vq = _lib.qtensor(*k_pool), _lib.qtensor(*v_pool)
+    # (only registered words: the unused rows of a pool's pages hold whatever was there)
+    kw, vw = range_word(k_pool[0]), range_word(v_pool[0])
+    kq, vq = _lib.qtensor(*k_pool, range_exp=kw), _lib.qtensor(*v_pool, range_exp=vw)
     fn = lib.kvq_paged_decode_attn if kernel == "decode" else lib.kvq_paged_prefill_attn
     rc = fn(ctypes.byref(qr), ctypes.byref(kq), ctypes.byref(vq), k_pool[0].shape[0], block_tables.data_ptr(),
             block_tables.stride(0), seq_lens.data_ptr(), ctypes.byref(orr), B, Hq, Hkv, L, D, S, int(bits),

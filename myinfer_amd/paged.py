@@ -112,7 +112,10 @@ class PagedRadixKVCache:
         def pool():
             codes = torch.zeros((max_blocks, num_kv_heads, PAGE_ROWS, W), dtype=torch.int32, device=device)
             scales = torch.zeros((max_blocks, num_kv_heads, PAGE_ROWS, G), dtype=dtype, device=device)
-            return codes.view(torch.uint32), scales, torch.zeros_like(scales)
+            codes = codes.view(torch.uint32)
+            # the pool's range exponent: raised by the paged appends, read by the paged prefill
+            kernels.register_range_word(codes, torch.zeros(1, dtype=torch.int32, device=device))
+            return codes, scales, torch.zeros_like(scales)
 
         self._k = [pool() for _ in range(num_layers)]
         self._v = [pool() for _ in range(num_layers)]

@@ -141,3 +141,26 @@ def dequantize(codes: np.ndarray, scales_bits: np.ndarray, biases_bits: np.ndarr
     D = c.shape[-1]
     cg = c.reshape(*c.shape[:-1], D // group_size, group_size)
     return (cg * s[..., None] + b[..., None]).reshape(c.shape)
+
+
+def range_exponent(scales_bits: np.ndarray, biases_bits: np.ndarray, dtype: str, bits: int) -> int:
+    """The range exponent of a quantized cache (include/kvq.h, kvq_qtensor.range_exp): the smallest
+    E >= 0 with max(|b|, |b + n s|) <= 2^15 * 2^E over every group (n = 2^bits - 1; the group's
+    dequantized values s * c + b, c in [0, n], have their extremes at c = 0 and c = n), from the
+    stored T scale and bias in fp32 (b + n s rounded after the product, then after the sum). An
+    unbounded group (inf) gives 127. No counterpart in the reference: it is this build's operand
+    range, and the checks are its defining inequality at the boundaries."""
+    s = from_bits(scales_bits, dtype).astype(np.float32)
+    b = from_bits(biases_bits, dtype).astype(np.float32)
+    if s.size == 0:
+        return 0
+    top = (b + (np.float32((1 << bits) - 1) * s).astype(np.float32)).astype(np.float32)
+    bound = float(np.nan_to_num(np.maximum(np.abs(b), np.abs(top)), nan=0.0, posinf=np.inf).max())
+    if bound <= 32768.0:
+        return 0
+    if not np.isfinite(bound):
+        return 127
+    e = 0
+    while bound > 32768.0 * 2.0**e:
+        e += 1
+    return e
