@@ -76,6 +76,13 @@ struct DecCfg {
   static constexpr int AS = 4 * SBC;  // bytes between the arrays
   static constexpr int SLOT = 2 * TB + (DENSE ? 0 : 4 * AS);
   static constexpr int IPT = 2 * CI + (DENSE ? 0 : 4 * NSB);  // DMA instructions per tile
+  // The XOR swizzle of the 16-byte chunks of K row r: r % CPR with one more bit of r folded in, so
+  // that the 16 keys x 2 lane groups of a 32-lane half of each operand read (ds_read_b128, 128
+  // banks of 4 bytes) fall on 32 distinct 16-byte bank groups. With r % CPR alone, keys r and r + 8
+  // (CPR 8, 4) or r and r + 4 (CPR 16) met in one bank group: a 2-way conflict on every K read.
+  static constexpr int kswz(int r) {
+    return (r % CPR) ^ (CPR == 16 ? (r >> 2) & 1 : CPR == 8 ? (r >> 3) & 1 : CPR == 4 ? 2 * ((r >> 3) & 1) : 0);
+  }
 };
 
 struct DecParams {
@@ -513,7 +520,7 @@ __global__ __launch_bounds__(NW * 64, (dec_min_wgs<D, BITS, NW, NSLOT, G>())) vo
     srs[3] = make_rsrc(p.vb + vo, vn);
   }
   // lane offsets: code lane l fills 16-byte cell l of each KiB, i.e. row l / CPR and -- for K,
-  // swizzled -- chunk (l % CPR) ^ (row % CPR); scale/bias lane l reads group l / 32 of key l % 32
+  // swizzled -- chunk (l % CPR) ^ kswz(row); scale/bias lane l reads group l / 32 of key l % 32
   // (for NG == 1 the upper half re-reads the lower half's keys)
   uint32_t dk[C::CI], dv[C::CI], dsb[4][C::NSB];
   {
@@ -521,7 +528,7 @@ __global__ __launch_bounds__(NW * 64, (dec_min_wgs<D, BITS, NW, NSLOT, G>())) vo
 #pragma unroll
     for (int c = 0; c < C::CI; ++c) {
       const int kr = c * C::RPI + rr;
-      dk[c] = (uint32_t)((int64_t)kr * p.kc_ss + 16 * (cc ^ (kr % C::CPR)));
+      dk[c] = (uint32_t)((int64_t)kr * p.kc_ss + 16 * (cc ^ C::kswz(kr)));
       dv[c] = (uint32_t)((int64_t)(c * C::RPI + rr) * p.vc_ss + 16 * cc);
     }
 #pragma unroll
@@ -649,7 +656,7 @@ __global__ __launch_bounds__(NW * 64, (dec_min_wgs<D, BITS, NW, NSLOT, G>())) vo
   for (int jn = 0; jn < C::NBLK; ++jn) acc_o[jn] = f4{0, 0, 0, 0};
 
   // per-lane LDS offsets of the tile operands, relative to a slot
-  const int sw = n % C::CPR;  // the swizzle of key n (and of key 16 + n)
+  const int sw = C::kswz(n);  // the swizzle of key n (and of key 16 + n)
   // K: chunk c of the lane's quarter row of key n (KLB / 16 chunks; below 16 bytes a half chunk)
   uint32_t off_k[4];
 #pragma unroll

@@ -72,6 +72,12 @@ struct WideCfg {
   static constexpr int KOPB = kWT * KROW;                  // bytes of a K operand tile
   static constexpr int VOPB = D * kWT * 2;                 // bytes of a V^T operand tile
   static constexpr int LDS = NR * SLOT + 2 * (KOPB + VOPB);  // ring + double-buffered K and V^T
+  // The raw K rows land with their 16-byte chunks XOR-swizzled: position x of row r holds chunk
+  // x ^ kswz(r). The K staging reads a chunk of 32 consecutive rows per 32-lane half; rows r and
+  // r + 32 / CPR share banks (128 banks of 4 bytes), and kswz gives the CPR rows of each such class
+  // distinct positions, so those reads are free of bank conflicts.
+  static_assert(CPR >= 8 && CPR <= 32, "raw rows of 128 to 512 bytes");
+  static constexpr int kswz(int r) { return (r / (32 / CPR)) % CPR; }
   static_assert(2 * CI % kWW == 0, "code DMAs divide over the waves");
   static_assert(LDS <= 160 * 1024, "fits the LDS");
 };
@@ -146,17 +152,21 @@ __device__ __forceinline__ uint32_t nibbles_hi(uint32_t w) {
 }
 
 // K of a raw tile into the K operand tile (OT elements): thread t dequantizes dims
-// [D/8 p, D/8 (p + 1)) of key r (t = 8 r + p) and writes them as KCH chunks of 8 dims. Rows are 16
+// [D/8 p, D/8 (p + 1)) of key r (t = 32 p + r) and writes them as KCH chunks of 8 dims. Rows are 16
 // bytes longer than the data (528 bytes at D = 256), so the 32 lanes that read one 16-byte column of
 // 32 keys hit distinct banks and a lane's reads of one row are one base address plus immediates.
+// Consecutive lanes take consecutive keys: a 16-byte LDS write is served 8 lanes at a time over 128
+// bytes, and 8 rows 528 bytes apart fill those 128 bytes without a conflict (8 lanes of one row,
+// 64 bytes apart, met 4 to a bank: 2.3x the write time). The raw reads follow kswz.
 template <typename T, typename OT, int D, int BITS, int G, bool SCALED = false>
 __device__ __forceinline__ void wide_stage_k(const uint8_t* raw, uint8_t* kop, int t, bool& range_bad, float kmul) {
   using C = WideCfg<D, BITS, G>;
-  const int r = t >> 3, p = t & 7;
+  const int r = t & 31, p = t >> 5, sw = C::kswz(r);
+  const uint8_t* row = raw + r * C::ROWB;
   u4 w[C::KCH];
   if constexpr (C::DENSE) {
 #pragma unroll
-    for (int c = 0; c < C::KCH; ++c) w[c] = *(const u4*)(raw + r * C::ROWB + 16 * (C::KCH * p + c));
+    for (int c = 0; c < C::KCH; ++c) w[c] = *(const u4*)(row + 16 * ((C::KCH * p + c) ^ sw));
   } else {
     const int g = 32 * p / G;
     const uint32_t* cells = (const uint32_t*)(raw + 2 * C::TB);
@@ -167,7 +177,7 @@ __device__ __forceinline__ void wide_stage_k(const uint8_t* raw, uint8_t* kop, i
     if constexpr (T::id == KVQ_DTYPE_BF16) range_bad |= __builtin_isinf((float)bh);
     const h2 s2 = {sh, sh}, b2 = {bh, bh};
     if constexpr (BITS == 8) {
-      const u4 a = *(const u4*)(raw + r * C::ROWB + 32 * p), b = *(const u4*)(raw + r * C::ROWB + 32 * p + 16);
+      const u4 a = *(const u4*)(row + 16 * ((2 * p) ^ sw)), b = *(const u4*)(row + 16 * ((2 * p + 1) ^ sw));
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const uint32_t wa = i < 2 ? a[2 * i] : b[2 * (i - 2)], wb = i < 2 ? a[2 * i + 1] : b[2 * (i - 2) + 1];
@@ -175,7 +185,7 @@ __device__ __forceinline__ void wide_stage_k(const uint8_t* raw, uint8_t* kop, i
                   dq_pair(wb, kSelHi, s2, b2)};
       }
     } else {
-      const u4 a = *(const u4*)(raw + r * C::ROWB + 16 * p);
+      const u4 a = *(const u4*)(row + 16 * (p ^ sw));
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const uint32_t lo = nibbles_lo(a[i]), hi = nibbles_hi(a[i]);
@@ -292,6 +302,10 @@ __global__ __launch_bounds__(kWW * 64, 1) void wide_attn_kernel(WideParams p) {
   __amdgpu_buffer_rsrc_t code_r[C::CPW];
   uint32_t code_vo[C::CPW], code_lds[C::CPW];
   int64_t code_ss[C::CPW];
+  // waves 0 and 1 load K (swizzled rows), waves 2 and 3 load V: a mask the compiler does not split
+  // the offsets on
+  static_assert(2 * C::CPW == C::CI, "two waves load each of K and V");
+  const int kmask = opaque(wave < 2 ? C::CPR - 1 : 0);
 #pragma unroll
   for (int j = 0; j < C::CPW; ++j) {
     const int q = wave * C::CPW + j;
@@ -299,7 +313,8 @@ __global__ __launch_bounds__(kWW * 64, 1) void wide_attn_kernel(WideParams p) {
     const int i = is_k ? q : q - C::CI;
     code_r[j] = is_k ? krs : vrs;
     code_ss[j] = is_k ? p.kc_ss : p.vc_ss;
-    code_vo[j] = (uint32_t)((i * C::RPI + lane / C::CPR) * code_ss[j] + 16 * (lane % C::CPR));
+    const int rr = i * C::RPI + lane / C::CPR;  // the row of the tile this lane's 16 bytes belong to
+    code_vo[j] = (uint32_t)(rr * code_ss[j] + 16 * ((lane % C::CPR) ^ (C::kswz(rr) & kmask)));
     code_lds[j] = (is_k ? 0 : C::TB) + 1024 * i;
   }
   __amdgpu_buffer_rsrc_t sb_r = krs;
