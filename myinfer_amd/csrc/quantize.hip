@@ -12,8 +12,9 @@
 // Every operation is IEEE fp32 with round-to-nearest-even (correctly rounded division, rint
 // half-to-even), so codes, scales and biases are bit-identical to the CPU restatement.
 //
-// Thread mapping: one thread per 8 consecutive elements (one 16-byte load); the G/8 threads of a
-// group reduce min/max with lane permutes. Grid.y selects the K or the V job of one launch.
+// Thread mapping: one thread per 32 (large launches) or 8 consecutive elements, 16 bytes a load, all
+// loads in flight at once; the threads of a group are neighbouring lanes and reduce min/max with
+// DPP lane permutes. Grid.y selects the K or the V job of one launch.
 //
 // RoPE (kvq_rope_quantize_append): the K job rotates its rows before quantizing, the way mlx-lm's
 // attention layers rotate keys before the cache update and the reference's native kernel fuses
@@ -117,6 +118,29 @@ __device__ __forceinline__ int group_range_exp(float s, float b, float n) {
   return m == 0.5f ? k - 1 : k;
 }
 
+// n / d for 0 <= n < 2^31 as one multiply and shift: with l = ceil(log2 d) and
+// m = ceil(2^(31 + l) / d) (which fits 32 bits), floor(n m / 2^(31 + l)) = floor(n / d)
+// (Granlund and Montgomery, "Division by invariant integers using multiplication", 1994, for
+// 31-bit dividends: the error n (m - 2^(31 + l) / d) / 2^(31 + l) stays below 1 / d).
+struct Div31 {
+  uint32_t m;
+  uint32_t sh;  // 31 + l
+};
+static Div31 make_div31(uint32_t d) {
+  uint32_t l = 0;
+  while ((1ull << l) < d) ++l;
+  return {(uint32_t)((((uint64_t)1 << (31 + l)) + d - 1) / d), 31 + l};
+}
+__device__ __forceinline__ uint32_t div31(uint32_t n, Div31 q) { return (uint32_t)(((uint64_t)n * q.m) >> q.sh); }
+
+// The rows [l0, l0 + L) of every (sequence, head) in one launch: thread t quantizes chunk
+// t % per_row of row t / per_row (per_row = D / EPT), rows ordered (b, h, l); total < 2^31.
+struct RowMap {
+  uint32_t total, L, H, per_row;
+  Div31 div_c, div_l, div_h;
+  int64_t l0;
+};
+
 // Paged destination: row r of sequence b goes to row r % 64 of page table[b][r / 64] (the job's
 // batch strides are then page strides); r = starts[b] + l when `starts` is given, else
 // row_offset + l. table == nullptr: the contiguous cache.
@@ -127,46 +151,95 @@ struct PageMap {
   int num_pages;
 };
 
-template <typename T, int BITS, int G, bool ROPE>
-__global__ __launch_bounds__(256) void quantize_append_kernel(QuantJob job0, QuantJob job1, int H, int L,
-                                                              int D, int64_t total, int64_t row_offset, RopeArgs rope,
-                                                              PageMap pm) {
-#pragma clang fp contract(off)
-  const QuantJob job = blockIdx.y == 0 ? job0 : job1;
-  const int64_t tid = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const bool active = tid < total;
-  const int per_row = D / 8;
-  const int64_t t = active ? tid : 0;
-  const int chunk = (int)(t % per_row);
-  const int64_t row = t / per_row;
-  const int l = (int)(row % L);
-  const int h = (int)((row / L) % H);
-  const int64_t b = row / ((int64_t)L * H);
+// v of another lane by a DPP lane permutation: quad_perm [1, 0, 3, 2] and [2, 3, 0, 1] (the lane
+// index XOR 1 and XOR 2), row_half_mirror (lane 7 - i of each 8) and row_mirror (15 - i of each 16)
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+constexpr int kQuadXor1 = 0xB1, kQuadXor2 = 0x4E, kHalfMirror = 0x141, kMirror = 0x140;
 
-  const uint16_t* srow = job.src + b * job.s_b + h * job.s_h + (int64_t)l * job.s_l;
-  float x[8];
-  load8<T>(srow + chunk * 8, x);
+// Max and min over the TPG neighbouring lanes of a group (TPG a power of two up to 16): after the
+// quad steps every lane of a quad holds its quad's value, so the mirrors exchange whole quads, then
+// whole 8-lane halves.
+template <int TPG>
+__device__ __forceinline__ void group_minmax(float& mx, float& mn) {
+  if constexpr (TPG >= 2) {
+    mx = fmaxf(mx, dpp<kQuadXor1>(mx));
+    mn = fminf(mn, dpp<kQuadXor1>(mn));
+  }
+  if constexpr (TPG >= 4) {
+    mx = fmaxf(mx, dpp<kQuadXor2>(mx));
+    mn = fminf(mn, dpp<kQuadXor2>(mn));
+  }
+  if constexpr (TPG >= 8) {
+    mx = fmaxf(mx, dpp<kHalfMirror>(mx));
+    mn = fminf(mn, dpp<kHalfMirror>(mn));
+  }
+  if constexpr (TPG >= 16) {
+    mx = fmaxf(mx, dpp<kMirror>(mx));
+    mn = fminf(mn, dpp<kMirror>(mn));
+  }
+}
+
+// EPT elements per thread (EPT / 8 16-byte loads in flight): 32 for launches large enough to fill
+// the GPU several times over (fewer instructions per element), 8 for small, latency-bound ones.
+template <typename T, int BITS, int G, bool ROPE, int EPT>
+__global__ __launch_bounds__(256) void quantize_append_kernel(QuantJob job0, QuantJob job1, RowMap rm,
+                                                              int64_t row_offset, RopeArgs rope, PageMap pm) {
+#pragma clang fp contract(off)
+  constexpr int kEPT = EPT;
+  constexpr int TPG = G / kEPT;  // threads per group: neighbouring lanes
+  const QuantJob job = blockIdx.y == 0 ? job0 : job1;
+  const uint32_t tid = blockIdx.x * 256u + threadIdx.x;
+  const bool active = tid < rm.total;
+  const uint32_t t = active ? tid : 0u;
+  const uint32_t row = div31(t, rm.div_c);
+  const int chunk = (int)(t - row * rm.per_row);
+  const uint32_t bh = div31(row, rm.div_l);
+  const int64_t l = rm.l0 + (int64_t)(row - bh * rm.L);  // the row's position among the appended rows
+  const uint32_t b32 = div31(bh, rm.div_h);
+  const int h = (int)(bh - b32 * rm.H);
+  const int64_t b = b32;
+
+  const uint16_t* srow = job.src + b * job.s_b + h * job.s_h + l * job.s_l;
+  float x[kEPT];
+  {
+    u4 raw[kEPT / 8];  // every load in flight before any conversion
+#pragma unroll
+    for (int j = 0; j < kEPT / 8; ++j) raw[j] = *(const u4*)(srow + chunk * kEPT + 8 * j);
+#pragma unroll
+    for (int j = 0; j < kEPT / 8; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        x[8 * j + 2 * i] = to_float((uint16_t)(raw[j][i] & 0xffffu), T{});
+        x[8 * j + 2 * i + 1] = to_float((uint16_t)(raw[j][i] >> 16), T{});
+      }
+  }
   if constexpr (ROPE) {
     if (blockIdx.y == 0) {  // the K job
-      const int d0 = chunk * 8, half = rope.dims / 2;
-      float xp[8];
-      if (!rope.traditional && d0 < rope.dims) load8<T>(srow + (d0 < half ? d0 + half : d0 - half), xp);
-      rope8(rope, rope.offset + (pm.starts ? pm.starts[b] : 0) + l, d0, x, xp);
+      const int half = rope.dims / 2;
+      const int64_t pos = rope.offset + (pm.starts ? pm.starts[b] : 0) + l;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) x[i] = to_float(from_float(x[i], T{}), T{});
+      for (int j = 0; j < kEPT / 8; ++j) {
+        const int d0 = chunk * kEPT + 8 * j;
+        float xs[8], xp[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) xs[i] = x[8 * j + i];
+        if (!rope.traditional && d0 < rope.dims) load8<T>(srow + (d0 < half ? d0 + half : d0 - half), xp);
+        rope8(rope, pos, d0, xs, xp);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) x[8 * j + i] = to_float(from_float(xs[i], T{}), T{});
+      }
     }
   }
   float mx = x[0], mn = x[0];
 #pragma unroll
-  for (int i = 1; i < 8; ++i) {
+  for (int i = 1; i < kEPT; ++i) {
     mx = fmaxf(mx, x[i]);
     mn = fminf(mn, x[i]);
   }
-#pragma unroll
-  for (int off = 1; off < G / 8; off <<= 1) {
-    mx = fmaxf(mx, shfl_xor(mx, off));
-    mn = fminf(mn, shfl_xor(mn, off));
-  }
+  group_minmax<TPG>(mx, mn);
   if (!active) return;
 
   constexpr float n_bins = (float)((1 << BITS) - 1);
@@ -181,14 +254,34 @@ __global__ __launch_bounds__(256) void quantize_append_kernel(QuantJob job0, Qua
     bias = edge;
   }
 
-  uint32_t packed[BITS] = {};  // 8 codes * BITS bits = BITS bytes -> BITS/4 words (at least 1)
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    float c = rintf((x[i] - bias) / s);
+  // code = rint((x - bias) / s) with the quotient rounded as the IEEE division rounds it. The
+  // reciprocal estimate (v_rcp_f32, within 1 ulp) refined by one residual step gives q1 within one
+  // ulp of that correctly rounded quotient, so rint(q1) can differ from its rint only when a
+  // half-integer lies within one ulp. A thread with any quotient within 2 ulp (|q1| 2^-22) of a
+  // half-integer, or of magnitude 2^21 or more, or not finite, divides all its elements exactly:
+  // the codes stay bit-identical and the division is the rare path.
+  constexpr int W = kEPT * BITS / 32 > 0 ? kEPT * BITS / 32 : 1;  // code words per thread (2-bit, 8 elements: half a word)
+  uint32_t packed[W];
+  auto put = [&](int i, float c) {
     c = fminf(fmaxf(c, 0.0f), n_bins);
-    const uint32_t code = (uint32_t)c;
     const int bit = i * BITS;
-    packed[bit / 32] |= code << (bit % 32);
+    if (bit % 32 == 0) packed[bit / 32] = 0u;
+    packed[bit / 32] |= (uint32_t)c << (bit % 32);
+  };
+  const float rs = __builtin_amdgcn_rcpf(s);
+  bool exact = false;
+#pragma unroll
+  for (int i = 0; i < kEPT; ++i) {
+    const float a = x[i] - bias;
+    const float qa = a * rs;
+    const float q1 = __builtin_fmaf(__builtin_fmaf(-qa, s, a), rs, qa);
+    const float c = rintf(q1);
+    exact |= !(fabsf(q1 - c) < __builtin_fmaf(fabsf(q1), -0x1p-22f, 0.5f));
+    put(i, c);
+  }
+  if (exact) {
+#pragma unroll
+    for (int i = 0; i < kEPT; ++i) put(i, rintf((x[i] - bias) / s));
   }
 
   int64_t drow = row_offset + l, bb = b;
@@ -203,16 +296,18 @@ __global__ __launch_bounds__(256) void quantize_append_kernel(QuantJob job0, Qua
     drow = r & 63;
   }
   uint32_t* cdst = job.codes + bb * job.c_b + h * job.c_h + drow * job.c_s;
-  if constexpr (BITS == 8) {
-    *(u2*)(cdst + chunk * 2) = u2{packed[0], packed[1]};
-  } else if constexpr (BITS == 4) {
-    cdst[chunk] = packed[0];
-  } else {  // 2-bit: 8 codes fill 16 bits; two neighbouring threads share a word
+  if constexpr (kEPT * BITS < 32) {  // 2-bit, 8 elements: 16 bits; two neighbouring threads share a word
     const uint32_t other = (uint32_t)__builtin_amdgcn_ds_bpermute((__lane_id() ^ 1) << 2, (int)packed[0]);
     if ((chunk & 1) == 0) cdst[chunk / 2] = packed[0] | (other << 16);
+  } else if constexpr (BITS == 8) {  // 8-byte aligned (checked on the host)
+#pragma unroll
+    for (int w = 0; w < W; w += 2) *(u2*)(cdst + chunk * W + w) = u2{packed[w], packed[w + 1]};
+  } else {
+#pragma unroll
+    for (int w = 0; w < W; ++w) cdst[chunk * W + w] = packed[w];
   }
-  if (chunk % (G / 8) == 0) {
-    const int64_t gi = bb * job.g_b + h * job.g_h + drow * job.g_s + chunk / (G / 8);
+  if (chunk % TPG == 0) {
+    const int64_t gi = bb * job.g_b + h * job.g_h + drow * job.g_s + chunk / TPG;
     const uint16_t sT = from_float(s, T{}), bT = from_float(bias, T{});
     job.scales[gi] = sT;
     job.biases[gi] = bT;
@@ -226,15 +321,42 @@ __global__ __launch_bounds__(256) void quantize_append_kernel(QuantJob job0, Qua
 template <typename T, int BITS, int G>
 static hipError_t launch_quant(const QuantJob& k, const QuantJob& v, int njobs, int B, int H, int L, int D,
                                int64_t row_offset, const RopeArgs* rope, const PageMap& pm, hipStream_t stream) {
-  const int64_t total = (int64_t)B * H * L * (D / 8);
-  const int64_t blocks = (total + 255) / 256;
-  if (rope)
-    hipLaunchKernelGGL((quantize_append_kernel<T, BITS, G, true>), dim3((unsigned)blocks, njobs), dim3(256), 0, stream,
-                       k, v, H, L, D, total, row_offset, *rope, pm);
-  else
-    hipLaunchKernelGGL((quantize_append_kernel<T, BITS, G, false>), dim3((unsigned)blocks, njobs), dim3(256), 0,
-                       stream, k, v, H, L, D, total, row_offset, RopeArgs{}, pm);
-  return hipGetLastError();
+  // rows per launch: the thread index of every launch stays below 2^31 (more rows take more launches)
+  // 32 elements per thread when that launch still has 8 or more workgroups per CU (2048 in all)
+  const bool wide = (int64_t)B * H * L * (D / 32) * njobs >= 2048 * 256;
+  const int ept = wide ? 32 : 8;
+  const int64_t per_l = (int64_t)B * H * (D / ept);
+  if (per_l >= ((int64_t)1 << 31)) return hipErrorInvalidValue;
+  const int64_t max_l = (((int64_t)1 << 31) - 1) / per_l;
+  RowMap rm{};
+  rm.H = (uint32_t)H;
+  rm.div_h = make_div31((uint32_t)H);
+  rm.per_row = (uint32_t)(D / ept);
+  rm.div_c = make_div31(rm.per_row);
+  for (int64_t l0 = 0; l0 < L; l0 += max_l) {
+    const int64_t nl = L - l0 < max_l ? L - l0 : max_l;
+    rm.L = (uint32_t)nl;
+    rm.div_l = make_div31((uint32_t)nl);
+    rm.total = (uint32_t)(per_l * nl);
+    rm.l0 = l0;
+    const unsigned blocks = (unsigned)((rm.total + 255u) / 256u);
+    const RopeArgs ra = rope ? *rope : RopeArgs{};
+    if (rope && wide)
+      hipLaunchKernelGGL((quantize_append_kernel<T, BITS, G, true, 32>), dim3(blocks, njobs), dim3(256), 0, stream, k, v,
+                         rm, row_offset, ra, pm);
+    else if (rope)
+      hipLaunchKernelGGL((quantize_append_kernel<T, BITS, G, true, 8>), dim3(blocks, njobs), dim3(256), 0, stream, k, v,
+                         rm, row_offset, ra, pm);
+    else if (wide)
+      hipLaunchKernelGGL((quantize_append_kernel<T, BITS, G, false, 32>), dim3(blocks, njobs), dim3(256), 0, stream, k,
+                         v, rm, row_offset, ra, pm);
+    else
+      hipLaunchKernelGGL((quantize_append_kernel<T, BITS, G, false, 8>), dim3(blocks, njobs), dim3(256), 0, stream, k,
+                         v, rm, row_offset, ra, pm);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
 template <typename T, int BITS>

@@ -104,6 +104,58 @@ def test_baseline_shapes(name, B, H, L, D, bits, dtype):
     _check_rows(x, dst, 3, bits, 64)
 
 
+@pytest.mark.parametrize("D,G,bits", [(96, 32, 8), (192, 64, 4), (320, 64, 8), (384, 128, 2), (32, 32, 8)])
+def test_row_widths_that_are_not_powers_of_two(D, G, bits):
+    """mx.quantize takes any row width that is a multiple of the group size: rows of D / 32
+    threads that do not divide a wave evenly, and a single-thread row."""
+    print(f"quantize D={D} G={G} bits={bits}", flush=True)
+    B, H, L = 2, 3, 45
+    x = _stress((B, H, L, D), 500 + D, torch.bfloat16)
+    dst = _alloc(B, H, L + 2, D, bits, G, torch.bfloat16)
+    kernels.quantize_append(x, dst, row_offset=2, group_size=G, bits=bits)
+    _check_rows(x, dst, 2, bits, G)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_half_integer_quotients(dtype):
+    """Groups whose quotients (x - bias) / s are exact half-integers (ties, rounded half to even)
+    and integers: a group spans [0, 255 * 2^-k], so s = -2^-k and bias = its maximum, and the other
+    values sit on the 2^-(k+1) grid. The kernel's fast quotient must hand every tie to the exact
+    division; the codes must equal the CPU restatement's."""
+    print(f"quantize ties dtype={dtype}", flush=True)
+    D, G = 128, 64
+    rows = []
+    for k in range(0, 6):
+        for shift in range(2):
+            top = 255.0 * 2.0 ** -k
+            step = 2.0 ** -(k + 1)
+            g = (torch.arange(G, dtype=torch.float64) * 2 + 1 + shift) % 510 * step  # odd multiples: ties
+            g[0], g[1] = 0.0, top
+            rows.append(torch.cat([g, g.flip(0)]))
+    x = torch.stack(rows).to(torch.float32)
+    assert torch.equal(x.to(dtype).to(torch.float32), x), "the grid values are exact in the dtype"
+    x = x.to(dtype).to(DEV).reshape(1, 1, -1, D)
+    dst = _alloc(1, 1, x.shape[2], D, 8, G, dtype)
+    kernels.quantize_append(x, dst, group_size=G, bits=8)
+    _check_rows(x, dst, 0, 8, G)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_c5_chunk_bit_exact(dtype):
+    """A whole C5 prefill chunk (B = 4, 16 KV heads, 2048 rows, head_dim 128: 16.8M values per
+    tensor) through the fused K/V launch: enough quotients land within a few ulp of a half-integer
+    to exercise the exact-division path."""
+    print(f"quantize C5 chunk dtype={dtype}", flush=True)
+    B, H, L, D = 4, 16, 2048, 128
+    kx = seeded_normal((B, H, L, D), 77, dtype, DEV)
+    vx = seeded_normal((B, H, L, D), 78, dtype, DEV) * 3.0
+    kd = _alloc(B, H, L + 16, D, 8, 64, dtype)
+    vd = _alloc(B, H, L + 16, D, 8, 64, dtype)
+    kernels.quantize_append(kx, kd, vx, vd, row_offset=16, group_size=64, bits=8)
+    _check_rows(kx, kd, 16, 8, 64)
+    _check_rows(vx, vd, 16, 8, 64)
+
+
 def test_quantize_counterpart_of_mx_quantize():
     x = seeded_normal((3, 5, 256), 31, torch.float16, DEV)
     c, s, b = kernels.quantize(x, 64, 4)
