@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define KVQ_ABI_VERSION 5
+#define KVQ_ABI_VERSION 6
 
 /* Element types of queries, K/V rows, outputs, scales and biases. */
 #define KVQ_DTYPE_F16 0
@@ -182,6 +182,48 @@ int kvq_decode_attn_static(const kvq_rows* q, const kvq_qtensor* k, const kvq_qt
                            int B, int Hq, int Hkv, int L, int D, int S,
                            int bits, int group_size, int dtype,
                            float scale, int causal, int window, void* stream);
+
+/*
+ * A general attention mask: element (b, kvh, j, l, key) of the [B][Hkv][Hq / Hkv][L][S] score
+ * layout the reference's GQA reshape uses (query head h = kvh * (Hq / Hkv) + j) sits at
+ *   data + b * stride_b + kvh * stride_kvh + j * stride_rep + l * stride_l + key
+ * (strides in elements; 0 broadcasts a dimension; keys are contiguous).
+ *   KVQ_MASK_BOOL: uint8, nonzero = the key is visible (the reference's boolean masks);
+ *   KVQ_MASK_F16 / _BF16 / _F32: additive, added to scale * q.k before the softmax.
+ * A row that sees no key returns 0 (the reference's blocked path does the same).
+ */
+#define KVQ_MASK_BOOL 1
+#define KVQ_MASK_F16 2
+#define KVQ_MASK_BF16 3
+#define KVQ_MASK_F32 4
+typedef struct kvq_mask {
+  const void* data;
+  int32_t kind; /* KVQ_MASK_* */
+  int64_t stride_b, stride_kvh, stride_rep, stride_l;
+} kvq_mask;
+
+/*
+ * kvq_decode_attn (any L) under a general mask instead of causal / window / seq_lens: boolean
+ * masks that are not causal, sliding-window or right-padding masks, per-head masks and additive
+ * masks. Replaces: m5engine/attention.py:55-56 and :76-80 (the array-mask branches of the
+ * blocked loop) and the mask handling of the L == 1 hand-off at :42-45. The decode kernel reads
+ * the mask beside each 32-key tile; rows beyond one pass take more passes over the keys, so long
+ * prompts under such masks run at the decode kernel's rate. Same requirements and workspace
+ * (kvq_decode_workspace_size with window 0) as kvq_decode_attn.
+ */
+int kvq_decode_attn_masked(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v,
+                           const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S,
+                           int bits, int group_size, int dtype, float scale, const kvq_mask* mask,
+                           void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * The same over an unquantized cache (kvq_decode_attn_dense's arguments; D in {64, 128}).
+ * Replaces the mask handling of mx.fast.scaled_dot_product_attention for array masks.
+ */
+int kvq_decode_attn_dense_masked(const kvq_rows* q, const kvq_rows* k, const kvq_rows* v,
+                                 const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S,
+                                 int dtype, float scale, const kvq_mask* mask,
+                                 void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Attention for prefill chunks (any L): same contract as kvq_decode_attn, MFMA tiles with

@@ -16,7 +16,7 @@ import torch  # noqa: F401  (binds the HIP runtime before libkvq.so is loaded)
 
 # The in-tree build, the only library this package loads.
 LIB_PATH = Path(__file__).resolve().parent / "libkvq.so"
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 DTYPE_F16 = 0
 DTYPE_BF16 = 1
@@ -86,6 +86,33 @@ _PAGED_ATTN_ARGS = [
 ]
 
 
+MASK_BOOL, MASK_F16, MASK_BF16, MASK_F32 = 1, 2, 3, 4  # KVQ_MASK_*
+
+
+class Mask(ctypes.Structure):
+    """kvq_mask: a general mask over the [B][Hkv][Hq / Hkv][L][S] score layout (keys contiguous;
+    strides in elements, 0 broadcasts)."""
+
+    _fields_ = [("data", c_void_p), ("kind", ctypes.c_int32), ("stride_b", c_int64), ("stride_kvh", c_int64),
+                ("stride_rep", c_int64), ("stride_l", c_int64)]
+
+
+_MASKED_ARGS = [
+    POINTER(Rows), POINTER(QTensor), POINTER(QTensor), POINTER(Rows),
+    c_int, c_int, c_int, c_int, c_int, c_int,  # B Hq Hkv L D S
+    c_int, c_int, c_int,  # bits group dtype
+    c_float, POINTER(Mask),  # scale mask
+    c_void_p, c_size_t, c_void_p,  # workspace bytes stream
+]
+_DENSE_MASKED_ARGS = [
+    POINTER(Rows), POINTER(Rows), POINTER(Rows), POINTER(Rows),
+    c_int, c_int, c_int, c_int, c_int, c_int,  # B Hq Hkv L D S
+    c_int,  # dtype
+    c_float, POINTER(Mask),  # scale mask
+    c_void_p, c_size_t, c_void_p,  # workspace bytes stream
+]
+
+
 class RadixInfo(ctypes.Structure):
     """kvq_radix_info: counters of a radix prefix cache."""
 
@@ -108,6 +135,8 @@ SIGNATURES = {
     ),
     "kvq_decode_attn": (c_int, _ATTN_ARGS),
     "kvq_decode_attn_static": (c_int, _ATTN_ARGS[:-3] + [c_void_p]),  # no workspace: the library's scratch
+    "kvq_decode_attn_masked": (c_int, _MASKED_ARGS),
+    "kvq_decode_attn_dense_masked": (c_int, _DENSE_MASKED_ARGS),
     "kvq_paged_quantize_append": (
         c_int,
         [POINTER(Rows), POINTER(QTensor), POINTER(Rows), POINTER(QTensor), c_int, c_void_p, c_int64, c_void_p, c_int64,

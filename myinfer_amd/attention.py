@@ -28,10 +28,12 @@ over torch tensors in MLX layout on the GPU, executed by libkvq.so's HIP kernels
 Masks (the reference accepts None, a string, or an array):
   None                  every cached key is visible
   any str               causal, queries at positions S - L .. S - 1 (reference :55-58)
-  bool tensor           recognised when it is a causal mask, a causal sliding window, or either
-                        with right padding per batch row (keys >= S_b masked); anything else
-                        raises NotImplementedError
-  additive float        all-zero only; anything else raises NotImplementedError
+  bool tensor           a causal mask, a causal sliding window, or either with right padding per
+                        batch row (keys >= S_b masked), is recognised and runs as that structure;
+                        any other boolean mask (per-head masks included) is read by the kernel
+  additive float        all-zero runs unmasked; any other is added to the scores by the kernel
+General masks (kernels.masked_attention) run on the decode kernel for any L, broadcast as the
+reference broadcasts them on the same path; a row that sees no key returns 0.
 Keyword extensions: ``window=`` (sliding window) and ``seq_lens=`` (int32 [B] valid key counts)
 give the same structure without building a mask.
 """
@@ -101,13 +103,20 @@ def mask_structure(mask, B: int, n_q_heads: int, L: int, S: int, device=None):
     if versioned:
         hit = _mask_cache.get(id(mask))
         if hit is not None and hit[0]() is mask and hit[1] == mask._version and hit[2] == key:
+            if isinstance(hit[3], NotImplementedError):
+                raise NotImplementedError(str(hit[3]))
             return hit[3]
-    causal, window, seq = _analyse_mask(mask.detach().cpu(), B, n_q_heads, L, S)
-    res = (causal, window, None if seq is None else seq.to(device))
+    try:
+        causal, window, seq = _analyse_mask(mask.detach().cpu(), B, n_q_heads, L, S)
+        res = (causal, window, None if seq is None else seq.to(device))
+    except NotImplementedError as e:
+        res = e  # remembered too: the layers of a forward pass do not analyse a general mask again
     if versioned:
         if len(_mask_cache) > 64:
             _mask_cache.clear()
         _mask_cache[id(mask)] = (weakref.ref(mask), mask._version, key, res)
+    if isinstance(res, NotImplementedError):
+        raise NotImplementedError(str(res))
     return res
 
 
@@ -158,7 +167,16 @@ def blocked_quantized_sdpa(queries: torch.Tensor, q_keys, q_values, scale: float
     """
     B, n_q_heads, L, D = queries.shape
     S = q_keys[0].shape[-2]
-    causal, window, seq_lens = _resolve_mask(mask, B, n_q_heads, L, S, window, seq_lens, queries.device)
+    try:
+        causal, window, seq_lens = _resolve_mask(mask, B, n_q_heads, L, S, window, seq_lens, queries.device)
+    except NotImplementedError:
+        if window or seq_lens is not None:
+            raise
+        # a general mask, broadcast as the reference does: a rank >= 3 mask gains a KV-head axis
+        # before it meets the grouped [B, Hkv, rep, L, S] scores, in the blocked loop (:55-56) and in
+        # the hand-off to mlx-lm's quantized SDPA (:42-45) alike
+        return kernels.masked_attention(queries, tuple(q_keys), tuple(q_values), scale, mask, layout="blocked",
+                                        group_size=group_size, bits=bits)
     return kernels.attention(queries, tuple(q_keys), tuple(q_values), scale, causal=causal, window=window,
                              seq_lens=seq_lens, group_size=group_size, bits=bits)
 
@@ -189,7 +207,13 @@ def fast_scaled_dot_product_attention(queries: torch.Tensor, keys: torch.Tensor,
     """
     B, n_q_heads, L, D = queries.shape
     S = keys.shape[-2]
-    causal, window, seq_lens = _resolve_mask(mask, B, n_q_heads, L, S, window, seq_lens, queries.device)
+    try:
+        causal, window, seq_lens = _resolve_mask(mask, B, n_q_heads, L, S, window, seq_lens, queries.device)
+    except NotImplementedError:
+        if window or seq_lens is not None:
+            raise
+        # a general mask broadcasts against the [B, Hq, L, S] scores, as mx.fast's does
+        return kernels.masked_attention(queries, keys, values, scale, mask, layout="heads")
     return kernels.attention(queries, keys, values, scale, causal=causal, window=window, seq_lens=seq_lens)
 
 

@@ -480,6 +480,44 @@ int kvq_decode_attn_dense(const kvq_rows* q, const kvq_rows* k, const kvq_rows* 
                     "decode_attn_dense launch");
 }
 
+// A general mask: a known kind, a pointer aligned to its element, non-negative strides (the key
+// stride is 1 by definition).
+static int check_mask(const kvq_mask* m) {
+  if (!m || !m->data) return fail(KVQ_ERR_INVALID, "mask and mask->data must not be NULL");
+  if (m->kind < KVQ_MASK_BOOL || m->kind > KVQ_MASK_F32) return fail(KVQ_ERR_INVALID, "unknown mask kind %d", m->kind);
+  const uintptr_t el = m->kind == KVQ_MASK_BOOL ? 1 : m->kind == KVQ_MASK_F32 ? 4 : 2;
+  if (!aligned(m->data, el)) return fail(KVQ_ERR_INVALID, "mask data is not aligned to its %zu-byte elements", (size_t)el);
+  if (m->stride_b < 0 || m->stride_kvh < 0 || m->stride_rep < 0 || m->stride_l < 0)
+    return fail(KVQ_ERR_INVALID, "mask strides must be non-negative");
+  return KVQ_OK;
+}
+
+int kvq_decode_attn_masked(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v, const kvq_rows* out, int B,
+                           int Hq, int Hkv, int L, int D, int S, int bits, int group_size, int dtype, float scale,
+                           const kvq_mask* mask, void* workspace, size_t workspace_bytes, void* stream) {
+  if (D != 64 && D != 128 && D != 256)
+    return fail(KVQ_ERR_UNSUPPORTED, "decode supports head_dim 64, 128 and 256, got %d", D);
+  int rc = check_attn(q, k, v, out, B, Hq, Hkv, L, D, S, bits, group_size, dtype, scale, 0,
+                      kvq_decode_workspace_size(B, Hq, Hkv, L, D, S, 0), workspace, workspace_bytes);
+  if (rc || (rc = check_mask(mask))) return rc;
+  return hip_status(kvq::launch_decode(q, k, v, nullptr, out, B, Hq, Hkv, L, D, S, bits, group_size, dtype, scale, 0, 0,
+                                       workspace, (hipStream_t)stream, mask),
+                    "decode_attn_masked launch");
+}
+
+int kvq_decode_attn_dense_masked(const kvq_rows* q, const kvq_rows* k, const kvq_rows* v, const kvq_rows* out, int B,
+                                 int Hq, int Hkv, int L, int D, int S, int dtype, float scale, const kvq_mask* mask,
+                                 void* workspace, size_t workspace_bytes, void* stream) {
+  if (D != 64 && D != 128)
+    return fail(KVQ_ERR_UNSUPPORTED, "masked unquantized attention supports head_dim 64 and 128, got %d", D);
+  int rc = check_attn_dense(q, k, v, out, B, Hq, Hkv, L, D, S, dtype, scale, 0,
+                            kvq_decode_workspace_size(B, Hq, Hkv, L, D, S, 0), workspace, workspace_bytes);
+  if (rc || (rc = check_mask(mask))) return rc;
+  return hip_status(kvq::launch_decode_dense(q, k, v, nullptr, out, B, Hq, Hkv, L, D, S, dtype, scale, 0, 0, workspace,
+                                             (hipStream_t)stream, mask),
+                    "decode_attn_dense_masked launch");
+}
+
 int kvq_prefill_attn_dense(const kvq_rows* q, const kvq_rows* k, const kvq_rows* v, const int32_t* seq_lens,
                            const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int dtype, float scale,
                            int causal, int window, void* workspace, size_t workspace_bytes, void* stream) {

@@ -114,7 +114,38 @@ struct DecParams {
   const int32_t* table;
   int64_t table_stride;
   int num_pages;
+  // general mask (kvq_mask): kind 0 = none; otherwise every tile is masked element by element
+  const void* mask;
+  int mask_kind;
+  int64_t m_sb, m_skv, m_srep, m_sl;
 };
+
+// A general mask (kvq_mask) on the lane's 8 scores of a tile (keys k0 + 16 (s / 4) + 4 lg + s % 4 of
+// query row (b, kvh, j, l), log2 units): a boolean mask sends hidden keys to -inf, an additive one
+// adds its value times log2(e). Keys outside [lo, hi) are already -inf and are not read.
+__device__ __forceinline__ void apply_mask(const DecParams& p, int b, int kvh, int j, int l, int k0, int lg, int lo, int hi,
+                                        float (&sc)[8]) {
+  const int64_t row = (int64_t)b * p.m_sb + (int64_t)kvh * p.m_skv + (int64_t)j * p.m_srep + (int64_t)l * p.m_sl;
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {
+    const int t = k0 + 16 * (s >> 2) + 4 * lg + (s & 3);
+    if (!(t >= lo && t < hi)) continue;
+    const int64_t i = row + t;
+    if (p.mask_kind == KVQ_MASK_BOOL) {
+      if (((const uint8_t*)p.mask)[i] == 0) sc[s] = -INFINITY;
+    } else {
+      float a;
+      if (p.mask_kind == KVQ_MASK_F32) {
+        a = ((const float*)p.mask)[i];
+      } else if (p.mask_kind == KVQ_MASK_BF16) {
+        a = to_float(((const uint16_t*)p.mask)[i], BF16{});
+      } else {
+        a = to_float(((const uint16_t*)p.mask)[i], F16{});
+      }
+      sc[s] += a * 1.4426950408889634f;
+    }
+  }
+}
 
 // Token (relative to the tile) of V slot i' (the MFMA k index 8*lg + i') for lane group lg.
 __device__ __forceinline__ int v_token(int lg, int i) { return (i < 4) ? 4 * lg + i : 16 + 4 * lg + (i - 4); }
@@ -447,7 +478,9 @@ constexpr int dec_min_wgs() {
   return (NW == 4 && 2 * NW * NSLOT * DecCfg<D, BITS, G>::SLOT <= 160 * 1024) ? 2 : 1;
 }
 
-template <typename T, int D, int BITS, int NW, int NSLOT, bool PAGED = false, int G = 64>
+// MASKED: compiled with a general mask (kvq_mask) read beside every tile; the other instantiations
+// carry no trace of it.
+template <typename T, int D, int BITS, int NW, int NSLOT, bool PAGED = false, int G = 64, bool MASKED = false>
 __global__ __launch_bounds__(NW * 64, (dec_min_wgs<D, BITS, NW, NSLOT, G>())) void decode_attn_kernel(DecParams p) {
   using C = DecCfg<D, BITS, G>;
   constexpr int R = C::R;
@@ -733,12 +766,15 @@ __global__ __launch_bounds__(NW * 64, (dec_min_wgs<D, BITS, NW, NSLOT, G>())) vo
           sc[4 * beta + i] = x;
         }
     }
-    const bool need_mask = !(k0 >= lo_all && k0 + kTile <= hi_all);
+    const bool need_mask = MASKED || !(k0 >= lo_all && k0 + kTile <= hi_all);
     if (need_mask) {
 #pragma unroll
       for (int s = 0; s < 8; ++s) {
         const int t = k0 + 16 * (s >> 2) + 4 * lg + (s & 3);
         if (!(t >= lo_r && t < hi_r)) sc[s] = -INFINITY;
+      }
+      if constexpr (MASKED) {
+        if (row_ok) apply_mask(p, b, kvh, hq - kvh * p.rep, lq, k0, lg, lo_r, hi_r, sc);
       }
     }
     float tm = sc[0];
@@ -1102,8 +1138,17 @@ size_t decode_workspace_bytes(int B, int Hq, int Hkv, int L, int D, int S, int w
 
 template <typename T, int D, int BITS, int NW, int NSLOT, bool PAGED = false, int G = 64>
 static hipError_t launch_decode_t(const DecParams& p, hipStream_t stream) {
-  hipLaunchKernelGGL((decode_attn_kernel<T, D, BITS, NW, NSLOT, PAGED, G>), dim3(p.nunits * p.nsplit), dim3(NW * 64), 0,
-                     stream, p);
+  if (p.mask_kind != 0) {
+    if constexpr (NW == 4 && NSLOT == 2 && !PAGED) {
+      hipLaunchKernelGGL((decode_attn_kernel<T, D, BITS, NW, NSLOT, PAGED, G, true>), dim3(p.nunits * p.nsplit),
+                         dim3(NW * 64), 0, stream, p);
+    } else {
+      return hipErrorInvalidValue;  // masked calls always take the default launch shape
+    }
+  } else {
+    hipLaunchKernelGGL((decode_attn_kernel<T, D, BITS, NW, NSLOT, PAGED, G>), dim3(p.nunits * p.nsplit), dim3(NW * 64),
+                       0, stream, p);
+  }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || p.nsplit == 1 || p.fused) return e;
   MergeParams m;
@@ -1126,6 +1171,7 @@ static hipError_t launch_decode_t(const DecParams& p, hipStream_t stream) {
 
 template <typename T, int D, int BITS, int G = 64>
 static hipError_t launch_decode_shape(const DecParams& p, const DecPlan& pl, hipStream_t stream) {
+  if (p.mask_kind != 0) return launch_decode_t<T, D, BITS, 4, 2, false, G>(p, stream);
   if constexpr (BITS == 16) {
     return launch_decode_t<T, D, BITS, 4, 2>(p, stream);  // a 3-slot ring of raw rows does not fit
   } else if constexpr (G != 64) {
@@ -1201,11 +1247,22 @@ static hipError_t dispatch_quant(int dtype, int D, int bits, int G, F&& f) {
   return dtype == KVQ_DTYPE_BF16 ? by_d(BF16{}) : by_d(F16{});
 }
 
+static void set_mask(DecParams& p, const kvq_mask* mask) {
+  if (!mask) return;
+  p.mask = mask->data;
+  p.mask_kind = mask->kind;
+  p.m_sb = mask->stride_b;
+  p.m_skv = mask->stride_kvh;
+  p.m_srep = mask->stride_rep;
+  p.m_sl = mask->stride_l;
+}
+
 hipError_t launch_decode(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v, const int32_t* seq_lens,
                          const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int bits, int G, int dtype,
-                         float scale, int causal, int window, void* workspace, hipStream_t stream) {
+                         float scale, int causal, int window, void* workspace, hipStream_t stream, const kvq_mask* mask) {
   const DecPlan pl = decode_plan(B, Hq, Hkv, L, D, S, window, bits, G);
   DecParams p = decode_params(q, seq_lens, out, Hq, Hkv, L, D, S, scale, causal, window, workspace, pl);
+  set_mask(p, mask);
   p.kc = (const uint8_t*)k->codes;
   p.vc = (const uint8_t*)v->codes;
   p.kc_sb = k->codes_stride_b * 4;
@@ -1263,9 +1320,10 @@ hipError_t launch_decode_paged(const kvq_rows* q, const kvq_qtensor* k, const kv
 
 hipError_t launch_decode_dense(const kvq_rows* q, const kvq_rows* k, const kvq_rows* v, const int32_t* seq_lens,
                                const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int dtype, float scale,
-                               int causal, int window, void* workspace, hipStream_t stream) {
+                               int causal, int window, void* workspace, hipStream_t stream, const kvq_mask* mask) {
   const DecPlan pl = decode_plan(B, Hq, Hkv, L, D, S, window, 16, 64);
   DecParams p = decode_params(q, seq_lens, out, Hq, Hkv, L, D, S, scale, causal, window, workspace, pl);
+  set_mask(p, mask);
   p.kc = (const uint8_t*)k->data;
   p.vc = (const uint8_t*)v->data;
   p.kc_sb = k->stride_b * 2;

@@ -20,9 +20,11 @@ hipError_t launch_paged_quantize_append(const kvq_rows* k_src, const kvq_qtensor
 hipError_t launch_rope(const kvq_rows* x, const kvq_rope_params* rope, int B, int H, int L, int dtype, hipStream_t stream);
 
 size_t decode_workspace_bytes(int B, int Hq, int Hkv, int L, int D, int S, int window, int bits, int G);
+// mask: a general mask (kvq_mask) or nullptr
 hipError_t launch_decode(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v, const int32_t* seq_lens,
                          const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int bits, int G, int dtype,
-                         float scale, int causal, int window, void* workspace, hipStream_t stream);
+                         float scale, int causal, int window, void* workspace, hipStream_t stream,
+                         const kvq_mask* mask = nullptr);
 
 hipError_t launch_decode_paged(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v, int num_pages,
                                const int32_t* table, int64_t table_stride, const int32_t* seq_lens, const kvq_rows* out,
@@ -30,7 +32,8 @@ hipError_t launch_decode_paged(const kvq_rows* q, const kvq_qtensor* k, const kv
                                int causal, int window, void* workspace, hipStream_t stream);
 hipError_t launch_decode_dense(const kvq_rows* q, const kvq_rows* k, const kvq_rows* v, const int32_t* seq_lens,
                                const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int dtype, float scale,
-                               int causal, int window, void* workspace, hipStream_t stream);
+                               int causal, int window, void* workspace, hipStream_t stream,
+                               const kvq_mask* mask = nullptr);
 
 size_t prefill_workspace_bytes(int B, int Hq, int Hkv, int L, int D, int S, int window, int bits);
 hipError_t launch_prefill(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v, const int32_t* seq_lens,

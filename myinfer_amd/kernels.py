@@ -465,6 +465,111 @@ def attention(queries: torch.Tensor, keys, values, scale: float, *, causal: bool
                              group_size=group_size, bits=bits, out=out, kernel=kernel, _one_shot=True)()
 
 
+# ---- general masks (kvq_mask): boolean masks with no causal / window / padding structure, per-head
+# masks and additive masks, read by the decode kernel beside every tile
+
+_MASK_KINDS = {torch.bool: _lib.MASK_BOOL, torch.float16: _lib.MASK_F16, torch.bfloat16: _lib.MASK_BF16,
+               torch.float32: _lib.MASK_F32}
+
+
+def mask_view(mask: torch.Tensor, B: int, Hq: int, Hkv: int, L: int, S: int, layout: str = "heads"):
+    """The mask as the kernels read it: (tensor, (stride_b, stride_kvh, stride_rep, stride_l)) over the
+    [B, Hkv, Hq / Hkv, L, S] score layout, keys contiguous, broadcast dimensions at stride 0.
+
+    ``layout`` is how the caller's reference broadcasts the mask against the scores:
+      "heads"    against [B, Hq, L, S] (mx.fast.scaled_dot_product_attention);
+      "grouped"  against [B, Hkv, Hq / Hkv, L, S] as given (mlx-lm's quantized SDPA, the L == 1 /
+                 short-S hand-off of m5engine/attention.py:42-45);
+      "blocked"  a mask of rank 3 or more gains an axis at -3 first (m5engine/attention.py:55-56),
+                 so its head axis indexes KV heads.
+    With Hq == Hkv the three agree."""
+    if layout not in ("heads", "grouped", "blocked"):
+        raise ValueError(f"layout must be 'heads', 'grouped' or 'blocked', got {layout!r}")
+    m = mask
+    if m.dtype == torch.float64:
+        m = m.float()
+    if m.dtype not in _MASK_KINDS:
+        raise ValueError(f"masks are bool (visible keys) or float (additive), got {m.dtype}")
+    if m.dim() == 0 or m.shape[-1] not in (1, S):
+        raise ValueError(f"the mask's last dimension {tuple(m.shape)[-1:]} does not broadcast to S = {S}")
+    if m.shape[-1] == 1 and S != 1:
+        m = m.expand(*m.shape[:-1], S)
+    if m.stride(-1) != 1:
+        m = m.contiguous()
+    rep = Hq // Hkv
+    try:
+        if rep == 1 or layout == "heads":
+            m4 = torch.broadcast_to(m, (B, Hq, L, S))
+            sb, sh, sl, _ = m4.stride()
+            return m4, (sb, rep * sh, sh, sl)
+        if layout == "blocked" and m.dim() >= 3:
+            m = m.unsqueeze(-3)
+        m5 = torch.broadcast_to(m, (B, Hkv, rep, L, S))
+    except RuntimeError as e:
+        raise ValueError(f"mask of shape {tuple(mask.shape)} does not broadcast to the scores: {e}") from None
+    sb, skv, srep, sl, _ = m5.stride()
+    return m5, (sb, skv, srep, sl)
+
+
+def masked_attention(queries: torch.Tensor, keys, values, scale: float, mask: torch.Tensor, *, layout: str = "heads",
+                     group_size: int = 64, bits: int = 8, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """softmax(scale * q K^T + mask) V under a general mask (boolean: visible keys; float: added to
+    the scores), keys/values quantized triples or unquantized tensors as for ``attention``. Runs the
+    decode kernel (any L: rows beyond one pass take more passes over the keys). A row that sees no
+    key returns 0. Unquantized caches at head_dim 256 are not supported."""
+    if queries.dim() != 4:
+        raise ValueError(f"queries must be [B, Hq, L, D], got {tuple(queries.shape)}")
+    B, Hq, L, D = queries.shape
+    dense = torch.is_tensor(keys)
+    if dense:
+        dev = _require_cuda(queries, keys, values)
+        Hkv, S = keys.shape[1], keys.shape[2]
+        for name, t in (("keys", keys), ("values", values)):
+            if t.dim() != 4 or tuple(t.shape) != (B, Hkv, S, D) or t.dtype != queries.dtype:
+                raise ValueError(f"{name} must be {queries.dtype} [B, Hkv, S, D] = {(B, Hkv, S, D)}")
+        if D == 256:
+            raise NotImplementedError("general masks over an unquantized head_dim-256 cache are not supported")
+        keys = keys if _rows_ok(keys) else keys.contiguous()
+        values = values if _rows_ok(values) else values.contiguous()
+    else:
+        _check_triple(keys, "keys")
+        _check_triple(values, "values")
+        dev = _require_cuda(queries, *keys, *values)
+        Hkv, S = keys[0].shape[1], keys[0].shape[2]
+        if keys[0].shape[0] != B or keys[0].shape[3] * 32 // bits != D or keys[1].shape[3] * group_size != D:
+            raise ValueError("keys triple does not match the queries' B and D at these bits and group_size")
+    if Hq % Hkv:
+        raise ValueError(f"Hq={Hq} is not a multiple of Hkv={Hkv}")
+    if not torch.is_tensor(mask):
+        raise ValueError("mask must be a tensor")
+    if mask.device != dev:
+        mask = mask.to(dev)
+    mview, strides = mask_view(mask, B, Hq, Hkv, L, S, layout)
+    desc = _lib.Mask(mview.data_ptr(), _MASK_KINDS[mview.dtype], *strides)
+    if not _rows_ok(queries):
+        queries = queries.contiguous()
+    out = _check_out(out, queries, dev)
+    lib = _lib.lib()
+    nbytes = lib.kvq_decode_workspace_size(B, Hq, Hkv, L, D, S, 0)
+    if nbytes == 0:
+        raise NotImplementedError(f"decode attention does not support B={B} Hq={Hq} Hkv={Hkv} L={L} D={D} S={S}")
+    stream = _lib.stream_ptr(dev)
+    ws = _workspace(dev, stream, nbytes)
+    qr, orr = _lib.rows(queries), _lib.rows(out)
+    tail = (float(scale), ctypes.byref(desc), ws.data_ptr(), ws.numel() * ws.element_size(), stream)
+    if dense:
+        kr, vr = _lib.rows(keys), _lib.rows(values)
+        rc = lib.kvq_decode_attn_dense_masked(ctypes.byref(qr), ctypes.byref(kr), ctypes.byref(vr), ctypes.byref(orr),
+                                              B, Hq, Hkv, L, D, S, _lib.dtype_code(queries.dtype), *tail)
+        _lib.check(rc, "kvq_decode_attn_dense_masked")
+    else:
+        kq, vq = _lib.qtensor(*keys), _lib.qtensor(*values)
+        rc = lib.kvq_decode_attn_masked(ctypes.byref(qr), ctypes.byref(kq), ctypes.byref(vq), ctypes.byref(orr), B, Hq,
+                                        Hkv, L, D, S, int(bits), int(group_size), _lib.dtype_code(queries.dtype), *tail)
+        _lib.check(rc, "kvq_decode_attn_masked")
+    return out
+
+
 # ---- paged pools (64-row pages; include/kvq.h "Paged layout")
 
 PAGE_ROWS = _lib.PAGE_ROWS

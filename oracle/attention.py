@@ -42,13 +42,19 @@ def key_mask(L: int, S: int, S_b: int, causal: bool, window: int) -> np.ndarray:
 
 
 def exact_attention(q: np.ndarray, kdq: np.ndarray, vdq: np.ndarray, scale: float, *, causal: bool = False,
-                    window: int = 0, seq_lens=None) -> np.ndarray:
+                    window: int = 0, seq_lens=None, vis=None, add=None) -> np.ndarray:
     """fp64 attention. q [B, Hq, L, D]; kdq/vdq dequantized [B, Hkv, S, D]. Rows with no visible
-    key return 0 (the value the reference's blocked path yields: acc / max(denom, 1e-30))."""
+    key return 0 (the value the reference's blocked path yields: acc / max(denom, 1e-30)).
+
+    General masks, per query head (m5engine/attention.py:76-80 after its GQA broadcast): vis, a
+    boolean array broadcastable to [B, Hq, L, S] (False hides the key, :77-78 and :81-82); add, an
+    array broadcastable to [B, Hq, L, S] added to scale * q.k (:79-80)."""
     q = np.asarray(q, np.float64)
     B, Hq, L, D = q.shape
     Hkv, S = kdq.shape[1], kdq.shape[2]
     rep = Hq // Hkv
+    vis = None if vis is None else np.broadcast_to(np.asarray(vis, bool), (B, Hq, L, S))
+    add = None if add is None else np.broadcast_to(np.asarray(add, np.float64), (B, Hq, L, S))
     out = np.zeros((B, Hq, L, vdq.shape[-1]), np.float64)
     for b in range(B):
         S_b = S if seq_lens is None else int(seq_lens[b])
@@ -60,6 +66,10 @@ def exact_attention(q: np.ndarray, kdq: np.ndarray, vdq: np.ndarray, scale: floa
             s = (qg @ K.T) * scale
             s = s.reshape(rep, L, S_b)
             s = np.where(m[None], s, -np.inf)
+            if vis is not None:
+                s = np.where(vis[b, h * rep:(h + 1) * rep, :, :S_b], s, -np.inf)
+            if add is not None:
+                s = s + add[b, h * rep:(h + 1) * rep, :, :S_b]
             mx = s.max(axis=-1, keepdims=True)
             mx = np.where(np.isfinite(mx), mx, 0.0)
             p = np.exp(s - mx)
