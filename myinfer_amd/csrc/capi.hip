@@ -508,11 +508,15 @@ int kvq_decode_attn_masked(const kvq_rows* q, const kvq_qtensor* k, const kvq_qt
 int kvq_decode_attn_dense_masked(const kvq_rows* q, const kvq_rows* k, const kvq_rows* v, const kvq_rows* out, int B,
                                  int Hq, int Hkv, int L, int D, int S, int dtype, float scale, const kvq_mask* mask,
                                  void* workspace, size_t workspace_bytes, void* stream) {
-  if (D != 64 && D != 128)
-    return fail(KVQ_ERR_UNSUPPORTED, "masked unquantized attention supports head_dim 64 and 128, got %d", D);
+  if (D != 64 && D != 128 && D != 256)
+    return fail(KVQ_ERR_UNSUPPORTED, "masked unquantized attention supports head_dim 64, 128 and 256, got %d", D);
   int rc = check_attn_dense(q, k, v, out, B, Hq, Hkv, L, D, S, dtype, scale, 0,
                             kvq_decode_workspace_size(B, Hq, Hkv, L, D, S, 0), workspace, workspace_bytes);
   if (rc || (rc = check_mask(mask))) return rc;
+  if (D == 256)  // the unquantized cache at head_dim 256 runs through the head_dim-256 kernel
+    return hip_status(kvq::launch_wide_dense(q, k, v, nullptr, out, B, Hq, Hkv, L, D, S, dtype, scale, 0, 0, workspace,
+                                             (hipStream_t)stream, mask),
+                      "decode_attn_dense_masked launch (head_dim 256)");
   return hip_status(kvq::launch_decode_dense(q, k, v, nullptr, out, B, Hq, Hkv, L, D, S, dtype, scale, 0, 0, workspace,
                                              (hipStream_t)stream, mask),
                     "decode_attn_dense_masked launch");

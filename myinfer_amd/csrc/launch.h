@@ -55,7 +55,8 @@ hipError_t launch_wide_paged(const kvq_rows* q, const kvq_qtensor* k, const kvq_
                              int window, void* workspace, hipStream_t stream);
 hipError_t launch_wide_dense(const kvq_rows* q, const kvq_rows* k, const kvq_rows* v, const int32_t* seq_lens,
                              const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int dtype, float scale,
-                             int causal, int window, void* workspace, hipStream_t stream);
+                             int causal, int window, void* workspace, hipStream_t stream,
+                             const kvq_mask* mask = nullptr);
 hipError_t launch_prefill_dense(const kvq_rows* q, const kvq_rows* k, const kvq_rows* v, const int32_t* seq_lens,
                                 const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int dtype,
                                 float scale, int causal, int window, void* workspace, hipStream_t stream);

@@ -112,7 +112,39 @@ struct WideParams {
   // times 2^-E, and 2^E returns in the score scale (K) and the output (V)
   const int32_t* k_rexp;
   const int32_t* v_rexp;
+  // general mask (kvq_mask, MASKED kernels): kind 0 = none
+  const void* mask;
+  int mask_kind;
+  int64_t m_sb, m_skv, m_srep, m_sl;
 };
+
+// A general mask (kvq_mask) on the lane's 16 scores of a tile (keys k0 + 8 (i / 4) + 4 h + i % 4 of
+// query row (b, kvh, j, l)), in the raw product units the kernel scales by kf later: a boolean mask
+// sends hidden keys to -inf, an additive one adds its value times log2(e) / kf. Keys outside
+// [lo, hi) are already -inf and are not read.
+__device__ __forceinline__ void wide_apply_mask(const WideParams& p, int b, int kvh, int j, int l, int k0, int h, int lo,
+                                                int hi, float add_scale, float (&s)[16]) {
+  const int64_t row = (int64_t)b * p.m_sb + (int64_t)kvh * p.m_skv + (int64_t)j * p.m_srep + (int64_t)l * p.m_sl;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int k = k0 + 8 * (i >> 2) + 4 * h + (i & 3);
+    if (k < lo || k >= hi) continue;
+    const int64_t e = row + k;
+    if (p.mask_kind == KVQ_MASK_BOOL) {
+      if (((const uint8_t*)p.mask)[e] == 0) s[i] = -INFINITY;
+    } else {
+      float a;
+      if (p.mask_kind == KVQ_MASK_F32) {
+        a = ((const float*)p.mask)[e];
+      } else if (p.mask_kind == KVQ_MASK_BF16) {
+        a = to_float(((const uint16_t*)p.mask)[e], BF16{});
+      } else {
+        a = to_float(((const uint16_t*)p.mask)[e], F16{});
+      }
+      s[i] += a * add_scale;
+    }
+  }
+}
 
 // The key held in V^T slot 8 c + e (c = 0..3, e = 0..7): PV k-step c / 2 takes, in lane half c % 2,
 // the probabilities the score layout gives that half as its values 8 (c / 2) + e, which are keys
@@ -260,7 +292,9 @@ __device__ __forceinline__ void wide_stage_v(const uint8_t* raw, uint8_t* vop, i
   }
 }
 
-template <typename T, int D, int BITS, int G, bool PAGED = false>
+// MASKED: compiled with a general mask (kvq_mask) read beside every tile; the other instantiations
+// carry no trace of it.
+template <typename T, int D, int BITS, int G, bool PAGED = false, bool MASKED = false>
 __global__ __launch_bounds__(kWW * 64, 1) void wide_attn_kernel(WideParams p) {
   using C = WideCfg<D, BITS, G>;
   static_assert(!PAGED || !C::DENSE, "paged pools hold quantized caches");
@@ -463,11 +497,19 @@ __global__ __launch_bounds__(kWW * 64, 1) void wide_attn_kernel(WideParams p) {
       if (j + KR < C::KSTEPS) ka[j % KR] = *(const u4*)(kt + k_off + 32 * (j + KR));
     }
     // value i of the lane is key k0 + 8 (i / 4) + 4 h + i % 4 of query row n
-    if (!(k0 >= lo_all && k0 + kWT <= hi_all)) {
+    if (MASKED || !(k0 >= lo_all && k0 + kWT <= hi_all)) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int k = k0 + 8 * (i >> 2) + 4 * h + (i & 3);
         if (k < lo_r || k >= hi_r) s[i] = -INFINITY;
+      }
+      if constexpr (MASKED) {
+        float sv[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) sv[i] = s[i];
+        if (row_ok) wide_apply_mask(p, b, kvh, hq - kvh * p.rep, lq, k0, h, lo_r, hi_r, 1.4426950408889634f / kf, sv);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) s[i] = sv[i];
       }
     }
     float tm = s[0];
@@ -621,7 +663,17 @@ size_t wide_workspace_bytes(int B, int Hq, int Hkv, int L, int D, int S, int win
 
 template <typename T, int D, int BITS, int G, bool PAGED = false>
 static hipError_t launch_wide_t(const WideParams& p, hipStream_t stream) {
-  hipLaunchKernelGGL((wide_attn_kernel<T, D, BITS, G, PAGED>), dim3(p.nunits * p.nsplit), dim3(kWW * 64), 0, stream, p);
+  if (p.mask_kind != 0) {
+    if constexpr (D == 256 && BITS == 16 && !PAGED) {
+      hipLaunchKernelGGL((wide_attn_kernel<T, D, BITS, G, PAGED, true>), dim3(p.nunits * p.nsplit), dim3(kWW * 64), 0,
+                         stream, p);
+    } else {
+      return hipErrorInvalidValue;  // general masks: the unquantized head_dim-256 cache only
+    }
+  } else {
+    hipLaunchKernelGGL((wide_attn_kernel<T, D, BITS, G, PAGED>), dim3(p.nunits * p.nsplit), dim3(kWW * 64), 0, stream,
+                       p);
+  }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || p.nsplit == 1) return e;
   MergeParams m;
@@ -732,8 +784,16 @@ hipError_t launch_wide_paged(const kvq_rows* q, const kvq_qtensor* k, const kvq_
 
 hipError_t launch_wide_dense(const kvq_rows* q, const kvq_rows* k, const kvq_rows* v, const int32_t* seq_lens,
                              const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int dtype, float scale,
-                             int causal, int window, void* workspace, hipStream_t stream) {
+                             int causal, int window, void* workspace, hipStream_t stream, const kvq_mask* mask) {
   WideParams p = wide_params(q, seq_lens, out, B, Hq, Hkv, L, S, scale, causal, window, workspace);
+  if (mask) {
+    p.mask = mask->data;
+    p.mask_kind = mask->kind;
+    p.m_sb = mask->stride_b;
+    p.m_skv = mask->stride_kvh;
+    p.m_srep = mask->stride_rep;
+    p.m_sl = mask->stride_l;
+  }
   p.kc = (const uint8_t*)k->data;
   p.vc = (const uint8_t*)v->data;
   p.kc_sb = k->stride_b * 2;

@@ -515,8 +515,8 @@ def masked_attention(queries: torch.Tensor, keys, values, scale: float, mask: to
                      group_size: int = 64, bits: int = 8, out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """softmax(scale * q K^T + mask) V under a general mask (boolean: visible keys; float: added to
     the scores), keys/values quantized triples or unquantized tensors as for ``attention``. Runs the
-    decode kernel (any L: rows beyond one pass take more passes over the keys). A row that sees no
-    key returns 0. Unquantized caches at head_dim 256 are not supported."""
+    decode kernel (any L: rows beyond one pass take more passes over the keys), or, for an
+    unquantized head_dim-256 cache, the head_dim-256 kernel. A row that sees no key returns 0."""
     if queries.dim() != 4:
         raise ValueError(f"queries must be [B, Hq, L, D], got {tuple(queries.shape)}")
     B, Hq, L, D = queries.shape
@@ -527,8 +527,6 @@ def masked_attention(queries: torch.Tensor, keys, values, scale: float, mask: to
         for name, t in (("keys", keys), ("values", values)):
             if t.dim() != 4 or tuple(t.shape) != (B, Hkv, S, D) or t.dtype != queries.dtype:
                 raise ValueError(f"{name} must be {queries.dtype} [B, Hkv, S, D] = {(B, Hkv, S, D)}")
-        if D == 256:
-            raise NotImplementedError("general masks over an unquantized head_dim-256 cache are not supported")
         keys = keys if _rows_ok(keys) else keys.contiguous()
         values = values if _rows_ok(values) else values.contiguous()
     else:

@@ -109,7 +109,7 @@ def test_fully_hidden_rows_return_zero():
     assert_close(out, _exact(q, kt, vt, 0.12, 8, 64, vis=m.numpy()), "fully hidden rows")
 
 
-@pytest.mark.parametrize("D,dtype", [(128, torch.float16), (64, torch.bfloat16)])
+@pytest.mark.parametrize("D,dtype", [(128, torch.float16), (64, torch.bfloat16), (256, torch.bfloat16)])
 def test_unquantized_per_query_head_mask(D, dtype):
     """mx.fast's layout: a [B, Hq, L, S] mask is per query head."""
     print(f"masked dense D={D} {dtype}", flush=True)
@@ -138,3 +138,25 @@ def test_structured_masks_still_take_the_structured_path(monkeypatch):
     out = A.blocked_quantized_sdpa(q, kt, vt, 0.09, causal.to(DEV), group_size=64, bits=8)
     assert not calls
     assert_close(out, _exact(q, kt, vt, 0.09, 8, 64, vis=causal.numpy()), "causal bool mask")
+
+
+@pytest.mark.parametrize("L,S", [(1, 2048), (40, 700)])
+def test_unquantized_head_dim_256_additive_mask(L, S):
+    """The unquantized head_dim-256 cache runs through the head_dim-256 kernel: an additive mask with
+    -inf entries, per query head, at decode and prefill lengths."""
+    print(f"masked dense D=256 additive L={L} S={S}", flush=True)
+    B, Hq, Hkv, D = 2, 8, 4, 256
+    dtype = torch.bfloat16
+    k = seeded_normal((B, Hkv, S, D), 970, dtype, DEV)
+    v = seeded_normal((B, Hkv, S, D), 971, dtype, DEV)
+    q = seeded_normal((B, Hq, L, D), 972, dtype, DEV)
+    g = torch.Generator().manual_seed(973)
+    add = torch.rand(B, Hq, L, S, generator=g) * 4.0 - 2.0
+    add[:, :, :, 50:90] = float("-inf")
+    scale = 1.0 / math.sqrt(D)
+    out = A.fast_scaled_dot_product_attention(q, k, v, scale, add.to(DEV))
+    kn = k.cpu().float().numpy().astype(np.float64)
+    vn = v.cpu().float().numpy().astype(np.float64)
+    qn = q.cpu().float().numpy().astype(np.float64)
+    ref = OA.exact_attention(qn, kn, vn, scale, add=add.numpy().astype(np.float64))
+    assert_close(out, ref, f"dense D=256 additive L={L}")
