@@ -86,6 +86,9 @@ DECODE = {
                bits=8, dtype="float16", seed=1001),
     "C2-b8": dict(desc="Qwen3-32B decode attention, 8-bit KV, batch 8, S_b ~ U[16384, 32768]", B=8, Hq=64, Hkv=8,
                   D=128, S=32768, bits=8, dtype="float16", seed=1002, varlen=(16384, 32768)),
+    # one GPU's share of C2 at tensor parallelism 8 (each GPU owns one KV head and its 8 query heads)
+    "C2-tp8": dict(desc="Qwen3-32B decode attention at TP=8, one GPU's shard: 1 KV head, 8 query heads, 8-bit KV, 32K "
+                        "context, batch 8", B=8, Hq=8, Hkv=1, D=128, S=32768, bits=8, dtype="float16", seed=1008),
     "C4": dict(desc="Qwen3-32B decode attention, 4-bit KV, 131072 context, 1% K outlier channels x8", B=1, Hq=64,
                Hkv=8, D=128, S=131072, bits=4, dtype="float16", seed=1004, outliers=True),
     "C5-global": dict(desc="Gemma-3-27B decode step after 8192 prefill, global causal layer, batch 4", B=4, Hq=32,
@@ -1041,7 +1044,7 @@ def main():
         f"per call {res['call_us_mean']:.2f} us mean -> {res['kernel_gbs']:.1f} GB/s")
     extra = {}
     if not args.no_extra:
-        for name in ("C1", "C2-b8", "C4", "C5-global", "C5-window", "C5-window-dense"):
+        for name in ("C1", "C2-b8", "C2-tp8", "C4", "C5-global", "C5-window", "C5-window-dense"):
             cfg = DECODE[name]
             quantized = cfg["bits"] != 16
             r = time_decode(cfg, args.steps, args.warmup, device, want_parity=True)
