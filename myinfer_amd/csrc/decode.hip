@@ -457,7 +457,11 @@ __device__ __forceinline__ h8 v_operand(const Bytes<VB> (&vc)[8], int jN) {
 #pragma unroll
   for (int a = 0; a < 4; ++a) {
     uint32_t y = perm(vc[2 * a + 1].w[wi], vc[2 * a].w[wi], sel);
-    if constexpr (BITS == 4) y &= (jN & 1) ? 0x00F000F0u : 0x000F000Fu;
+    // 4 bits: an even block takes the byte's low nibble; an odd block takes the whole byte,
+    // lo + 16 hi, and the even block's sum is subtracted from it at the end (one AND fewer)
+    if constexpr (BITS == 4) {
+      if (!(jN & 1)) y &= 0x000F000Fu;
+    }
     r[a] = y;
   }
   return __builtin_bit_cast(h8, r);
@@ -896,9 +900,13 @@ __global__ __launch_bounds__(NW * 64, (dec_min_wgs<D, BITS, NW, NSLOT, G>())) vo
     if (m / R == n / R) {
 #pragma unroll
       for (int jn = 0; jn < C::NBLK; ++jn) {
-        float sc = C::DENSE ? 1.0f : 16777216.0f;
-        if constexpr (BITS == 4) sc = (jn & 1) ? 1048576.0f : 16777216.0f;
-        w_o[(wave * R + m % R) * D + (D / 16) * n + jn] = acc_o[jn][i] * sc + obi[i];
+        // codes entered the MFMA as fp16 subnormals c 2^-24; at 4 bits an odd block holds the sums
+        // over lo + 16 hi of its byte, so the hi nibbles' sum is (odd - even) / 16
+        float x = C::DENSE ? acc_o[jn][i] : acc_o[jn][i] * 16777216.0f;
+        if constexpr (BITS == 4) {
+          if (jn & 1) x = (acc_o[jn][i] - acc_o[jn - 1][i]) * 1048576.0f;
+        }
+        w_o[(wave * R + m % R) * D + (D / 16) * n + jn] = x + obi[i];
       }
     }
   }
