@@ -141,9 +141,13 @@ int kvq_rope_quantize_append(const kvq_rows* k_src, const kvq_qtensor* k_dst,
  * out = softmax(scale * q K^T + mask) V over the dequantized K/V.
  * Replaces: m5engine/attention.py:42-45 (the L == 1 hand-off to mlx-lm's
  * quantized_scaled_dot_product_attention) and, for L > 1, the blocked loop at :64-103.
- * Requirements: D in {64, 128, 256}; group_size in {32, 64, 128} with D / 4 <= group_size <= D;
- *   bits in {4, 8}. One pass of the kernel serves 16 * group_size / D query rows ((Hq / Hkv) * L)
- *   of a KV head; more rows take more passes over the keys.
+ * Requirements: D a multiple of 8 up to 256 and of group_size; group_size in {32, 64, 128} with
+ *   W / 4 <= group_size <= W, where W is the kernel width: D itself for D in {64, 128, 256}, else
+ *   the next of them (32 dims run at 64, 96 at 128, 192 at 256: the queries' dims past D are zero,
+ *   and each K/V row is read W wide at its own stride, so the scale and bias rows of such a cache
+ *   must hold exactly D / group_size elements); bits in {4, 8}. One pass of the kernel serves
+ *   16 * group_size / W query rows ((Hq / Hkv) * L) of a KV head; more rows take more passes over
+ *   the keys. Only D dims of each output row are written.
  *   seq_lens: NULL (every sequence has S keys) or device int32[B] with 1 <= seq_lens[b] <= S.
  *   causal:   query l of sequence b sits at position seq_len_b - L + l and sees keys <= it.
  *   window:   0 = none; otherwise keys k > position - window only (sliding window).
@@ -217,7 +221,7 @@ int kvq_decode_attn_masked(const kvq_rows* q, const kvq_qtensor* k, const kvq_qt
                            void* workspace, size_t workspace_bytes, void* stream);
 
 /*
- * The same over an unquantized cache (kvq_decode_attn_dense's arguments; D in {64, 128}).
+ * The same over an unquantized cache (kvq_decode_attn_dense's arguments and head dims).
  * Replaces the mask handling of mx.fast.scaled_dot_product_attention for array masks.
  */
 int kvq_decode_attn_dense_masked(const kvq_rows* q, const kvq_rows* k, const kvq_rows* v,
@@ -228,11 +232,12 @@ int kvq_decode_attn_dense_masked(const kvq_rows* q, const kvq_rows* k, const kvq
 /*
  * Attention for prefill chunks (any L): same contract as kvq_decode_attn, MFMA tiles with
  * K/V tiles dequantized into LDS. Replaces m5engine/attention.py:29-103 for L > 1.
- * Requirements: D in {64, 128, 256}; group_size in {32, 64, 128} with D / 4 <= group_size <= D;
- *   bits in {4, 8}; Hq a multiple of Hkv; at D = 64 or 128 with two or more scale groups per row,
- *   scale and bias rows 4-byte aligned (even strides; MLX's contiguous layout is).
+ * Requirements: those of kvq_decode_attn; Hq a multiple of Hkv; at D = 64 or 128 with two or
+ *   more scale groups per row, scale and bias rows 4-byte aligned (even strides; MLX's contiguous
+ *   layout is).
  * D = 256 runs a kernel of its own (128 query rows per workgroup, 32-key tiles) whose split key
- * ranges are merged by a second, small launch on the same stream.
+ * ranges are merged by a second, small launch on the same stream. Head dims other than 64, 128
+ * and 256 run the decode kernel (any L) and take kvq_decode_attn's workspace size.
  */
 int kvq_prefill_attn(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v,
                      const int32_t* seq_lens, const kvq_rows* out,
@@ -253,9 +258,10 @@ size_t kvq_prefill_workspace_size(int B, int Hq, int Hkv, int L, int D, int S, i
  * unquantized.
  * The products run on MFMA in the cache's own type (fp16 or bf16, exact operands) with fp32
  * accumulation; the probabilities enter the PV product in that type.
- * Requirements: D in {64, 128, 256}; rows 16-byte aligned with strides that are multiples of 8
- * elements. At D = 256 both entry points run the head_dim-256 prefill kernel (any L); the prefill
- * entry point runs the same kernel at D = 64.
+ * Requirements: D in {64, 128, 256}, or another multiple of 8 below 128 (run by the decode kernel
+ * at width 64 or 128, any L; the key rows must then be exactly D elements apart); rows 16-byte
+ * aligned with strides that are multiples of 8 elements. At D = 256 both entry points run the
+ * head_dim-256 prefill kernel (any L); the prefill entry point runs the same kernel at D = 64.
  */
 int kvq_decode_attn_dense(const kvq_rows* q, const kvq_rows* k, const kvq_rows* v,
                           const int32_t* seq_lens, const kvq_rows* out,

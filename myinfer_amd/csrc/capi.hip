@@ -91,6 +91,17 @@ int check_attn_common(const kvq_rows* q, const kvq_rows* out, int B, int Hq, int
   return KVQ_OK;
 }
 
+// Head dimensions 64, 128 and 256 have kernels of their own width; any other multiple of 8 up to 256
+// (unquantized: up to 128) runs the decode kernel at the next width, for every query length
+// (kvq::decode_kernel_dim).
+bool native_dim(int D) { return D == 64 || D == 128 || D == 256; }
+
+int check_head_dim(int D, bool dense, const char* what) {
+  if (D > 0 && D % 8 == 0 && (native_dim(D) || D <= (dense ? 128 : 256))) return KVQ_OK;
+  return fail(KVQ_ERR_UNSUPPORTED, "%s supports head_dim 64, 128, 256 and other multiples of 8 up to %d, got %d", what,
+              dense ? 128 : 256, D);
+}
+
 int check_workspace(size_t ws_needed, void* workspace, size_t workspace_bytes) {
   if (!workspace || workspace_bytes < ws_needed)
     return fail(KVQ_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", ws_needed, workspace ? workspace_bytes : (size_t)0);
@@ -98,13 +109,15 @@ int check_workspace(size_t ws_needed, void* workspace, size_t workspace_bytes) {
   return KVQ_OK;
 }
 
-// Scale-group sizes the attention kernels are built for: 32, 64 and 128, at most D and at least D / 4
-// (a decode lane's quarter of a row lies in one group).
+// Scale-group sizes the attention kernels are built for: 32, 64 and 128, at most the kernel width and
+// at least a quarter of it (a decode lane's quarter of a row lies in one group), dividing D.
 int check_attn_group(int group_size, int D) {
-  if ((group_size != 32 && group_size != 64 && group_size != 128) || group_size > D || 4 * group_size < D)
+  const int Dk = kvq::decode_kernel_dim(D);
+  if ((group_size != 32 && group_size != 64 && group_size != 128) || group_size > Dk || 4 * group_size < Dk ||
+      D % group_size)
     return fail(KVQ_ERR_UNSUPPORTED,
-                "attention supports group_size 32, 64 and 128 between head_dim/4 and head_dim (%d), got %d", D,
-                group_size);
+                "attention supports group_size 32, 64 and 128 dividing head_dim (%d) and between %d/4 and %d, got %d",
+                D, Dk, Dk, group_size);
   return KVQ_OK;
 }
 
@@ -124,6 +137,11 @@ int check_attn_args(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* 
     if (t->codes_stride_s < row_words) return fail(KVQ_ERR_INVALID, "codes row stride %lld is smaller than D*bits/32=%lld", (long long)t->codes_stride_s, (long long)row_words);
     if (t->sb_stride_s < D / group_size)
       return fail(KVQ_ERR_INVALID, "scales row stride %lld is smaller than D/group=%d", (long long)t->sb_stride_s, D / group_size);
+    // a row narrower than its kernel reads the next row's first groups past its own: they must be
+    // rows of the cache, not padding
+    if (D < kvq::decode_kernel_dim(D) && t->sb_stride_s != D / group_size)
+      return fail(KVQ_ERR_UNSUPPORTED, "head_dim %d needs scale and bias rows of exactly D/group=%d elements, got a stride "
+                  "of %lld", D, D / group_size, (long long)t->sb_stride_s);
     // the kernels address each (sequence, KV head)'s rows with 32-bit byte offsets
     if ((int64_t)S * t->codes_stride_s * 4 > (int64_t)UINT32_MAX || (int64_t)S * t->sb_stride_s * 2 > (int64_t)UINT32_MAX)
       return fail(KVQ_ERR_UNSUPPORTED, "attention needs S times each row stride within 4 GiB (S=%d)", S);
@@ -147,6 +165,11 @@ int check_attn_dense(const kvq_rows* q, const kvq_rows* k, const kvq_rows* v, co
   if ((rc = check_attn_common(q, out, B, Hq, Hkv, L, D, S, dtype, scale, window))) return rc;
   if ((rc = check_rows(k, "keys", D, true))) return rc;
   if ((rc = check_rows(v, "values", D, true))) return rc;
+  // a key row narrower than its kernel reads the next row's first elements past its own: they must
+  // be a row of the cache, not padding
+  if (D < kvq::decode_kernel_dim(D) && k->stride_l != D)
+    return fail(KVQ_ERR_UNSUPPORTED, "head_dim %d needs key rows of exactly D elements, got a stride of %lld", D,
+                (long long)k->stride_l);
   for (const kvq_rows* t : {k, v}) {
     if (t->stride_l < D) return fail(KVQ_ERR_INVALID, "K/V row stride %lld is smaller than D=%d", (long long)t->stride_l, D);
     // the kernels address each (sequence, KV head)'s rows with 32-bit byte offsets
@@ -193,6 +216,9 @@ int check_pool(const kvq_qtensor* t, const char* name, int H, int D, int bits, i
   const int64_t row_words = (int64_t)D * bits / 32, groups = D / group_size;
   if (t->codes_stride_s < row_words || t->sb_stride_s < groups)
     return fail(KVQ_ERR_INVALID, "%s row strides are smaller than one row", name);
+  if (D < kvq::decode_kernel_dim(D) && t->sb_stride_s != groups)
+    return fail(KVQ_ERR_UNSUPPORTED, "head_dim %d needs %s scale and bias rows of exactly D/group=%lld elements", D, name,
+                (long long)groups);
   if (t->codes_stride_h < KVQ_PAGE_ROWS * t->codes_stride_s || t->sb_stride_h < KVQ_PAGE_ROWS * t->sb_stride_s ||
       t->codes_stride_b < H * t->codes_stride_h || t->sb_stride_b < H * t->sb_stride_h)
     return fail(KVQ_ERR_INVALID, "%s is not [num_pages][H][%d][row]: its strides overlap", name, KVQ_PAGE_ROWS);
@@ -310,13 +336,14 @@ int kvq_paged_quantize_append(const kvq_rows* k_src, const kvq_qtensor* k_pool, 
 }
 
 size_t kvq_decode_workspace_size(int B, int Hq, int Hkv, int L, int D, int S, int window) {
-  if (B <= 0 || Hq <= 0 || Hkv <= 0 || L <= 0 || S <= 0 || (D != 64 && D != 128 && D != 256) || window < 0) return 0;
+  if (B <= 0 || Hq <= 0 || Hkv <= 0 || L <= 0 || S <= 0 || D <= 0 || D > 256 || D % 8 || window < 0) return 0;
   // one size serves every cache format: the quantized (8-, 4-bit) and the unquantized (16) plans
   // and every scale-group size (the group sets the query rows per workgroup)
+  const int Dk = kvq::decode_kernel_dim(D);
   size_t n = 0;
   for (int bits : {8, 4, 16})
     for (int G : {32, 64, 128}) {
-      if (G > D || 4 * G < D || (bits == 16 && D > 128)) continue;
+      if (G > Dk || 4 * G < Dk || (bits == 16 && Dk > 128)) continue;
       const size_t x = kvq::decode_workspace_bytes(B, Hq, Hkv, L, D, S, window, bits, G);
       n = x > n ? x : n;
     }
@@ -331,8 +358,7 @@ int kvq_decode_attn(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* 
                     const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int bits, int group_size,
                     int dtype, float scale, int causal, int window, void* workspace, size_t workspace_bytes,
                     void* stream) {
-  if (D != 64 && D != 128 && D != 256)
-    return fail(KVQ_ERR_UNSUPPORTED, "decode supports head_dim 64, 128 and 256, got %d", D);
+  if (check_head_dim(D, false, "decode")) return KVQ_ERR_UNSUPPORTED;
   int rc = check_attn(q, k, v, out, B, Hq, Hkv, L, D, S, bits, group_size, dtype, scale, window,
                       kvq_decode_workspace_size(B, Hq, Hkv, L, D, S, window), workspace, workspace_bytes);
   if (rc) return rc;
@@ -344,8 +370,7 @@ int kvq_decode_attn(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* 
 int kvq_decode_attn_static(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v, const int32_t* seq_lens,
                            const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int bits, int group_size,
                            int dtype, float scale, int causal, int window, void* stream) {
-  if (D != 64 && D != 128 && D != 256)
-    return fail(KVQ_ERR_UNSUPPORTED, "decode supports head_dim 64, 128 and 256, got %d", D);
+  if (check_head_dim(D, false, "decode")) return KVQ_ERR_UNSUPPORTED;
   int rc = check_attn_args(q, k, v, out, B, Hq, Hkv, L, D, S, bits, group_size, dtype, scale, window);
   if (rc) return rc;
   // the scratch has to hold this call's own plan (its format and group size), not the largest plan
@@ -362,8 +387,8 @@ int kvq_decode_attn_static(const kvq_rows* q, const kvq_qtensor* k, const kvq_qt
 }
 
 size_t kvq_prefill_workspace_size(int B, int Hq, int Hkv, int L, int D, int S, int window) {
-  if (B <= 0 || Hq <= 0 || Hkv <= 0 || L <= 0 || S <= 0 || (D != 64 && D != 128 && D != 256) || window < 0 || Hq % Hkv)
-    return 0;
+  if (B <= 0 || Hq <= 0 || Hkv <= 0 || L <= 0 || S <= 0 || window < 0 || Hq % Hkv) return 0;
+  if (!native_dim(D)) return kvq_decode_workspace_size(B, Hq, Hkv, L, D, S, window);  // the decode kernel serves
   if (D == 256) return kvq::wide_workspace_bytes(B, Hq, Hkv, L, D, S, window);
   const size_t n = kvq::prefill_workspace_bytes(B, Hq, Hkv, L, D, S, window, 8);
   if (D == 64) {  // the unquantized cache at head_dim 64 runs through wide.hip's kernel
@@ -388,11 +413,14 @@ int kvq_prefill_attn(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor*
                      const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int bits, int group_size,
                      int dtype, float scale, int causal, int window, void* workspace, size_t workspace_bytes,
                      void* stream) {
-  if (D != 64 && D != 128 && D != 256)
-    return fail(KVQ_ERR_UNSUPPORTED, "prefill supports head_dim 64, 128 and 256, got %d", D);
+  if (check_head_dim(D, false, "prefill")) return KVQ_ERR_UNSUPPORTED;
   int rc = check_attn(q, k, v, out, B, Hq, Hkv, L, D, S, bits, group_size, dtype, scale, window,
                       kvq_prefill_workspace_size(B, Hq, Hkv, L, D, S, window), workspace, workspace_bytes);
   if (rc) return rc;
+  if (!native_dim(D))
+    return hip_status(kvq::launch_decode(q, k, v, seq_lens, out, B, Hq, Hkv, L, D, S, bits, group_size, dtype, scale,
+                                         causal, window, workspace, (hipStream_t)stream),
+                      "prefill_attn launch (the decode kernel, head_dim other than 64/128/256)");
   if (D == 256)
     return hip_status(kvq::launch_wide(q, k, v, seq_lens, out, B, Hq, Hkv, L, S, bits, group_size, dtype, scale, causal,
                                        window, workspace, (hipStream_t)stream),
@@ -427,8 +455,7 @@ int kvq_paged_decode_attn(const kvq_rows* q, const kvq_qtensor* k_pool, const kv
                           const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int bits, int group_size,
                           int dtype, float scale, int causal, int window, void* workspace, size_t workspace_bytes,
                           void* stream) {
-  if (D != 64 && D != 128 && D != 256)
-    return fail(KVQ_ERR_UNSUPPORTED, "decode supports head_dim 64, 128 and 256, got %d", D);
+  if (check_head_dim(D, false, "decode")) return KVQ_ERR_UNSUPPORTED;
   int rc = check_paged_attn(q, k_pool, v_pool, num_pages, block_table, table_stride, out, B, Hq, Hkv, L, D, S, bits,
                             group_size, dtype, scale, window, kvq_decode_workspace_size(B, Hq, Hkv, L, D, S, window),
                             workspace, workspace_bytes);
@@ -444,12 +471,16 @@ int kvq_paged_prefill_attn(const kvq_rows* q, const kvq_qtensor* k_pool, const k
                            const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int bits, int group_size,
                            int dtype, float scale, int causal, int window, void* workspace, size_t workspace_bytes,
                            void* stream) {
-  if (D != 64 && D != 128 && D != 256)
-    return fail(KVQ_ERR_UNSUPPORTED, "prefill supports head_dim 64, 128 and 256, got %d", D);
+  if (check_head_dim(D, false, "prefill")) return KVQ_ERR_UNSUPPORTED;
   int rc = check_paged_attn(q, k_pool, v_pool, num_pages, block_table, table_stride, out, B, Hq, Hkv, L, D, S, bits,
                             group_size, dtype, scale, window, kvq_prefill_workspace_size(B, Hq, Hkv, L, D, S, window),
                             workspace, workspace_bytes);
   if (rc) return rc;
+  if (!native_dim(D))
+    return hip_status(kvq::launch_decode_paged(q, k_pool, v_pool, num_pages, block_table, table_stride, seq_lens, out,
+                                               B, Hq, Hkv, L, D, S, bits, group_size, dtype, scale, causal, window,
+                                               workspace, (hipStream_t)stream),
+                      "paged_prefill_attn launch (the decode kernel, head_dim other than 64/128/256)");
   if (D == 256)
     return hip_status(kvq::launch_wide_paged(q, k_pool, v_pool, num_pages, block_table, table_stride, seq_lens, out, B,
                                              Hq, Hkv, L, S, bits, group_size, dtype, scale, causal, window, workspace,
@@ -466,8 +497,7 @@ int kvq_paged_prefill_attn(const kvq_rows* q, const kvq_qtensor* k_pool, const k
 int kvq_decode_attn_dense(const kvq_rows* q, const kvq_rows* k, const kvq_rows* v, const int32_t* seq_lens,
                           const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int dtype, float scale,
                           int causal, int window, void* workspace, size_t workspace_bytes, void* stream) {
-  if (D != 64 && D != 128 && D != 256)
-    return fail(KVQ_ERR_UNSUPPORTED, "unquantized decode supports head_dim 64, 128 and 256, got %d", D);
+  if (check_head_dim(D, true, "unquantized decode")) return KVQ_ERR_UNSUPPORTED;
   int rc = check_attn_dense(q, k, v, out, B, Hq, Hkv, L, D, S, dtype, scale, window,
                             kvq_decode_workspace_size(B, Hq, Hkv, L, D, S, window), workspace, workspace_bytes);
   if (rc) return rc;
@@ -495,8 +525,7 @@ static int check_mask(const kvq_mask* m) {
 int kvq_decode_attn_masked(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v, const kvq_rows* out, int B,
                            int Hq, int Hkv, int L, int D, int S, int bits, int group_size, int dtype, float scale,
                            const kvq_mask* mask, void* workspace, size_t workspace_bytes, void* stream) {
-  if (D != 64 && D != 128 && D != 256)
-    return fail(KVQ_ERR_UNSUPPORTED, "decode supports head_dim 64, 128 and 256, got %d", D);
+  if (check_head_dim(D, false, "decode")) return KVQ_ERR_UNSUPPORTED;
   int rc = check_attn(q, k, v, out, B, Hq, Hkv, L, D, S, bits, group_size, dtype, scale, 0,
                       kvq_decode_workspace_size(B, Hq, Hkv, L, D, S, 0), workspace, workspace_bytes);
   if (rc || (rc = check_mask(mask))) return rc;
@@ -508,8 +537,7 @@ int kvq_decode_attn_masked(const kvq_rows* q, const kvq_qtensor* k, const kvq_qt
 int kvq_decode_attn_dense_masked(const kvq_rows* q, const kvq_rows* k, const kvq_rows* v, const kvq_rows* out, int B,
                                  int Hq, int Hkv, int L, int D, int S, int dtype, float scale, const kvq_mask* mask,
                                  void* workspace, size_t workspace_bytes, void* stream) {
-  if (D != 64 && D != 128 && D != 256)
-    return fail(KVQ_ERR_UNSUPPORTED, "masked unquantized attention supports head_dim 64, 128 and 256, got %d", D);
+  if (check_head_dim(D, true, "masked unquantized attention")) return KVQ_ERR_UNSUPPORTED;
   int rc = check_attn_dense(q, k, v, out, B, Hq, Hkv, L, D, S, dtype, scale, 0,
                             kvq_decode_workspace_size(B, Hq, Hkv, L, D, S, 0), workspace, workspace_bytes);
   if (rc || (rc = check_mask(mask))) return rc;
@@ -525,11 +553,14 @@ int kvq_decode_attn_dense_masked(const kvq_rows* q, const kvq_rows* k, const kvq
 int kvq_prefill_attn_dense(const kvq_rows* q, const kvq_rows* k, const kvq_rows* v, const int32_t* seq_lens,
                            const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int dtype, float scale,
                            int causal, int window, void* workspace, size_t workspace_bytes, void* stream) {
-  if (D != 64 && D != 128 && D != 256)
-    return fail(KVQ_ERR_UNSUPPORTED, "unquantized prefill supports head_dim 64, 128 and 256, got %d", D);
+  if (check_head_dim(D, true, "unquantized prefill")) return KVQ_ERR_UNSUPPORTED;
   int rc = check_attn_dense(q, k, v, out, B, Hq, Hkv, L, D, S, dtype, scale, window,
                             kvq_prefill_workspace_size(B, Hq, Hkv, L, D, S, window), workspace, workspace_bytes);
   if (rc) return rc;
+  if (!native_dim(D))
+    return hip_status(kvq::launch_decode_dense(q, k, v, seq_lens, out, B, Hq, Hkv, L, D, S, dtype, scale, causal, window,
+                                               workspace, (hipStream_t)stream),
+                      "prefill_attn_dense launch (the decode kernel, head_dim other than 64/128/256)");
   if (D != 128)
     return hip_status(kvq::launch_wide_dense(q, k, v, seq_lens, out, B, Hq, Hkv, L, D, S, dtype, scale, causal, window,
                                              workspace, (hipStream_t)stream),

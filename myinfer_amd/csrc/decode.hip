@@ -118,6 +118,9 @@ struct DecParams {
   const void* mask;
   int mask_kind;
   int64_t m_sb, m_skv, m_srep, m_sl;
+  // the head dimension of the rows (a multiple of 8, at most the kernel's D): a narrower row is
+  // computed as a D-wide one whose dims past dv carry zero queries, and only dims below dv are stored
+  int dv;
 };
 
 // A general mask (kvq_mask) on the lane's 8 scores of a tile (keys k0 + 16 (s / 4) + 4 lg + s % 4 of
@@ -482,9 +485,10 @@ constexpr int dec_min_wgs() {
   return (NW == 4 && 2 * NW * NSLOT * DecCfg<D, BITS, G>::SLOT <= 160 * 1024) ? 2 : 1;
 }
 
-// MASKED: compiled with a general mask (kvq_mask) read beside every tile; the other instantiations
-// carry no trace of it.
-template <typename T, int D, int BITS, int NW, int NSLOT, bool PAGED = false, int G = 64, bool MASKED = false>
+// MASKED: compiled with a general mask (kvq_mask) read beside every tile; NARROW: for rows of p.dv < D
+// dims. The other instantiations carry no trace of either.
+template <typename T, int D, int BITS, int NW, int NSLOT, bool PAGED = false, int G = 64, bool MASKED = false,
+          bool NARROW = false>
 __global__ __launch_bounds__(NW * 64, (dec_min_wgs<D, BITS, NW, NSLOT, G>())) void decode_attn_kernel(DecParams p) {
   using C = DecCfg<D, BITS, G>;
   constexpr int R = C::R;
@@ -508,6 +512,8 @@ __global__ __launch_bounds__(NW * 64, (dec_min_wgs<D, BITS, NW, NSLOT, G>())) vo
   asm volatile("" ::"s"(p.q_sb), "s"(p.q_sh), "s"(p.q_sl), "s"(p.kc_sb), "s"(p.kc_sh), "s"(p.kc_ss), "s"(p.vc_sb),
                "s"(p.vc_sh), "s"(p.vc_ss));
   asm volatile("" ::"s"(p.ksb_sb), "s"(p.ksb_sh), "s"(p.ksb_ss), "s"(p.vsb_sb), "s"(p.vsb_sh), "s"(p.vsb_ss));
+  const int dims = NARROW ? p.dv : D;  // dims of a row (a compile-time D unless NARROW)
+  if constexpr (NARROW) asm volatile("" ::"s"(dims));
   const int wg0 = blockIdx.x;
   const int wg = p.xcd_remap ? (wg0 % kXcds) * ((p.nunits * p.nsplit) / kXcds) + wg0 / kXcds : wg0;
   const int unit = wg / p.nsplit;
@@ -536,8 +542,10 @@ __global__ __launch_bounds__(NW * 64, (dec_min_wgs<D, BITS, NW, NSLOT, G>())) vo
   u4 qraw[C::KSTEPS];
   {
     const uint16_t* qrow = p.q + (int64_t)b * p.q_sb + (int64_t)hq * p.q_sh + (int64_t)lq * p.q_sl + lg * (D / 4);
+    // in bounds: row and head are clamped, and dims from dv on (a row narrower than D) are not read
 #pragma unroll
-    for (int j = 0; j < C::KSTEPS; ++j) qraw[j] = *(const u4*)(qrow + 8 * j);  // in bounds: row and head are clamped
+    for (int j = 0; j < C::KSTEPS; ++j)
+      qraw[j] = (!NARROW || lg * (D / 4) + 8 * j < dims) ? *(const u4*)(qrow + 8 * j) : u4{0, 0, 0, 0};
   }
 
   // ---- tile stream: buffer resources over the S_b valid rows of this (sequence, KV head); the
@@ -930,7 +938,7 @@ __global__ __launch_bounds__(NW * 64, (dec_min_wgs<D, BITS, NW, NSLOT, G>())) vo
     s.rr = (4 * s.i4) / D;
     s.d0 = (4 * s.i4) % D;
     const int rw = rb * R + s.rr;
-    s.mine = s.i4 < NV && rw < p.nrows;
+    s.mine = s.i4 < NV && rw < p.nrows && (!NARROW || s.d0 < dims);
     const int hh = kvh * p.rep + rw / p.L, ll = rw % p.L;
     s.orow = p.out + (int64_t)b * p.o_sb + (int64_t)hh * p.o_sh + (int64_t)ll * p.o_sl + s.d0;
     return s;
@@ -1139,14 +1147,45 @@ static DecLayout decode_layout(const DecPlan& pl, int D) {
   return l;
 }
 
+int decode_kernel_dim(int D) { return D <= 64 ? 64 : D <= 128 ? 128 : 256; }
+
 size_t decode_workspace_bytes(int B, int Hq, int Hkv, int L, int D, int S, int window, int bits, int G) {
-  const DecPlan pl = decode_plan(B, Hq, Hkv, L, D, S, window, bits, G);
-  return decode_layout(pl, D).total;
+  const int Dk = decode_kernel_dim(D);
+  const DecPlan pl = decode_plan(B, Hq, Hkv, L, Dk, S, window, bits, G);
+  return decode_layout(pl, Dk).total;
+}
+
+// Whether kernel width D with scale group G serves narrower rows: head dims that run at width D
+// (decode_kernel_dim) and are multiples of G, i.e. 32 dims at width 64 (G 32), 96 at 128 (G 32) and
+// 192 at 256 (G 64); unquantized rows (G stands at 64) of any multiple of 8 at width 64 or 128.
+template <int D, int BITS, int G>
+constexpr bool narrow_rows() {
+  if constexpr (BITS == 16) return D <= 128;
+  const int lo = D == 64 ? 0 : D / 2;  // the widths below D end here
+  return (lo / G + 1) * G < D;
 }
 
 template <typename T, int D, int BITS, int NW, int NSLOT, bool PAGED = false, int G = 64>
 static hipError_t launch_decode_t(const DecParams& p, hipStream_t stream) {
-  if (p.mask_kind != 0) {
+  if (p.dv != D) {
+    // rows narrower than the kernel (decode_kernel_dim): the default launch shape, plain, paged or
+    // masked
+    if constexpr (NW == 4 && NSLOT == 2 && narrow_rows<D, BITS, G>()) {
+      if (p.mask_kind != 0) {
+        if constexpr (!PAGED) {
+          hipLaunchKernelGGL((decode_attn_kernel<T, D, BITS, NW, NSLOT, PAGED, G, true, true>),
+                             dim3(p.nunits * p.nsplit), dim3(NW * 64), 0, stream, p);
+        } else {
+          return hipErrorInvalidValue;
+        }
+      } else {
+        hipLaunchKernelGGL((decode_attn_kernel<T, D, BITS, NW, NSLOT, PAGED, G, false, true>), dim3(p.nunits * p.nsplit),
+                           dim3(NW * 64), 0, stream, p);
+      }
+    } else {
+      return hipErrorInvalidValue;
+    }
+  } else if (p.mask_kind != 0) {
     if constexpr (NW == 4 && NSLOT == 2 && !PAGED) {
       hipLaunchKernelGGL((decode_attn_kernel<T, D, BITS, NW, NSLOT, PAGED, G, true>), dim3(p.nunits * p.nsplit),
                          dim3(NW * 64), 0, stream, p);
@@ -1174,12 +1213,12 @@ static hipError_t launch_decode_t(const DecParams& p, hipStream_t stream) {
   m.rowblocks = p.rowblocks;
   m.nsplit = p.nsplit;
   m.xcd_remap = p.xcd_remap;
-  return launch_combine<T, D>(m, p.nunits / (p.Hkv * p.rowblocks), stream);
+  return launch_combine<T, D>(m, p.nunits / (p.Hkv * p.rowblocks), stream, p.dv);
 }
 
 template <typename T, int D, int BITS, int G = 64>
 static hipError_t launch_decode_shape(const DecParams& p, const DecPlan& pl, hipStream_t stream) {
-  if (p.mask_kind != 0) return launch_decode_t<T, D, BITS, 4, 2, false, G>(p, stream);
+  if (p.mask_kind != 0 || p.dv != D) return launch_decode_t<T, D, BITS, 4, 2, false, G>(p, stream);
   if constexpr (BITS == 16) {
     return launch_decode_t<T, D, BITS, 4, 2>(p, stream);  // a 3-slot ring of raw rows does not fit
   } else if constexpr (G != 64) {
@@ -1227,6 +1266,7 @@ static DecParams decode_params(const kvq_rows* q, const int32_t* seq_lens, const
   p.scale_log2 = scale * 1.4426950408889634f;
   p.causal = causal;
   p.window = window;
+  p.dv = D;
   return p;
 }
 
@@ -1268,8 +1308,10 @@ static void set_mask(DecParams& p, const kvq_mask* mask) {
 hipError_t launch_decode(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v, const int32_t* seq_lens,
                          const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int bits, int G, int dtype,
                          float scale, int causal, int window, void* workspace, hipStream_t stream, const kvq_mask* mask) {
-  const DecPlan pl = decode_plan(B, Hq, Hkv, L, D, S, window, bits, G);
-  DecParams p = decode_params(q, seq_lens, out, Hq, Hkv, L, D, S, scale, causal, window, workspace, pl);
+  const int Dk = decode_kernel_dim(D);
+  const DecPlan pl = decode_plan(B, Hq, Hkv, L, Dk, S, window, bits, G);
+  DecParams p = decode_params(q, seq_lens, out, Hq, Hkv, L, Dk, S, scale, causal, window, workspace, pl);
+  p.dv = D;
   set_mask(p, mask);
   p.kc = (const uint8_t*)k->codes;
   p.vc = (const uint8_t*)v->codes;
@@ -1289,7 +1331,7 @@ hipError_t launch_decode(const kvq_rows* q, const kvq_qtensor* k, const kvq_qten
   p.vsb_sb = v->sb_stride_b;
   p.vsb_sh = v->sb_stride_h;
   p.vsb_ss = v->sb_stride_s;
-  return dispatch_quant(dtype, D, bits, G, [&](auto t, auto d, auto b, auto g) {
+  return dispatch_quant(dtype, Dk, bits, G, [&](auto t, auto d, auto b, auto g) {
     return launch_decode_shape<decltype(t), decltype(d)::value, decltype(b)::value, decltype(g)::value>(p, pl, stream);
   });
 }
@@ -1298,8 +1340,10 @@ hipError_t launch_decode_paged(const kvq_rows* q, const kvq_qtensor* k, const kv
                                const int32_t* table, int64_t table_stride, const int32_t* seq_lens, const kvq_rows* out,
                                int B, int Hq, int Hkv, int L, int D, int S, int bits, int G, int dtype, float scale,
                                int causal, int window, void* workspace, hipStream_t stream) {
-  const DecPlan pl = decode_plan(B, Hq, Hkv, L, D, S, window, bits, G);
-  DecParams p = decode_params(q, seq_lens, out, Hq, Hkv, L, D, S, scale, causal, window, workspace, pl);
+  const int Dk = decode_kernel_dim(D);
+  const DecPlan pl = decode_plan(B, Hq, Hkv, L, Dk, S, window, bits, G);
+  DecParams p = decode_params(q, seq_lens, out, Hq, Hkv, L, Dk, S, scale, causal, window, workspace, pl);
+  p.dv = D;
   p.kc = (const uint8_t*)k->codes;
   p.vc = (const uint8_t*)v->codes;
   p.kc_sb = k->codes_stride_b * 4;  // page strides
@@ -1321,7 +1365,7 @@ hipError_t launch_decode_paged(const kvq_rows* q, const kvq_qtensor* k, const kv
   p.table = table;
   p.table_stride = table_stride;
   p.num_pages = num_pages;
-  return dispatch_quant(dtype, D, bits, G, [&](auto t, auto d, auto b, auto g) {
+  return dispatch_quant(dtype, Dk, bits, G, [&](auto t, auto d, auto b, auto g) {
     return launch_decode_t<decltype(t), decltype(d)::value, decltype(b)::value, 4, 2, true, decltype(g)::value>(p, stream);
   });
 }
@@ -1329,8 +1373,10 @@ hipError_t launch_decode_paged(const kvq_rows* q, const kvq_qtensor* k, const kv
 hipError_t launch_decode_dense(const kvq_rows* q, const kvq_rows* k, const kvq_rows* v, const int32_t* seq_lens,
                                const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int dtype, float scale,
                                int causal, int window, void* workspace, hipStream_t stream, const kvq_mask* mask) {
-  const DecPlan pl = decode_plan(B, Hq, Hkv, L, D, S, window, 16, 64);
-  DecParams p = decode_params(q, seq_lens, out, Hq, Hkv, L, D, S, scale, causal, window, workspace, pl);
+  const int Dk = decode_kernel_dim(D);
+  const DecPlan pl = decode_plan(B, Hq, Hkv, L, Dk, S, window, 16, 64);
+  DecParams p = decode_params(q, seq_lens, out, Hq, Hkv, L, Dk, S, scale, causal, window, workspace, pl);
+  p.dv = D;
   set_mask(p, mask);
   p.kc = (const uint8_t*)k->data;
   p.vc = (const uint8_t*)v->data;
@@ -1341,7 +1387,8 @@ hipError_t launch_decode_dense(const kvq_rows* q, const kvq_rows* k, const kvq_r
   p.vc_sh = v->stride_h * 2;
   p.vc_ss = v->stride_l * 2;
   const bool bf = dtype == KVQ_DTYPE_BF16;
-  if (D == 128) return bf ? launch_decode_shape<BF16, 128, 16>(p, pl, stream) : launch_decode_shape<F16, 128, 16>(p, pl, stream);
+  if (Dk == 256) return hipErrorInvalidValue;  // unquantized rows past 128 dims run through the head_dim-256 kernel
+  if (Dk == 128) return bf ? launch_decode_shape<BF16, 128, 16>(p, pl, stream) : launch_decode_shape<F16, 128, 16>(p, pl, stream);
   return bf ? launch_decode_shape<BF16, 64, 16>(p, pl, stream) : launch_decode_shape<F16, 64, 16>(p, pl, stream);
 }
 

@@ -19,6 +19,11 @@ hipError_t launch_paged_quantize_append(const kvq_rows* k_src, const kvq_qtensor
                                         int group_size, int dtype, hipStream_t stream);
 hipError_t launch_rope(const kvq_rows* x, const kvq_rope_params* rope, int B, int H, int L, int dtype, hipStream_t stream);
 
+// The decode kernel's width for head dimension D: 64, 128 or 256. A narrower row (D a multiple of 8)
+// runs at the next width: its K/V rows are read that wide at their own stride (the bytes past the row
+// are the next row's or, past the sequence, zero), the queries' dims past D are zero and only D dims
+// of the output are stored.
+int decode_kernel_dim(int D);
 size_t decode_workspace_bytes(int B, int Hq, int Hkv, int L, int D, int S, int window, int bits, int G);
 // mask: a general mask (kvq_mask) or nullptr
 hipError_t launch_decode(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v, const int32_t* seq_lens,

@@ -70,8 +70,9 @@ __device__ __forceinline__ float quad_sum(float v) {
 // placed each unit's splits on one XCD, the workgroups here are numbered the same way (a grid that
 // is a multiple of 8, rows in unit order), so a unit's partials are merged on the XCD that wrote
 // them (+1% at 32 splits).
-template <typename T, int D, int R>
-__global__ __launch_bounds__(256) void combine_kernel(MergeParams p, int nrows) {
+// NARROW: output rows of dv < D dims (the partials stay D wide); otherwise dv is not read.
+template <typename T, int D, int R, bool NARROW = false>
+__global__ __launch_bounds__(256) void combine_kernel(MergeParams p, int nrows, int dv) {
   constexpr int F4 = D / 4;              // float4s per row
   constexpr int RPB = 256 / (4 * F4);    // rows per workgroup
   constexpr int CH = 8;                  // splits per thread loaded in the first round
@@ -126,7 +127,7 @@ __global__ __launch_bounds__(256) void combine_kernel(MergeParams p, int nrows) 
   for (int e = 0; e < 4; ++e) acc[e] = quad_sum(acc[e]);
   Ls = quad_sum(Ls);
   acc *= Ls > 0.0f ? 1.0f / Ls : 0.0f;
-  if (!ok || q != 0) return;
+  if (!ok || q != 0 || (NARROW && 4 * j >= dv)) return;
   uint16_t* dst = p.out + (int64_t)b * p.o_sb + (int64_t)h * p.o_sh + (int64_t)l * p.o_sl + 4 * j;
   u2 w;
   w[0] = (uint32_t)from_float(acc[0], T{}) | ((uint32_t)from_float(acc[1], T{}) << 16);
@@ -135,7 +136,8 @@ __global__ __launch_bounds__(256) void combine_kernel(MergeParams p, int nrows) 
 }
 
 template <typename T, int D>
-inline hipError_t launch_combine(const MergeParams& m, int B, hipStream_t stream) {
+// dv: dims of an output row (D unless the decode kernel ran narrower rows at width D)
+inline hipError_t launch_combine(const MergeParams& m, int B, hipStream_t stream, int dv = D) {
   const int nrows = B * m.Hq * m.L;
   constexpr int rpb = 256 / D;  // rows per 256-thread workgroup
   const dim3 grid((nrows + rpb - 1) / rpb);
@@ -143,11 +145,20 @@ inline hipError_t launch_combine(const MergeParams& m, int B, hipStream_t stream
   mm.xcd_remap = m.xcd_remap && grid.x % 8 == 0;
   // R (rows per unit: 16 / scale groups per row for decode, 128 for the head_dim-256 kernel) fixes
   // the kernel's split strides
+  if (dv != D) {
+    switch (m.R) {
+      case 4: hipLaunchKernelGGL((combine_kernel<T, D, 4, true>), grid, dim3(256), 0, stream, mm, nrows, dv); break;
+      case 8: hipLaunchKernelGGL((combine_kernel<T, D, 8, true>), grid, dim3(256), 0, stream, mm, nrows, dv); break;
+      case 16: hipLaunchKernelGGL((combine_kernel<T, D, 16, true>), grid, dim3(256), 0, stream, mm, nrows, dv); break;
+      default: return hipErrorInvalidValue;  // narrow rows come from the decode kernel (4, 8 or 16 rows a unit)
+    }
+    return hipGetLastError();
+  }
   switch (m.R) {
-    case 4: hipLaunchKernelGGL((combine_kernel<T, D, 4>), grid, dim3(256), 0, stream, mm, nrows); break;
-    case 8: hipLaunchKernelGGL((combine_kernel<T, D, 8>), grid, dim3(256), 0, stream, mm, nrows); break;
-    case 16: hipLaunchKernelGGL((combine_kernel<T, D, 16>), grid, dim3(256), 0, stream, mm, nrows); break;
-    case 128: hipLaunchKernelGGL((combine_kernel<T, D, 128>), grid, dim3(256), 0, stream, mm, nrows); break;
+    case 4: hipLaunchKernelGGL((combine_kernel<T, D, 4>), grid, dim3(256), 0, stream, mm, nrows, dv); break;
+    case 8: hipLaunchKernelGGL((combine_kernel<T, D, 8>), grid, dim3(256), 0, stream, mm, nrows, dv); break;
+    case 16: hipLaunchKernelGGL((combine_kernel<T, D, 16>), grid, dim3(256), 0, stream, mm, nrows, dv); break;
+    case 128: hipLaunchKernelGGL((combine_kernel<T, D, 128>), grid, dim3(256), 0, stream, mm, nrows, dv); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

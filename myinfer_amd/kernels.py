@@ -291,16 +291,30 @@ def fits_fp16_operands(triple: Triple, bits: int) -> bool:
     return bool(torch.isfinite(worst).all().item()) and bool((worst <= FP16_MAX).all().item())
 
 
+NATIVE_HEAD_DIMS = (64, 128, 256)
+
+
+def kernel_dim(D: int) -> int:
+    """The width the kernels compute head dimension D at: 64, 128 or 256. Other multiples of 8 (up to
+    256 for quantized caches, 128 for unquantized ones) run the decode kernel at the next width, with
+    zero queries past their last dim, for every query length."""
+    return 64 if D <= 64 else 128 if D <= 128 else 256
+
+
 def decode_rows_per_pass(D: int, group_size: int = 64) -> int:
     """Query rows (heads of a GQA group x query positions) one decode pass serves: the 16 MFMA
-    columns hold each row once per scale group (an unquantized cache counts as group 64)."""
-    return 16 * group_size // D
+    columns hold each row once per scale group of the kernel's width (an unquantized cache counts as
+    group 64)."""
+    return 16 * group_size // kernel_dim(D)
 
 
 def _auto_kernel(rep_rows: int, D: int, group_size: int) -> str:
     """Decode while a KV head's query rows fit at most two decode passes over its keys (one pass for
-    group 64, where 8 rows fit one pass), the prefill kernel otherwise (every head dim has one). At
-    head_dim 256 the unquantized entry points run the head_dim-256 kernel for every query length."""
+    group 64, where 8 rows fit one pass), the prefill kernel otherwise (head dims 64, 128 and 256 have
+    one; the others run the decode kernel at every length). At head_dim 256 the unquantized entry
+    points run the head_dim-256 kernel for every query length."""
+    if D not in NATIVE_HEAD_DIMS:
+        return "decode"
     return "decode" if rep_rows <= max(decode_rows_per_pass(D, group_size), 8) else "prefill"
 
 

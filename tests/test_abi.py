@@ -58,7 +58,9 @@ def _attn(fn, **kw):
     (dict(bits=3), _lib.ERR_UNSUPPORTED, "bits"),
     (dict(group=48), _lib.ERR_UNSUPPORTED, "group_size"),
     (dict(group=128, D=64, S=256), _lib.ERR_UNSUPPORTED, "group_size"),
-    (dict(D=96), _lib.ERR_UNSUPPORTED, "head_dim"),
+    (dict(D=96), _lib.ERR_UNSUPPORTED, "dividing head_dim"),  # groups of 64 do not divide 96
+    (dict(D=160, group=32), _lib.ERR_UNSUPPORTED, "group_size"),  # runs at width 256: groups of 64 or 128
+    (dict(D=100), _lib.ERR_UNSUPPORTED, "multiples of 8"),
     (dict(D=512), _lib.ERR_UNSUPPORTED, "head_dim"),
     (dict(group=32, D=256, S=256), _lib.ERR_UNSUPPORTED, "group_size"),
     (dict(Hq=7, Hkv=2), _lib.ERR_INVALID, "multiple"),
@@ -117,7 +119,10 @@ def test_workspace_sizes():
     b = lib.kvq_decode_workspace_size(8, 64, 8, 1, 128, 32768, 0)
     # the split count targets a fixed number of workgroups, so the partials do not shrink with B
     assert 0 < a <= b
-    assert lib.kvq_decode_workspace_size(1, 64, 8, 1, 96, 32768, 0) == 0
+    # head dims other than 64/128/256 run at the next width: the same partials as that width
+    assert lib.kvq_decode_workspace_size(1, 64, 8, 1, 96, 32768, 0) == a
+    assert lib.kvq_decode_workspace_size(1, 64, 8, 1, 100, 32768, 0) == 0
+    assert lib.kvq_decode_workspace_size(1, 64, 8, 1, 264, 32768, 0) == 0
     assert lib.kvq_decode_workspace_size(1, 64, 8, 1, 256, 32768, 0) > 0  # head_dim 256 (quantized caches)
     # a sliding window never needs more splits than the full context
     assert 0 < lib.kvq_decode_workspace_size(4, 32, 16, 1, 128, 8192, 1024) <= lib.kvq_decode_workspace_size(4, 32, 16, 1, 128, 8192, 0)

@@ -50,7 +50,10 @@ def test_prefill_workspace_size():
     # counter block
     assert lib.kvq_prefill_workspace_size(1, 32, 4, 128, 128, 128, 0) == 256
     assert lib.kvq_prefill_workspace_size(1, 32, 4, 512, 128, 512, 0) > 256
-    assert lib.kvq_prefill_workspace_size(1, 32, 4, 512, 96, 16384, 0) == 0  # head_dim 64 or 128 only
+    # head dims other than 64/128/256 run the decode kernel: its workspace
+    assert lib.kvq_prefill_workspace_size(1, 32, 4, 512, 96, 16384, 0) == lib.kvq_decode_workspace_size(1, 32, 4, 512, 96,
+                                                                                                      16384, 0) > 0
+    assert lib.kvq_prefill_workspace_size(1, 32, 4, 512, 100, 16384, 0) == 0
     assert 0 < lib.kvq_prefill_workspace_size(1, 32, 4, 512, 64, 16384, 0) < c3  # half the dims per partial row
     assert lib.kvq_prefill_workspace_size(1, 30, 4, 512, 128, 16384, 0) == 0  # Hq not a multiple of Hkv
     assert lib.kvq_prefill_workspace_size(1, 32, 4, 0, 128, 16384, 0) == 0
@@ -58,7 +61,8 @@ def test_prefill_workspace_size():
 
 
 @pytest.mark.parametrize("kw,code,needle", [
-    (dict(D=512), _lib.ERR_UNSUPPORTED, "head_dim 64, 128 and 256"),
+    (dict(D=512), _lib.ERR_UNSUPPORTED, "head_dim 64, 128, 256"),
+    (dict(D=96), _lib.ERR_UNSUPPORTED, "group_size"),
     (dict(D=256, group=32), _lib.ERR_UNSUPPORTED, "group_size"),
     (dict(D=64, group=128), _lib.ERR_UNSUPPORTED, "group_size"),
     (dict(bits=3), _lib.ERR_UNSUPPORTED, "bits"),
@@ -96,7 +100,8 @@ def test_prefill_rejects_bad_layouts():
 @pytest.mark.parametrize("entry", ["kvq_decode_attn_dense", "kvq_prefill_attn_dense"])
 def test_dense_entry_points_reject_bad_arguments(entry):
     fn = getattr(_lib.lib(), entry)
-    _expect(_dense(fn, D=96), _lib.ERR_UNSUPPORTED, "head_dim")
+    _expect(_dense(fn, D=160), _lib.ERR_UNSUPPORTED, "head_dim")  # unquantized rows past 128: 256 only
+    _expect(_dense(fn, D=100), _lib.ERR_UNSUPPORTED, "multiples of 8")
     _expect(_dense(fn, dtype=3), _lib.ERR_INVALID, "dtype")
     _expect(_dense(fn, Hq=5, Hkv=2), _lib.ERR_INVALID, "multiple")
     _expect(_dense(fn, k=_lib.Rows(1 << 21, 8 * 128, 4 * 128, 120)), _lib.ERR_INVALID, "row stride")
@@ -111,7 +116,8 @@ def test_dense_entry_points_reject_bad_arguments(entry):
 def test_paged_entry_points_reject_bad_arguments(entry):
     lib = _lib.lib()
     fn = getattr(lib, entry)
-    _expect(_paged(fn, D=96), _lib.ERR_UNSUPPORTED, "head_dim")
+    _expect(_paged(fn, D=96), _lib.ERR_UNSUPPORTED, "group_size")
+    _expect(_paged(fn, D=100), _lib.ERR_UNSUPPORTED, "head_dim")
     _expect(_paged(fn, bits=2), _lib.ERR_UNSUPPORTED, "bits")
     _expect(_paged(fn, pages=0), _lib.ERR_INVALID, "num_pages")
     _expect(_paged(fn, table=None), _lib.ERR_INVALID, "block_table")
@@ -163,9 +169,53 @@ def test_prefill_rejects_unaligned_scale_rows(field, value):
 def test_unquantized_head_dims():
     # the unquantized kernels take head_dim 64/128/256 (decode and prefill)
     lib = _lib.lib()
-    _expect(_dense(lib.kvq_prefill_attn_dense, D=512), _lib.ERR_UNSUPPORTED, "head_dim 64, 128 and 256")
-    _expect(_dense(lib.kvq_decode_attn_dense, D=512), _lib.ERR_UNSUPPORTED, "head_dim 64, 128 and 256")
+    _expect(_dense(lib.kvq_prefill_attn_dense, D=512), _lib.ERR_UNSUPPORTED, "head_dim 64, 128, 256")
+    _expect(_dense(lib.kvq_decode_attn_dense, D=512), _lib.ERR_UNSUPPORTED, "head_dim 64, 128, 256")
     # head_dim 256 needs a workspace from both size queries
     assert lib.kvq_prefill_workspace_size(1, 8, 4, 512, 256, 4096, 0) >= 256
     assert lib.kvq_decode_workspace_size(1, 8, 4, 1, 256, 4096, 0) >= lib.kvq_prefill_workspace_size(1, 8, 4, 1, 256,
                                                                                                     4096, 0)
+
+
+def _rows96(ptr, D=96):
+    return _lib.Rows(ptr, 8 * D, 4 * D, D)
+
+
+def _q96(ptr=1 << 20, D=96, bits=8, G=32):
+    w, ng = D * bits // 32, D // G
+    return _lib.QTensor(ptr, ptr + (1 << 16), ptr + (1 << 17), 8 * 256 * w, 256 * w, w, 8 * 256 * ng, 256 * ng, ng)
+
+
+@pytest.mark.parametrize("entry", ["kvq_decode_attn", "kvq_prefill_attn", "kvq_decode_attn_static"])
+def test_narrow_head_dims_need_tight_scale_rows(entry):
+    """A head dimension below its kernel's width (96 -> 128) reads the next row's first scale groups
+    past its own, so scale/bias rows must hold exactly D/G elements; a well-formed call reaches the
+    workspace check (no device memory is touched)."""
+    lib = _lib.lib()
+    fn = getattr(lib, entry)
+    common = dict(q=_rows96(16 * 1024), out=_rows96(1 << 23), D=96, group=32)
+    static = entry.endswith("static")
+
+    def call(**kw):
+        a = dict(common, **kw)
+        if static:
+            return fn(byref(a["q"]), byref(a["k"]), byref(a["v"]), None, byref(a["out"]), 1, 8, 1, 1, 96, 256, 8, 32,
+                      0, 0.1, 0, 0, None)
+        return _attn(fn, **a)
+
+    k = _q96()
+    k.sb_stride_s = 4  # a padded scale row
+    _expect(call(k=k, v=_q96(1 << 24)), _lib.ERR_UNSUPPORTED, "exactly D/group=3")
+    if not static:
+        _expect(call(k=_q96(), v=_q96(1 << 24)), _lib.ERR_WORKSPACE, "workspace")
+
+
+def test_narrow_unquantized_head_dims_need_tight_key_rows():
+    lib = _lib.lib()
+    for fn in (lib.kvq_decode_attn_dense, lib.kvq_prefill_attn_dense):
+        q, out = _rows96(16 * 1024, 80), _rows96(1 << 23, 80)
+        padded = _lib.Rows(1 << 21, 8 * 88 * 256, 88 * 256, 88)
+        _expect(_dense(fn, q=q, out=out, D=80, k=padded, v=_rows96(1 << 22, 80)), _lib.ERR_UNSUPPORTED,
+                "key rows of exactly D")
+        _expect(_dense(fn, q=q, out=out, D=80, k=_rows96(1 << 21, 80), v=_rows96(1 << 22, 80)), _lib.ERR_WORKSPACE,
+                "workspace")

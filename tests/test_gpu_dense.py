@@ -127,9 +127,11 @@ def test_rejects_bad_dense_arguments():
         kernels.attention(q, k[:, :, :, :64], k[:, :, :, :64], 0.1)
     with pytest.raises(ValueError):
         kernels.attention(q, k, (k, k, k), 0.1)
-    with pytest.raises(NotImplementedError):  # no kernel at head_dim 32
-        kernels.attention(q[..., :32].contiguous(), k[..., :32].contiguous(), k[..., :32].contiguous(), 0.1,
-                          kernel="prefill")
+    # unquantized rows between 128 and 256 dims have no kernel (narrower ones run at width 64 or 128)
+    q160 = torch.zeros((1, 8, 1, 160), dtype=torch.float16, device=DEV)
+    k160 = torch.zeros((1, 2, 64, 160), dtype=torch.float16, device=DEV)
+    with pytest.raises(NotImplementedError):
+        kernels.attention(q160, k160, k160, 0.1, kernel="prefill")
 
 
 # ---- the sliding-window cache through the kernels

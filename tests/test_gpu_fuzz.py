@@ -119,6 +119,29 @@ def test_head_dim_256_fuzz(case):
                     seed=7700 + case, cap=cap, what=f"fuzz-d256 {case}")
 
 
+@pytest.mark.parametrize("case", range(16))
+def test_other_head_dims_fuzz(case):
+    # head dims other than 64/128/256 (the decode kernel at the next width, any query length):
+    # quantized 32/96/192 at their groups, unquantized multiples of 8 below 128, through either
+    # entry point
+    rng = random.Random(7900 + case)
+    dtype = rng.choice(DTYPES)
+    Hkv, rep = rng.choice([1, 2, 4]), rng.choice([1, 2, 4, 8])
+    B = rng.choice([1, 2, 3])
+    L = rng.choice([1, 1, 3, rng.randrange(1, 200)])
+    S = rng.randrange(L, 2500)
+    cap = S + rng.choice([0, 0, rng.randrange(1, 300)])
+    causal, window, seq_lens = _masks(rng, B, L, S)
+    if case % 2 == 0:
+        D, group = rng.choice([(32, 32), (96, 32), (192, 64)])
+        TD.run_case(B, Hkv * rep, Hkv, L, S, D, rng.choice([4, 8]), dtype, causal=causal, window=window,
+                    seq_lens=seq_lens, seed=7900 + case, cap=cap, group=group, what=f"fuzz-hd {case}")
+    else:
+        D = rng.choice([16, 24, 40, 48, 72, 80, 96, 112, 120])
+        TN.run_case(rng.choice(["decode", "prefill"]), B, Hkv * rep, Hkv, L, S, D, dtype, causal=causal,
+                    window=window, seq_lens=seq_lens, seed=7900 + case, cap=cap, what=f"fuzz-hd {case}")
+
+
 @pytest.mark.parametrize("case", range(24))
 def test_unquantized_fuzz(case):
     rng = random.Random(7300 + case)
