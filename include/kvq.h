@@ -258,10 +258,11 @@ size_t kvq_prefill_workspace_size(int B, int Hq, int Hkv, int L, int D, int S, i
  * unquantized.
  * The products run on MFMA in the cache's own type (fp16 or bf16, exact operands) with fp32
  * accumulation; the probabilities enter the PV product in that type.
- * Requirements: D in {64, 128, 256}, or another multiple of 8 below 128 (run by the decode kernel
- * at width 64 or 128, any L; the key rows must then be exactly D elements apart); rows 16-byte
- * aligned with strides that are multiples of 8 elements. At D = 256 both entry points run the
- * head_dim-256 prefill kernel (any L); the prefill entry point runs the same kernel at D = 64.
+ * Requirements: D in {64, 128, 256}, or another multiple of 8 up to 256, run at the next of those
+ * widths for any L (by the decode kernel up to 128 dims, by the head_dim-256 kernel past them; the
+ * key rows must then be exactly D elements apart); rows 16-byte aligned with strides that are
+ * multiples of 8 elements. At D = 256 both entry points run the head_dim-256 prefill kernel (any
+ * L); the prefill entry point runs the same kernel at D = 64.
  */
 int kvq_decode_attn_dense(const kvq_rows* q, const kvq_rows* k, const kvq_rows* v,
                           const int32_t* seq_lens, const kvq_rows* out,

@@ -92,14 +92,14 @@ int check_attn_common(const kvq_rows* q, const kvq_rows* out, int B, int Hq, int
 }
 
 // Head dimensions 64, 128 and 256 have kernels of their own width; any other multiple of 8 up to 256
-// (unquantized: up to 128) runs the decode kernel at the next width, for every query length
-// (kvq::decode_kernel_dim).
+// runs at the next width (kvq::decode_kernel_dim), for every query length: on the decode kernel, or
+// for unquantized rows past 128 dims on the head_dim-256 kernel.
 bool native_dim(int D) { return D == 64 || D == 128 || D == 256; }
 
-int check_head_dim(int D, bool dense, const char* what) {
-  if (D > 0 && D % 8 == 0 && (native_dim(D) || D <= (dense ? 128 : 256))) return KVQ_OK;
-  return fail(KVQ_ERR_UNSUPPORTED, "%s supports head_dim 64, 128, 256 and other multiples of 8 up to %d, got %d", what,
-              dense ? 128 : 256, D);
+int check_head_dim(int D, const char* what) {
+  if (D > 0 && D % 8 == 0 && D <= 256) return KVQ_OK;
+  return fail(KVQ_ERR_UNSUPPORTED, "%s supports head_dim 64, 128, 256 and other multiples of 8 up to 256, got %d", what,
+              D);
 }
 
 int check_workspace(size_t ws_needed, void* workspace, size_t workspace_bytes) {
@@ -347,8 +347,8 @@ size_t kvq_decode_workspace_size(int B, int Hq, int Hkv, int L, int D, int S, in
       const size_t x = kvq::decode_workspace_bytes(B, Hq, Hkv, L, D, S, window, bits, G);
       n = x > n ? x : n;
     }
-  if (D == 256) {  // the unquantized cache at head_dim 256 runs through the head_dim-256 kernel
-    const size_t x = kvq::wide_workspace_bytes(B, Hq, Hkv, L, D, S, window);
+  if (Dk == 256) {  // unquantized rows past 128 dims run through the head_dim-256 kernel
+    const size_t x = kvq::wide_workspace_bytes(B, Hq, Hkv, L, Dk, S, window);
     n = x > n ? x : n;
   }
   return n;
@@ -358,7 +358,7 @@ int kvq_decode_attn(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* 
                     const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int bits, int group_size,
                     int dtype, float scale, int causal, int window, void* workspace, size_t workspace_bytes,
                     void* stream) {
-  if (check_head_dim(D, false, "decode")) return KVQ_ERR_UNSUPPORTED;
+  if (check_head_dim(D, "decode")) return KVQ_ERR_UNSUPPORTED;
   int rc = check_attn(q, k, v, out, B, Hq, Hkv, L, D, S, bits, group_size, dtype, scale, window,
                       kvq_decode_workspace_size(B, Hq, Hkv, L, D, S, window), workspace, workspace_bytes);
   if (rc) return rc;
@@ -370,7 +370,7 @@ int kvq_decode_attn(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* 
 int kvq_decode_attn_static(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v, const int32_t* seq_lens,
                            const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int bits, int group_size,
                            int dtype, float scale, int causal, int window, void* stream) {
-  if (check_head_dim(D, false, "decode")) return KVQ_ERR_UNSUPPORTED;
+  if (check_head_dim(D, "decode")) return KVQ_ERR_UNSUPPORTED;
   int rc = check_attn_args(q, k, v, out, B, Hq, Hkv, L, D, S, bits, group_size, dtype, scale, window);
   if (rc) return rc;
   // the scratch has to hold this call's own plan (its format and group size), not the largest plan
@@ -413,7 +413,7 @@ int kvq_prefill_attn(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor*
                      const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int bits, int group_size,
                      int dtype, float scale, int causal, int window, void* workspace, size_t workspace_bytes,
                      void* stream) {
-  if (check_head_dim(D, false, "prefill")) return KVQ_ERR_UNSUPPORTED;
+  if (check_head_dim(D, "prefill")) return KVQ_ERR_UNSUPPORTED;
   int rc = check_attn(q, k, v, out, B, Hq, Hkv, L, D, S, bits, group_size, dtype, scale, window,
                       kvq_prefill_workspace_size(B, Hq, Hkv, L, D, S, window), workspace, workspace_bytes);
   if (rc) return rc;
@@ -455,7 +455,7 @@ int kvq_paged_decode_attn(const kvq_rows* q, const kvq_qtensor* k_pool, const kv
                           const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int bits, int group_size,
                           int dtype, float scale, int causal, int window, void* workspace, size_t workspace_bytes,
                           void* stream) {
-  if (check_head_dim(D, false, "decode")) return KVQ_ERR_UNSUPPORTED;
+  if (check_head_dim(D, "decode")) return KVQ_ERR_UNSUPPORTED;
   int rc = check_paged_attn(q, k_pool, v_pool, num_pages, block_table, table_stride, out, B, Hq, Hkv, L, D, S, bits,
                             group_size, dtype, scale, window, kvq_decode_workspace_size(B, Hq, Hkv, L, D, S, window),
                             workspace, workspace_bytes);
@@ -471,7 +471,7 @@ int kvq_paged_prefill_attn(const kvq_rows* q, const kvq_qtensor* k_pool, const k
                            const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int bits, int group_size,
                            int dtype, float scale, int causal, int window, void* workspace, size_t workspace_bytes,
                            void* stream) {
-  if (check_head_dim(D, false, "prefill")) return KVQ_ERR_UNSUPPORTED;
+  if (check_head_dim(D, "prefill")) return KVQ_ERR_UNSUPPORTED;
   int rc = check_paged_attn(q, k_pool, v_pool, num_pages, block_table, table_stride, out, B, Hq, Hkv, L, D, S, bits,
                             group_size, dtype, scale, window, kvq_prefill_workspace_size(B, Hq, Hkv, L, D, S, window),
                             workspace, workspace_bytes);
@@ -497,14 +497,14 @@ int kvq_paged_prefill_attn(const kvq_rows* q, const kvq_qtensor* k_pool, const k
 int kvq_decode_attn_dense(const kvq_rows* q, const kvq_rows* k, const kvq_rows* v, const int32_t* seq_lens,
                           const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int dtype, float scale,
                           int causal, int window, void* workspace, size_t workspace_bytes, void* stream) {
-  if (check_head_dim(D, true, "unquantized decode")) return KVQ_ERR_UNSUPPORTED;
+  if (check_head_dim(D, "unquantized decode")) return KVQ_ERR_UNSUPPORTED;
   int rc = check_attn_dense(q, k, v, out, B, Hq, Hkv, L, D, S, dtype, scale, window,
                             kvq_decode_workspace_size(B, Hq, Hkv, L, D, S, window), workspace, workspace_bytes);
   if (rc) return rc;
-  if (D == 256)
+  if (D > 128)
     return hip_status(kvq::launch_wide_dense(q, k, v, seq_lens, out, B, Hq, Hkv, L, D, S, dtype, scale, causal, window,
                                              workspace, (hipStream_t)stream),
-                      "decode_attn_dense launch (head_dim 256)");
+                      "decode_attn_dense launch (the head_dim-256 kernel)");
   return hip_status(kvq::launch_decode_dense(q, k, v, seq_lens, out, B, Hq, Hkv, L, D, S, dtype, scale, causal, window,
                                              workspace, (hipStream_t)stream),
                     "decode_attn_dense launch");
@@ -525,7 +525,7 @@ static int check_mask(const kvq_mask* m) {
 int kvq_decode_attn_masked(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor* v, const kvq_rows* out, int B,
                            int Hq, int Hkv, int L, int D, int S, int bits, int group_size, int dtype, float scale,
                            const kvq_mask* mask, void* workspace, size_t workspace_bytes, void* stream) {
-  if (check_head_dim(D, false, "decode")) return KVQ_ERR_UNSUPPORTED;
+  if (check_head_dim(D, "decode")) return KVQ_ERR_UNSUPPORTED;
   int rc = check_attn(q, k, v, out, B, Hq, Hkv, L, D, S, bits, group_size, dtype, scale, 0,
                       kvq_decode_workspace_size(B, Hq, Hkv, L, D, S, 0), workspace, workspace_bytes);
   if (rc || (rc = check_mask(mask))) return rc;
@@ -537,14 +537,14 @@ int kvq_decode_attn_masked(const kvq_rows* q, const kvq_qtensor* k, const kvq_qt
 int kvq_decode_attn_dense_masked(const kvq_rows* q, const kvq_rows* k, const kvq_rows* v, const kvq_rows* out, int B,
                                  int Hq, int Hkv, int L, int D, int S, int dtype, float scale, const kvq_mask* mask,
                                  void* workspace, size_t workspace_bytes, void* stream) {
-  if (check_head_dim(D, true, "masked unquantized attention")) return KVQ_ERR_UNSUPPORTED;
+  if (check_head_dim(D, "masked unquantized attention")) return KVQ_ERR_UNSUPPORTED;
   int rc = check_attn_dense(q, k, v, out, B, Hq, Hkv, L, D, S, dtype, scale, 0,
                             kvq_decode_workspace_size(B, Hq, Hkv, L, D, S, 0), workspace, workspace_bytes);
   if (rc || (rc = check_mask(mask))) return rc;
-  if (D == 256)  // the unquantized cache at head_dim 256 runs through the head_dim-256 kernel
+  if (D > 128)  // unquantized rows past 128 dims run through the head_dim-256 kernel
     return hip_status(kvq::launch_wide_dense(q, k, v, nullptr, out, B, Hq, Hkv, L, D, S, dtype, scale, 0, 0, workspace,
                                              (hipStream_t)stream, mask),
-                      "decode_attn_dense_masked launch (head_dim 256)");
+                      "decode_attn_dense_masked launch (the head_dim-256 kernel)");
   return hip_status(kvq::launch_decode_dense(q, k, v, nullptr, out, B, Hq, Hkv, L, D, S, dtype, scale, 0, 0, workspace,
                                              (hipStream_t)stream, mask),
                     "decode_attn_dense_masked launch");
@@ -553,10 +553,14 @@ int kvq_decode_attn_dense_masked(const kvq_rows* q, const kvq_rows* k, const kvq
 int kvq_prefill_attn_dense(const kvq_rows* q, const kvq_rows* k, const kvq_rows* v, const int32_t* seq_lens,
                            const kvq_rows* out, int B, int Hq, int Hkv, int L, int D, int S, int dtype, float scale,
                            int causal, int window, void* workspace, size_t workspace_bytes, void* stream) {
-  if (check_head_dim(D, true, "unquantized prefill")) return KVQ_ERR_UNSUPPORTED;
+  if (check_head_dim(D, "unquantized prefill")) return KVQ_ERR_UNSUPPORTED;
   int rc = check_attn_dense(q, k, v, out, B, Hq, Hkv, L, D, S, dtype, scale, window,
                             kvq_prefill_workspace_size(B, Hq, Hkv, L, D, S, window), workspace, workspace_bytes);
   if (rc) return rc;
+  if (D > 128 && D < 256)
+    return hip_status(kvq::launch_wide_dense(q, k, v, seq_lens, out, B, Hq, Hkv, L, D, S, dtype, scale, causal, window,
+                                             workspace, (hipStream_t)stream),
+                      "prefill_attn_dense launch (the head_dim-256 kernel)");
   if (!native_dim(D))
     return hip_status(kvq::launch_decode_dense(q, k, v, seq_lens, out, B, Hq, Hkv, L, D, S, dtype, scale, causal, window,
                                                workspace, (hipStream_t)stream),

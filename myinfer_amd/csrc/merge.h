@@ -150,7 +150,8 @@ inline hipError_t launch_combine(const MergeParams& m, int B, hipStream_t stream
       case 4: hipLaunchKernelGGL((combine_kernel<T, D, 4, true>), grid, dim3(256), 0, stream, mm, nrows, dv); break;
       case 8: hipLaunchKernelGGL((combine_kernel<T, D, 8, true>), grid, dim3(256), 0, stream, mm, nrows, dv); break;
       case 16: hipLaunchKernelGGL((combine_kernel<T, D, 16, true>), grid, dim3(256), 0, stream, mm, nrows, dv); break;
-      default: return hipErrorInvalidValue;  // narrow rows come from the decode kernel (4, 8 or 16 rows a unit)
+      case 128: hipLaunchKernelGGL((combine_kernel<T, D, 128, true>), grid, dim3(256), 0, stream, mm, nrows, dv); break;
+      default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
   }

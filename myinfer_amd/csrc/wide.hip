@@ -116,6 +116,9 @@ struct WideParams {
   const void* mask;
   int mask_kind;
   int64_t m_sb, m_skv, m_srep, m_sl;
+  // the head dimension of the rows (NARROW kernels: a multiple of 8 below D, the unquantized rows
+  // past 128 dims): their queries' dims from dv on are zero and only dv dims are stored
+  int dv;
 };
 
 // A general mask (kvq_mask) on the lane's 16 scores of a tile (keys k0 + 8 (i / 4) + 4 h + i % 4 of
@@ -294,9 +297,10 @@ __device__ __forceinline__ void wide_stage_v(const uint8_t* raw, uint8_t* vop, i
 
 // MASKED: compiled with a general mask (kvq_mask) read beside every tile; the other instantiations
 // carry no trace of it.
-template <typename T, int D, int BITS, int G, bool PAGED = false, bool MASKED = false>
+template <typename T, int D, int BITS, int G, bool PAGED = false, bool MASKED = false, bool NARROW = false>
 __global__ __launch_bounds__(kWW * 64, 1) void wide_attn_kernel(WideParams p) {
   using C = WideCfg<D, BITS, G>;
+  static_assert(!NARROW || C::DENSE, "narrow rows: unquantized caches");
   static_assert(!PAGED || !C::DENSE, "paged pools hold quantized caches");
   using OT = std::conditional_t<C::DENSE, T, F16>;  // operand type
   __shared__ __align__(16) uint8_t smem[C::LDS];
@@ -436,7 +440,8 @@ __global__ __launch_bounds__(kWW * 64, 1) void wide_attn_kernel(WideParams p) {
   {
     const uint16_t* qrow = p.q + (int64_t)b * p.q_sb + (int64_t)hq * p.q_sh + (int64_t)lq * p.q_sl + 8 * h;
 #pragma unroll
-    for (int j = 0; j < C::KSTEPS; ++j) qop[j] = *(const u4*)(qrow + 16 * j);
+    for (int j = 0; j < C::KSTEPS; ++j)
+      qop[j] = (!NARROW || 16 * j + 8 * h < p.dv) ? *(const u4*)(qrow + 16 * j) : u4{0, 0, 0, 0};
     if constexpr (!C::DENSE && T::id == KVQ_DTYPE_BF16) {
       if (p.k_rexp) ek = min(max(*p.k_rexp, 0), 127);
       if (p.v_rexp) ev = min(max(*p.v_rexp, 0), 127);
@@ -614,7 +619,7 @@ __global__ __launch_bounds__(kWW * 64, 1) void wide_attn_kernel(WideParams p) {
         u2 w;
         w[0] = pack2(oacc[db][4 * i] * inv, oacc[db][4 * i + 1] * inv, T{});
         w[1] = pack2(oacc[db][4 * i + 2] * inv, oacc[db][4 * i + 3] * inv, T{});
-        *(u2*)(orow + 32 * db + 8 * i) = w;
+        if (!NARROW || 32 * db + 8 * i + 4 * h < p.dv) *(u2*)(orow + 32 * db + 8 * i) = w;
       }
   } else {
     const int64_t pi = ((int64_t)unit * p.nsplit + split) * kWRows + (row - r0);
@@ -663,7 +668,20 @@ size_t wide_workspace_bytes(int B, int Hq, int Hkv, int L, int D, int S, int win
 
 template <typename T, int D, int BITS, int G, bool PAGED = false>
 static hipError_t launch_wide_t(const WideParams& p, hipStream_t stream) {
-  if (p.mask_kind != 0) {
+  if (p.dv != D) {
+    // unquantized rows narrower than 256 dims (decode_kernel_dim), plain or masked
+    if constexpr (D == 256 && BITS == 16 && !PAGED) {
+      if (p.mask_kind != 0) {
+        hipLaunchKernelGGL((wide_attn_kernel<T, D, BITS, G, PAGED, true, true>), dim3(p.nunits * p.nsplit),
+                           dim3(kWW * 64), 0, stream, p);
+      } else {
+        hipLaunchKernelGGL((wide_attn_kernel<T, D, BITS, G, PAGED, false, true>), dim3(p.nunits * p.nsplit),
+                           dim3(kWW * 64), 0, stream, p);
+      }
+    } else {
+      return hipErrorInvalidValue;
+    }
+  } else if (p.mask_kind != 0) {
     if constexpr (D == 256 && BITS == 16 && !PAGED) {
       hipLaunchKernelGGL((wide_attn_kernel<T, D, BITS, G, PAGED, true>), dim3(p.nunits * p.nsplit), dim3(kWW * 64), 0,
                          stream, p);
@@ -691,7 +709,7 @@ static hipError_t launch_wide_t(const WideParams& p, hipStream_t stream) {
   m.rowblocks = p.rowblocks;
   m.nsplit = p.nsplit;
   m.xcd_remap = 0;
-  return launch_combine<T, D>(m, p.nunits / (p.Hkv * p.rowblocks), stream);
+  return launch_combine<T, D>(m, p.nunits / (p.Hkv * p.rowblocks), stream, p.dv);
 }
 
 static WideParams wide_params(const kvq_rows* q, const int32_t* seq_lens, const kvq_rows* out, int B, int Hq, int Hkv,
@@ -722,6 +740,7 @@ static WideParams wide_params(const kvq_rows* q, const int32_t* seq_lens, const 
   p.scale_log2 = scale * 1.4426950408889634f;
   p.causal = causal;
   p.window = window;
+  p.dv = 256;  // the quantized launches run head_dim 256; launch_wide_dense sets its own
   return p;
 }
 
@@ -802,6 +821,8 @@ hipError_t launch_wide_dense(const kvq_rows* q, const kvq_rows* k, const kvq_row
   p.vc_sb = v->stride_b * 2;
   p.vc_sh = v->stride_h * 2;
   p.vc_ss = v->stride_l * 2;
+  p.dv = D;
+  if (D > 128 && D < 256) D = 256;  // rows narrower than the kernel: read 256 wide at their own stride
   if (D == 64)
     return dtype == KVQ_DTYPE_BF16 ? launch_wide_t<BF16, 64, 16, 64>(p, stream) : launch_wide_t<F16, 64, 16, 64>(p, stream);
   if (D == 256)

@@ -100,7 +100,7 @@ def test_prefill_rejects_bad_layouts():
 @pytest.mark.parametrize("entry", ["kvq_decode_attn_dense", "kvq_prefill_attn_dense"])
 def test_dense_entry_points_reject_bad_arguments(entry):
     fn = getattr(_lib.lib(), entry)
-    _expect(_dense(fn, D=160), _lib.ERR_UNSUPPORTED, "head_dim")  # unquantized rows past 128: 256 only
+    _expect(_dense(fn, D=264), _lib.ERR_UNSUPPORTED, "multiples of 8 up to 256")
     _expect(_dense(fn, D=100), _lib.ERR_UNSUPPORTED, "multiples of 8")
     _expect(_dense(fn, dtype=3), _lib.ERR_INVALID, "dtype")
     _expect(_dense(fn, Hq=5, Hkv=2), _lib.ERR_INVALID, "multiple")

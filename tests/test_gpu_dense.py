@@ -127,11 +127,11 @@ def test_rejects_bad_dense_arguments():
         kernels.attention(q, k[:, :, :, :64], k[:, :, :, :64], 0.1)
     with pytest.raises(ValueError):
         kernels.attention(q, k, (k, k, k), 0.1)
-    # unquantized rows between 128 and 256 dims have no kernel (narrower ones run at width 64 or 128)
-    q160 = torch.zeros((1, 8, 1, 160), dtype=torch.float16, device=DEV)
-    k160 = torch.zeros((1, 2, 64, 160), dtype=torch.float16, device=DEV)
+    # no kernel past 256 dims
+    q264 = torch.zeros((1, 8, 1, 264), dtype=torch.float16, device=DEV)
+    k264 = torch.zeros((1, 2, 64, 264), dtype=torch.float16, device=DEV)
     with pytest.raises(NotImplementedError):
-        kernels.attention(q160, k160, k160, 0.1, kernel="prefill")
+        kernels.attention(q264, k264, k264, 0.1, kernel="prefill")
 
 
 # ---- the sliding-window cache through the kernels

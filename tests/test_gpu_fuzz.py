@@ -122,7 +122,7 @@ def test_head_dim_256_fuzz(case):
 @pytest.mark.parametrize("case", range(16))
 def test_other_head_dims_fuzz(case):
     # head dims other than 64/128/256 (the decode kernel at the next width, any query length):
-    # quantized 32/96/192 at their groups, unquantized multiples of 8 below 128, through either
+    # quantized 32/96/192 at their groups, unquantized multiples of 8 up to 248, through either
     # entry point
     rng = random.Random(7900 + case)
     dtype = rng.choice(DTYPES)
@@ -137,7 +137,7 @@ def test_other_head_dims_fuzz(case):
         TD.run_case(B, Hkv * rep, Hkv, L, S, D, rng.choice([4, 8]), dtype, causal=causal, window=window,
                     seq_lens=seq_lens, seed=7900 + case, cap=cap, group=group, what=f"fuzz-hd {case}")
     else:
-        D = rng.choice([16, 24, 40, 48, 72, 80, 96, 112, 120])
+        D = rng.choice([16, 24, 40, 48, 72, 80, 96, 112, 120, 136, 160, 192, 248])
         TN.run_case(rng.choice(["decode", "prefill"]), B, Hkv * rep, Hkv, L, S, D, dtype, causal=causal,
                     window=window, seq_lens=seq_lens, seed=7900 + case, cap=cap, what=f"fuzz-hd {case}")
 

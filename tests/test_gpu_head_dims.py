@@ -1,9 +1,9 @@
-"""Head dimensions other than 64, 128 and 256: any multiple of 8 up to 256 for quantized caches
-(whose group size must divide it and lie between a quarter of the kernel width and the width) and
-up to 128 for unquantized ones. They run the decode kernel at the next width (64, 128 or 256) for
-every query length, with zero queries past the row's last dim and only its own dims stored. The
-reference takes D from the queries (m5engine/attention.py:38) and is generic over it; mlx-lm's
-quantized cache needs D to be a multiple of the group size.
+"""Head dimensions other than 64, 128 and 256: any multiple of 8 up to 256 (for quantized caches the
+group size must divide it and lie between a quarter of the kernel width and the width). They run
+at the next width (64, 128 or 256) for every query length, with zero queries past the row's last
+dim and only its own dims stored: on the decode kernel, or for unquantized rows past 128 dims on the
+head_dim-256 kernel. The reference takes D from the queries (m5engine/attention.py:38) and is
+generic over it; mlx-lm's quantized cache needs D to be a multiple of the group size.
 
 Every case is checked against the exact fp64 oracle. Rows past each sequence's end hold NaN scales
 and biases (NaN values in the unquantized caches), and paged pools are poisoned the same way, so a
@@ -104,6 +104,10 @@ def test_drop_in_blocked_sdpa(monkeypatch, L):
     (112, torch.float16, 20, True, 64),
     (32, torch.float16, 9, True, 0),
     (48, torch.bfloat16, 1, False, 0),
+    (160, torch.bfloat16, 1, False, 0),
+    (192, torch.float16, 37, True, 0),
+    (224, torch.bfloat16, 20, True, 96),
+    (136, torch.float16, 130, True, 0),
 ])
 def test_unquantized_head_dims(D, dtype, L, causal, window):
     print(f"unquantized head dim D={D} {dtype} L={L} causal={causal} window={window}", flush=True)
@@ -125,9 +129,11 @@ def test_unquantized_head_dims(D, dtype, L, causal, window):
     assert torch.equal(out_p, out)
 
 
-def test_unquantized_head_dim_80_per_head_mask():
-    """mx.fast's SDPA over Phi-2-shaped heads (D = 80) with a per-query-head boolean mask."""
-    B, Hq, Hkv, L, S, D = 1, 8, 8, 21, 333, 80
+@pytest.mark.parametrize("D", [80, 192])
+def test_unquantized_per_head_mask(D):
+    """mx.fast's SDPA with a per-query-head boolean mask over Phi-2-shaped heads (D = 80, the decode
+    kernel) and 192-dim heads (the head_dim-256 kernel)."""
+    B, Hq, Hkv, L, S = 1, 8, 8, 21, 333
     k = seeded_normal((B, Hkv, S, D), 1240, torch.float16, DEV)
     v = seeded_normal((B, Hkv, S, D), 1241, torch.float16, DEV)
     q = seeded_normal((B, Hq, L, D), 1242, torch.float16, DEV)
@@ -137,7 +143,7 @@ def test_unquantized_head_dim_80_per_head_mask():
     out = A.fast_scaled_dot_product_attention(q, k, v, 0.11, m.to(DEV))
     ref = OA.exact_attention(q.cpu().double().numpy(), k.cpu().double().numpy(), v.cpu().double().numpy(), 0.11,
                              vis=m.numpy())
-    assert_close(out, ref, "D=80 per-head mask")
+    assert_close(out, ref, f"D={D} per-head mask")
 
 
 def test_paged_head_dim_96():
@@ -177,7 +183,8 @@ def test_rejected_head_dims_raise():
     kt, vt = make_cache(1, 2, 64, 160, 8, torch.float16, 1270, group=32)
     with pytest.raises((ValueError, NotImplementedError, RuntimeError)):
         kernels.attention(q, kt, vt, 0.1, group_size=32, bits=8)  # width 256 needs groups of 64 or 128
-    k = torch.zeros((1, 2, 64, 160), dtype=torch.float16, device=DEV)
+    q = torch.zeros((1, 4, 1, 264), dtype=torch.float16, device=DEV)
+    k = torch.zeros((1, 2, 64, 264), dtype=torch.float16, device=DEV)
     with pytest.raises((ValueError, NotImplementedError, RuntimeError)):
-        kernels.attention(q, k, k, 0.1)  # unquantized rows past 128 dims: 256 only
+        kernels.attention(q, k, k, 0.1)  # past 256 dims
     assert ctypes  # the C ABI's own rejections are covered by the CPU tests
