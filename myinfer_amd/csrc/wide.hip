@@ -14,8 +14,8 @@
 //  * Keys stream in 32-key tiles through a ring of raw slots filled by buffer->LDS DMA (codes, and
 //    scales/biases into 4-byte cells, cell 32 g + k = group g of key k; raw T rows for an
 //    unquantized cache). Each tile is dequantized once per workgroup, LDS to LDS, into MFMA operands:
-//    K row-major with padded rows, V transposed with its key slots permuted to the score layout. The staging of tile t + 1 runs beside the MFMAs of tile t, one
-//    barrier per tile.
+//    K row-major with padded rows, V transposed with its key slots permuted to the score layout.
+//    The staging of tile t + 1 runs beside the MFMAs of tile t, one barrier per tile.
 //  * Scores S^T = K Q^T with v_mfma_f32_32x32x16 (16 k-steps over the head): each lane holds 16
 //    keys of one query, so the row max / sum are lane-local plus one permlane swap; the packed
 //    probabilities are the B operand of O^T = V^T P^T (2 k-steps x 8 column blocks). The softmax
@@ -24,8 +24,10 @@
 //    to fp16 whatever T is (a packed fp16 subtract and FMA per pair of elements: the code enters
 //    exactly as 1024 + c, the FMA rounds once), with the query entering the
 //    fp16 MFMA exactly as q * 2^qe (the power of two that puts the row's largest element in
-//    [2^13, 2^14)) and 2^-qe folded into the softmax scale. A bf16 cache group whose values do not
-//    fit fp16 dequantizes to inf and the rows that read it come out NaN, never a finite wrong value.
+//    [2^13, 2^14)) and 2^-qe folded into the softmax scale. A bf16 cache whose groups exceed the
+//    fp16 range is staged times 2^-E (its range exponent, include/kvq.h) with 2^E folded back into
+//    the score scale and the output; with no range word such a group dequantizes to inf and the
+//    rows that read it come out NaN, never a finite wrong value.
 //  * Online softmax in log2 units with threshold rescaling (the running maximum moves only when a
 //    tile's maximum exceeds it by more than 2^6, so probabilities stay below 64).
 //  * Keys are split over workgroups when the row blocks alone do not fill the GPU; the splits
