@@ -130,6 +130,22 @@ __device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel)
 // Raw buffer resource over `bytes` bytes at `base` (gfx9 word 3: 32-bit data format, no
 // swizzle). Loads through it take a 32-bit lane offset plus a wave-uniform offset, and read 0
 // outside the range instead of faulting.
+// n / d for 0 <= n < 2^31 as one multiply and shift: with l = ceil(log2 d) and
+// m = ceil(2^(31 + l) / d) (which fits 32 bits), floor(n m / 2^(31 + l)) = floor(n / d)
+// (Granlund and Montgomery, "Division by invariant integers using multiplication", 1994, for
+// 31-bit dividends: the error n (m - 2^(31 + l) / d) / 2^(31 + l) stays below 1 / d). The host
+// builds the pair for a launch's divisors; a runtime division on the device is a long sequence.
+struct Div31 {
+  uint32_t m;
+  uint32_t sh;  // 31 + l
+};
+inline Div31 make_div31(uint32_t d) {
+  uint32_t l = 0;
+  while ((1ull << l) < d) ++l;
+  return {(uint32_t)((((uint64_t)1 << (31 + l)) + d - 1) / d), 31 + l};
+}
+__device__ __forceinline__ uint32_t div31(uint32_t n, Div31 q) { return (uint32_t)(((uint64_t)n * q.m) >> q.sh); }
+
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
 }

@@ -121,6 +121,8 @@ struct DecParams {
   // the head dimension of the rows (a multiple of 8, at most the kernel's D): a narrower row is
   // computed as a D-wide one whose dims past dv carry zero queries, and only dims below dv are stored
   int dv;
+  // nsplit, rowblocks, Hkv and L as multiply-shift divisors (the workgroup and row numbering)
+  Div31 d_nsplit, d_rowblocks, d_hkv, d_l;
 };
 
 // A general mask (kvq_mask) on the lane's 8 scores of a tile (keys k0 + 16 (s / 4) + 4 lg + s % 4 of
@@ -516,11 +518,12 @@ __global__ __launch_bounds__(NW * 64, (dec_min_wgs<D, BITS, NW, NSLOT, G>())) vo
   if constexpr (NARROW) asm volatile("" ::"s"(dims));
   const int wg0 = blockIdx.x;
   const int wg = p.xcd_remap ? (wg0 % kXcds) * ((p.nunits * p.nsplit) / kXcds) + wg0 / kXcds : wg0;
-  const int unit = wg / p.nsplit;
-  const int split = wg % p.nsplit;
-  const int b = unit / (p.Hkv * p.rowblocks);
-  const int kvh = (unit / p.rowblocks) % p.Hkv;
-  const int rb = unit % p.rowblocks;
+  const int unit = (int)div31((uint32_t)wg, p.d_nsplit);
+  const int split = wg - unit * p.nsplit;
+  const int bk = (int)div31((uint32_t)unit, p.d_rowblocks);  // b * Hkv + kvh
+  const int rb = unit - bk * p.rowblocks;
+  const int b = (int)div31((uint32_t)bk, p.d_hkv);
+  const int kvh = bk - b * p.Hkv;
 
   const int S_b = p.seq_lens ? min(max(p.seq_lens[b], 0), p.S) : p.S;  // clamped: never read past the view
   // the first key any row sees, rounded down to a tile boundary (tiles stay 32-aligned, so a tile of
@@ -536,8 +539,9 @@ __global__ __launch_bounds__(NW * 64, (dec_min_wgs<D, BITS, NW, NSLOT, G>())) vo
   const int r = n % R, g = n / R;
   const int row = rb * R + r;
   const bool row_ok = row < p.nrows;
-  const int hq = kvh * p.rep + (row_ok ? row / p.L : 0);
-  const int lq = row_ok ? row % p.L : 0;
+  const int rq = (int)div31((uint32_t)row, p.d_l);  // row / L
+  const int hq = kvh * p.rep + (row_ok ? rq : 0);
+  const int lq = row_ok ? row - rq * p.L : 0;
   const bool in_group = (lg * (D / 4)) / G == g;
   u4 qraw[C::KSTEPS];
   {
@@ -939,7 +943,8 @@ __global__ __launch_bounds__(NW * 64, (dec_min_wgs<D, BITS, NW, NSLOT, G>())) vo
     s.d0 = (4 * s.i4) % D;
     const int rw = rb * R + s.rr;
     s.mine = s.i4 < NV && rw < p.nrows && (!NARROW || s.d0 < dims);
-    const int hh = kvh * p.rep + rw / p.L, ll = rw % p.L;
+    const int rq = (int)div31((uint32_t)rw, p.d_l);
+    const int hh = kvh * p.rep + rq, ll = rw - rq * p.L;
     s.orow = p.out + (int64_t)b * p.o_sb + (int64_t)hh * p.o_sh + (int64_t)ll * p.o_sl + s.d0;
     return s;
   };
@@ -1267,6 +1272,10 @@ static DecParams decode_params(const kvq_rows* q, const int32_t* seq_lens, const
   p.causal = causal;
   p.window = window;
   p.dv = D;
+  p.d_nsplit = make_div31((uint32_t)pl.nsplit);
+  p.d_rowblocks = make_div31((uint32_t)pl.rowblocks);
+  p.d_hkv = make_div31((uint32_t)Hkv);
+  p.d_l = make_div31((uint32_t)L);
   return p;
 }
 

@@ -46,6 +46,7 @@ struct MergeParams {
   int64_t o_sb, o_sh, o_sl;
   int Hq, Hkv, L, rep, R, rowblocks, nsplit;
   int xcd_remap;  // 1: the decode launch numbered its workgroups by XCD (see decode_attn_kernel)
+  Div31 d_l, d_hq, d_rep;  // L, Hq and rep as multiply-shift divisors (set by launch_combine)
 };
 
 // Quad lane exchanges (lane i with lane i ^ 1, i ^ 2) through DPP quad permutes.
@@ -82,8 +83,11 @@ __global__ __launch_bounds__(256) void combine_kernel(MergeParams p, int nrows, 
   const int grow = bx * RPB + t / (4 * F4);
   const bool ok = grow < nrows;
   const int g = ok ? grow : 0;
-  const int l = g % p.L, h = (g / p.L) % p.Hq, b = g / (p.L * p.Hq);
-  const int kvh = h / p.rep;
+  const int gl = (int)div31((uint32_t)g, p.d_l);  // g / L: the (sequence, head) of the row
+  const int l = g - gl * p.L;
+  const int b = (int)div31((uint32_t)gl, p.d_hq);
+  const int h = gl - b * p.Hq;
+  const int kvh = (int)div31((uint32_t)h, p.d_rep);
   const int rw = (h - kvh * p.rep) * p.L + l;
   const int unit = (b * p.Hkv + kvh) * p.rowblocks + rw / R;
   const int64_t base = (int64_t)unit * p.nsplit * R + rw % R;  // split s at base + s * R
@@ -143,6 +147,9 @@ inline hipError_t launch_combine(const MergeParams& m, int B, hipStream_t stream
   const dim3 grid((nrows + rpb - 1) / rpb);
   MergeParams mm = m;
   mm.xcd_remap = m.xcd_remap && grid.x % 8 == 0;
+  mm.d_l = make_div31((uint32_t)m.L);
+  mm.d_hq = make_div31((uint32_t)m.Hq);
+  mm.d_rep = make_div31((uint32_t)m.rep);
   // R (rows per unit: 16 / scale groups per row for decode, 128 for the head_dim-256 kernel) fixes
   // the kernel's split strides
   if (dv != D) {

@@ -118,21 +118,6 @@ __device__ __forceinline__ int group_range_exp(float s, float b, float n) {
   return m == 0.5f ? k - 1 : k;
 }
 
-// n / d for 0 <= n < 2^31 as one multiply and shift: with l = ceil(log2 d) and
-// m = ceil(2^(31 + l) / d) (which fits 32 bits), floor(n m / 2^(31 + l)) = floor(n / d)
-// (Granlund and Montgomery, "Division by invariant integers using multiplication", 1994, for
-// 31-bit dividends: the error n (m - 2^(31 + l) / d) / 2^(31 + l) stays below 1 / d).
-struct Div31 {
-  uint32_t m;
-  uint32_t sh;  // 31 + l
-};
-static Div31 make_div31(uint32_t d) {
-  uint32_t l = 0;
-  while ((1ull << l) < d) ++l;
-  return {(uint32_t)((((uint64_t)1 << (31 + l)) + d - 1) / d), 31 + l};
-}
-__device__ __forceinline__ uint32_t div31(uint32_t n, Div31 q) { return (uint32_t)(((uint64_t)n * q.m) >> q.sh); }
-
 // The rows [l0, l0 + L) of every (sequence, head) in one launch: thread t quantizes chunk
 // t % per_row of row t / per_row (per_row = D / EPT), rows ordered (b, h, l); total < 2^31.
 struct RowMap {
