@@ -146,6 +146,14 @@ inline Div31 make_div31(uint32_t d) {
 }
 __device__ __forceinline__ uint32_t div31(uint32_t n, Div31 q) { return (uint32_t)(((uint64_t)n * q.m) >> q.sh); }
 
+// A read-only int32 at a wave-uniform index, read through the constant address space so that it is
+// one scalar load: a plain load of caller memory is a vector load (the compiler cannot rule out
+// that the kernel writes it), whose whole round trip the first address computations would wait
+// for. Used for the per-sequence lengths, which no kernel writes.
+__device__ __forceinline__ int load_uniform_i32(const int32_t* p, int i) {
+  return ((const __attribute__((address_space(4))) int32_t*)p)[i];
+}
+
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
 }

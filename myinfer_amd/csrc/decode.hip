@@ -525,7 +525,7 @@ __global__ __launch_bounds__(NW * 64, (dec_min_wgs<D, BITS, NW, NSLOT, G>())) vo
   const int b = (int)div31((uint32_t)bk, p.d_hkv);
   const int kvh = bk - b * p.Hkv;
 
-  const int S_b = p.seq_lens ? min(max(p.seq_lens[b], 0), p.S) : p.S;  // clamped: never read past the view
+  const int S_b = p.seq_lens ? min(max(load_uniform_i32(p.seq_lens, b), 0), p.S) : p.S;  // clamped: never read past the view
   // the first key any row sees, rounded down to a tile boundary (tiles stay 32-aligned, so a tile of
   // a paged cache lies in one page; the keys before the window are masked)
   const int key_base = p.window > 0 ? max(0, S_b - p.L - p.window + 1) & ~(kTile - 1) : 0;

@@ -446,7 +446,7 @@ __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) 
   const int bk = wg / (p.rowblocks * p.nsplit);  // b * Hkv + kvh
   const int b = bk / p.Hkv, kvh = bk % p.Hkv;
   const int unit = bk * p.rowblocks + rb;
-  const int S_b = p.seq_lens ? min(max(p.seq_lens[b], 0), p.S) : p.S;
+  const int S_b = p.seq_lens ? min(max(load_uniform_i32(p.seq_lens, b), 0), p.S) : p.S;
 
   // ---- the workgroup's rows, their positions, and the key range they see
   const int fr0 = rb * kPRows;

@@ -320,7 +320,7 @@ __global__ __launch_bounds__(kWW * 64, 1) void wide_attn_kernel(WideParams p) {
   const int b = unit / (p.Hkv * p.rowblocks);
   const int kvh = (unit / p.rowblocks) % p.Hkv;
   const int rb = unit % p.rowblocks;
-  const int S_b = p.seq_lens ? min(max(p.seq_lens[b], 0), p.S) : p.S;
+  const int S_b = p.seq_lens ? min(max(load_uniform_i32(p.seq_lens, b), 0), p.S) : p.S;
 
   // the row block's positions: one head's contiguous run, or every position when it spans heads
   const int r0 = rb * kWRows, r1 = min(r0 + kWRows, p.nrows) - 1;
