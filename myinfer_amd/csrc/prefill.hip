@@ -1021,20 +1021,49 @@ __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) 
 #pragma unroll
     for (int db = 0; db < NDB; ++db) oacc[db] = macc[db];
   }
-  if (!row_ok) return;
+  // ---- output. A lane holds 8-byte pieces of one row; stored directly, each store instruction
+  // would write 8 bytes into each of 32 rows. Each wave instead stages its 32 rows in LDS (the
+  // rings are free once every wave is past this barrier) and stores whole rows: 16 bytes a lane, so
+  // an instruction writes 4 (D = 128) or 8 (D = 64) complete rows.
   // (after a split merge l_tot and oacc are in true units; else the V operands' 2^-ev returns here)
   const float inv = l_tot > 0.0f ? (1.0f / l_tot) * (p.nsplit > 1 ? 1.0f : vback) : 0.0f;
-  uint16_t* orow = p.out + (int64_t)b * p.o_sb + (int64_t)head * p.o_sh + (int64_t)lq * p.o_sl;
+  constexpr int OP = D + 8;                 // fp16 per staged row: rows shift by 4 banks
+  constexpr int WSB = 32 * OP * 2;          // staging bytes per wave
+  constexpr int NRW = kRawSlots * RC::SLOT / WSB;           // waves staged in the raw ring
+  constexpr int NVW = (DENSE ? 2 : 3) * D * kVS * 2 / WSB;  // ... and in the V^T ring
+  static_assert(NRW + NVW >= kPW, "every wave's rows fit the raw and V^T rings");
+  __syncthreads();
+  uint16_t* const stage =
+      (uint16_t*)(wave < NRW ? &raw[0][0] + wave * WSB : (uint8_t*)&v_lds[0][0] + (wave - NRW) * WSB);
 #pragma unroll
   for (int db = 0; db < NDB; ++db)
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-      const int d = 32 * db + 8 * c + 4 * hh;
       u2 w;
       w[0] = (uint32_t)from_float(oacc[db][4 * c] * inv, T{}) | ((uint32_t)from_float(oacc[db][4 * c + 1] * inv, T{}) << 16);
       w[1] = (uint32_t)from_float(oacc[db][4 * c + 2] * inv, T{}) | ((uint32_t)from_float(oacc[db][4 * c + 3] * inv, T{}) << 16);
-      *(u2*)(orow + d) = w;
+      *(u2*)(stage + qc * OP + 32 * db + 8 * c + 4 * hh) = w;
     }
+  // the output offset of this lane's row (lanes 0-31 own the wave's rows), read by the lanes that
+  // store it
+  const int64_t roff = (int64_t)b * p.o_sb + (int64_t)head * p.o_sh + (int64_t)lq * p.o_sl;
+  const int roff_lo = (int)(uint32_t)roff, roff_hi = (int)(roff >> 32);
+  __builtin_amdgcn_wave_barrier();  // the wave's LDS writes are issued before its reads (LDS keeps a wave's order)
+  constexpr int CPR = D / 8;   // 16-byte chunks per row
+  constexpr int RPI = 64 / CPR;  // rows per store instruction
+  const int cc = lane % CPR;
+#pragma unroll
+  for (int it = 0; it < 32 / RPI; ++it) {
+    const int r = it * RPI + lane / CPR;
+    const u4 v = *(const u4*)(stage + r * OP + 8 * cc);
+    const int64_t ro = (int64_t)(((uint64_t)(uint32_t)__shfl(roff_hi, r) << 32) | (uint32_t)__shfl(roff_lo, r));
+    if (fr0 + wave * 32 + r < p.nrows) {
+      // two 8-byte stores (the output is 8-byte aligned); the compiler issues them as one 16-byte store
+      uint16_t* dst = p.out + ro + 8 * cc;
+      *(u2*)dst = u2{v[0], v[1]};
+      *(u2*)(dst + 4) = u2{v[2], v[3]};
+    }
+  }
 }
 
 // ------------------------------------------------------------------------------------------
