@@ -425,7 +425,7 @@ int kvq_prefill_attn(const kvq_rows* q, const kvq_qtensor* k, const kvq_qtensor*
     return hip_status(kvq::launch_wide(q, k, v, seq_lens, out, B, Hq, Hkv, L, S, bits, group_size, dtype, scale, causal,
                                        window, workspace, (hipStream_t)stream),
                       "prefill_attn launch (head_dim 256)");
-  if ((rc = check_rows(out, "out", D, true))) return rc;  // rows are written 8 bytes at a time
+  if ((rc = check_rows(out, "out", D, true))) return rc;  // rows are stored 16 bytes at a time
   if ((rc = check_prefill_sb(k, v, D, group_size))) return rc;
   return hip_status(kvq::launch_prefill(q, k, v, seq_lens, out, B, Hq, Hkv, L, D, S, bits, group_size, dtype, scale,
                                         causal, window, workspace, (hipStream_t)stream),
@@ -486,7 +486,7 @@ int kvq_paged_prefill_attn(const kvq_rows* q, const kvq_qtensor* k_pool, const k
                                              Hq, Hkv, L, S, bits, group_size, dtype, scale, causal, window, workspace,
                                              (hipStream_t)stream),
                       "paged_prefill_attn launch (head_dim 256)");
-  if ((rc = check_rows(out, "out", D, true))) return rc;  // rows are written 8 bytes at a time
+  if ((rc = check_rows(out, "out", D, true))) return rc;  // rows are stored 16 bytes at a time
   if ((rc = check_prefill_sb(k_pool, v_pool, D, group_size))) return rc;
   return hip_status(kvq::launch_prefill_paged(q, k_pool, v_pool, num_pages, block_table, table_stride, seq_lens, out, B,
                                               Hq, Hkv, L, D, S, bits, group_size, dtype, scale, causal, window,

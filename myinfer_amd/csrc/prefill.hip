@@ -1058,10 +1058,7 @@ __global__ __launch_bounds__(kPW * 64, 1) void prefill_attn_kernel(PreParams p) 
     const u4 v = *(const u4*)(stage + r * OP + 8 * cc);
     const int64_t ro = (int64_t)(((uint64_t)(uint32_t)__shfl(roff_hi, r) << 32) | (uint32_t)__shfl(roff_lo, r));
     if (fr0 + wave * 32 + r < p.nrows) {
-      // two 8-byte stores (the output is 8-byte aligned); the compiler issues them as one 16-byte store
-      uint16_t* dst = p.out + ro + 8 * cc;
-      *(u2*)dst = u2{v[0], v[1]};
-      *(u2*)(dst + 4) = u2{v[2], v[3]};
+      *(u4*)(p.out + ro + 8 * cc) = v;  // the host checks 16-byte aligned rows and strides
     }
   }
 }

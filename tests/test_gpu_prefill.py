@@ -129,6 +129,30 @@ def test_blocked_sdpa_string_mask_routes_to_prefill():
     assert_close(out, ref, "string-mask")
 
 
+@pytest.mark.parametrize("D,S", [(128, 300), (128, 6000), (64, 300)])
+def test_output_views(D, S):
+    """Output rows stored whole from LDS, 16 bytes a lane: into a view 16 bytes past the start of
+    each row, with a row stride of D + 16 elements, and a partial last row block (with S = 6000 the
+    keys are split and merged). Every row matches the contiguous call bit for bit and the elements
+    around the rows keep their values. The prefill entry point requires 16-byte aligned rows and
+    strides; an 8-byte aligned view is rejected."""
+    print(f"prefill output view D={D} S={S}", flush=True)
+    B, Hq, Hkv, L = 1, 16, 4, 77  # 16 / 4 * 77 = 308 rows: a full and a partial row block
+    kt, vt = make_cache(B, Hkv, S, D, 8, torch.float16, 40 + D)
+    q = seeded_normal((B, Hq, L, D), 41 + D, torch.float16, DEV)
+    ref = kernels.attention(q, kt, vt, 0.1, causal=True, bits=8, kernel="prefill")
+    big = torch.full((B, Hq, L, D + 16), 5.0, dtype=torch.float16, device=DEV)
+    view = big[..., 8:8 + D]
+    out = kernels.attention(q, kt, vt, 0.1, causal=True, bits=8, kernel="prefill", out=view)
+    torch.cuda.synchronize()
+    assert out.data_ptr() == view.data_ptr()
+    assert torch.equal(view, ref)
+    assert torch.all(big[..., :8] == 5.0) and torch.all(big[..., 8 + D:] == 5.0)
+    assert_close(ref, exact_reference(q, kt, vt, 0.1, bits=8, causal=True), f"D={D} S={S}")
+    with pytest.raises(ValueError, match="16-byte aligned"):
+        kernels.attention(q, kt, vt, 0.1, causal=True, bits=8, kernel="prefill", out=big[..., 4:4 + D])
+
+
 def test_repeated_calls_are_bit_identical():
     # the key splits are merged in split order whichever workgroup merges them
     print("prefill repeat", flush=True)
