@@ -232,9 +232,10 @@ int kvq_decode_attn_dense_masked(const kvq_rows* q, const kvq_rows* k, const kvq
 /*
  * Attention for prefill chunks (any L): same contract as kvq_decode_attn, MFMA tiles with
  * K/V tiles dequantized into LDS. Replaces m5engine/attention.py:29-103 for L > 1.
- * Requirements: those of kvq_decode_attn; Hq a multiple of Hkv; at D = 64 or 128 with two or
- *   more scale groups per row, scale and bias rows 4-byte aligned (even strides; MLX's contiguous
- *   layout is).
+ * Requirements: those of kvq_decode_attn; Hq a multiple of Hkv; at D = 64 or 128 the output rows
+ *   are stored 16 bytes at a time, so out 16-byte aligned with strides in multiples of 8 elements;
+ *   there too, with two or more scale groups per row, scale and bias rows 4-byte aligned (even
+ *   strides; MLX's contiguous layout is).
  * D = 256 runs a kernel of its own (128 query rows per workgroup, 32-key tiles) whose split key
  * ranges are merged by a second, small launch on the same stream. Head dims other than 64, 128
  * and 256 run the decode kernel (any L) and take kvq_decode_attn's workspace size.
@@ -262,7 +263,9 @@ size_t kvq_prefill_workspace_size(int B, int Hq, int Hkv, int L, int D, int S, i
  * widths for any L (by the decode kernel up to 128 dims, by the head_dim-256 kernel past them; the
  * key rows must then be exactly D elements apart); rows 16-byte aligned with strides that are
  * multiples of 8 elements. At D = 256 both entry points run the head_dim-256 prefill kernel (any
- * L); the prefill entry point runs the same kernel at D = 64.
+ * L); the prefill entry point runs the same kernel at D = 64. At D = 128 the prefill entry point
+ * stores output rows 16 bytes at a time, so out must be 16-byte aligned with strides in multiples
+ * of 8 elements there too.
  */
 int kvq_decode_attn_dense(const kvq_rows* q, const kvq_rows* k, const kvq_rows* v,
                           const int32_t* seq_lens, const kvq_rows* out,

@@ -569,6 +569,7 @@ int kvq_prefill_attn_dense(const kvq_rows* q, const kvq_rows* k, const kvq_rows*
     return hip_status(kvq::launch_wide_dense(q, k, v, seq_lens, out, B, Hq, Hkv, L, D, S, dtype, scale, causal, window,
                                              workspace, (hipStream_t)stream),
                       "prefill_attn_dense launch (head_dim 64 / 256)");
+  if ((rc = check_rows(out, "out", D, true))) return rc;  // rows are stored 16 bytes at a time
   return hip_status(kvq::launch_prefill_dense(q, k, v, seq_lens, out, B, Hq, Hkv, L, D, S, dtype, scale, causal, window,
                                               workspace, (hipStream_t)stream),
                     "prefill_attn_dense launch");

@@ -219,3 +219,23 @@ def test_dense_repeated_calls_are_bit_identical():
     torch.cuda.synchronize()
     assert torch.equal(a, b) and torch.equal(c, d)
     assert np.isfinite(c.float().cpu().numpy()).all()
+
+
+def test_prefill_output_views():
+    """The D = 128 prefill kernel stores whole output rows 16 bytes a lane: a 16-byte aligned view
+    with a row stride of D + 16 elements gets the contiguous call's bits and keeps its neighbours;
+    an 8-byte aligned view is rejected by the entry point."""
+    print("dense prefill output view", flush=True)
+    B, Hq, Hkv, L, S, D = 1, 16, 4, 77, 700, 128  # 308 rows: a full and a partial row block
+    k, v = make_kv(B, Hkv, S, D, torch.bfloat16, 74)
+    q = seeded_normal((B, Hq, L, D), 75, torch.bfloat16, DEV)
+    ref = kernels.attention(q, k, v, 0.09, causal=True, kernel="prefill")
+    big = torch.full((B, Hq, L, D + 16), 3.0, dtype=torch.bfloat16, device=DEV)
+    view = big[..., 8:8 + D]
+    kernels.attention(q, k, v, 0.09, causal=True, kernel="prefill", out=view)
+    torch.cuda.synchronize()
+    assert torch.equal(view, ref)
+    assert torch.all(big[..., :8] == 3.0) and torch.all(big[..., 8 + D:] == 3.0)
+    assert_close(ref, exact(q, k, v, 0.09, causal=True), "dense prefill into a view")
+    with pytest.raises(ValueError, match="16-byte aligned"):
+        kernels.attention(q, k, v, 0.09, causal=True, kernel="prefill", out=big[..., 4:4 + D])
