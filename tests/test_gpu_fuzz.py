@@ -35,7 +35,7 @@ def _masks(rng, B, L, S):
     return causal, window, seq_lens
 
 
-@pytest.mark.parametrize("case", range(24))
+@pytest.mark.parametrize("case", range(48))
 def test_decode_fuzz(case):
     rng = random.Random(7100 + case)
     D, bits, dtype = rng.choice([64, 128]), rng.choice([4, 8]), rng.choice(DTYPES)
@@ -48,7 +48,7 @@ def test_decode_fuzz(case):
                 seed=7100 + case, cap=cap, outliers=rng.random() < 0.3, what=f"fuzz {case}")
 
 
-@pytest.mark.parametrize("case", range(24))
+@pytest.mark.parametrize("case", range(48))
 def test_prefill_fuzz(case):
     rng = random.Random(7200 + case)
     bits, dtype = rng.choice([4, 8]), rng.choice(DTYPES)
@@ -65,7 +65,7 @@ def _group(rng, D):
     return rng.choice([g for g in (32, 64, 128) if D // 4 <= g <= D])
 
 
-@pytest.mark.parametrize("case", range(16))
+@pytest.mark.parametrize("case", range(32))
 def test_decode_fuzz_groups_and_head_dims(case):
     # group sizes 32/64/128 and head_dim 64/128/256, with the masks, lengths and views above
     rng = random.Random(7500 + case)
@@ -80,7 +80,7 @@ def test_decode_fuzz_groups_and_head_dims(case):
                 seed=7500 + case, cap=cap, outliers=rng.random() < 0.3, group=group, what=f"fuzz-gd {case}")
 
 
-@pytest.mark.parametrize("case", range(16))
+@pytest.mark.parametrize("case", range(32))
 def test_prefill_fuzz_groups_and_head_dims(case):
     rng = random.Random(7600 + case)
     D, bits, dtype = rng.choice([64, 128]), rng.choice([4, 8]), rng.choice(DTYPES)
@@ -94,7 +94,7 @@ def test_prefill_fuzz_groups_and_head_dims(case):
                 seed=7600 + case, cap=cap, group=group, D=D, what=f"fuzz-gd {case}")
 
 
-@pytest.mark.parametrize("case", range(16))
+@pytest.mark.parametrize("case", range(32))
 def test_head_dim_256_fuzz(case):
     # the head_dim-256 kernel: quantized prefill (groups 64/128) and unquantized decode / prefill
     rng = random.Random(7700 + case)
@@ -119,7 +119,7 @@ def test_head_dim_256_fuzz(case):
                     seed=7700 + case, cap=cap, what=f"fuzz-d256 {case}")
 
 
-@pytest.mark.parametrize("case", range(16))
+@pytest.mark.parametrize("case", range(32))
 def test_other_head_dims_fuzz(case):
     # head dims other than 64/128/256 (the decode kernel at the next width, any query length):
     # quantized 32/96/192 at their groups, unquantized multiples of 8 up to 248, through either
@@ -142,7 +142,7 @@ def test_other_head_dims_fuzz(case):
                     window=window, seq_lens=seq_lens, seed=7900 + case, cap=cap, what=f"fuzz-hd {case}")
 
 
-@pytest.mark.parametrize("case", range(24))
+@pytest.mark.parametrize("case", range(48))
 def test_unquantized_fuzz(case):
     rng = random.Random(7300 + case)
     kernel = rng.choice(["decode", "prefill"])
@@ -158,7 +158,7 @@ def test_unquantized_fuzz(case):
                 seed=7300 + case, cap=cap, what=f"fuzz {case}")
 
 
-@pytest.mark.parametrize("case", range(16))
+@pytest.mark.parametrize("case", range(32))
 def test_paged_fuzz(case):
     # pools in shuffled 64-row pages, unused rows poisoned with NaN scales; the paged kernels must
     # equal the contiguous ones bit for bit, and both the oracle
