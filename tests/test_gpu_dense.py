@@ -239,3 +239,20 @@ def test_prefill_output_views():
     assert_close(ref, exact(q, k, v, 0.09, causal=True), "dense prefill into a view")
     with pytest.raises(ValueError, match="16-byte aligned"):
         kernels.attention(q, k, v, 0.09, causal=True, kernel="prefill", out=big[..., 4:4 + D])
+
+
+@pytest.mark.parametrize("D,L,kernel", [(128, 6, "decode"), (128, 90, "prefill"), (64, 90, "prefill"),
+                                        (256, 33, "prefill")])
+def test_sequences_shorter_than_the_chunk(D, L, kernel):
+    """Unquantized caches: a sequence with fewer keys than the chunk has queries leaves its first
+    rows at negative causal positions; they see no key and come out 0."""
+    print(f"dense short sequence D={D} L={L} {kernel}", flush=True)
+    B, Hq, Hkv, S = 2, 8, 2, 300
+    lens = [300, L // 2]
+    k, v = make_kv(B, Hkv, S, D, torch.float16, 76 + D)
+    q = seeded_normal((B, Hq, L, D), 77 + L, torch.float16, DEV)
+    seq = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    out = kernels.attention(q, k, v, 0.1, causal=True, seq_lens=seq, kernel=kernel)
+    torch.cuda.synchronize()
+    assert_close(out, exact(q, k, v, 0.1, causal=True, seq_lens=seq), f"dense short sequence D={D} {kernel}")
+    assert torch.all(out[1, :, :L - lens[1]] == 0)

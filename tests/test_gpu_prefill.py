@@ -246,3 +246,29 @@ def test_rising_key_norms(dtype, causal, bits):
     pst = OA.error_stats(port.float().numpy().astype(np.float64), ref)
     print(f"  gpu {st}  fp16-key floor {floor}  reference port {pst}", flush=True)
     assert st["max_abs"] <= pst["max_abs"] and st["rel_l2"] <= pst["rel_l2"], (st, pst)
+
+
+@pytest.mark.parametrize("D,L,kernel,window", [
+    (128, 5, "decode", 0), (128, 100, "prefill", 0), (128, 100, "prefill", 48), (64, 70, "prefill", 0),
+    (256, 40, "prefill", 0),
+])
+def test_sequences_shorter_than_the_chunk(D, L, kernel, window):
+    """A batch row whose sequence holds fewer keys than the chunk has queries: under the causal
+    mask its first rows sit at negative positions and see no key, so they come out 0 (the
+    reference's blocked path gives acc / max(denom, 1e-30) = 0); the rest see the keys up to their
+    position."""
+    print(f"short sequence D={D} L={L} {kernel} window={window}", flush=True)
+    B, Hq, Hkv, S = 2, 8, 2, 400
+    lens = [400, L // 2]
+    G = 64
+    kt, vt = make_cache(B, Hkv, S, D, 8, torch.bfloat16, 90 + D + L, group=G)
+    q = seeded_normal((B, Hq, L, D), 91 + L, torch.bfloat16, DEV)
+    seq = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    kw = dict(causal=True, window=window, seq_lens=seq, bits=8, group_size=G)
+    out = kernels.attention(q, kt, vt, 0.1, kernel=kernel, **kw)
+    torch.cuda.synchronize()
+    ref = exact_reference(q, kt, vt, 0.1, **kw)
+    assert_close(out, ref, f"short sequence D={D} L={L} {kernel}")
+    dark = L - lens[1]  # rows of sequence 1 at negative positions
+    assert torch.all(out[1, :, :dark] == 0)
+    assert torch.isfinite(out).all()
