@@ -58,6 +58,8 @@ def exact_attention(q: np.ndarray, kdq: np.ndarray, vdq: np.ndarray, scale: floa
     out = np.zeros((B, Hq, L, vdq.shape[-1]), np.float64)
     for b in range(B):
         S_b = S if seq_lens is None else int(seq_lens[b])
+        if S_b <= 0:
+            continue  # no key at all: every row of the sequence stays 0
         m = key_mask(L, S, S_b, causal, window)[:, :S_b]
         for h in range(Hkv):
             K = np.asarray(kdq[b, h, :S_b], np.float64)

@@ -256,3 +256,18 @@ def test_sequences_shorter_than_the_chunk(D, L, kernel):
     torch.cuda.synchronize()
     assert_close(out, exact(q, k, v, 0.1, causal=True, seq_lens=seq), f"dense short sequence D={D} {kernel}")
     assert torch.all(out[1, :, :L - lens[1]] == 0)
+
+
+@pytest.mark.parametrize("D,L,kernel", [(128, 1, "decode"), (128, 64, "prefill"), (64, 64, "prefill"),
+                                        (256, 20, "prefill")])
+def test_empty_sequence_in_batch(D, L, kernel):
+    """Unquantized caches: a batch row with seq_lens 0 returns 0 in every row."""
+    print(f"dense empty sequence D={D} L={L} {kernel}", flush=True)
+    B, Hq, Hkv, S = 2, 8, 2, 3000
+    k, v = make_kv(B, Hkv, S, D, torch.bfloat16, 78 + D)
+    q = seeded_normal((B, Hq, L, D), 79 + L, torch.bfloat16, DEV)
+    seq = torch.tensor([S, 0], dtype=torch.int32, device=DEV)
+    out = kernels.attention(q, k, v, 0.1, causal=True, seq_lens=seq, kernel=kernel)
+    torch.cuda.synchronize()
+    assert torch.all(out[1] == 0)
+    assert_close(out, exact(q, k, v, 0.1, causal=True, seq_lens=seq), f"dense empty sequence D={D} {kernel}")

@@ -272,3 +272,23 @@ def test_sequences_shorter_than_the_chunk(D, L, kernel, window):
     dark = L - lens[1]  # rows of sequence 1 at negative positions
     assert torch.all(out[1, :, :dark] == 0)
     assert torch.isfinite(out).all()
+
+
+@pytest.mark.parametrize("D,L,kernel,causal", [
+    (128, 1, "decode", False), (128, 1, "decode", True), (128, 64, "prefill", True), (64, 64, "prefill", False),
+    (256, 20, "prefill", True),
+])
+def test_empty_sequence_in_batch(D, L, kernel, causal):
+    """A batch row with no keys at all (seq_lens 0): every one of its rows sees no key and comes
+    out 0, with and without the causal mask, and with the keys split over workgroups for the
+    other row (S = 3000)."""
+    print(f"empty sequence D={D} L={L} {kernel} causal={causal}", flush=True)
+    B, Hq, Hkv, S = 2, 8, 2, 3000
+    kt, vt = make_cache(B, Hkv, S, D, 8, torch.float16, 95 + D + L)
+    q = seeded_normal((B, Hq, L, D), 96 + L, torch.float16, DEV)
+    seq = torch.tensor([S, 0], dtype=torch.int32, device=DEV)
+    kw = dict(causal=causal, seq_lens=seq, bits=8)
+    out = kernels.attention(q, kt, vt, 0.1, kernel=kernel, **kw)
+    torch.cuda.synchronize()
+    assert torch.all(out[1] == 0)
+    assert_close(out, exact_reference(q, kt, vt, 0.1, **kw), f"empty sequence D={D} {kernel}")

@@ -94,6 +94,21 @@ def test_fully_masked_rows_are_zero():
     assert np.all(out[0, 0, 0] == 0) and np.allclose(out[0, 0, 1], V[0, 0, 0])
 
 
+@pytest.mark.parametrize("causal", [False, True])
+def test_empty_sequence_is_zero(causal):
+    # a batch row with no keys (seq_lens 0) returns 0 in every row; the other row is the plain
+    # softmax average over its keys (a single query against all keys, checked by hand)
+    rng = np.random.default_rng(6)
+    q = rng.standard_normal((2, 1, 1, 4))
+    K = rng.standard_normal((2, 1, 5, 4))
+    V = rng.standard_normal((2, 1, 5, 4))
+    out = A.exact_attention(q, K, V, 0.5, causal=causal, seq_lens=[5, 0])
+    assert np.all(out[1] == 0)
+    s = 0.5 * K[0, 0] @ q[0, 0, 0]
+    w = np.exp(s - s.max())
+    assert np.allclose(out[0, 0, 0], (w / w.sum()) @ V[0, 0])
+
+
 def _fp32_triple(x, bits=8, G=64):
     c, s, b = Q.quantize_values(x, G, bits)
     return (torch.from_numpy(Q.pack(c, bits).astype(np.int64)).to(torch.int64),
