@@ -266,3 +266,23 @@ def test_paged_prefill_head_dim_64(bits, group):
     assert torch.equal(out_p, out_c)
     assert_close(out_p, exact_reference(q, kc, vc, scale, bits=bits, group_size=group, causal=True, seq_lens=sl),
                  "paged prefill D=64")
+
+
+@pytest.mark.parametrize("D,L,kernel", [(128, 1, "decode"), (128, 40, "prefill"), (256, 20, "prefill")])
+def test_paged_short_and_empty_sequences(D, L, kernel):
+    """Paged pools with one sequence shorter than the chunk (its first rows at negative causal
+    positions) and one with no keys at all: those rows come out 0, the pools' poisoned rows are
+    never read, and the result equals the contiguous call's bit for bit."""
+    print(f"paged short/empty sequences D={D} L={L} {kernel}", flush=True)
+    B, Hq, Hkv, bits, dtype = 3, 8, 2, 8, torch.float16
+    rows, tables, kp, vp, kc, vc = build(B, Hkv, [700, 64, 64], D, bits, dtype, 41)
+    lens = [700, L // 2, 0]
+    q = seeded_normal((B, Hq, L, D), 42, dtype, DEV)
+    sl = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    out_p = kernels.paged_attention(q, kp, vp, tables, sl, 0.1, causal=True, bits=bits, max_len=700, kernel=kernel)
+    out_c = kernels.attention(q, kc, vc, 0.1, causal=True, seq_lens=sl, bits=bits, kernel=kernel)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out_p.float()).all()
+    assert torch.all(out_p[2] == 0) and torch.all(out_p[1, :, :L - lens[1]] == 0)
+    assert torch.equal(out_p, out_c)
+    assert_close(out_p, exact_reference(q, kc, vc, 0.1, bits=bits, causal=True, seq_lens=sl), "paged short/empty")
