@@ -127,7 +127,7 @@ def test_capacity_padded_views():
     run_case(1, 8, 2, 1, 4097, 128, 4, torch.bfloat16, cap=4352, seed=9, what="padded-4bit")
 
 
-@pytest.mark.parametrize("name", ["C1", "C2-b1", "C2-b8", "C4", "C5-decode"])
+@pytest.mark.parametrize("name", ["C1", "C2-b1", "C2-b8", "C2-tp8", "C4", "C5-decode"])
 def test_baseline_configs(name):
     if name == "C1":
         # Qwen3-0.6B shapes, 4096 cached + 1 appended token
@@ -138,6 +138,9 @@ def test_baseline_configs(name):
         g = torch.Generator().manual_seed(1002)
         lens = torch.randint(16384, 32769, (8,), generator=g).tolist()
         st = run_case(8, 64, 8, 1, 32768, 128, 8, torch.float16, seq_lens=lens, seed=1012, what=name)
+    elif name == "C2-tp8":
+        # one GPU's share of C2 at tensor parallelism 8: one KV head, so the keys split 128 ways
+        st = run_case(1, 8, 1, 1, 32768, 128, 8, torch.float16, seed=1013, what=name)
     elif name == "C4":
         st = run_case(1, 64, 8, 1, 131072, 128, 4, torch.float16, seed=1004, outliers=True, what=name)
     else:
@@ -168,3 +171,13 @@ def test_repeated_calls_are_bit_identical():
             out = c()
             assert torch.equal(out, first[i]), f"repetition {rep}, case {i}: output changed"
     torch.cuda.synchronize()
+
+
+def test_large_batch_variable_lengths():
+    """32 sequences of lengths from 0 to 3000 (one empty, one of a single key) in one decode call:
+    many units, split and unsplit, merged in the kernel or by the combine launch."""
+    g = torch.Generator().manual_seed(1400)
+    lens = torch.randint(2, 3001, (32,), generator=g).tolist()
+    lens[5], lens[17], lens[30] = 0, 1, 3000
+    for dtype, bits in ((torch.float16, 8), (torch.bfloat16, 4)):
+        run_case(32, 32, 8, 1, 3000, 128, bits, dtype, seq_lens=lens, seed=1401 + bits, what=f"batch 32 {bits}-bit")
