@@ -5,9 +5,10 @@ work and synchronisations between the replays, and every replay is checked bit f
 same calls run eagerly.
 
 The plans cover both decode split merges (the in-kernel merge, whose arrival counters each call
-leaves at zero, and the combine launch) and the prefill kernel's in-kernel split merge. Nothing in
-the graphs is a memset: the workspaces are zeroed once, when they are allocated, outside the
-capture.
+leaves at zero, and the combine launch), the prefill kernel's in-kernel split merge, and a
+serving step over paged pools (per-sequence append positions and lengths read on the device).
+Nothing in the graphs is a memset: the workspaces are zeroed once, when they are allocated,
+outside the capture.
 """
 
 import math
@@ -88,4 +89,52 @@ def test_graph_replays_match_eager(name, B, Hq, Hkv, S, L, kernel, dtype):
                                else x[:, :, S - L:S].view(torch.int32)), f"replay {r}: appended rows differ"
         assert torch.equal(got_out, ref_out), f"replay {r}: the graph's attention differs from the eager call"
         assert torch.isfinite(other).all()
+    del graph
+
+
+def test_paged_decode_step_replays_match_eager():
+    """A serving step over paged pools captured as one graph: each sequence's new token appended at
+    its own position (starts) and the paged decode over seq_lens = starts + 1. New tokens and
+    queries are written in place between replays; every replay equals the same calls run eagerly,
+    bit for bit, and reads no poisoned pool row."""
+    from tests.test_gpu_paged import build
+
+    print("graph replay: paged decode step", flush=True)
+    B, Hq, Hkv, D, bits, dtype = 3, 16, 4, 128, 8, torch.float16
+    lens = [700, 300, 65]  # the next row of each sequence lies in its last page
+    rows, tables, kp, vp, kc, vc = build(B, Hkv, lens, D, bits, dtype, 1350)
+    starts = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    seq = starts + 1
+    S = max(lens) + 1
+    new_k = seeded_normal((B, Hkv, 1, D), 1351, dtype, DEV)
+    new_v = seeded_normal((B, Hkv, 1, D), 1352, dtype, DEV)
+    q = seeded_normal((B, Hq, 1, D), 1353, dtype, DEV)
+    out = torch.empty((B, Hq, 1, D), dtype=dtype, device=DEV)
+
+    def step(dst):
+        kernels.paged_quantize_append(new_k, kp, new_v, vp, tables, starts=starts, bits=bits)
+        return kernels.paged_attention(q, kp, vp, tables, seq, 0.1, causal=True, bits=bits, max_len=S, out=dst,
+                                       kernel="decode")
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step(out)  # warm-up on the capture stream: its workspace is allocated and zeroed here
+    side.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        step(out)
+
+    for r in range(4):
+        new_k.copy_(seeded_normal((B, Hkv, 1, D), 1360 + r, dtype, DEV))
+        new_v.copy_(seeded_normal((B, Hkv, 1, D), 1370 + r, dtype, DEV))
+        q.copy_(seeded_normal((B, Hq, 1, D), 1380 + r, dtype, DEV))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        got = out.clone()
+        ref = step(None)  # the same calls, eagerly, into a new output
+        torch.cuda.synchronize()
+        assert torch.isfinite(got.float()).all(), f"replay {r}: a poisoned pool row was read"
+        assert torch.equal(got, ref), f"replay {r}: the graph's paged decode differs from the eager call"
     del graph
