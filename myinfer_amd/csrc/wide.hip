@@ -238,7 +238,7 @@ __device__ __forceinline__ void wide_stage_k(const uint8_t* raw, uint8_t* kop, i
 // V of a raw tile into the V^T operand tile: thread t = 64 c + j dequantizes dims
 // [VPT j, VPT (j + 1)) (VPT = D / 64) of the 8 keys of slot chunk c and writes, for each of those
 // dims, the chunk's 8 slots (16 bytes) to row d at chunk position c ^ ((d >> 2) & 3) (rows are 64
-// bytes: 32 slots).
+// bytes: 32 slots), the row itself stored at row d ^ ((d >> 4) & 1).
 template <typename T, typename OT, int D, int BITS, int G, bool SCALED = false>
 __device__ __forceinline__ void wide_stage_v(const uint8_t* raw, uint8_t* vop, int t, bool& range_bad, float vmul) {
   using C = WideCfg<D, BITS, G>;
@@ -292,8 +292,10 @@ __device__ __forceinline__ void wide_stage_v(const uint8_t* raw, uint8_t* vop, i
         o[a] = perm(xp[2 * a + 1][i >> 1], xp[2 * a][i >> 1], (i & 1) ? 0x07060302u : 0x05040100u);
       }
     }
+    // row d is stored at row d ^ ((d >> 4) & 1): the 8 consecutive lanes of a write (rows 4 apart)
+    // then fill both 64-byte halves of a 128-byte bank window, 8 distinct 16-byte slots
     const int d = C::VPT * j + i;
-    *(u4*)(vop + d * (kWT * 2) + 16 * (c ^ ((d >> 2) & 3))) = o;
+    *(u4*)(vop + (d ^ ((d >> 4) & 1)) * (kWT * 2) + 16 * (c ^ ((d >> 2) & 3))) = o;
   }
 }
 
@@ -480,9 +482,9 @@ __global__ __launch_bounds__(kWW * 64, 1) void wide_attn_kernel(WideParams p) {
   for (int db = 0; db < C::NDB; ++db) oacc[db] = f16v{};
 
   // K operand of k-step j: key n, dims 16 j + 8 h .. + 8; V^T operand of column block db, k-step s:
-  // row d = 32 db + n, chunk position (2 s + h) ^ ((n >> 2) & 3)
+  // row d = 32 db + n (stored at row d ^ ((d >> 4) & 1)), chunk position (2 s + h) ^ ((n >> 2) & 3)
   const uint32_t k_off = (uint32_t)(n * C::KROW + 16 * h);
-  const uint32_t v_off = (uint32_t)(n * (kWT * 2));
+  const uint32_t v_off = (uint32_t)((n ^ ((n >> 4) & 1)) * (kWT * 2));  // row n's place (see wide_stage_v)
   const int v_sw = (n >> 2) & 3;
 
   // One step: tile t's products from operand buffers (kt, vt), and tile t + 1's staging from raw
